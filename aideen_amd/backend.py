@@ -1,0 +1,221 @@
+"""Host-side mirror of the reference's GPU backend surfaces, over the C ABI.
+
+Names, argument meaning and error behaviour follow the Rust API this path replaces:
+
+* ``GpuDeqBackend`` -- ``aideen-backbone/src/gpu_deq.rs:80-219``: ``new_blocking`` returns
+  ``None`` when no GPU is present (:3122-3124), ``upload_weights`` (:3529-3667),
+  ``reset_state`` (:3127-3164), ``run_forward_deq`` returning ``(h_next, iters)``
+  (:3687-3727), ``run_forward_deq_pooled`` (:3729-3768), readbacks ``read_hnext_seq`` /
+  ``read_hpooled_seq`` (:5833-5894) and the exact logits of
+  ``GpuLmHeadTrainer::read_exact_logits_from_h`` (gpu_lm_head.rs:1813-1879).
+* ``HipBlockBackend.fpm_batch_step`` -- ``BlockBackend`` (aideen-core/src/block_backend.rs:22-31).
+* ``HipComputeBackend`` -- ``ComputeBackend`` (aideen-core/src/compute.rs:11-23).
+
+Failures raise ``AdnError`` carrying the library's message (the Rust side returns
+``Err(&'static str)`` / ``Err(String)``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Dict, Optional
+
+import numpy as np
+
+from . import _lib
+from ._lib import AdnConfig, AdnOutputs, AdnRun, AdnWeights, check, lib
+
+_F32P = _lib.F32P
+_I32P = _lib.I32P
+
+
+def _fp(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], "float32 C-contiguous array expected"
+    return a.ctypes.data_as(_F32P)
+
+
+def _ip(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"], "int32 C-contiguous array expected"
+    return a.ctypes.data_as(_I32P)
+
+
+def _dev_f(t) -> Optional[C.POINTER(C.c_float)]:
+    return None if t is None else C.cast(C.c_void_p(t.data_ptr()), _F32P)
+
+
+def _dev_i(t) -> Optional[C.POINTER(C.c_int32)]:
+    return None if t is None else C.cast(C.c_void_p(t.data_ptr()), _I32P)
+
+
+def device_count() -> int:
+    n = C.c_int32(0)
+    check(lib().adn_device_count(C.byref(n)))
+    return n.value
+
+
+class GpuDeqBackend:
+    """One context on the current HIP device (single-threaded, like the reference backend)."""
+
+    def __init__(self, model, max_batch: int, max_seq: int):
+        self.model = model
+        cfg = AdnConfig(model.d, model.H, model.V, model.N, model.r, max_batch, max_seq,
+                        model.anderson_m, model.flags)
+        self._ctx = C.c_void_p()
+        check(lib().adn_create(C.byref(cfg), C.byref(self._ctx)))
+        self.max_batch, self.max_seq = max_batch, max_seq
+        self._weights_keepalive = None
+
+    @classmethod
+    def new_blocking(cls, model, max_batch: int = 1, max_seq: int = 1) -> Optional["GpuDeqBackend"]:
+        """``None`` when no GPU is present (gpu_deq.rs:3122-3124)."""
+        try:
+            return cls(model, max_batch, max_seq)
+        except _lib.AdnError as e:
+            if e.code == _lib.ADN_E_NO_DEVICE:
+                return None
+            raise
+
+    def close(self) -> None:
+        if self._ctx:
+            lib().adn_destroy(self._ctx)
+            self._ctx = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------------------------
+    def set_stream(self, stream_handle: Optional[int]) -> None:
+        check(lib().adn_set_stream(self._ctx, C.c_void_p(stream_handle) if stream_handle else None))
+
+    def synchronize(self) -> None:
+        check(lib().adn_synchronize(self._ctx))
+
+    def upload_weights(self, w: Dict[str, Optional[np.ndarray]], layout: int = _lib.ADN_LAYOUT_OUT_IN) -> None:
+        keep = {k: (None if v is None else np.ascontiguousarray(v, dtype=np.float32)) for k, v in w.items()}
+        cw = AdnWeights(**{k: _fp(keep.get(k)) for k in _lib.WEIGHT_FIELDS})
+        check(lib().adn_upload_weights(self._ctx, C.byref(cw), layout))
+        self._weights_keepalive = keep
+
+    def reset_state(self) -> None:
+        check(lib().adn_reset_state(self._ctx))
+
+    # ------------------------------------------------------------------------------------
+    def forward(self, tokens: Optional[np.ndarray] = None, s_in: Optional[np.ndarray] = None, *,
+                max_iters: Optional[int] = None, eps: Optional[float] = None,
+                damping: Optional[float] = None, want=("h_star", "pooled", "logits", "argmax", "iters",
+                                                        "scan_y", "scan_state"),
+                scan_state_in: Optional[np.ndarray] = None) -> Dict[str, np.ndarray]:
+        """Host-memory forward (blocking).  Returns the requested outputs."""
+        m = self.model
+        if tokens is not None:
+            tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+            B, T = tokens.shape
+        else:
+            s_in = np.ascontiguousarray(s_in, dtype=np.float32)
+            B, T = s_in.shape[:2]
+        run = AdnRun(B, T, m.max_iters if max_iters is None else max_iters,
+                     m.eps if eps is None else eps, m.beta if damping is None else damping,
+                     _ip(tokens), _fp(s_in),
+                     _fp(None if scan_state_in is None else np.ascontiguousarray(scan_state_in, np.float32)))
+        shapes = dict(h_star=((B, T, m.H, m.d), np.float32), pooled=((B, T, m.d), np.float32),
+                      logits=((B, T, m.V), np.float32), argmax=((B, T), np.int32),
+                      iters=((B, T), np.int32), scan_y=((B, T, m.H, m.d), np.float32),
+                      scan_state=((B, m.H, m.d, m.N), np.float32))
+        outs = {k: np.zeros(*shapes[k]) for k in want}
+        co = AdnOutputs(**{k: (_fp(v) if v.dtype == np.float32 else _ip(v)) for k, v in outs.items()})
+        check(lib().adn_forward(self._ctx, C.byref(run), C.byref(co)))
+        return outs
+
+    def forward_async(self, tokens=None, s_in=None, *, outputs: Dict[str, object],
+                      max_iters: Optional[int] = None, eps: Optional[float] = None,
+                      damping: Optional[float] = None, scan_state_in=None) -> None:
+        """Device-memory forward (enqueue only).  ``tokens`` / ``s_in`` / outputs are torch
+        tensors on the GPU (anything with ``data_ptr()``)."""
+        m = self.model
+        if tokens is not None:
+            B, T = tokens.shape
+        else:
+            B, T = s_in.shape[:2]
+        run = AdnRun(B, T, m.max_iters if max_iters is None else max_iters,
+                     m.eps if eps is None else eps, m.beta if damping is None else damping,
+                     _dev_i(tokens), _dev_f(s_in), _dev_f(scan_state_in))
+        co = AdnOutputs(h_star=_dev_f(outputs.get("h_star")), pooled=_dev_f(outputs.get("pooled")),
+                        logits=_dev_f(outputs.get("logits")), argmax=_dev_i(outputs.get("argmax")),
+                        iters=_dev_i(outputs.get("iters")), scan_y=_dev_f(outputs.get("scan_y")),
+                        scan_state=_dev_f(outputs.get("scan_state")))
+        check(lib().adn_forward_async(self._ctx, C.byref(run), C.byref(co)))
+
+    # reference-named conveniences ---------------------------------------------------------
+    def run_forward_deq(self, batch, seq, max_iters, eps, damping, s_in):
+        """``run_forward_deq`` (gpu_deq.rs:3687-3727): H_next [B*T*H*d] and iteration counts."""
+        s = np.asarray(s_in, np.float32).reshape(batch, seq, self.model.d)
+        o = self.forward(s_in=s, max_iters=max_iters, eps=eps, damping=damping, want=("h_star", "iters"))
+        return o["h_star"].reshape(-1), o["iters"].reshape(-1).astype(np.uint32)
+
+    def run_forward_deq_pooled(self, batch, seq, max_iters, eps, damping, s_in):
+        """``run_forward_deq_pooled`` (gpu_deq.rs:3729-3768): pooled [B*T*d] and iteration counts."""
+        s = np.asarray(s_in, np.float32).reshape(batch, seq, self.model.d)
+        o = self.forward(s_in=s, max_iters=max_iters, eps=eps, damping=damping, want=("pooled", "iters"))
+        return o["pooled"].reshape(-1), o["iters"].reshape(-1).astype(np.uint32)
+
+    def decode_greedy(self, start_tokens, n_new: int, *, max_iters=None, eps=None, damping=None):
+        m = self.model
+        start = np.ascontiguousarray(start_tokens, dtype=np.int32).reshape(-1)
+        out = np.zeros((start.size, n_new), np.int32)
+        check(lib().adn_decode_greedy(self._ctx, start.size, _ip(start), n_new,
+                                      m.max_iters if max_iters is None else max_iters,
+                                      m.eps if eps is None else eps, m.beta if damping is None else damping,
+                                      _ip(out)))
+        return out
+
+    # weight preparation --------------------------------------------------------------------
+    def spectral_norm(self, w: np.ndarray, n_iter: int = 20) -> float:
+        w = np.ascontiguousarray(w, np.float32)
+        s = C.c_float(0.0)
+        check(lib().adn_spectral_norm(self._ctx, _fp(w), w.shape[0], w.shape[1], n_iter, C.byref(s)))
+        return s.value
+
+    def normalize_if_needed(self, w: np.ndarray, threshold: float, n_iter: int = 20) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.float32).copy()
+        check(lib().adn_normalize_if_needed(self._ctx, _fp(w), w.shape[0], w.shape[1], threshold, n_iter))
+        return w
+
+
+class HipBlockBackend:
+    """``BlockBackend`` over HIP (the reference's WgpuBlockBackend, gpu_backend.rs:71-248)."""
+
+    def __init__(self, ctx_owner: GpuDeqBackend):
+        self._owner = ctx_owner
+
+    def fpm_batch_step(self, x, dt, a, b, c) -> np.ndarray:
+        arrs = [np.ascontiguousarray(v, np.float32) for v in (x, dt, a, b, c)]
+        d = arrs[0].size
+        if any(v.size != d for v in arrs):
+            raise _lib.AdnError(_lib.ADN_E_INVALID, "HipBlockBackend: dim mismatch")
+        y = np.zeros(d, np.float32)
+        check(lib().adn_block_step(self._owner._ctx, d, *[_fp(v) for v in arrs], _fp(y)))
+        return y
+
+
+class HipComputeBackend:
+    """``ComputeBackend`` over HIP (the reference's aideen-engine WgpuBackend)."""
+
+    def __init__(self, ctx_owner: GpuDeqBackend):
+        self._owner = ctx_owner
+
+    def load_tensor(self, data) -> int:
+        a = np.ascontiguousarray(data, np.float32).reshape(-1)
+        tid = C.c_int32(0)
+        check(lib().adn_load_tensor(self._owner._ctx, _fp(a), a.size, C.byref(tid)))
+        return tid.value
+
+    def ffn_forward(self, weights: int, inp: int, out_dim: int) -> np.ndarray:
+        y = np.zeros(out_dim, np.float32)
+        check(lib().adn_ffn_forward(self._owner._ctx, weights, inp, out_dim, _fp(y)))
+        return y

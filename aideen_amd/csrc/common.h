@@ -1,0 +1,56 @@
+// Shared definitions for the gfx950 kernels and the runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "aideen_hip.h"
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+#define ADN_WAVE 64
+
+// Device error flags (set by kernels, read back by adn_synchronize).
+#define ADN_DEVERR_TOKEN 1u
+
+namespace adn {
+
+// Error state of the calling thread (adn_last_error).
+void set_error(const std::string &msg);
+
+struct HipError {
+    hipError_t code;
+    std::string where;
+};
+
+#define ADN_HIP(call)                                                  \
+    do {                                                               \
+        hipError_t e_ = (call);                                        \
+        if (e_ != hipSuccess) throw ::adn::HipError{e_, #call};        \
+    } while (0)
+
+// Fixed parameters of a forward pass shared by the kernels.
+struct Dims {
+    int d, H, V, N, r;
+    uint32_t flags;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Sequential-in-slot order of the reference is kept where it matters (pooling); wave
+// reductions are tree-ordered (fp32 reassociation within the parity tolerance).
+
+}  // namespace adn

@@ -1,0 +1,168 @@
+// fp32 MFMA GEMM for the slot projections, the input projection, the carrier readout and the
+// LM head:  C[m][n] = sum_k A[row(m)][k] * B[n][k]  (+ epilogue), batched over slots.
+//
+// A and B are both k-contiguous ("NT"): A rows are token/slot state vectors, B rows are weight
+// rows W[s][out][:] (the y = W x orientation), so neither operand needs a transpose.
+//
+// Tiling for gfx950 (64-wide waves, v_mfma_f32_32x32x2f32, 64 FLOP/clk/SIMD fp32 peak):
+//   workgroup 256 threads = 4 waves in 2x2, block tile 128x128, k-step 32, double-buffered LDS
+//   (2 x (128+128) x 36 floats = 73.7 KB, 2 workgroups per CU); each wave owns 64x64 = 2x2
+//   MFMA 32x32 tiles (64 accumulators per lane).  A lane feeds 4 consecutive MFMAs from one
+//   ds_read_b128 of A and one of B: the k-pair of MFMA q on lane-half hh is {q, 4+q}, so the
+//   k order is a fixed permutation shared by A and B.
+//   Block order: slot-major, then groups of 8 m-tiles with n fastest inside a group, spread so
+//   each XCD (own L2) gets a contiguous range -> one slot's weights stay resident in one L2.
+#include "kernels.h"
+
+namespace adn {
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, NT = 256, GROUP_M = 8, NXCD = 8;
+
+__device__ __forceinline__ void map_block(int bid, int total, int nM, int nN, int &s, int &mt,
+                                          int &nt) {
+    // XCD-contiguous remap: hardware sends workgroup i to XCD i % 8.
+    const int q = total / NXCD, rem = total % NXCD;
+    const int x = bid % NXCD, j = bid / NXCD;
+    const int logical = x * q + (x < rem ? x : rem) + j;
+    const int per_slot = nM * nN;
+    s = logical / per_slot;
+    const int l = logical - s * per_slot;
+    const int group = l / (GROUP_M * nN);
+    const int first_m = group * GROUP_M;
+    const int gsz = min(nM - first_m, GROUP_M);
+    const int within = l - group * GROUP_M * nN;
+    mt = first_m + within % gsz;
+    nt = within / gsz;
+}
+
+__global__ __launch_bounds__(NT, 2) void k_gemm_nt(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float As[2][BM][LDK];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BN][LDK];
+
+    const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+    int s, mt, nt;
+    map_block(blockIdx.x, nM * nN * p.S, nM, nN, s, mt, nt);
+    const int M = p.m_count ? min(*p.m_count, p.M) : p.M;
+    const int m0 = mt * BM, n0 = nt * BN;
+    if (m0 >= M) return;
+
+    const int tid = threadIdx.x;
+    const int lrow = tid >> 3;       // 0..31
+    const int lk = (tid & 7) * 4;    // 0..28
+    const float *arow[4];
+    const float *brow[4];
+    bool aval[4], bval[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = m0 + lrow + 32 * j;
+        aval[j] = m < M;
+        long r = 0;
+        if (aval[j]) {
+            r = p.a_idx ? (long)p.a_idx[m] : (long)m;
+            if (p.a_idx && (r < 0 || r >= p.a_idx_max)) {
+                if (p.err) atomicOr(p.err, ADN_DEVERR_TOKEN);
+                r = 0;
+            }
+        }
+        arow[j] = p.A + r * p.a_sm + (long)s * p.a_ss;
+        const int n = n0 + lrow + 32 * j;
+        bval[j] = n < p.N;
+        brow[j] = p.B + (long)s * p.b_ss + (long)(bval[j] ? n : 0) * p.K;
+    }
+
+    floatx4 ga[4], gb[4];
+    auto gload = [&](int kt) {
+        const int k = kt * BK + lk;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ga[j] = aval[j] ? *reinterpret_cast<const floatx4 *>(arow[j] + k) : floatx4{0, 0, 0, 0};
+            gb[j] = bval[j] ? *reinterpret_cast<const floatx4 *>(brow[j] + k) : floatx4{0, 0, 0, 0};
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            *reinterpret_cast<floatx4 *>(&As[buf][lrow + 32 * j][lk]) = ga[j];
+            *reinterpret_cast<floatx4 *>(&Bs[buf][lrow + 32 * j][lk]) = gb[j];
+        }
+    };
+
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r = lane & 31, hh = lane >> 5;
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    const int nk = p.K / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 8) {
+            floatx4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const floatx4 *>(&As[buf][wm * 64 + i * 32 + r][kk + hh * 4]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const floatx4 *>(&Bs[buf][wn * 64 + j * 32 + r][kk + hh * 4]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][q], b[j][q], acc[i][j],
+                                                                          0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue.  Output layout of a 32x32 MFMA tile: lane holds column lane%32, register e holds
+    // row 8*(e/4) + 4*(lane/32) + e%4.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
+            if (m >= M) continue;
+            float *crow = p.C + (long)m * p.c_sm + (long)s * p.c_ss;
+            const float *res_row = nullptr;
+            if (p.epi == EPI_ADD_A) res_row = p.A + (long)m * p.a_sm + (long)s * p.a_ss;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 64 + j * 32 + r;
+                if (n >= p.N) continue;
+                float v = acc[i][j][e];
+                if (p.epi == EPI_BIAS) {
+                    if (n < p.bias_n) v += p.bias[(long)s * p.bias_ss + n];
+                } else if (p.epi == EPI_ADD_A) {
+                    v = res_row[n] + v;
+                }
+                crow[n] = v;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+void launch_gemm(const GemmParams &p, hipStream_t st) {
+    const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+    const int total = nM * nN * p.S;
+    if (total <= 0) return;
+    hipLaunchKernelGGL(k_gemm_nt, dim3(total), dim3(NT), 0, st, p);
+}
+
+}  // namespace adn

@@ -1,0 +1,100 @@
+// Kernel launch interfaces shared by the runtime (runtime.cpp) and the kernel sources.
+#pragma once
+
+#include "common.h"
+
+namespace adn {
+
+enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS = 1, EPI_ADD_A = 2 };
+
+// C[m][n] = sum_k A(m,s)[k] * B(s)[n][k] (+ epilogue), for m < M (or *m_count), n < N, s < S.
+//   A(m,s) = A + row(m)*a_sm + s*a_ss, row(m) = a_idx ? a_idx[m] : m   (a_idx checked < a_idx_max)
+//   B(s)   = B + s*b_ss, rows of length K
+//   C(m,s) = C + m*c_sm + s*c_ss
+struct GemmParams {
+    const float *A;
+    const int32_t *a_idx;
+    long a_sm, a_ss;
+    int a_idx_max;
+    const float *B;
+    long b_ss;
+    float *C;
+    long c_sm, c_ss;
+    const float *bias;
+    long bias_ss;
+    int bias_n;
+    int M, N, K, S;
+    const int32_t *m_count;
+    unsigned *err;
+    int epi;
+};
+void launch_gemm(const GemmParams &p, hipStream_t st);
+
+// ---- DEQ solve kernels (deq.hip) ------------------------------------------------------
+struct SolveBuffers {
+    float *signal;      // [ntok][H][d]
+    float *h;           // [ntok][H][d] iterate (in place)
+    float *qkv;         // [ntok][H][3d] compact by active index
+    float *mix;         // [ntok][H][d]  compact
+    float *o;           // [ntok][H][d]  compact
+    float *res_part;    // [ntok][H]     compact
+    int32_t *act[2];    // active token lists
+    int32_t *cnt;       // [4]: counts of act[0], act[1]; cnt[2] unused; cnt[3] = total tokens
+    int32_t *iters;     // [ntok]
+    float *hist;        // Anderson ring [m][ntok][H][d] or null
+    unsigned *err;
+};
+
+// h0 per token and the first active list (all tokens, in order).
+void launch_init(const Dims &D, const SolveBuffers &b, const float *x_src, const int32_t *tokens,
+                 int ntok, const float *anchor, hipStream_t st);
+// Slot attention: scores, softmax, mix for each active token.
+void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int ntok, hipStream_t st);
+// Damped RMS update and per-(token,slot) residual partials.
+void launch_update(const Dims &D, const SolveBuffers &b, int cur, int ntok, const float *anchor,
+                   const float *norm_scale, float beta, hipStream_t st);
+// Residual reduction, exit test, iteration counts and the next active list.
+void launch_converge(const Dims &D, const SolveBuffers &b, int cur, int ntok, int k, int max_iters,
+                     float eps, hipStream_t st);
+// Anderson store + mix for the tokens still active after iteration k.
+void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int k, int m,
+                     hipStream_t st);
+
+// ---- LM head (head.hip) -----------------------------------------------------------------
+// pooled = mean_s h*, pnorm = (pooled/rms(pooled, 1e-5)) * g
+void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
+                      float *pnorm, hipStream_t st);
+// argmax over each row of logits with the last-max tie rule.
+void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st);
+// S_in gather for the embedded-input path: x[t] = E[tok[t]] (for init/signal when tokens given)
+void launch_copy_tokens_from_argmax(const int32_t *argmax, int32_t *tokens, int32_t *out_seq,
+                                    int B, int n_new, int j, hipStream_t st);
+
+// ---- carrier scan (scan.hip) -------------------------------------------------------------
+struct ScanBuffers {
+    float *rec;        // [ntok][H][REC] per-(token,slot) record: rms, bn[r], B[N], C[N]
+    float *y;          // [ntok][H][d] pre-readout output (or final if no W_out)
+    float *chunk_s;    // [B][nch][H][d][N]
+    float *chunk_p;    // [B][nch][H][d]
+};
+int scan_rec_len(const Dims &D);
+void launch_scan_prep(const Dims &D, const float *h, int ntok, const float *w_kw, const float *w_b,
+                      const float *w_c, float *rec, hipStream_t st);
+void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, const float *a_log,
+                 const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in,
+                 float *y, float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st);
+int scan_chunks(int B, int T, int H, int d);
+
+// ---- misc (misc.hip) ----------------------------------------------------------------------
+void launch_spectral_norm(const float *w, int rows, int cols, int n_iter, float *sigma,
+                          float *work, hipStream_t st);
+void launch_scale_if(float *w, long n, const float *sigma, float threshold, hipStream_t st);
+void launch_zoh(int d, const float *x, const float *dt, const float *a, const float *b,
+                const float *c, float *y, hipStream_t st);
+void launch_gemv_colmajor(const float *w, const float *x, int in_dim, int out_dim, float *y,
+                          hipStream_t st);
+void launch_transpose(const float *src, int rows, int cols, long batch, float *dst,
+                      hipStream_t st);
+void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
+
+}  // namespace adn

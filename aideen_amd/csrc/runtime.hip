@@ -1,0 +1,713 @@
+// Runtime and C ABI (include/aideen_hip.h): one context per thread owns a HIP stream, the
+// device copies of the weights and the work buffers for its batch*seq capacity.
+//
+// Replaces the reference's wgpu device/queue runtime for this path: RustDeqBridge
+// (deq_bridge.rs:55-2785) and GpuDeqBackend's forward surface (gpu_deq.rs:80-219, 3454-4078).
+// The whole Picard loop is enqueued up front: the active-token count lives in device memory,
+// so no iteration reads anything back to the host (the reference submits one fused kernel per
+// forward and blocks on map_async, deq_bridge.rs:2017-2038).
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "kernels.h"
+
+using namespace adn;
+
+namespace adn {
+static thread_local std::string g_last_error;
+void set_error(const std::string &msg) { g_last_error = msg; }
+}  // namespace adn
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+
+struct adn_ctx {
+    adn_config cfg{};
+    Dims D{};
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    bool has_weights = false;
+    long cap_tok = 0;
+
+    // weights (device)
+    float *w_qkv = nullptr;  // [H][3d][d]
+    float *qk_bias = nullptr;  // [H][2d] or null
+    float *w_o = nullptr, *w_in = nullptr;  // [H][d][d]
+    float *anchor = nullptr, *norm_scale = nullptr, *embed = nullptr, *lm_w = nullptr;
+    float *lm_b = nullptr, *lm_g = nullptr, *a_log = nullptr, *wx_diag = nullptr, *w_out = nullptr;
+    float *b_delta = nullptr, *w_kw = nullptr, *w_vw = nullptr, *w_b = nullptr, *w_c = nullptr;
+
+    // work buffers (capacity-sized)
+    SolveBuffers sb{};
+    ScanBuffers scb{};
+    int scan_nch_cap = 1;
+    float *pnorm = nullptr;
+    float *logits_scratch = nullptr;  // lazy [cap_tok][V]
+    int32_t *argmax_scratch = nullptr;
+    unsigned *d_err = nullptr;
+
+    // host-API staging (lazy, capacity-sized)
+    std::vector<DevBuf> staging;
+    int32_t *tok_dev = nullptr;
+    float *sin_dev = nullptr;
+
+    // ComputeBackend tensors
+    std::vector<DevBuf> tensors;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+void *dmalloc(adn_ctx *c, size_t bytes) {
+    void *p = nullptr;
+    if (bytes == 0) bytes = 4;
+    ADN_HIP(hipMalloc(&p, bytes));
+    c->allocs.push_back(p);
+    return p;
+}
+
+void dfree_all(adn_ctx *c) {
+    for (void *p : c->allocs) (void)hipFree(p);
+    c->allocs.clear();
+    for (auto &t : c->tensors)
+        if (t.p) (void)hipFree(t.p);
+    c->tensors.clear();
+}
+
+int fail(int code, const std::string &msg) {
+    set_error(msg);
+    return code;
+}
+
+int hip_fail(const HipError &e) {
+    return fail(ADN_E_HIP, std::string("HIP error ") + hipGetErrorString(e.code) + " in " + e.where);
+}
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+std::string validate_config(const adn_config &c) {
+    if (c.d_r < 64 || c.d_r > 2048 || !is_pow2(c.d_r)) return "d_r must be a power of two in [64, 2048]";
+    if (!(c.h_slots == 1 || c.h_slots == 2 || c.h_slots == 4 || c.h_slots == 8 || c.h_slots == 16))
+        return "h_slots must be 1, 2, 4, 8 or 16";
+    if (c.vocab < 1) return "vocab must be >= 1";
+    if (c.d_state < 1 || c.d_state > 32) return "d_state must be in [1, 32]";
+    if (c.rank < 1 || c.rank > 64) return "rank must be in [1, 64]";
+    if (c.max_batch < 1 || c.max_seq < 1) return "max_batch and max_seq must be >= 1";
+    if ((long)c.max_batch * c.max_seq > (1L << 24)) return "max_batch*max_seq must be <= 2^24";
+    if (c.anderson_m < 0 || c.anderson_m > 5) return "anderson_m must be in [0, 5]";
+    if (c.flags & ~0x3Fu) return "unknown flag bits";
+    return "";
+}
+
+void upload(adn_ctx *c, float **dst, const float *src, size_t n, const char *name, bool required) {
+    if (!src) {
+        if (required) throw std::string("missing weight tensor: ") + name;
+        *dst = nullptr;
+        return;
+    }
+    if (!*dst) *dst = (float *)dmalloc(c, n * sizeof(float));
+    ADN_HIP(hipMemcpyAsync(*dst, src, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+}
+
+// Copy a [H][rows][cols] host tensor to the device, transposing each matrix when asked.
+void upload_mats(adn_ctx *c, float *dst, const float *src, int H, int rows, int cols, bool transpose,
+                 float *tmp) {
+    const size_t n = (size_t)H * rows * cols;
+    if (!transpose) {
+        ADN_HIP(hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        return;
+    }
+    ADN_HIP(hipMemcpyAsync(tmp, src, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    launch_transpose(tmp, rows, cols, H, dst, c->stream);
+}
+
+float *staging_f(adn_ctx *c, int slot, size_t bytes) {
+    if ((int)c->staging.size() <= slot) c->staging.resize(slot + 1);
+    DevBuf &b = c->staging[slot];
+    if (b.bytes < bytes) {
+        if (b.p) (void)hipFree(b.p);
+        b.p = nullptr;
+        ADN_HIP(hipMalloc(&b.p, bytes));
+        b.bytes = bytes;
+    }
+    return (float *)b.p;
+}
+
+// ---------------------------------------------------------------------------------------
+// the forward pipeline (device pointers; enqueue only)
+// ---------------------------------------------------------------------------------------
+void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
+    const Dims &D = c->D;
+    const int ntok = r.batch * r.seq;
+    const int d = D.d, H = D.H;
+    hipStream_t st = c->stream;
+    SolveBuffers b = c->sb;
+    if (o.h_star) b.h = o.h_star;
+    if (o.iters) b.iters = o.iters;
+
+    // signal[t][s] = W_in[s] x_t   (x gathered from the embedding when tokens are given)
+    {
+        GemmParams g{};
+        g.A = r.tokens ? c->embed : r.s_in;
+        g.a_idx = r.tokens;
+        g.a_idx_max = D.V;
+        g.a_sm = d;
+        g.a_ss = 0;
+        g.B = c->w_in;
+        g.b_ss = (long)d * d;
+        g.C = b.signal;
+        g.c_sm = (long)H * d;
+        g.c_ss = d;
+        g.M = ntok;
+        g.N = d;
+        g.K = d;
+        g.S = H;
+        g.err = b.err;
+        g.epi = EPI_NONE;
+        launch_gemm(g, st);
+    }
+    launch_init(D, b, r.tokens ? c->embed : r.s_in, r.tokens, ntok, c->anchor, st);
+
+    const int m = c->cfg.anderson_m;
+    for (int k = 0; k < r.max_iters; ++k) {
+        const int cur = k & 1;
+        {  // Q|K|V for every slot of every active token
+            GemmParams g{};
+            g.A = b.h;
+            g.a_idx = b.act[cur];
+            g.a_idx_max = ntok;
+            g.a_sm = (long)H * d;
+            g.a_ss = d;
+            g.B = c->w_qkv;
+            g.b_ss = 3L * d * d;
+            g.C = b.qkv;
+            g.c_sm = 3L * H * d;
+            g.c_ss = 3L * d;
+            g.bias = c->qk_bias;
+            g.bias_ss = 2L * d;
+            g.bias_n = 2 * d;
+            g.M = ntok;
+            g.N = 3 * d;
+            g.K = d;
+            g.S = H;
+            g.m_count = b.cnt + cur;
+            g.err = b.err;
+            g.epi = c->qk_bias ? EPI_BIAS : EPI_NONE;
+            launch_gemm(g, st);
+        }
+        launch_attn(D, b, cur, ntok, st);
+        {  // o = W_o mix
+            GemmParams g{};
+            g.A = b.mix;
+            g.a_sm = (long)H * d;
+            g.a_ss = d;
+            g.B = c->w_o;
+            g.b_ss = (long)d * d;
+            g.C = b.o;
+            g.c_sm = (long)H * d;
+            g.c_ss = d;
+            g.M = ntok;
+            g.N = d;
+            g.K = d;
+            g.S = H;
+            g.m_count = b.cnt + cur;
+            g.err = b.err;
+            g.epi = EPI_NONE;
+            launch_gemm(g, st);
+        }
+        launch_update(D, b, cur, ntok, c->anchor, c->norm_scale, r.damping, st);
+        launch_converge(D, b, cur, ntok, k, r.max_iters, r.eps, st);
+        if (m > 0 && k + 1 < r.max_iters) launch_anderson(D, b, cur ^ 1, ntok, k, m, st);
+    }
+
+    // LM head
+    const bool want_logits = o.logits || o.argmax;
+    if (o.pooled || want_logits)
+        launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr, st);
+    if (want_logits) {
+        float *logits = o.logits;
+        if (!logits) {
+            if (!c->logits_scratch)
+                c->logits_scratch = (float *)dmalloc(c, (size_t)c->cap_tok * D.V * sizeof(float));
+            logits = c->logits_scratch;
+        }
+        GemmParams g{};
+        g.A = c->pnorm;
+        g.a_sm = d;
+        g.B = c->lm_w;
+        g.C = logits;
+        g.c_sm = D.V;
+        g.bias = c->lm_b;
+        g.bias_n = D.V;
+        g.M = ntok;
+        g.N = D.V;
+        g.K = d;
+        g.S = 1;
+        g.err = b.err;
+        g.epi = c->lm_b ? EPI_BIAS : EPI_NONE;
+        launch_gemm(g, st);
+        if (o.argmax) launch_argmax(logits, ntok, D.V, o.argmax, st);
+    }
+
+    // temporal carrier
+    if (o.scan_y || o.scan_state) {
+        launch_scan_prep(D, b.h, ntok, c->w_kw, c->w_b, c->w_c, c->scb.rec, st);
+        // chunk buffers hold max_batch * scan_nch_cap sequence-chunks
+        const int nch_fit = std::max(1, (c->cfg.max_batch * c->scan_nch_cap) / r.batch);
+        const int nch = std::min(std::min(scan_chunks(r.batch, r.seq, H, d), c->scan_nch_cap), nch_fit);
+        float *y = (o.scan_y && !c->w_out) ? o.scan_y : c->scb.y;
+        launch_scan(D, b.h, c->scb.rec, r.batch, r.seq, c->a_log, c->wx_diag, c->b_delta, c->w_vw,
+                    r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch, st);
+        if (o.scan_y && c->w_out) {
+            GemmParams g{};
+            g.A = y;
+            g.a_sm = (long)H * d;
+            g.a_ss = d;
+            g.B = c->w_out;
+            g.b_ss = (long)d * d;
+            g.C = o.scan_y;
+            g.c_sm = (long)H * d;
+            g.c_ss = d;
+            g.M = ntok;
+            g.N = d;
+            g.K = d;
+            g.S = H;
+            g.err = b.err;
+            g.epi = EPI_ADD_A;
+            launch_gemm(g, st);
+        }
+    }
+}
+
+int check_run(adn_ctx *c, const adn_run *r) {
+    if (!c) return fail(ADN_E_INVALID, "null context");
+    if (!r) return fail(ADN_E_INVALID, "null run");
+    if (!c->has_weights) return fail(ADN_E_NO_WEIGHTS, "forward before adn_upload_weights");
+    if (r->batch < 1 || r->seq < 1) return fail(ADN_E_INVALID, "batch and seq must be >= 1");
+    if ((long)r->batch * r->seq > c->cap_tok)
+        return fail(ADN_E_CAPACITY, "batch*seq exceeds the context capacity");
+    if (r->max_iters < 1) return fail(ADN_E_INVALID, "max_iters must be >= 1");
+    if (!(r->damping > 0.0f && r->damping <= 1.0f)) return fail(ADN_E_INVALID, "damping must be in (0, 1]");
+    if (!(r->eps >= 0.0f)) return fail(ADN_E_INVALID, "eps must be >= 0");
+    if ((r->tokens == nullptr) == (r->s_in == nullptr))
+        return fail(ADN_E_INVALID, "exactly one of tokens / s_in must be given");
+    return ADN_OK;
+}
+
+int check_device_error(adn_ctx *c) {
+    unsigned err = 0;
+    ADN_HIP(hipMemcpyAsync(&err, c->d_err, sizeof(unsigned), hipMemcpyDeviceToHost, c->stream));
+    ADN_HIP(hipStreamSynchronize(c->stream));
+    if (err) {
+        ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        if (err & ADN_DEVERR_TOKEN) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
+        return fail(ADN_E_INVALID, "device-side error");
+    }
+    return ADN_OK;
+}
+
+}  // namespace
+
+// =========================================================================================
+// C ABI
+// =========================================================================================
+extern "C" {
+
+int adn_abi_version(void) { return ADN_ABI_VERSION; }
+
+const char *adn_last_error(void) { return g_last_error.c_str(); }
+
+int adn_device_count(int32_t *count) {
+    if (!count) return fail(ADN_E_INVALID, "null count");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return ADN_OK;
+}
+
+int adn_create(const adn_config *cfg, adn_ctx **out) {
+    if (!cfg || !out) return fail(ADN_E_INVALID, "null argument");
+    *out = nullptr;
+    const std::string msg = validate_config(*cfg);
+    if (!msg.empty()) return fail(ADN_E_INVALID, msg);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(ADN_E_NO_DEVICE, "no HIP device");
+    adn_ctx *c = new adn_ctx();
+    try {
+        c->cfg = *cfg;
+        c->D = Dims{cfg->d_r, cfg->h_slots, cfg->vocab, cfg->d_state, cfg->rank, cfg->flags};
+        ADN_HIP(hipGetDevice(&c->device));
+        ADN_HIP(hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking));
+        c->stream = c->own_stream;
+        const long T = (long)cfg->max_batch * cfg->max_seq;
+        c->cap_tok = T;
+        const long d = cfg->d_r, H = cfg->h_slots;
+        const size_t hd = (size_t)T * H * d * sizeof(float);
+        SolveBuffers &b = c->sb;
+        b.signal = (float *)dmalloc(c, hd);
+        b.h = (float *)dmalloc(c, hd);
+        b.qkv = (float *)dmalloc(c, 3 * hd);
+        b.mix = (float *)dmalloc(c, hd);
+        b.o = (float *)dmalloc(c, hd);
+        b.res_part = (float *)dmalloc(c, (size_t)T * H * sizeof(float));
+        b.act[0] = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        b.act[1] = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        b.cnt = (int32_t *)dmalloc(c, 4 * sizeof(int32_t));
+        b.iters = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
+        c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
+        b.err = c->d_err;
+        ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
+        c->pnorm = (float *)dmalloc(c, (size_t)T * d * sizeof(float));
+        c->argmax_scratch = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        c->scb.rec = (float *)dmalloc(c, (size_t)T * H * scan_rec_len(c->D) * sizeof(float));
+        c->scb.y = (float *)dmalloc(c, hd);
+        c->scan_nch_cap = 16;
+        const size_t chunk_states = (size_t)cfg->max_batch * c->scan_nch_cap * H * d;
+        c->scb.chunk_s = (float *)dmalloc(c, chunk_states * cfg->d_state * sizeof(float));
+        c->scb.chunk_p = (float *)dmalloc(c, chunk_states * sizeof(float));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        int rc = hip_fail(e);
+        dfree_all(c);
+        if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return rc;
+    }
+    *out = c;
+    return ADN_OK;
+}
+
+void adn_destroy(adn_ctx *c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    dfree_all(c);
+    for (auto &b : c->staging)
+        if (b.p) (void)hipFree(b.p);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    delete c;
+}
+
+int adn_set_stream(adn_ctx *c, void *s) {
+    if (!c) return fail(ADN_E_INVALID, "null context");
+    try {
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    c->stream = s ? (hipStream_t)s : c->own_stream;
+    return ADN_OK;
+}
+
+int adn_synchronize(adn_ctx *c) {
+    if (!c) return fail(ADN_E_INVALID, "null context");
+    try {
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+}
+
+int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
+    if (!c || !w) return fail(ADN_E_INVALID, "null argument");
+    if (layout != ADN_LAYOUT_OUT_IN && layout != ADN_LAYOUT_IN_OUT) return fail(ADN_E_INVALID, "unknown layout");
+    const adn_config &cf = c->cfg;
+    const int d = cf.d_r, H = cf.h_slots, V = cf.vocab, N = cf.d_state, r = cf.rank;
+    const size_t mat = (size_t)d * d;
+    try {
+        for (const float *p : {w->w_q, w->w_k, w->w_v, w->w_o, w->w_in, w->anchor, w->norm_scale, w->embed,
+                               w->lm_w, w->a_log, w->wx_diag})
+            if (!p) return fail(ADN_E_INVALID, "missing required weight tensor");
+        if ((cf.flags & ADN_F_SCAN_SELECTIVE) && (!w->w_kw || !w->w_vw))
+            return fail(ADN_E_INVALID, "selective carrier needs w_kw and w_vw");
+        if ((w->w_b == nullptr) != (w->w_c == nullptr)) return fail(ADN_E_INVALID, "w_b and w_c go together");
+        float *tmp = staging_f(c, 15, (size_t)H * mat * sizeof(float));
+        const bool in_out = layout == ADN_LAYOUT_IN_OUT;
+        if (!c->w_qkv) c->w_qkv = (float *)dmalloc(c, 3 * H * mat * sizeof(float));
+        if (!c->w_o) c->w_o = (float *)dmalloc(c, H * mat * sizeof(float));
+        if (!c->w_in) c->w_in = (float *)dmalloc(c, H * mat * sizeof(float));
+        // W_qkv[s] = [W_q[s]; W_k[s]; W_v[s]] as rows [3d][d]: one strided transpose/copy per part.
+        const float *parts[3] = {w->w_q, w->w_k, w->w_v};
+        float *qkv_tmp = staging_f(c, 14, H * mat * sizeof(float));
+        for (int p = 0; p < 3; ++p) {
+            upload_mats(c, qkv_tmp, parts[p], H, d, d, in_out, tmp);
+            ADN_HIP(hipMemcpy2DAsync(c->w_qkv + p * mat, 3 * mat * sizeof(float), qkv_tmp, mat * sizeof(float),
+                                     mat * sizeof(float), H, hipMemcpyDeviceToDevice, c->stream));
+        }
+        upload_mats(c, c->w_o, w->w_o, H, d, d, in_out, tmp);
+        // signal = W_in x, or W_in^T x under ADN_F_WIN_TRANSPOSED: the GEMM wants rows = outputs.
+        const bool win_t = (cf.flags & ADN_F_WIN_TRANSPOSED) != 0;
+        upload_mats(c, c->w_in, w->w_in, H, d, d, in_out != win_t, tmp);
+        if (w->q_bias || w->k_bias) {
+            if (!c->qk_bias) c->qk_bias = (float *)dmalloc(c, 2 * (size_t)H * d * sizeof(float));
+            ADN_HIP(hipMemsetAsync(c->qk_bias, 0, 2 * (size_t)H * d * sizeof(float), c->stream));
+            if (w->q_bias)
+                ADN_HIP(hipMemcpy2DAsync(c->qk_bias, 2 * d * sizeof(float), w->q_bias, d * sizeof(float),
+                                         d * sizeof(float), H, hipMemcpyHostToDevice, c->stream));
+            if (w->k_bias)
+                ADN_HIP(hipMemcpy2DAsync(c->qk_bias + d, 2 * d * sizeof(float), w->k_bias, d * sizeof(float),
+                                         d * sizeof(float), H, hipMemcpyHostToDevice, c->stream));
+        } else {
+            c->qk_bias = nullptr;
+        }
+        upload(c, &c->anchor, w->anchor, (size_t)H * d, "anchor", true);
+        upload(c, &c->norm_scale, w->norm_scale, d, "norm_scale", true);
+        upload(c, &c->embed, w->embed, (size_t)V * d, "embed", true);
+        upload(c, &c->lm_w, w->lm_w, (size_t)V * d, "lm_w", true);
+        upload(c, &c->lm_b, w->lm_b, V, "lm_b", false);
+        upload(c, &c->lm_g, w->lm_g, d, "lm_g", false);
+        upload(c, &c->a_log, w->a_log, (size_t)H * d, "a_log", true);
+        upload(c, &c->wx_diag, w->wx_diag, (size_t)H * d, "wx_diag", true);
+        if (w->w_out) {
+            if (!c->w_out) c->w_out = (float *)dmalloc(c, H * mat * sizeof(float));
+            upload_mats(c, c->w_out, w->w_out, H, d, d, in_out, tmp);
+        } else {
+            c->w_out = nullptr;
+        }
+        upload(c, &c->b_delta, w->b_delta, (size_t)H * d, "b_delta", false);
+        upload(c, &c->w_kw, w->w_kw, (size_t)H * d * r, "w_kw", false);
+        upload(c, &c->w_vw, w->w_vw, (size_t)H * r * d, "w_vw", false);
+        upload(c, &c->w_b, w->w_b, (size_t)H * N * d, "w_b", false);
+        upload(c, &c->w_c, w->w_c, (size_t)H * N * d, "w_c", false);
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    } catch (const std::string &s) {
+        return fail(ADN_E_INVALID, s);
+    }
+    c->has_weights = true;
+    return ADN_OK;
+}
+
+int adn_reset_state(adn_ctx *c) {
+    if (!c) return fail(ADN_E_INVALID, "null context");
+    // The carried carrier state is caller-owned (adn_run.scan_state_in); the context keeps no
+    // state between calls besides the device error flag, which is cleared here.
+    try {
+        ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_forward_async(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
+    int rc = check_run(c, r);
+    if (rc) return rc;
+    if (!o) return fail(ADN_E_INVALID, "null outputs");
+    try {
+        enqueue_forward(c, *r, *o);
+        ADN_HIP(hipGetLastError());
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
+    int rc = check_run(c, r);
+    if (rc) return rc;
+    if (!o) return fail(ADN_E_INVALID, "null outputs");
+    const long ntok = (long)r->batch * r->seq;
+    const Dims &D = c->D;
+    if (r->tokens) {
+        for (long i = 0; i < ntok; ++i)
+            if (r->tokens[i] < 0 || r->tokens[i] >= D.V)
+                return fail(ADN_E_INVALID, "token id outside [0, vocab)");
+    }
+    try {
+        adn_run dr = *r;
+        if (r->tokens) {
+            if (!c->tok_dev) c->tok_dev = (int32_t *)dmalloc(c, (size_t)c->cap_tok * sizeof(int32_t));
+            ADN_HIP(hipMemcpyAsync(c->tok_dev, r->tokens, ntok * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+            dr.tokens = c->tok_dev;
+        } else {
+            float *sd = staging_f(c, 8, (size_t)ntok * D.d * sizeof(float));
+            ADN_HIP(hipMemcpyAsync(sd, r->s_in, (size_t)ntok * D.d * sizeof(float), hipMemcpyHostToDevice, c->stream));
+            dr.s_in = sd;
+        }
+        const size_t hsz = (size_t)ntok * D.H * D.d, stsz = (size_t)r->batch * D.H * D.d * D.N;
+        if (r->scan_state_in) {
+            float *si = staging_f(c, 9, stsz * sizeof(float));
+            ADN_HIP(hipMemcpyAsync(si, r->scan_state_in, stsz * sizeof(float), hipMemcpyHostToDevice, c->stream));
+            dr.scan_state_in = si;
+        }
+        adn_outputs dout{};
+        if (o->h_star) dout.h_star = staging_f(c, 0, hsz * sizeof(float));
+        if (o->pooled) dout.pooled = staging_f(c, 1, (size_t)ntok * D.d * sizeof(float));
+        if (o->logits) dout.logits = staging_f(c, 2, (size_t)ntok * D.V * sizeof(float));
+        if (o->argmax) dout.argmax = (int32_t *)staging_f(c, 3, (size_t)ntok * sizeof(int32_t));
+        if (o->iters) dout.iters = (int32_t *)staging_f(c, 4, (size_t)ntok * sizeof(int32_t));
+        if (o->scan_y) dout.scan_y = staging_f(c, 5, hsz * sizeof(float));
+        if (o->scan_state) dout.scan_state = staging_f(c, 6, stsz * sizeof(float));
+        enqueue_forward(c, dr, dout);
+        ADN_HIP(hipGetLastError());
+        auto d2h = [&](void *dst, const void *src, size_t bytes) {
+            if (dst) ADN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+        };
+        d2h(o->h_star, dout.h_star, hsz * sizeof(float));
+        d2h(o->pooled, dout.pooled, (size_t)ntok * D.d * sizeof(float));
+        d2h(o->logits, dout.logits, (size_t)ntok * D.V * sizeof(float));
+        d2h(o->argmax, dout.argmax, (size_t)ntok * sizeof(int32_t));
+        d2h(o->iters, dout.iters, (size_t)ntok * sizeof(int32_t));
+        d2h(o->scan_y, dout.scan_y, hsz * sizeof(float));
+        d2h(o->scan_state, dout.scan_state, stsz * sizeof(float));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+}
+
+int adn_decode_greedy(adn_ctx *c, int32_t batch, const int32_t *start, int32_t n_new, int32_t max_iters,
+                      float eps, float damping, int32_t *out_tokens) {
+    if (!c || !start || !out_tokens) return fail(ADN_E_INVALID, "null argument");
+    if (!c->has_weights) return fail(ADN_E_NO_WEIGHTS, "decode before adn_upload_weights");
+    if (batch < 1 || n_new < 0) return fail(ADN_E_INVALID, "batch must be >= 1 and n_new >= 0");
+    if (batch > c->cap_tok) return fail(ADN_E_CAPACITY, "batch exceeds the context capacity");
+    for (int b = 0; b < batch; ++b)
+        if (start[b] < 0 || start[b] >= c->D.V) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
+    if (n_new == 0) return ADN_OK;
+    adn_run r{};
+    r.batch = batch;
+    r.seq = 1;
+    r.max_iters = max_iters;
+    r.eps = eps;
+    r.damping = damping;
+    r.tokens = start;
+    int rc = check_run(c, &r);
+    if (rc) return rc;
+    try {
+        int32_t *tok = (int32_t *)staging_f(c, 10, (size_t)batch * sizeof(int32_t));
+        int32_t *seq = (int32_t *)staging_f(c, 11, (size_t)batch * n_new * sizeof(int32_t));
+        ADN_HIP(hipMemcpyAsync(tok, start, batch * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+        r.tokens = tok;
+        adn_outputs o{};
+        o.argmax = c->argmax_scratch;
+        for (int j = 0; j < n_new; ++j) {
+            enqueue_forward(c, r, o);
+            launch_copy_tokens_from_argmax(c->argmax_scratch, tok, seq, batch, n_new, j, c->stream);
+        }
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(out_tokens, seq, (size_t)batch * n_new * sizeof(int32_t), hipMemcpyDeviceToHost,
+                               c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+}
+
+int adn_spectral_norm(adn_ctx *c, const float *w, int32_t rows, int32_t cols, int32_t n_iter, float *sigma) {
+    if (!c || !w || !sigma) return fail(ADN_E_INVALID, "null argument");
+    if (rows < 0 || cols < 0 || n_iter < 0) return fail(ADN_E_INVALID, "negative size");
+    if (rows == 0 || cols == 0) {
+        *sigma = 1.0f;
+        return ADN_OK;
+    }
+    try {
+        const size_t n = (size_t)rows * cols;
+        float *dw = staging_f(c, 12, n * sizeof(float));
+        float *work = staging_f(c, 13, ((size_t)rows + 2 * cols + 1) * sizeof(float));
+        ADN_HIP(hipMemcpyAsync(dw, w, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        float *ds = work + rows + 2 * cols;
+        launch_spectral_norm(dw, rows, cols, n_iter, ds, work, c->stream);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(sigma, ds, sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_normalize_if_needed(adn_ctx *c, float *w, int32_t rows, int32_t cols, float threshold, int32_t n_iter) {
+    if (!c || !w) return fail(ADN_E_INVALID, "null argument");
+    if (rows < 0 || cols < 0 || n_iter < 0) return fail(ADN_E_INVALID, "negative size");
+    if (rows == 0 || cols == 0) return ADN_OK;  // sigma = 1 (spectral_norm.rs:28-30)
+    try {
+        const size_t n = (size_t)rows * cols;
+        float *dw = staging_f(c, 12, n * sizeof(float));
+        float *work = staging_f(c, 13, ((size_t)rows + 2 * cols + 1) * sizeof(float));
+        ADN_HIP(hipMemcpyAsync(dw, w, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        float *ds = work + rows + 2 * cols;
+        launch_spectral_norm(dw, rows, cols, n_iter, ds, work, c->stream);
+        launch_scale_if(dw, (long)n, ds, threshold, c->stream);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(w, dw, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_block_step(adn_ctx *c, int32_t d, const float *x, const float *dt, const float *a, const float *b,
+                   const float *cc, float *y) {
+    if (!c || !x || !dt || !a || !b || !cc || !y) return fail(ADN_E_INVALID, "null argument");
+    if (d <= 0) return fail(ADN_E_INVALID, "d_model=0");
+    try {
+        float *buf = staging_f(c, 16, 6 * (size_t)d * sizeof(float));
+        const float *src[5] = {x, dt, a, b, cc};
+        for (int i = 0; i < 5; ++i)
+            ADN_HIP(hipMemcpyAsync(buf + (size_t)i * d, src[i], d * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        launch_zoh(d, buf, buf + d, buf + 2 * (size_t)d, buf + 3 * (size_t)d, buf + 4 * (size_t)d,
+                   buf + 5 * (size_t)d, c->stream);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(y, buf + 5 * (size_t)d, d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_load_tensor(adn_ctx *c, const float *data, int64_t n, int32_t *id) {
+    if (!c || !data || !id) return fail(ADN_E_INVALID, "null argument");
+    if (n <= 0) return fail(ADN_E_INVALID, "empty tensor");
+    try {
+        DevBuf t;
+        t.bytes = (size_t)n * sizeof(float);
+        ADN_HIP(hipMalloc(&t.p, t.bytes));
+        ADN_HIP(hipMemcpyAsync(t.p, data, t.bytes, hipMemcpyHostToDevice, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        c->tensors.push_back(t);
+        *id = (int32_t)c->tensors.size() - 1;
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_ffn_forward(adn_ctx *c, int32_t w_id, int32_t in_id, int32_t out_dim, float *y) {
+    if (!c || !y) return fail(ADN_E_INVALID, "null argument");
+    if (w_id < 0 || w_id >= (int)c->tensors.size() || in_id < 0 || in_id >= (int)c->tensors.size())
+        return fail(ADN_E_INVALID, "unknown tensor id");
+    if (out_dim <= 0) return fail(ADN_E_INVALID, "out_dim must be >= 1");
+    const DevBuf &w = c->tensors[w_id];
+    const DevBuf &x = c->tensors[in_id];
+    const long in_dim = (long)(x.bytes / sizeof(float));
+    if ((long)(w.bytes / sizeof(float)) != in_dim * out_dim)
+        return fail(ADN_E_INVALID, "weight size != in_dim * out_dim");
+    try {
+        float *dy = staging_f(c, 17, (size_t)out_dim * sizeof(float));
+        launch_gemv_colmajor((const float *)w.p, (const float *)x.p, (int)in_dim, out_dim, dy, c->stream);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(y, dy, out_dim * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+}  // extern "C"

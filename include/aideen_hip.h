@@ -1,0 +1,183 @@
+/*
+ * aideen_hip.h -- C ABI of the MI355X (gfx950) DEQ forward path.
+ *
+ * Drop-in boundary for the reference's wgpu compute block (SergioAriel/aideen):
+ * the entry points below replace, one for one, the GPU surfaces the Rust crates bind to.
+ * Each declaration cites the reference interface it replaces (file:line).  A thin Rust FFI
+ * crate binds exactly these symbols (see INTEGRATION.md in the repository root).
+ *
+ * Conventions
+ *   - Every entry point returns ADN_OK (0) or a negative ADN_E_* code; adn_last_error()
+ *     returns the message of the last failure on the calling thread (the reference returns
+ *     `&'static str` / `String` errors, gpu_deq.rs:3687-3727, block_backend.rs:22-31).
+ *   - Plain pointers and sizes only.  "host" entry points take host memory and block until the
+ *     results are back (the reference's map_async + device.poll(Wait), deq_bridge.rs:2017-2038);
+ *     "_async" entry points take device memory and only enqueue work on the context's stream
+ *     (the reference's *_no_readback / *_from_seq_buf forms, gpu_deq.rs:3855-4078).
+ *   - One context per thread (the reference's backends are !Sync).  Contexts own their HIP
+ *     stream (default priority) unless adn_set_stream() hands them another.
+ *   - Layouts (fp32 everywhere):
+ *       per-slot matrices  W[s][out][in]  (ADN_LAYOUT_OUT_IN), so y = W[s] x, or the reference's
+ *                          GPU flat layout W[s][in][out] (ADN_LAYOUT_IN_OUT, fixed_point_memory_
+ *                          reasoning.rs:516-561 `w_*_gpu_flat`)
+ *       slot vectors       [H][d]                 (aideen-core/src/state.rs:85-146 HSlots)
+ *       hidden states      [B][T][H][d]           (deq_slot_attn_unified_clean.wgsl:711-712)
+ *       inputs S_in        [B][T][d]              (deq_bridge.rs:2672-2720)
+ *       pooled             [B][T][d]              (deq_forward_pool.wgsl:32-65)
+ *       logits             [B][T][V]              (lm_exact_forward.wgsl:21-47)
+ *       carrier state      [B][H][d][N]
+ */
+#ifndef AIDEEN_HIP_H
+#define AIDEEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ADN_ABI_VERSION 1
+
+/* status codes */
+#define ADN_OK 0
+#define ADN_E_INVALID (-1)    /* bad argument, shape or token id                          */
+#define ADN_E_NO_DEVICE (-2)  /* no usable GPU (reference: new_blocking() -> None)         */
+#define ADN_E_HIP (-3)        /* HIP runtime failure                                       */
+#define ADN_E_NO_WEIGHTS (-4) /* forward before adn_upload_weights                         */
+#define ADN_E_CAPACITY (-5)   /* batch*seq beyond the context's capacity                   */
+
+/* semantic switches (adn_config.flags); defaults reproduce the CPU reference forward
+ * FixedPointMemoryReasoning::step (fixed_point_memory_reasoning.rs:1372-1424)          */
+#define ADN_F_WIN_TRANSPOSED (1u << 0)  /* signal = W_in^T x (deq_slot_attn_unified_clean.wgsl:773) */
+#define ADN_F_SCORE_CLAMP4 (1u << 1)    /* clamp slot scores to [-4,4] (picard_pipeline_test.rs:216) */
+#define ADN_F_RMS_EXCL_ANCHOR (1u << 2) /* RMS over o+signal only (ARCHITECTURE.md:160-170)          */
+#define ADN_F_INIT_SIGNAL_RMS (1u << 3) /* h0 = signal/rms(signal) (deq_slot_attn_unified_clean.wgsl:900-943) */
+#define ADN_F_RESID_L2 (1u << 4)        /* L2 exit residual (aideen-node/src/inference.rs:214-221)    */
+#define ADN_F_SCAN_SELECTIVE (1u << 5)  /* input-dependent carrier decay (gpu_deq.rs:6129-6214)      */
+
+/* weight layouts for adn_upload_weights */
+#define ADN_LAYOUT_OUT_IN 0u /* W[s][out][in] row-major                                   */
+#define ADN_LAYOUT_IN_OUT 1u /* W[s][in][out]: the reference's GPU flat layout            */
+
+/* Shapes and solver configuration (reference: ArchitectureConfig, aideen-core/src/state.rs:7-58;
+ * batch/seq capacities AIDEEN_BATCH_SIZE / AIDEEN_SEQ_CAP, gpu_deq.rs:577-596;
+ * Anderson depth AIDEEN_ANDERSON_M, gpu_deq.rs:2093). */
+typedef struct adn_config {
+    int32_t d_r;        /* slot width d (multiple of 64)                         */
+    int32_t h_slots;    /* H: 1, 2, 4, 8 or 16                                   */
+    int32_t vocab;      /* V                                                     */
+    int32_t d_state;    /* N: carrier states per channel (1..32)                 */
+    int32_t rank;       /* write/selective rank r (multiple of 4, <= 64; ref 32) */
+    int32_t max_batch;  /* capacity: sequences per call                          */
+    int32_t max_seq;    /* capacity: tokens per sequence                         */
+    int32_t anderson_m; /* 0 = plain Picard, else ring depth 2..5                */
+    uint32_t flags;     /* ADN_F_*                                               */
+} adn_config;
+
+/* Model tensors (host memory, fp32).  NULL where noted means the documented default.
+ * Reference upload: GpuDeqBackend::upload_weights, gpu_deq.rs:3529-3667 (AllWeights +
+ * HistParams), LmHead (lm_head.rs:9-33), Tokenizer::embeddings (tokenizer.rs:22-23). */
+typedef struct adn_weights {
+    const float *w_q, *w_k, *w_v, *w_o, *w_in; /* [H][d][d]                          */
+    const float *q_bias, *k_bias;               /* [H][d], NULL = 0                   */
+    const float *anchor;                        /* [H][d] slot_anchor                 */
+    const float *norm_scale;                    /* [d]                                */
+    const float *embed;                         /* [V][d] token embeddings            */
+    const float *lm_w;                          /* [V][d]                             */
+    const float *lm_b;                          /* [V], NULL = 0                      */
+    const float *lm_g;                          /* [d], NULL = 1                      */
+    const float *a_log;                         /* [H][d] carrier decay logits        */
+    const float *wx_diag;                       /* [H][d] diagonal of W_x             */
+    const float *w_out;                         /* [H][d][d] readout, NULL = 0        */
+    const float *b_delta;                       /* [H][d], NULL = 0                   */
+    const float *w_kw;                          /* [H][d][r] selective write down     */
+    const float *w_vw;                          /* [H][r][d] selective write up       */
+    const float *w_b, *w_c;                     /* [H][N][d] carrier B/C, NULL = 1    */
+} adn_weights;
+
+/* One forward call (reference: run_forward_deq(batch, seq, max_iters, eps, damping, s_in, ...),
+ * gpu_deq.rs:3687-3727).  Exactly one of tokens / s_in is non-NULL. */
+typedef struct adn_run {
+    int32_t batch, seq;
+    int32_t max_iters;            /* >= 1                                              */
+    float eps;                    /* exit when the residual is below eps               */
+    float damping;                /* Picard beta in (0, 1]                             */
+    const int32_t *tokens;        /* [B][T] token ids (embedding gather fused)         */
+    const float *s_in;            /* [B][T][d] pre-embedded inputs                     */
+    const float *scan_state_in;   /* [B][H][d][N] carried state, NULL = zeros          */
+} adn_run;
+
+/* Requested outputs; NULL = not computed.  (read_hnext_seq gpu_deq.rs:5833-5851,
+ * read_hpooled_seq gpu_deq.rs:5886-5894, read_exact_logits_from_h gpu_lm_head.rs:1813-1879) */
+typedef struct adn_outputs {
+    float *h_star;      /* [B][T][H][d] fixed points                            */
+    float *pooled;      /* [B][T][d]    mean over slots                         */
+    float *logits;      /* [B][T][V]                                            */
+    int32_t *argmax;    /* [B][T]       greedy token, last-max tie rule         */
+    int32_t *iters;     /* [B][T]       Picard updates applied                  */
+    float *scan_y;      /* [B][T][H][d] carrier output Y_t                      */
+    float *scan_state;  /* [B][H][d][N] carrier state after the last token      */
+} adn_outputs;
+
+typedef struct adn_ctx adn_ctx;
+
+/* --- library ------------------------------------------------------------------------ */
+int adn_abi_version(void);
+const char *adn_last_error(void);
+/* Number of visible GPUs (no device is initialised by a count of 0). */
+int adn_device_count(int32_t *count);
+
+/* --- context (GpuDeqBackend::new_blocking gpu_deq.rs:3122-3124; RustDeqBridge::new
+ *     deq_bridge.rs:159) -------------------------------------------------------------- */
+int adn_create(const adn_config *cfg, adn_ctx **out);
+void adn_destroy(adn_ctx *ctx);
+/* Run on a caller-owned hipStream_t (NULL restores the context's own stream). */
+int adn_set_stream(adn_ctx *ctx, void *hip_stream);
+int adn_synchronize(adn_ctx *ctx);
+
+/* --- weights (GpuDeqBackend::upload_weights gpu_deq.rs:3529-3667) -------------------- */
+int adn_upload_weights(adn_ctx *ctx, const adn_weights *w, uint32_t layout);
+/* GpuDeqBackend::reset_state gpu_deq.rs:3127-3164: zero the carried carrier state. */
+int adn_reset_state(adn_ctx *ctx);
+
+/* --- forward ------------------------------------------------------------------------ */
+/* Host memory, blocking: run_forward_deq / run_forward_deq_pooled + readbacks
+ * (gpu_deq.rs:3687-3768, 5833-5894; gpu_lm_head.rs:1813-1879). */
+int adn_forward(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
+/* Device memory, enqueue only: run_forward_deq_no_readback / run_forward_from_seq_buf
+ * (gpu_deq.rs:3855-4078).  Errors detected on the device (a token id outside [0, V)) are
+ * reported by the next adn_synchronize(). */
+int adn_forward_async(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
+
+/* Greedy decode, host memory, blocking (Trainer::generate trainer.rs:4219-4431 with
+ * LmHead::sample at temperature <= 1e-4 = argmax, lm_head.rs:104-112).  Each step solves the
+ * last token of every sequence and appends its argmax; all n_new steps run on the device
+ * without host round trips.  out_tokens is [B][n_new]. */
+int adn_decode_greedy(adn_ctx *ctx, int32_t batch, const int32_t *start_tokens, int32_t n_new,
+                      int32_t max_iters, float eps, float damping, int32_t *out_tokens);
+
+/* --- weight preparation (spectral_norm.rs:25-80; spectral_renorm.wgsl:83-196) ----------- */
+/* sigma_max by n_iter power iterations from u0 = 1/sqrt(rows); host memory, blocking. */
+int adn_spectral_norm(adn_ctx *ctx, const float *w, int32_t rows, int32_t cols, int32_t n_iter,
+                      float *sigma);
+/* In place: W *= threshold/sigma when sigma > threshold (normalize_if_needed). */
+int adn_normalize_if_needed(adn_ctx *ctx, float *w, int32_t rows, int32_t cols, float threshold,
+                            int32_t n_iter);
+
+/* --- BlockBackend (aideen-core/src/block_backend.rs:22-31) ------------------------------ */
+/* fpm_batch_step: ZOH single step, h_prev = 0 (gpu_backend.rs:18-56, :98-248).  All [d]. */
+int adn_block_step(adn_ctx *ctx, int32_t d, const float *x, const float *dt, const float *a,
+                   const float *b, const float *c, float *y);
+
+/* --- ComputeBackend (aideen-core/src/compute.rs:11-23; aideen-engine/src/gpu/mod.rs:23-223) */
+/* load_tensor: copies n floats to the device and returns a handle. */
+int adn_load_tensor(adn_ctx *ctx, const float *data, int64_t n, int32_t *id);
+/* ffn_forward: y[row] = sum_i w[i*out_dim + row] * x[i] (column-major, ffn_forward.wgsl:22-37);
+ * in_dim = element count of the input tensor; y is host memory [out_dim]. */
+int adn_ffn_forward(adn_ctx *ctx, int32_t w_id, int32_t in_id, int32_t out_dim, float *y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AIDEEN_HIP_H */

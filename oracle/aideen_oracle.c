@@ -1,0 +1,759 @@
+/*
+ * aideen_oracle.c -- CPU restatement of the AIDEEN DEQ forward.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the HIP path is compared against; it is
+ * never linked into, called by or shipped with the product library.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ *
+ * Arithmetic order follows the reference's f32 code (nalgebra gemv accumulates each output
+ * sequentially over the input index; sums and means fold left to right).  Build with
+ * -ffp-contract=off so no multiply-add is fused, as Rust never fuses them.
+ *
+ * Pinning (how each function is checked; tests/test_oracle_pins.py):
+ *   orc_spectral_norm / normalize*  -- the reference's own unit tests (spectral_norm.rs:98-149)
+ *                                      plus sigma of matrices with a known SVD.
+ *   orc_picard_step / orc_solve_token -- zero-attention closed form (iteration count known
+ *                                      exactly), H=1 closed form, uniform-attention closed form,
+ *                                      float64 brute force at d<=16, slot-permutation
+ *                                      equivariance, fixed-point residual invariant.
+ *   orc_lm_head_token / orc_argmax   -- lm_head.rs:249-310 tests, closed-form W entries,
+ *                                      RMSNorm scale invariance, last-max tie rule.
+ *   orc_scan_seq / recirculate       -- geometric-series closed form, readout==recirculate at
+ *                                      W_out=0, sequential==chunked invariants.
+ *   Anderson mixing                  -- m=1 equals Picard; the solved coefficients satisfy the
+ *                                      regularised system; convergence on a linear map.
+ *   orc_zoh_step / orc_gemv_colmajor -- closed forms of gpu_backend.rs:18-56 and the engine
+ *                                      GEMV known answer (aideen-engine/src/gpu/mod.rs:229-257).
+ */
+#include "aideen_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------- */
+/* small linear algebra in reference order                                    */
+/* ------------------------------------------------------------------------- */
+
+/* y = W x, W row-major [out][in]; y[o] accumulates sequentially over i (nalgebra gemv). */
+static void gemv_rm(const float *W, int out, int in, const float *x, float *y) {
+    for (int o = 0; o < out; ++o) {
+        const float *row = W + (size_t)o * in;
+        float acc = 0.0f;
+        for (int i = 0; i < in; ++i) acc += row[i] * x[i];
+        y[o] = acc;
+    }
+}
+
+/* y = W x with W given transposed, Wt [in][out]: same per-output order as gemv_rm, but the
+ * loop runs across outputs so it vectorises.  Bit-identical to gemv_rm without FP contraction. */
+static void gemv_t(const float *Wt, int out, int in, const float *x, float *y) {
+    for (int o = 0; o < out; ++o) y[o] = 0.0f;
+    for (int i = 0; i < in; ++i) {
+        const float xi = x[i];
+        const float *col = Wt + (size_t)i * out;
+        for (int o = 0; o < out; ++o) y[o] += col[o] * xi;
+    }
+}
+
+static float dot_seq(const float *a, const float *b, int n) {
+    float acc = 0.0f;
+    for (int i = 0; i < n; ++i) acc += a[i] * b[i];
+    return acc;
+}
+
+static void transpose(const float *src, int rows, int cols, float *dst) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) dst[(size_t)c * rows + r] = src[(size_t)r * cols + c];
+}
+
+/* ------------------------------------------------------------------------- */
+/* spectral_norm.rs                                                           */
+/* ------------------------------------------------------------------------- */
+
+static float norm2(const float *v, int n) { return sqrtf(dot_seq(v, v, n)); }
+
+/* spectral_norm.rs:25-59 -- power iteration from u0 = 1/sqrt(rows). */
+float orc_spectral_norm(const float *w, int rows, int cols, int n_iter) {
+    if (rows == 0 || cols == 0) return 1.0f;
+    float *u = (float *)malloc(sizeof(float) * rows);
+    float *v = (float *)malloc(sizeof(float) * cols);
+    float *wv = (float *)malloc(sizeof(float) * rows);
+    const float inv = 1.0f / sqrtf((float)rows);
+    for (int i = 0; i < rows; ++i) u[i] = inv;
+    float sigma = 1.0f;
+    for (int it = 0; it < n_iter; ++it) {
+        /* v = W^T u / ||W^T u||; each output of W^T u accumulates over rows in order */
+        for (int j = 0; j < cols; ++j) {
+            float acc = 0.0f;
+            for (int i = 0; i < rows; ++i) acc += w[(size_t)i * cols + j] * u[i];
+            v[j] = acc;
+        }
+        float nv = norm2(v, cols);
+        if (nv < 1e-12f) { sigma = 0.0f; goto done_zero; }
+        for (int j = 0; j < cols; ++j) v[j] = v[j] / nv;
+        gemv_rm(w, rows, cols, v, wv);
+        float nu = norm2(wv, rows);
+        if (nu < 1e-12f) { sigma = 0.0f; goto done_zero; }
+        for (int i = 0; i < rows; ++i) u[i] = wv[i] / nu;
+        /* sigma = (u^T W) v: nalgebra evaluates the row vector u^T W first */
+        float acc_s = 0.0f;
+        for (int j = 0; j < cols; ++j) {
+            float z = 0.0f;
+            for (int i = 0; i < rows; ++i) z += u[i] * w[(size_t)i * cols + j];
+            acc_s += z * v[j];
+        }
+        sigma = acc_s;
+    }
+    free(u); free(v); free(wv);
+    sigma = fabsf(sigma);
+    return sigma > 1e-12f ? sigma : 1e-12f;
+done_zero:
+    free(u); free(v); free(wv);
+    return 0.0f;
+}
+
+/* spectral_norm.rs:65-71 */
+void orc_normalize(float *w, int rows, int cols, float target, int n_iter) {
+    float sigma = orc_spectral_norm(w, rows, cols, n_iter);
+    if (sigma < 1e-12f) return;
+    const float s = target / sigma;
+    for (size_t i = 0; i < (size_t)rows * cols; ++i) w[i] *= s;
+}
+
+/* spectral_norm.rs:75-80 */
+void orc_normalize_if_needed(float *w, int rows, int cols, float threshold, int n_iter) {
+    float sigma = orc_spectral_norm(w, rows, cols, n_iter);
+    if (sigma > threshold) {
+        const float s = threshold / sigma;
+        for (size_t i = 0; i < (size_t)rows * cols; ++i) w[i] *= s;
+    }
+}
+
+/* spectral_norm.rs:93-95: f*beta + h*(1-beta) */
+void orc_damped_update(const float *h, const float *f, float beta, int n, float *out) {
+    const float omb = 1.0f - beta;
+    for (int i = 0; i < n; ++i) out[i] = f[i] * beta + h[i] * omb;
+}
+
+/* ------------------------------------------------------------------------- */
+/* prepared (transposed) weights for the fast per-token path                  */
+/* ------------------------------------------------------------------------- */
+
+typedef struct prep {
+    orc_cfg c;
+    const orc_weights *w;
+    float *wq_t, *wk_t, *wv_t, *wo_t, *win_t; /* [H][in][out] */
+} prep;
+
+static void prep_init(prep *p, const orc_cfg *c, const orc_weights *w) {
+    const int d = c->d, H = c->H;
+    const size_t mat = (size_t)d * d;
+    p->c = *c;
+    p->w = w;
+    float **dst[5] = {&p->wq_t, &p->wk_t, &p->wv_t, &p->wo_t, &p->win_t};
+    const float *src[5] = {w->w_q, w->w_k, w->w_v, w->w_o, w->w_in};
+    for (int m = 0; m < 5; ++m) {
+        *dst[m] = (float *)malloc(sizeof(float) * mat * H);
+        for (int s = 0; s < H; ++s) {
+            if (m == 4 && (c->flags & ORC_F_WIN_TRANSPOSED)) {
+                /* signal = W_in^T x: the transposed matrix of W_in^T is W_in itself */
+                memcpy(*dst[m] + s * mat, src[m] + s * mat, sizeof(float) * mat);
+            } else {
+                transpose(src[m] + s * mat, d, d, *dst[m] + s * mat);
+            }
+        }
+    }
+}
+
+static void prep_free(prep *p) {
+    free(p->wq_t); free(p->wk_t); free(p->wv_t); free(p->wo_t); free(p->win_t);
+}
+
+/* per-thread scratch */
+typedef struct scratch {
+    float *q, *k, *v, *mix, *o, *comb, *hn, *hist; /* hist: Anderson ring [m][H*d] */
+    float *scores, *attn;
+} scratch;
+
+static void scratch_init(scratch *s, const orc_cfg *c) {
+    const size_t hd = (size_t)c->H * c->d;
+    s->q = (float *)malloc(sizeof(float) * hd);
+    s->k = (float *)malloc(sizeof(float) * hd);
+    s->v = (float *)malloc(sizeof(float) * hd);
+    s->mix = (float *)malloc(sizeof(float) * c->d);
+    s->o = (float *)malloc(sizeof(float) * c->d);
+    s->comb = (float *)malloc(sizeof(float) * c->d);
+    s->hn = (float *)malloc(sizeof(float) * hd);
+    int m = c->anderson_m > 0 ? c->anderson_m : 1;
+    s->hist = (float *)malloc(sizeof(float) * hd * m);
+    s->scores = (float *)malloc(sizeof(float) * c->H);
+    s->attn = (float *)malloc(sizeof(float) * c->H * c->H);
+}
+
+static void scratch_free(scratch *s) {
+    free(s->q); free(s->k); free(s->v); free(s->mix); free(s->o); free(s->comb); free(s->hn);
+    free(s->hist); free(s->scores); free(s->attn);
+}
+
+/* FPMR:1305-1315 project_input_signal (per slot: signal_s = W_in[s] x). */
+static void signal_p(const prep *p, const float *x, float *signal) {
+    const int d = p->c.d;
+    for (int s = 0; s < p->c.H; ++s)
+        gemv_t(p->win_t + (size_t)s * d * d, d, d, x, signal + (size_t)s * d);
+}
+
+/* FPMR:1432-1448 init (h0 = x + anchor); UWGSL:900-943 signal/rms variant. */
+static void init_p(const prep *p, const float *x, const float *signal, float *h0) {
+    const int d = p->c.d, H = p->c.H;
+    for (int s = 0; s < H; ++s) {
+        float *hs = h0 + (size_t)s * d;
+        if (p->c.flags & ORC_F_INIT_SIGNAL_RMS) {
+            const float *sg = signal + (size_t)s * d;
+            float ss = 0.0f;
+            for (int i = 0; i < d; ++i) ss += sg[i] * sg[i];
+            const float rms = sqrtf(ss / (float)d + 1e-6f);
+            for (int i = 0; i < d; ++i) hs[i] = sg[i] / rms;
+        } else {
+            const float *an = p->w->anchor + (size_t)s * d;
+            for (int i = 0; i < d; ++i) hs[i] = x[i] + an[i];
+        }
+    }
+}
+
+/* FPMR:1397-1424 cross_slot_attn followed by FPMR:1372-1395 step_with_fixed_hist_ctx
+ * (hist = 0, FPMR:1450-1453), FPMR:1300-1303 rms_norm and spectral_norm.rs:93 damped_update. */
+static void step_p(const prep *p, scratch *sc, const float *h, const float *signal, float *h_next,
+                   float *attn_out) {
+    const int d = p->c.d, H = p->c.H;
+    const orc_weights *w = p->w;
+    const size_t mat = (size_t)d * d;
+    for (int s = 0; s < H; ++s) {
+        const float *hs = h + (size_t)s * d;
+        gemv_t(p->wq_t + s * mat, d, d, hs, sc->q + (size_t)s * d);
+        gemv_t(p->wk_t + s * mat, d, d, hs, sc->k + (size_t)s * d);
+        gemv_t(p->wv_t + s * mat, d, d, hs, sc->v + (size_t)s * d);
+        if (w->q_bias)
+            for (int i = 0; i < d; ++i) sc->q[(size_t)s * d + i] += w->q_bias[(size_t)s * d + i];
+        if (w->k_bias)
+            for (int i = 0; i < d; ++i) sc->k[(size_t)s * d + i] += w->k_bias[(size_t)s * d + i];
+    }
+    const float scale = 1.0f / sqrtf((float)d);
+    for (int a = 0; a < H; ++a) {
+        /* raw scores, max-subtracted softmax (FPMR:1405-1413) */
+        float mx = -INFINITY;
+        for (int cc = 0; cc < H; ++cc) {
+            float sc_ = dot_seq(sc->q + (size_t)a * d, sc->k + (size_t)cc * d, d) * scale;
+            if (p->c.flags & ORC_F_SCORE_CLAMP4) sc_ = fminf(fmaxf(sc_, -4.0f), 4.0f);
+            sc->scores[cc] = sc_;
+            mx = fmaxf(mx, sc_);
+        }
+        float sum = 0.0f;
+        for (int cc = 0; cc < H; ++cc) {
+            sc->scores[cc] = expf(sc->scores[cc] - mx);
+            sum += sc->scores[cc];
+        }
+        for (int cc = 0; cc < H; ++cc) sc->attn[a * H + cc] = sc->scores[cc] / sum;
+        /* mixed = fold(0, acc + v_c * attn_c) (FPMR:1415-1419) */
+        for (int i = 0; i < d; ++i) sc->mix[i] = 0.0f;
+        for (int cc = 0; cc < H; ++cc) {
+            const float at = sc->attn[a * H + cc];
+            const float *vc = sc->v + (size_t)cc * d;
+            for (int i = 0; i < d; ++i) sc->mix[i] = sc->mix[i] + vc[i] * at;
+        }
+        gemv_t(p->wo_t + a * mat, d, d, sc->mix, sc->o);
+        /* combined = attn + signal + hist(0) + anchor; f = g*c/rms (FPMR:1386-1391) */
+        const float *sg = signal + (size_t)a * d;
+        const float *an = w->anchor + (size_t)a * d;
+        float ss = 0.0f;
+        if (p->c.flags & ORC_F_RMS_EXCL_ANCHOR) {
+            for (int i = 0; i < d; ++i) {
+                const float as_ = sc->o[i] + sg[i];
+                ss += as_ * as_;
+                sc->comb[i] = as_ + an[i];
+            }
+        } else {
+            for (int i = 0; i < d; ++i) {
+                sc->comb[i] = ((sc->o[i] + sg[i]) + 0.0f) + an[i];
+                ss += sc->comb[i] * sc->comb[i];
+            }
+        }
+        const float rms = sqrtf(ss / (float)d + 1e-6f);
+        const float beta = p->c.beta, omb = 1.0f - p->c.beta;
+        const float *ha = h + (size_t)a * d;
+        float *hn = h_next + (size_t)a * d;
+        for (int i = 0; i < d; ++i) {
+            const float f = w->norm_scale[i] * sc->comb[i] / rms;
+            hn[i] = f * beta + ha[i] * omb;
+        }
+    }
+    if (attn_out) memcpy(attn_out, sc->attn, sizeof(float) * H * H);
+}
+
+/* Residual between consecutive iterates: max-abs (ARCHITECTURE.md:178-185) or L2 over the
+ * token's flat [H*d] state (aideen-node/src/inference.rs:214-221). */
+static float residual(const orc_cfg *c, const float *a, const float *b) {
+    const int n = c->H * c->d;
+    if (c->flags & ORC_F_RESID_L2) {
+        float acc = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const float df = a[i] - b[i];
+            acc += df * df;
+        }
+        return sqrtf(acc);
+    }
+    float mx = 0.0f;
+    for (int i = 0; i < n; ++i) mx = fmaxf(mx, fabsf(a[i] - b[i]));
+    return mx;
+}
+
+/* Anderson coefficients: the reference's iterate-difference scheme
+ * (staged_adjoint_picard_clean.wgsl:1043-1121).  g[n*n] is the Gram matrix of the pseudo-
+ * residuals; solves (G + reg I) beta = 1 by Cramer's rule for n = 2, 3 (the reference's
+ * formulas) and by cofactor expansion for n = 4 (build extension, same determinant clamp),
+ * clamps to [-2, 3] and normalises to sum 1. */
+void orc_anderson_coeffs(int n, const float *g_in, float *beta) {
+    float g[16];
+    memcpy(g, g_in, sizeof(float) * n * n);
+    if (n == 2) {
+        const float reg = fmaxf(1e-8f, 1e-4f * (fabsf(g[0]) + fabsf(g[3])));
+        const float g00 = g[0] + reg, g01 = g[1], g10 = g[2], g11 = g[3] + reg;
+        const float det = g00 * g11 - g01 * g10;
+        const float sdet = det < 0.0f ? fminf(det, -1e-10f) : fmaxf(det, 1e-10f);
+        beta[0] = (g11 - g01) / sdet;
+        beta[1] = (g00 - g10) / sdet;
+    } else if (n == 3) {
+        const float reg = fmaxf(1e-8f, 1e-4f * (fabsf(g[0]) + fabsf(g[4]) + fabsf(g[8])));
+        const float g00 = g[0] + reg, g01 = g[1], g02 = g[2];
+        const float g10 = g[3], g11 = g[4] + reg, g12 = g[5];
+        const float g20 = g[6], g21 = g[7], g22 = g[8] + reg;
+        const float det = g00 * (g11 * g22 - g12 * g21) - g01 * (g10 * g22 - g12 * g20) +
+                          g02 * (g10 * g21 - g11 * g20);
+        const float sdet = det < 0.0f ? fminf(det, -1e-8f) : fmaxf(det, 1e-8f);
+        beta[0] = (1.0f * (g11 * g22 - g12 * g21) - g01 * (g22 - g12) + g02 * (g21 - g11)) / sdet;
+        beta[1] = (g00 * (g22 - g12) - 1.0f * (g10 * g22 - g12 * g20) + g02 * (g10 - g20)) / sdet;
+        beta[2] = (g00 * (g11 - g21) - g01 * (g10 - g20) + 1.0f * (g10 * g21 - g11 * g20)) / sdet;
+    } else { /* n == 4: Cramer by 3x3 cofactors */
+        float a[16];
+        float tr = 0.0f;
+        for (int i = 0; i < 4; ++i) tr += fabsf(g[i * 4 + i]);
+        const float reg = fmaxf(1e-8f, 1e-4f * tr);
+        memcpy(a, g, sizeof(a));
+        for (int i = 0; i < 4; ++i) a[i * 4 + i] += reg;
+#define M3(r0, r1, r2, c0, c1, c2)                                                   \
+    (m[r0 * 4 + c0] * (m[r1 * 4 + c1] * m[r2 * 4 + c2] - m[r1 * 4 + c2] * m[r2 * 4 + c1]) - \
+     m[r0 * 4 + c1] * (m[r1 * 4 + c0] * m[r2 * 4 + c2] - m[r1 * 4 + c2] * m[r2 * 4 + c0]) + \
+     m[r0 * 4 + c2] * (m[r1 * 4 + c0] * m[r2 * 4 + c1] - m[r1 * 4 + c1] * m[r2 * 4 + c0]))
+        const float *m = a;
+        const float det = a[0] * M3(1, 2, 3, 1, 2, 3) - a[1] * M3(1, 2, 3, 0, 2, 3) +
+                          a[2] * M3(1, 2, 3, 0, 1, 3) - a[3] * M3(1, 2, 3, 0, 1, 2);
+        const float sdet = det < 0.0f ? fminf(det, -1e-8f) : fmaxf(det, 1e-8f);
+        for (int col = 0; col < 4; ++col) {
+            float b[16];
+            memcpy(b, a, sizeof(b));
+            for (int r = 0; r < 4; ++r) b[r * 4 + col] = 1.0f;
+            m = b;
+            const float dc = b[0] * M3(1, 2, 3, 1, 2, 3) - b[1] * M3(1, 2, 3, 0, 2, 3) +
+                             b[2] * M3(1, 2, 3, 0, 1, 3) - b[3] * M3(1, 2, 3, 0, 1, 2);
+            beta[col] = dc / sdet;
+        }
+#undef M3
+    }
+    float s = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        beta[i] = fminf(fmaxf(beta[i], -2.0f), 3.0f);
+        s += beta[i];
+    }
+    if (fabsf(s) < 1e-6f) {
+        for (int i = 0; i < n; ++i) beta[i] = 0.0f;
+        beta[0] = 1.0f;
+    } else {
+        for (int i = 0; i < n; ++i) beta[i] = beta[i] / s;
+    }
+}
+
+/* Per-token solve.  Loop/exit: aideen-node/src/inference.rs:196-228 (apply the step, then
+ * exit when the residual between consecutive iterates is below eps); iteration count = number
+ * of updates applied.  Converged tokens are frozen.  Optional Anderson mixing after each step
+ * (staged_adjoint_picard_clean.wgsl:1012-1134, gpu_deq.rs:4278-4293): the ring stores the
+ * un-mixed Picard iterate; mixing starts at k >= 2 with n_res = min(k, m-1) >= 2. */
+static int solve_p(const prep *p, scratch *sc, const float *x, float *h, float *resid_trace) {
+    const orc_cfg *c = &p->c;
+    const int d = c->d, H = c->H;
+    const size_t hd = (size_t)H * d;
+    float *signal = (float *)malloc(sizeof(float) * hd);
+    signal_p(p, x, signal);
+    init_p(p, x, signal, h);
+    int iters = 0;
+    const int m = c->anderson_m;
+    for (int k = 0; k < c->max_iters; ++k) {
+        step_p(p, sc, h, signal, sc->hn, NULL);
+        const float r = residual(c, sc->hn, h);
+        if (resid_trace) resid_trace[k] = r;
+        iters = k + 1;
+        if (r < c->eps || m <= 0) {
+            memcpy(h, sc->hn, sizeof(float) * hd);
+            if (r < c->eps) break;
+            continue;
+        }
+        /* Anderson: store g into ring slot k % m, then mix */
+        memcpy(sc->hist + (size_t)(k % m) * hd, sc->hn, sizeof(float) * hd);
+        const int n_res = k < m - 1 ? k : m - 1;
+        if (k >= 2 && n_res >= 2) {
+            float g[16], beta[4];
+            for (int ri = 0; ri < n_res; ++ri) {
+                for (int rj = ri; rj < n_res; ++rj) {
+                    const float *xi = sc->hist + (size_t)((k + m - ri) % m) * hd;
+                    const float *xi1 = sc->hist + (size_t)((k + m - ri - 1) % m) * hd;
+                    const float *xj = sc->hist + (size_t)((k + m - rj) % m) * hd;
+                    const float *xj1 = sc->hist + (size_t)((k + m - rj - 1) % m) * hd;
+                    float acc = 0.0f;
+                    for (size_t e = 0; e < hd; ++e) acc += (xi[e] - xi1[e]) * (xj[e] - xj1[e]);
+                    g[ri * n_res + rj] = acc;
+                    g[rj * n_res + ri] = acc;
+                }
+            }
+            orc_anderson_coeffs(n_res, g, beta);
+            for (size_t e = 0; e < hd; ++e) {
+                float acc = 0.0f;
+                for (int i = 0; i < n_res; ++i)
+                    acc += beta[i] * sc->hist[(size_t)((k + m - i) % m) * hd + e];
+                h[e] = acc;
+            }
+        } else {
+            memcpy(h, sc->hn, sizeof(float) * hd);
+        }
+    }
+    free(signal);
+    return iters;
+}
+
+/* ------------------------------------------------------------------------- */
+/* public per-token API                                                       */
+/* ------------------------------------------------------------------------- */
+
+void orc_signal(const orc_cfg *c, const orc_weights *w, const float *x, float *signal) {
+    prep p;
+    prep_init(&p, c, w);
+    signal_p(&p, x, signal);
+    prep_free(&p);
+}
+
+void orc_init(const orc_cfg *c, const orc_weights *w, const float *x, const float *signal,
+              float *h0) {
+    prep p;
+    p.c = *c;
+    p.w = w;
+    init_p(&p, x, signal, h0);
+}
+
+void orc_picard_step(const orc_cfg *c, const orc_weights *w, const float *h, const float *signal,
+                     float *h_next, float *attn) {
+    prep p;
+    scratch sc;
+    prep_init(&p, c, w);
+    scratch_init(&sc, c);
+    step_p(&p, &sc, h, signal, h_next, attn);
+    scratch_free(&sc);
+    prep_free(&p);
+}
+
+int orc_solve_token(const orc_cfg *c, const orc_weights *w, const float *x, float *h_star,
+                    float *resid_trace) {
+    prep p;
+    scratch sc;
+    prep_init(&p, c, w);
+    scratch_init(&sc, c);
+    int it = solve_p(&p, &sc, x, h_star, resid_trace);
+    scratch_free(&sc);
+    prep_free(&p);
+    return it;
+}
+
+/* ------------------------------------------------------------------------- */
+/* lm_head.rs                                                                 */
+/* ------------------------------------------------------------------------- */
+
+/* lm_head.rs:35-54: pooled = fold(0, acc + slot)/H; rmsnorm(eps 1e-5): (v/rms)*g; W x + b. */
+static void lm_head_tok(const orc_cfg *c, const orc_weights *w, const float *lm_wt,
+                        const float *h_star, float *pooled, float *logits, float *tmp) {
+    const int d = c->d, H = c->H, V = c->V;
+    for (int i = 0; i < d; ++i) tmp[i] = 0.0f;
+    for (int s = 0; s < H; ++s)
+        for (int i = 0; i < d; ++i) tmp[i] = tmp[i] + h_star[(size_t)s * d + i];
+    for (int i = 0; i < d; ++i) tmp[i] = tmp[i] / (float)H;
+    if (pooled) memcpy(pooled, tmp, sizeof(float) * d);
+    if (!logits) return;
+    float ss = 0.0f;
+    for (int i = 0; i < d; ++i) ss += tmp[i] * tmp[i];
+    const float rms = sqrtf(ss / (float)d + 1e-5f);
+    for (int i = 0; i < d; ++i) tmp[i] = (tmp[i] / rms) * (w->lm_g ? w->lm_g[i] : 1.0f);
+    if (lm_wt)
+        gemv_t(lm_wt, V, d, tmp, logits);
+    else
+        gemv_rm(w->lm_w, V, d, tmp, logits);
+    if (w->lm_b)
+        for (int v = 0; v < V; ++v) logits[v] = logits[v] + w->lm_b[v];
+}
+
+void orc_lm_head_token(const orc_cfg *c, const orc_weights *w, const float *h_star, float *pooled,
+                       float *logits) {
+    float *tmp = (float *)malloc(sizeof(float) * c->d);
+    lm_head_tok(c, w, NULL, h_star, pooled, logits, tmp);
+    free(tmp);
+}
+
+/* lm_head.rs:62-69: Iterator::max_by keeps the LAST maximal element; NaN compares Equal. */
+int orc_argmax(const float *logits, int V) {
+    if (V <= 0) return 0;
+    int best = 0;
+    float bv = logits[0];
+    for (int v = 1; v < V; ++v) {
+        const float x = logits[v];
+        /* max_by replaces the running max when the new element is >= it (or unordered) */
+        if (!(x < bv)) {
+            best = v;
+            bv = x;
+        }
+    }
+    return best;
+}
+
+/* ------------------------------------------------------------------------- */
+/* temporal carrier (selective scan)                                          */
+/* ------------------------------------------------------------------------- */
+
+/* One slot-token of the carrier prologue: u = h/rms(h) (FPMR:1462-1464), x = u + 0.5 tanh(wx) u
+ * (FPMR:1471-1477), abar per FPMR:1468-1470 or the selective form of gpu_deq.rs:6172-6199,
+ * B/C = W_B u, W_C u (rank-N readout, build-defined beyond N=1). */
+static void carrier_inputs(const orc_cfg *c, const orc_weights *w, int s, const float *h,
+                           float *x, float *abar, float *Bv, float *Cv, float *bn) {
+    const int d = c->d, N = c->N, r = c->r;
+    float ss = 0.0f;
+    for (int i = 0; i < d; ++i) ss += h[i] * h[i];
+    const float rms = sqrtf(ss / (float)d + 1e-6f);
+    float *u = (float *)malloc(sizeof(float) * d);
+    for (int i = 0; i < d; ++i) u[i] = h[i] / rms;
+    for (int i = 0; i < d; ++i) {
+        const float wx = 0.5f * tanhf(w->wx_diag[(size_t)s * d + i]);
+        x[i] = u[i] + wx * u[i];
+    }
+    if (c->flags & ORC_F_SCAN_SELECTIVE) {
+        const float *wkw = w->w_kw + (size_t)s * d * r;
+        const float *wvw = w->w_vw + (size_t)s * r * d;
+        for (int j = 0; j < r; ++j) bn[j] = 0.0f;
+        for (int i = 0; i < d; ++i)
+            for (int j = 0; j < r; ++j) bn[j] += wkw[(size_t)i * r + j] * u[i];
+        for (int i = 0; i < d; ++i) {
+            float pre = w->b_delta ? w->b_delta[(size_t)s * d + i] : 0.0f;
+            for (int j = 0; j < r; ++j) pre += wvw[(size_t)j * d + i] * bn[j];
+            const float delta = logf(1.0f + expf(pre));
+            const float abase = 1.0f / (1.0f + expf(w->a_log[(size_t)s * d + i]));
+            const float acore = expf(delta * logf(fmaxf(abase, 1.0e-6f)));
+            abar[i] = 0.10f + (1.0f - 0.10f) * acore;
+        }
+    } else {
+        for (int i = 0; i < d; ++i) abar[i] = 1.0f / (1.0f + expf(w->a_log[(size_t)s * d + i]));
+    }
+    for (int n = 0; n < N; ++n) {
+        Bv[n] = w->w_b ? dot_seq(w->w_b + ((size_t)s * N + n) * d, u, d) : 1.0f;
+        Cv[n] = w->w_c ? dot_seq(w->w_c + ((size_t)s * N + n) * d, u, d) : 1.0f;
+    }
+    free(u);
+}
+
+/* Readout carrier over one sequence: m_t[n] = abar m_{t-1}[n] + (1-abar) B_t[n] x_t,
+ * y_t = sum_n C_t[n] m_t[n], Y_t = y_t + W_out y_t (FPMR:1478-1482 with the recurrent state kept
+ * before W_out, UWGSL:2121-2140).  h_star [T][H][d]; state [H][d][N]; y [T][H][d]. */
+void orc_scan_seq(const orc_cfg *c, const orc_weights *w, int T, const float *h_star,
+                  const float *state_in, float *y, float *state_out) {
+    const int d = c->d, H = c->H, N = c->N, r = c->r > 0 ? c->r : 1;
+    float *m = (float *)malloc(sizeof(float) * (size_t)d * N);
+    float *x = (float *)malloc(sizeof(float) * d);
+    float *ab = (float *)malloc(sizeof(float) * d);
+    float *yt = (float *)malloc(sizeof(float) * d);
+    float *wy = (float *)malloc(sizeof(float) * d);
+    float *Bv = (float *)malloc(sizeof(float) * N);
+    float *Cv = (float *)malloc(sizeof(float) * N);
+    float *bn = (float *)malloc(sizeof(float) * r);
+    for (int s = 0; s < H; ++s) {
+        if (state_in)
+            memcpy(m, state_in + (size_t)s * d * N, sizeof(float) * d * N);
+        else
+            memset(m, 0, sizeof(float) * d * N);
+        for (int t = 0; t < T; ++t) {
+            const float *h = h_star + ((size_t)t * H + s) * d;
+            carrier_inputs(c, w, s, h, x, ab, Bv, Cv, bn);
+            for (int i = 0; i < d; ++i) {
+                const float bb = 1.0f - ab[i];
+                float acc = 0.0f;
+                for (int n = 0; n < N; ++n) {
+                    float *mi = m + (size_t)i * N + n;
+                    *mi = ab[i] * *mi + bb * (Bv[n] * x[i]);
+                    acc += Cv[n] * *mi;
+                }
+                yt[i] = acc;
+            }
+            float *out = y + ((size_t)t * H + s) * d;
+            if (w->w_out) {
+                gemv_rm(w->w_out + (size_t)s * d * d, d, d, yt, wy);
+                for (int i = 0; i < d; ++i) out[i] = yt[i] + wy[i];
+            } else {
+                memcpy(out, yt, sizeof(float) * d);
+            }
+        }
+        if (state_out) memcpy(state_out + (size_t)s * d * N, m, sizeof(float) * d * N);
+    }
+    free(m); free(x); free(ab); free(yt); free(wy); free(Bv); free(Cv); free(bn);
+}
+
+/* FPMR:1455-1486 temporal_step iterated over a sequence: the carried state is the output
+ * (I + W_out) m (dense recirculation, N = 1, B = C = 1). */
+void orc_scan_recirculate(const orc_cfg *c, const orc_weights *w, int T, const float *h_star,
+                          const float *m_in, float *y) {
+    const int d = c->d, H = c->H, r = c->r > 0 ? c->r : 1;
+    float *m = (float *)malloc(sizeof(float) * d);
+    float *mn = (float *)malloc(sizeof(float) * d);
+    float *x = (float *)malloc(sizeof(float) * d);
+    float *ab = (float *)malloc(sizeof(float) * d);
+    float *wy = (float *)malloc(sizeof(float) * d);
+    float Bv[1], Cv[1];
+    float *bn = (float *)malloc(sizeof(float) * r);
+    orc_cfg c1 = *c;
+    c1.N = 1;
+    orc_weights w1 = *w;
+    w1.w_b = NULL;
+    w1.w_c = NULL;
+    for (int s = 0; s < H; ++s) {
+        if (m_in)
+            memcpy(m, m_in + (size_t)s * d, sizeof(float) * d);
+        else
+            memset(m, 0, sizeof(float) * d);
+        for (int t = 0; t < T; ++t) {
+            carrier_inputs(&c1, &w1, s, h_star + ((size_t)t * H + s) * d, x, ab, Bv, Cv, bn);
+            for (int i = 0; i < d; ++i) mn[i] = ab[i] * m[i] + (1.0f - ab[i]) * x[i];
+            float *out = y + ((size_t)t * H + s) * d;
+            if (w->w_out) {
+                gemv_rm(w->w_out + (size_t)s * d * d, d, d, mn, wy);
+                for (int i = 0; i < d; ++i) out[i] = mn[i] + wy[i];
+            } else {
+                memcpy(out, mn, sizeof(float) * d);
+            }
+            memcpy(m, out, sizeof(float) * d);
+        }
+    }
+    free(m); free(mn); free(x); free(ab); free(wy); free(bn);
+}
+
+/* ------------------------------------------------------------------------- */
+/* whole forward                                                              */
+/* ------------------------------------------------------------------------- */
+
+/* Canonical forward (TRAINER:4677-4731 per-token structure with x_t = E[tok] as in the
+ * fixed-history query, tokenizer.rs:117-119): solve every token independently, pool, LM head,
+ * greedy argmax; then the carrier over each sequence. */
+void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
+                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
+                 float *scan_y, float *scan_state, int nthreads) {
+    const int d = c->d, H = c->H, V = c->V;
+    const size_t hd = (size_t)H * d;
+    const long ntok = (long)B * T;
+    prep p;
+    prep_init(&p, c, w);
+    float *lm_wt = NULL;
+    if (logits || argmax) {
+        lm_wt = (float *)malloc(sizeof(float) * (size_t)V * d);
+        transpose(w->lm_w, V, d, lm_wt);
+    }
+    float *hs_all = h_star;
+    int own_h = 0;
+    if (!hs_all) {
+        hs_all = (float *)malloc(sizeof(float) * hd * ntok);
+        own_h = 1;
+    }
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        scratch sc;
+        scratch_init(&sc, c);
+        float *tmp = (float *)malloc(sizeof(float) * d);
+        float *lg = (float *)malloc(sizeof(float) * V);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (long t = 0; t < ntok; ++t) {
+            const int32_t tok = tokens[t];
+            float *h = hs_all + hd * t;
+            int it = solve_p(&p, &sc, w->embed + (size_t)tok * d, h, NULL);
+            if (iters) iters[t] = it;
+            if (pooled || logits || argmax) {
+                float *lt = logits ? logits + (size_t)V * t : lg;
+                lm_head_tok(c, w, lm_wt, h, pooled ? pooled + (size_t)d * t : NULL,
+                            (logits || argmax) ? lt : NULL, tmp);
+                if (argmax) argmax[t] = orc_argmax(lt, V);
+            }
+        }
+        free(tmp);
+        free(lg);
+        scratch_free(&sc);
+    }
+    if (scan_y || scan_state) {
+        float *ybuf = scan_y;
+        if (!ybuf) ybuf = (float *)malloc(sizeof(float) * hd * ntok);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+        for (int b = 0; b < B; ++b)
+            orc_scan_seq(c, w, T, hs_all + hd * (size_t)b * T, NULL, ybuf + hd * (size_t)b * T,
+                         scan_state ? scan_state + (size_t)b * hd * c->N : NULL);
+        if (!scan_y) free(ybuf);
+    }
+    if (own_h) free(hs_all);
+    free(lm_wt);
+    prep_free(&p);
+}
+
+/* Greedy decode (TRAINER:4219-4431 loop with LmHead::sample at temperature <= 1e-4 =
+ * argmax, lm_head.rs:104-112): the next query is the embedding of the last token. */
+void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int32_t *start,
+                       int n_new, int32_t *out_tokens, int nthreads) {
+    int32_t *cur = (int32_t *)malloc(sizeof(int32_t) * B);
+    int32_t *nxt = (int32_t *)malloc(sizeof(int32_t) * B);
+    memcpy(cur, start, sizeof(int32_t) * B);
+    for (int j = 0; j < n_new; ++j) {
+        orc_forward(c, w, B, 1, cur, NULL, NULL, NULL, NULL, nxt, NULL, NULL, nthreads);
+        for (int b = 0; b < B; ++b) out_tokens[(size_t)b * n_new + j] = nxt[b];
+        memcpy(cur, nxt, sizeof(int32_t) * B);
+    }
+    free(cur);
+    free(nxt);
+}
+
+/* ------------------------------------------------------------------------- */
+/* trait surfaces                                                             */
+/* ------------------------------------------------------------------------- */
+
+/* gpu_backend.rs:18-56 CpuBlockBackend::fpm_batch_step (ZOH, h_prev = 0). */
+void orc_zoh_step(int d, const float *x, const float *dt, const float *a, const float *b,
+                  const float *c, float *y) {
+    for (int i = 0; i < d; ++i) {
+        const float abar = expf(dt[i] * a[i]);
+        const float bbar = fabsf(a[i]) > 1e-8f ? (abar - 1.0f) / a[i] * b[i] : dt[i] * b[i];
+        const float hn = bbar * x[i];
+        y[i] = c[i] * hn;
+    }
+}
+
+/* aideen-engine/src/gpu/shaders/ffn_forward.wgsl:22-37: y[row] = sum_i w[i*out + row] x[i]. */
+void orc_gemv_colmajor(const float *w, const float *x, int in_dim, int out_dim, float *y) {
+    for (int r = 0; r < out_dim; ++r) {
+        float acc = 0.0f;
+        for (int i = 0; i < in_dim; ++i) acc += w[(size_t)i * out_dim + r] * x[i];
+        y[r] = acc;
+    }
+}

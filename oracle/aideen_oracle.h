@@ -1,0 +1,99 @@
+/*
+ * aideen_oracle.h -- CPU restatement of the AIDEEN DEQ forward (TEST INFRASTRUCTURE).
+ *
+ * This library is the checker, never the product: only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load it.  Every function cites the reference
+ * (SergioAriel/aideen) file:line whose arithmetic it restates.
+ *
+ * Layout conventions (identical to the product C-ABI, include/aideen_hip.h):
+ *   per-slot matrices   W[s][out][in]   row-major, so y = W[s] . x  (FPMR:1314, FPMR:1402-1421)
+ *   slot vectors        [H][d]          HSlots row-major [slot][d]   (aideen-core/src/state.rs:85-146)
+ *   hidden states       [B][T][H][d]    token-major                  (UWGSL:711-712)
+ *   LM head             lm_w [V][d]     row-major                    (lm_head.rs:11-12)
+ */
+#ifndef AIDEEN_ORACLE_H
+#define AIDEEN_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Semantic switches; the values equal the ADN_F_* bits of include/aideen_hip.h. */
+#define ORC_F_WIN_TRANSPOSED   (1u << 0) /* signal = W_in^T x        (UWGSL:773, PPT:161)            */
+#define ORC_F_SCORE_CLAMP4     (1u << 1) /* scores clamped to [-4,4] (PPT:216, ARCHITECTURE.md:128)  */
+#define ORC_F_RMS_EXCL_ANCHOR  (1u << 2) /* RMS over o+signal only   (ARCHITECTURE.md:160-170)       */
+#define ORC_F_INIT_SIGNAL_RMS  (1u << 3) /* h0 = signal/rms(signal)  (UWGSL:900-943)                 */
+#define ORC_F_RESID_L2         (1u << 4) /* L2 residual over [H*d]   (aideen-node/src/inference.rs:214-221) */
+#define ORC_F_SCAN_SELECTIVE   (1u << 5) /* input-dependent decay    (gpu_deq.rs:6129-6214)          */
+
+typedef struct orc_cfg {
+    int32_t d, H, V, N, r;     /* d_r, h_slots, vocab, d_state, write rank (FPMR:290 RETAIN_RANK=32) */
+    uint32_t flags;
+    int32_t max_iters;
+    float eps;                 /* residual tolerance (ArchitectureConfig::deq_epsilon) */
+    float beta;                /* Picard damping (FPMR:458, 0.70)                     */
+    int32_t anderson_m;        /* 0 = plain Picard                                    */
+} orc_cfg;
+
+typedef struct orc_weights {
+    const float *w_q, *w_k, *w_v, *w_o, *w_in; /* [H][d][d]                      */
+    const float *q_bias, *k_bias;               /* [H][d] or NULL (zero)          */
+    const float *anchor;                        /* [H][d] slot_anchor             */
+    const float *norm_scale;                    /* [d]                            */
+    const float *embed;                         /* [V][d]                         */
+    const float *lm_w;                          /* [V][d]                         */
+    const float *lm_b;                          /* [V] or NULL (zero)             */
+    const float *lm_g;                          /* [d] or NULL (ones)             */
+    const float *a_log;                         /* [H][d]                         */
+    const float *wx_diag;                       /* [H][d] diagonal of W_x         */
+    const float *w_out;                         /* [H][d][d] or NULL (zero)       */
+    const float *b_delta;                       /* [H][d] or NULL (zero)          */
+    const float *w_kw;                          /* [H][d][r]                      */
+    const float *w_vw;                          /* [H][r][d]                      */
+    const float *w_b, *w_c;                     /* [H][N][d] or NULL (ones)       */
+} orc_weights;
+
+/* --- spectral_norm.rs ---------------------------------------------------- */
+float orc_spectral_norm(const float *w, int rows, int cols, int n_iter);
+void  orc_normalize(float *w, int rows, int cols, float target, int n_iter);
+void  orc_normalize_if_needed(float *w, int rows, int cols, float threshold, int n_iter);
+void  orc_damped_update(const float *h, const float *f, float beta, int n, float *out);
+
+/* --- FPMR per-token pieces ------------------------------------------------ */
+void orc_signal(const orc_cfg *c, const orc_weights *w, const float *x, float *signal);
+void orc_init(const orc_cfg *c, const orc_weights *w, const float *x, const float *signal, float *h0);
+void orc_picard_step(const orc_cfg *c, const orc_weights *w, const float *h, const float *signal,
+                     float *h_next, float *attn /* [H][H] or NULL */);
+/* Anderson coefficients for n = 2..4 pseudo-residuals (g is the n x n Gram matrix). */
+void orc_anderson_coeffs(int n, const float *g, float *beta);
+int  orc_solve_token(const orc_cfg *c, const orc_weights *w, const float *x, float *h_star,
+                     float *resid_trace /* [max_iters] or NULL */);
+
+/* --- lm_head.rs ----------------------------------------------------------- */
+void orc_lm_head_token(const orc_cfg *c, const orc_weights *w, const float *h_star,
+                       float *pooled /* [d] or NULL */, float *logits /* [V] or NULL */);
+int  orc_argmax(const float *logits, int V);
+
+/* --- temporal carrier ------------------------------------------------------ */
+void orc_scan_seq(const orc_cfg *c, const orc_weights *w, int T, const float *h_star,
+                  const float *state_in, float *y, float *state_out);
+void orc_scan_recirculate(const orc_cfg *c, const orc_weights *w, int T, const float *h_star,
+                          const float *m_in, float *y);
+
+/* --- whole forward and decode ----------------------------------------------- */
+void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
+                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
+                 float *scan_y, float *scan_state, int nthreads);
+void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int32_t *start,
+                       int n_new, int32_t *out_tokens, int nthreads);
+
+/* --- other trait surfaces --------------------------------------------------- */
+void orc_zoh_step(int d, const float *x, const float *dt, const float *a, const float *b,
+                  const float *c, float *y);
+void orc_gemv_colmajor(const float *w, const float *x, int in_dim, int out_dim, float *y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

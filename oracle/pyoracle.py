@@ -1,0 +1,234 @@
+"""ctypes binding of the C oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module; the
+product package never does.  ``build()`` compiles ``liboracle.so`` from ``aideen_oracle.c``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from typing import Dict, Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32P = C.POINTER(C.c_float)
+I32P = C.POINTER(C.c_int32)
+
+
+class OrcCfg(C.Structure):
+    _fields_ = [("d", C.c_int32), ("H", C.c_int32), ("V", C.c_int32), ("N", C.c_int32),
+                ("r", C.c_int32), ("flags", C.c_uint32), ("max_iters", C.c_int32),
+                ("eps", C.c_float), ("beta", C.c_float), ("anderson_m", C.c_int32)]
+
+
+WEIGHT_FIELDS = ["w_q", "w_k", "w_v", "w_o", "w_in", "q_bias", "k_bias", "anchor", "norm_scale",
+                 "embed", "lm_w", "lm_b", "lm_g", "a_log", "wx_diag", "w_out", "b_delta", "w_kw",
+                 "w_vw", "w_b", "w_c"]
+
+
+class OrcWeights(C.Structure):
+    _fields_ = [(n, F32P) for n in WEIGHT_FIELDS]
+
+
+def build(quiet: bool = True) -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True,
+                   stdout=subprocess.DEVNULL if quiet else None)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.orc_spectral_norm.restype = C.c_float
+        L.orc_spectral_norm.argtypes = [F32P, C.c_int, C.c_int, C.c_int]
+        L.orc_normalize.argtypes = [F32P, C.c_int, C.c_int, C.c_float, C.c_int]
+        L.orc_normalize_if_needed.argtypes = [F32P, C.c_int, C.c_int, C.c_float, C.c_int]
+        L.orc_damped_update.argtypes = [F32P, F32P, C.c_float, C.c_int, F32P]
+        L.orc_signal.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P]
+        L.orc_init.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
+        L.orc_picard_step.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P, F32P]
+        L.orc_anderson_coeffs.argtypes = [C.c_int, F32P, F32P]
+        L.orc_solve_token.restype = C.c_int
+        L.orc_solve_token.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
+        L.orc_lm_head_token.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
+        L.orc_argmax.restype = C.c_int
+        L.orc_argmax.argtypes = [F32P, C.c_int]
+        L.orc_scan_seq.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, F32P, F32P, F32P, F32P]
+        L.orc_scan_recirculate.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, F32P, F32P, F32P]
+        L.orc_forward.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, C.c_int, I32P,
+                                  F32P, F32P, F32P, I32P, I32P, F32P, F32P, C.c_int]
+        L.orc_decode_greedy.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, I32P,
+                                        C.c_int, I32P, C.c_int]
+        L.orc_zoh_step.argtypes = [C.c_int, F32P, F32P, F32P, F32P, F32P, F32P]
+        L.orc_gemv_colmajor.argtypes = [F32P, F32P, C.c_int, C.c_int, F32P]
+        _lib = L
+    return _lib
+
+
+def fp(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(F32P)
+
+
+def ip(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(I32P)
+
+
+class Oracle:
+    """Holds one model (config + weights) for repeated oracle calls."""
+
+    def __init__(self, cfg, weights: Dict[str, Optional[np.ndarray]]):
+        self.mc = cfg
+        self.c = OrcCfg(cfg.d, cfg.H, cfg.V, cfg.N, cfg.r, cfg.flags, cfg.max_iters,
+                        cfg.eps, cfg.beta, cfg.anderson_m)
+        self._keep = {k: (None if v is None else np.ascontiguousarray(v, dtype=np.float32))
+                      for k, v in weights.items()}
+        self.w = OrcWeights(**{k: fp(self._keep.get(k)) for k in WEIGHT_FIELDS})
+        self.L = lib()
+
+    # --- per-token pieces -------------------------------------------------
+    def signal(self, x):
+        out = np.zeros((self.mc.H, self.mc.d), np.float32)
+        self.L.orc_signal(C.byref(self.c), C.byref(self.w), fp(np.ascontiguousarray(x, np.float32)), fp(out))
+        return out
+
+    def init(self, x, signal):
+        out = np.zeros((self.mc.H, self.mc.d), np.float32)
+        self.L.orc_init(C.byref(self.c), C.byref(self.w), fp(np.ascontiguousarray(x, np.float32)),
+                        fp(np.ascontiguousarray(signal, np.float32)), fp(out))
+        return out
+
+    def step(self, h, signal):
+        out = np.zeros((self.mc.H, self.mc.d), np.float32)
+        attn = np.zeros((self.mc.H, self.mc.H), np.float32)
+        self.L.orc_picard_step(C.byref(self.c), C.byref(self.w), fp(np.ascontiguousarray(h, np.float32)),
+                               fp(np.ascontiguousarray(signal, np.float32)), fp(out), fp(attn))
+        return out, attn
+
+    def solve(self, x):
+        h = np.zeros((self.mc.H, self.mc.d), np.float32)
+        trace = np.zeros(max(self.mc.max_iters, 1), np.float32)
+        it = self.L.orc_solve_token(C.byref(self.c), C.byref(self.w),
+                                    fp(np.ascontiguousarray(x, np.float32)), fp(h), fp(trace))
+        return h, it, trace[:it]
+
+    def lm_head(self, h_star):
+        pooled = np.zeros(self.mc.d, np.float32)
+        logits = np.zeros(self.mc.V, np.float32)
+        self.L.orc_lm_head_token(C.byref(self.c), C.byref(self.w),
+                                 fp(np.ascontiguousarray(h_star, np.float32)), fp(pooled), fp(logits))
+        return pooled, logits
+
+    def scan(self, h_star_seq, state_in=None):
+        T = h_star_seq.shape[0]
+        y = np.zeros((T, self.mc.H, self.mc.d), np.float32)
+        st = np.zeros((self.mc.H, self.mc.d, self.mc.N), np.float32)
+        self.L.orc_scan_seq(C.byref(self.c), C.byref(self.w), T,
+                            fp(np.ascontiguousarray(h_star_seq, np.float32)),
+                            fp(None if state_in is None else np.ascontiguousarray(state_in, np.float32)),
+                            fp(y), fp(st))
+        return y, st
+
+    def scan_recirculate(self, h_star_seq, m_in=None):
+        T = h_star_seq.shape[0]
+        y = np.zeros((T, self.mc.H, self.mc.d), np.float32)
+        self.L.orc_scan_recirculate(C.byref(self.c), C.byref(self.w), T,
+                                    fp(np.ascontiguousarray(h_star_seq, np.float32)),
+                                    fp(None if m_in is None else np.ascontiguousarray(m_in, np.float32)),
+                                    fp(y))
+        return y
+
+    # --- whole forward ------------------------------------------------------
+    def forward(self, tokens, want_logits=True, want_scan=True, nthreads=0):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, T = tokens.shape
+        mc = self.mc
+        out = dict(
+            h_star=np.zeros((B, T, mc.H, mc.d), np.float32),
+            pooled=np.zeros((B, T, mc.d), np.float32),
+            iters=np.zeros((B, T), np.int32),
+            argmax=np.zeros((B, T), np.int32),
+        )
+        if want_logits:
+            out["logits"] = np.zeros((B, T, mc.V), np.float32)
+        if want_scan:
+            out["scan_y"] = np.zeros((B, T, mc.H, mc.d), np.float32)
+            out["scan_state"] = np.zeros((B, mc.H, mc.d, mc.N), np.float32)
+        self.L.orc_forward(C.byref(self.c), C.byref(self.w), B, T, ip(tokens),
+                           fp(out["h_star"]), fp(out["pooled"]), fp(out.get("logits")),
+                           ip(out["iters"]), ip(out["argmax"]), fp(out.get("scan_y")),
+                           fp(out.get("scan_state")), nthreads)
+        return out
+
+    def decode_greedy(self, start, n_new, nthreads=0):
+        start = np.ascontiguousarray(start, dtype=np.int32)
+        out = np.zeros((start.shape[0], n_new), np.int32)
+        self.L.orc_decode_greedy(C.byref(self.c), C.byref(self.w), start.shape[0], ip(start),
+                                 n_new, ip(out), nthreads)
+        return out
+
+
+def spectral_norm(w: np.ndarray, n_iter: int = 20) -> float:
+    w = np.ascontiguousarray(w, np.float32)
+    return lib().orc_spectral_norm(fp(w), w.shape[0], w.shape[1], n_iter)
+
+
+def normalize(w: np.ndarray, target: float, n_iter: int = 20) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.float32).copy()
+    lib().orc_normalize(fp(w), w.shape[0], w.shape[1], target, n_iter)
+    return w
+
+
+def normalize_if_needed(w: np.ndarray, threshold: float, n_iter: int = 20) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.float32).copy()
+    lib().orc_normalize_if_needed(fp(w), w.shape[0], w.shape[1], threshold, n_iter)
+    return w
+
+
+def damped_update(h, f, beta):
+    h = np.ascontiguousarray(h, np.float32)
+    f = np.ascontiguousarray(f, np.float32)
+    out = np.zeros_like(h)
+    lib().orc_damped_update(fp(h), fp(f), beta, h.size, fp(out))
+    return out
+
+
+def anderson_coeffs(g: np.ndarray) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    beta = np.zeros(g.shape[0], np.float32)
+    lib().orc_anderson_coeffs(g.shape[0], fp(g), fp(beta))
+    return beta
+
+
+def argmax(logits: np.ndarray) -> int:
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().orc_argmax(fp(logits), logits.size)
+
+
+def zoh_step(x, dt, a, b, c):
+    arrs = [np.ascontiguousarray(v, np.float32) for v in (x, dt, a, b, c)]
+    y = np.zeros_like(arrs[0])
+    lib().orc_zoh_step(arrs[0].size, *[fp(v) for v in arrs], fp(y))
+    return y
+
+
+def gemv_colmajor(w, x, out_dim):
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(out_dim, np.float32)
+    lib().orc_gemv_colmajor(fp(w), fp(x), x.size, out_dim, fp(y))
+    return y

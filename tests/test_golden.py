@@ -1,0 +1,40 @@
+"""The oracle reproduces the committed C1 golden fixtures bit for bit (no GPU)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from aideen_amd import synth
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load_case(name):
+    import dataclasses
+    meta = json.load(open(os.path.join(HERE, name + ".json")))
+    mc = synth.ModelConfig(**meta["config"])
+    w = synth.make_weights(mc, seed=meta["weights_seed"])
+    assert synth.weights_digest(w) == meta["weights_sha256"], "synthetic generator drifted"
+    data = dict(np.load(os.path.join(HERE, name + ".npz")))
+    toks = synth.make_tokens("uniform", meta["B"], meta["T"], mc.V, seed=meta["tokens_seed"])
+    assert np.array_equal(toks, data["tokens"])
+    return mc, w, data
+
+
+@pytest.mark.parametrize("name", ["c1_forward", "c1_anderson_m5"])
+def test_oracle_reproduces_golden(oracle_lib, name):
+    mc, w, data = load_case(name)
+    out = oracle_lib.Oracle(mc, w).forward(data["tokens"])
+    for k, v in out.items():
+        assert np.array_equal(v, data[k]), k
+
+
+def test_golden_fixed_points_are_fixed_points(oracle_lib):
+    """Size-independent property of the fixture itself: one more step moves h* by < eps."""
+    mc, w, data = load_case("c1_forward")
+    o = oracle_lib.Oracle(mc, w)
+    for t in range(0, 64, 7):
+        x = w["embed"][data["tokens"][0, t]]
+        hn, _ = o.step(data["h_star"][0, t], o.signal(x))
+        assert np.abs(hn - data["h_star"][0, t]).max() < mc.eps
