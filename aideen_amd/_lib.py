@@ -52,6 +52,18 @@ class AdnOutputs(C.Structure):
                 ("iters", I32P), ("scan_y", F32P), ("scan_state", F32P)]
 
 
+STAGES = ["signal_gemm", "init", "qkv_gemm", "attn", "wo_gemm", "update", "converge", "anderson",
+          "pool", "lmhead_gemm", "argmax", "scan_prep", "scan", "readout_gemm"]
+PROFILE_MAX_ITERS = 256
+
+
+class AdnProfile(C.Structure):
+    _fields_ = [("ms", C.c_double * len(STAGES)), ("flops", C.c_double * len(STAGES)),
+                ("bytes", C.c_double * len(STAGES)), ("launches", C.c_int32 * len(STAGES)),
+                ("active", C.c_int32 * PROFILE_MAX_ITERS), ("n_iters", C.c_int32),
+                ("total_ms", C.c_double)]
+
+
 class AdnError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"[{code}] {msg}")
@@ -96,6 +108,8 @@ def lib():
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),
         "adn_load_tensor": (C.c_int, [ctx_p, F32P, C.c_int64, I32P]),
         "adn_ffn_forward": (C.c_int, [ctx_p, C.c_int32, C.c_int32, C.c_int32, F32P]),
+        "adn_profile_forward": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs),
+                                          C.POINTER(AdnProfile)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

@@ -151,6 +151,29 @@ class GpuDeqBackend:
                         scan_state=_dev_f(outputs.get("scan_state")))
         check(lib().adn_forward_async(self._ctx, C.byref(run), C.byref(co)))
 
+    def profile_forward(self, tokens=None, s_in=None, *, outputs: Dict[str, object],
+                        max_iters: Optional[int] = None, eps: Optional[float] = None,
+                        damping: Optional[float] = None) -> dict:
+        """One device-memory forward with a HIP event pair around every kernel; returns per-stage
+        device time, algorithmic FLOPs/bytes, launch counts and the active tokens per iteration."""
+        m = self.model
+        B, T = (tokens.shape if tokens is not None else s_in.shape[:2])
+        run = AdnRun(B, T, m.max_iters if max_iters is None else max_iters,
+                     m.eps if eps is None else eps, m.beta if damping is None else damping,
+                     _dev_i(tokens), _dev_f(s_in), None)
+        co = AdnOutputs(h_star=_dev_f(outputs.get("h_star")), pooled=_dev_f(outputs.get("pooled")),
+                        logits=_dev_f(outputs.get("logits")), argmax=_dev_i(outputs.get("argmax")),
+                        iters=_dev_i(outputs.get("iters")), scan_y=_dev_f(outputs.get("scan_y")),
+                        scan_state=_dev_f(outputs.get("scan_state")))
+        prof = _lib.AdnProfile()
+        check(lib().adn_profile_forward(self._ctx, C.byref(run), C.byref(co), C.byref(prof)))
+        stages = {}
+        for i, name in enumerate(_lib.STAGES):
+            if prof.launches[i]:
+                stages[name] = dict(ms=prof.ms[i], flops=prof.flops[i], bytes=prof.bytes[i],
+                                    launches=prof.launches[i])
+        return dict(stages=stages, active=list(prof.active[:prof.n_iters]), total_ms=prof.total_ms)
+
     # reference-named conveniences ---------------------------------------------------------
     def run_forward_deq(self, batch, seq, max_iters, eps, damping, s_in):
         """``run_forward_deq`` (gpu_deq.rs:3687-3727): H_next [B*T*H*d] and iteration counts."""

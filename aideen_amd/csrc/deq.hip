@@ -67,11 +67,16 @@ __global__ void k_init(Dims D, SolveBuffers b, const float *x_src, const int32_t
 // dot products per lane, all-reduced across the wave so every lane holds every score.
 // ---------------------------------------------------------------------------------------
 template <int H, int QA, int VEC>
-__global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur) {
+__global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, int k) {
     constexpr int NG = H / QA;
     const int gw = blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int n = b.cnt[cur];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        // the update kernel of this iteration appends survivors to the other list
+        b.cnt[cur ^ 1] = 0;
+        b.cnt_hist[k] = n;
+    }
     const int i = gw / NG, g = gw - (gw / NG) * NG;
     if (i >= n) return;
     const int d = D.d;
@@ -148,105 +153,85 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Damped update of one (token, slot) row (FPMR:1386-1393): c = o + signal + anchor,
-// f = g*c/sqrt(mean(c^2)+1e-6), h' = f*beta + h*(1-beta); residual partial over the row.
+// Damped update and exit test of one active token (one wave; FPMR:1386-1393): per slot
+// c = o + signal + anchor, f = g*c/sqrt(mean(c^2)+1e-6), h' = f*beta + h*(1-beta); the token's
+// residual (max-abs, or L2 over [H*d]) decides the exit: a done token records k+1 applied
+// updates, a continuing one is appended to the next active list (one atomic per workgroup).
+// The list order is not deterministic, which is harmless: every token's arithmetic is
+// independent of its position.
 // ---------------------------------------------------------------------------------------
 template <int E>
-__global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
-                                                const float *anchor, const float *norm_scale,
+__global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur, int k, int max_iters,
+                                                float eps, const float *anchor, const float *norm_scale,
                                                 float beta) {
-    const int gw = blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    __shared__ int keep_s[WAVES_PER_BLOCK];
+    __shared__ int tok_s[WAVES_PER_BLOCK];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int n = b.cnt[cur];
+    if (blockIdx.x * WAVES_PER_BLOCK >= n) return;
+    const int i = blockIdx.x * WAVES_PER_BLOCK + wave;
     const int H = D.H;
     constexpr int d = 64 * E;
-    const int i = gw / H, s = gw - (gw / H) * H;
-    if (i >= n) return;
-    const int t = b.act[cur][i];
-    const float *o = b.o + ((long)i * H + s) * d;
-    const float *sg = b.signal + ((long)t * H + s) * d;
-    const float *an = anchor + (long)s * d;
-    float *h = b.h + ((long)t * H + s) * d;
-    float cval[E];
-    float ss = 0.0f;
     const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int idx = lane + 64 * e;
-        const float as_ = o[idx] + sg[idx];
-        const float c = (as_ + 0.0f) + an[idx];
-        cval[e] = c;
-        ss += excl ? as_ * as_ : c * c;
-    }
-    ss = wave_sum(ss);
-    const float rms = sqrtf(ss / (float)d + 1e-6f);
-    const float omb = 1.0f - beta;
-    float r = 0.0f;
     const bool l2 = (D.flags & ADN_F_RESID_L2) != 0;
+    bool keep = false;
+    int t = -1;
+    if (i < n) {
+        t = b.act[cur][i];
+        float g[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int idx = lane + 64 * e;
-        const float f = norm_scale[idx] * cval[e] / rms;
-        const float hold = h[idx];
-        const float hn = f * beta + hold * omb;
-        h[idx] = hn;
-        const float df = hn - hold;
-        r = l2 ? r + df * df : fmaxf(r, fabsf(df));
-    }
-    r = l2 ? wave_sum(r) : wave_max(r);
-    if (lane == 0) b.res_part[(long)i * H + s] = r;
-}
-
-// ---------------------------------------------------------------------------------------
-// Exit test and compaction (single workgroup, order-preserving, deterministic): a token is
-// done when its residual is below eps or the iteration budget is spent; done tokens record
-// the number of applied updates and drop out of the next active list.
-// ---------------------------------------------------------------------------------------
-constexpr int CONV_NT = 1024;
-
-__global__ __launch_bounds__(CONV_NT) void k_converge(Dims D, SolveBuffers b, int cur, int k,
-                                                      int max_iters, float eps) {
-    __shared__ int wave_tot[CONV_NT / 64];
-    __shared__ int base_s;
-    const int n = b.cnt[cur];
-    const int nxt = cur ^ 1;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool l2 = (D.flags & ADN_F_RESID_L2) != 0;
-    if (tid == 0) base_s = 0;
-    __syncthreads();
-    for (int c0 = 0; c0 < n; c0 += CONV_NT) {
-        const int i = c0 + tid;
-        bool keep = false;
-        int t = 0;
-        if (i < n) {
-            t = b.act[cur][i];
-            float r = 0.0f;
-            for (int s = 0; s < D.H; ++s) {
-                const float p = b.res_part[(long)i * D.H + s];
-                r = l2 ? r + p : fmaxf(r, p);
+        for (int e = 0; e < E; ++e) g[e] = norm_scale[lane + 64 * e];
+        const float omb = 1.0f - beta;
+        float rtok = 0.0f;
+        for (int s = 0; s < H; ++s) {
+            const float *o = b.o + ((long)i * H + s) * d;
+            const float *sg = b.signal + ((long)t * H + s) * d;
+            const float *an = anchor + (long)s * d;
+            float *h = b.h + ((long)t * H + s) * d;
+            float cval[E], hold[E];
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int idx = lane + 64 * e;
+                const float as_ = o[idx] + sg[idx];
+                const float c = (as_ + 0.0f) + an[idx];
+                cval[e] = c;
+                hold[e] = h[idx];
+                ss += excl ? as_ * as_ : c * c;
             }
-            if (l2) r = sqrtf(r);
-            const bool done = (r < eps) || (k + 1 >= max_iters);
-            if (done) b.iters[t] = k + 1;
-            keep = !done;
+            ss = wave_sum(ss);
+            const float rms = sqrtf(ss / (float)d + 1e-6f);
+            float r = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float f = g[e] * cval[e] / rms;
+                const float hn = f * beta + hold[e] * omb;
+                h[lane + 64 * e] = hn;
+                const float df = hn - hold[e];
+                r = l2 ? r + df * df : fmaxf(r, fabsf(df));
+            }
+            r = l2 ? wave_sum(r) : wave_max(r);
+            rtok = l2 ? rtok + r : fmaxf(rtok, r);
         }
-        const unsigned long long bal = __ballot(keep);
-        const int pos_in_wave = __popcll(bal & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_tot[wave] = __popcll(bal);
-        __syncthreads();
-        int off = 0;
-        for (int w = 0; w < wave; ++w) off += wave_tot[w];
-        const int base = base_s;
-        if (keep) b.act[nxt][base + off + pos_in_wave] = t;
-        __syncthreads();
-        if (tid == 0) {
-            int tot = 0;
-            for (int w = 0; w < CONV_NT / 64; ++w) tot += wave_tot[w];
-            base_s = base + tot;
-        }
-        __syncthreads();
+        if (l2) rtok = sqrtf(rtok);
+        const bool done = (rtok < eps) || (k + 1 >= max_iters);
+        if (done && lane == 0) b.iters[t] = k + 1;
+        keep = !done;
     }
-    if (tid == 0) b.cnt[nxt] = base_s;
+    if (lane == 0) {
+        keep_s[wave] = keep;
+        tok_s[wave] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int nk = 0;
+        for (int w = 0; w < WAVES_PER_BLOCK; ++w) nk += keep_s[w];
+        if (nk) {
+            int pos = atomicAdd(&b.cnt[cur ^ 1], nk);
+            for (int w = 0; w < WAVES_PER_BLOCK; ++w)
+                if (keep_s[w]) b.act[cur ^ 1][pos++] = tok_s[w];
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -377,16 +362,16 @@ __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int
 }
 
 template <int H, int QA>
-void attn_dispatch_vec(const Dims &D, const SolveBuffers &b, int cur, int ntok, hipStream_t st) {
+void attn_dispatch_vec(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok, hipStream_t st) {
     constexpr int NG = H / QA;
     const long waves = (long)ntok * NG;
     const dim3 grid((unsigned)((waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK));
     if (D.d % 256 == 0)
-        hipLaunchKernelGGL((k_attn<H, QA, 4>), grid, dim3(256), 0, st, D, b, cur);
+        hipLaunchKernelGGL((k_attn<H, QA, 4>), grid, dim3(256), 0, st, D, b, cur, k);
     else if (D.d % 128 == 0)
-        hipLaunchKernelGGL((k_attn<H, QA, 2>), grid, dim3(256), 0, st, D, b, cur);
+        hipLaunchKernelGGL((k_attn<H, QA, 2>), grid, dim3(256), 0, st, D, b, cur, k);
     else
-        hipLaunchKernelGGL((k_attn<H, QA, 1>), grid, dim3(256), 0, st, D, b, cur);
+        hipLaunchKernelGGL((k_attn<H, QA, 1>), grid, dim3(256), 0, st, D, b, cur, k);
 }
 
 }  // namespace
@@ -398,36 +383,31 @@ void launch_init(const Dims &D, const SolveBuffers &b, const float *x_src, const
                        dim3(64 * WAVES_PER_BLOCK), 0, st, D, b, x_src, tokens, ntok, anchor);
 }
 
-void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int ntok, hipStream_t st) {
+void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok, hipStream_t st) {
     switch (D.H) {
-        case 1: attn_dispatch_vec<1, 1>(D, b, cur, ntok, st); break;
-        case 2: attn_dispatch_vec<2, 2>(D, b, cur, ntok, st); break;
-        case 4: attn_dispatch_vec<4, 4>(D, b, cur, ntok, st); break;
-        case 8: attn_dispatch_vec<8, 8>(D, b, cur, ntok, st); break;
-        case 16: attn_dispatch_vec<16, 4>(D, b, cur, ntok, st); break;
+        case 1: attn_dispatch_vec<1, 1>(D, b, cur, k, ntok, st); break;
+        case 2: attn_dispatch_vec<2, 2>(D, b, cur, k, ntok, st); break;
+        case 4: attn_dispatch_vec<4, 4>(D, b, cur, k, ntok, st); break;
+        case 8: attn_dispatch_vec<8, 8>(D, b, cur, k, ntok, st); break;
+        case 16: attn_dispatch_vec<16, 4>(D, b, cur, k, ntok, st); break;
         default: break;  // rejected at context creation
     }
 }
 
-void launch_update(const Dims &D, const SolveBuffers &b, int cur, int ntok, const float *anchor,
-                   const float *norm_scale, float beta, hipStream_t st) {
-    const long waves = (long)ntok * D.H;
-    const dim3 grid((unsigned)((waves + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), blk(64 * WAVES_PER_BLOCK);
+void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps, int ntok,
+                   const float *anchor, const float *norm_scale, float beta, hipStream_t st) {
+    const dim3 grid((unsigned)((ntok + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), blk(64 * WAVES_PER_BLOCK);
+#define ADN_UPD_ARGS D, b, cur, k, max_iters, eps, anchor, norm_scale, beta
     switch (D.d) {
-        case 64: hipLaunchKernelGGL(k_update<1>, grid, blk, 0, st, D, b, cur, anchor, norm_scale, beta); break;
-        case 128: hipLaunchKernelGGL(k_update<2>, grid, blk, 0, st, D, b, cur, anchor, norm_scale, beta); break;
-        case 256: hipLaunchKernelGGL(k_update<4>, grid, blk, 0, st, D, b, cur, anchor, norm_scale, beta); break;
-        case 512: hipLaunchKernelGGL(k_update<8>, grid, blk, 0, st, D, b, cur, anchor, norm_scale, beta); break;
-        case 1024: hipLaunchKernelGGL(k_update<16>, grid, blk, 0, st, D, b, cur, anchor, norm_scale, beta); break;
-        case 2048: hipLaunchKernelGGL(k_update<32>, grid, blk, 0, st, D, b, cur, anchor, norm_scale, beta); break;
+        case 64: hipLaunchKernelGGL(k_update<1>, grid, blk, 0, st, ADN_UPD_ARGS); break;
+        case 128: hipLaunchKernelGGL(k_update<2>, grid, blk, 0, st, ADN_UPD_ARGS); break;
+        case 256: hipLaunchKernelGGL(k_update<4>, grid, blk, 0, st, ADN_UPD_ARGS); break;
+        case 512: hipLaunchKernelGGL(k_update<8>, grid, blk, 0, st, ADN_UPD_ARGS); break;
+        case 1024: hipLaunchKernelGGL(k_update<16>, grid, blk, 0, st, ADN_UPD_ARGS); break;
+        case 2048: hipLaunchKernelGGL(k_update<32>, grid, blk, 0, st, ADN_UPD_ARGS); break;
         default: break;  // rejected at context creation
     }
-}
-
-void launch_converge(const Dims &D, const SolveBuffers &b, int cur, int ntok, int k, int max_iters,
-                     float eps, hipStream_t st) {
-    (void)ntok;
-    hipLaunchKernelGGL(k_converge, dim3(1), dim3(CONV_NT), 0, st, D, b, cur, k, max_iters, eps);
+#undef ADN_UPD_ARGS
 }
 
 void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int k, int m,

@@ -82,6 +82,27 @@ __global__ __launch_bounds__(AM_NT) void k_argmax(const float *logits, int V, in
     }
 }
 
+// Reduce the LM-head tile partials of one row (one wave per row), same tie rule.
+__global__ __launch_bounds__(256) void k_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok,
+                                                       int ntiles, int32_t *out) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= ntok) return;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int t = lane; t < ntiles; t += 64) {
+        const float v = am_val[(long)t * ntok + row];
+        const int i = am_idx[(long)t * ntok + row];
+        am_combine(bv, bi, v, i);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float v2 = __shfl_xor(bv, off, 64);
+        const int i2 = __shfl_xor(bi, off, 64);
+        am_combine(bv, bi, v2, i2);
+    }
+    if (lane == 0) out[row] = bi < 0 ? 0 : bi;
+}
+
 // Greedy decode bookkeeping: tokens[b] = argmax[b]; out_seq[b][j] = argmax[b].
 __global__ void k_decode_step(const int32_t *argmax, int32_t *tokens, int32_t *out_seq, int B,
                               int n_new, int j) {
@@ -102,6 +123,12 @@ void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, f
 
 void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st) {
     hipLaunchKernelGGL(k_argmax, dim3((unsigned)ntok), dim3(AM_NT), 0, st, logits, V, out);
+}
+
+void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 3) / 4)), dim3(256), 0, st, am_val, am_idx, ntok,
+                       ntiles, out);
 }
 
 void launch_copy_tokens_from_argmax(const int32_t *argmax, int32_t *tokens, int32_t *out_seq,

@@ -6,6 +6,10 @@
 namespace adn {
 
 enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS = 1, EPI_ADD_A = 2 };
+// GemmParams.am_val/am_idx != null: also write each row's (max, last arg-max) over every
+// 128-column tile into [ceil(N/128)][M] partials (LM head + greedy decode).
+// Each use of the GEMM is a separate kernel symbol so profilers report them apart.
+enum GemmRole { ROLE_SIGNAL = 0, ROLE_QKV, ROLE_WO, ROLE_LMHEAD, ROLE_READOUT, ROLE_SCAN_PROJ, ROLE_COUNT };
 
 // C[m][n] = sum_k A(m,s)[k] * B(s)[n][k] (+ epilogue), for m < M (or *m_count), n < N, s < S.
 //   A(m,s) = A + row(m)*a_sm + s*a_ss, row(m) = a_idx ? a_idx[m] : m   (a_idx checked < a_idx_max)
@@ -27,7 +31,11 @@ struct GemmParams {
     const int32_t *m_count;
     unsigned *err;
     int epi;
+    int role;
+    float *am_val;
+    int32_t *am_idx;
 };
+constexpr int GEMM_BN = 128;
 void launch_gemm(const GemmParams &p, hipStream_t st);
 
 // ---- DEQ solve kernels (deq.hip) ------------------------------------------------------
@@ -37,10 +45,10 @@ struct SolveBuffers {
     float *qkv;         // [ntok][H][3d] compact by active index
     float *mix;         // [ntok][H][d]  compact
     float *o;           // [ntok][H][d]  compact
-    float *res_part;    // [ntok][H]     compact
     int32_t *act[2];    // active token lists
     int32_t *cnt;       // [4]: counts of act[0], act[1]; cnt[2] unused; cnt[3] = total tokens
     int32_t *iters;     // [ntok]
+    int32_t *cnt_hist;  // [ADN_PROFILE_MAX_ITERS] active tokens entering iteration k
     float *hist;        // Anderson ring [m][ntok][H][d] or null
     unsigned *err;
 };
@@ -48,14 +56,12 @@ struct SolveBuffers {
 // h0 per token and the first active list (all tokens, in order).
 void launch_init(const Dims &D, const SolveBuffers &b, const float *x_src, const int32_t *tokens,
                  int ntok, const float *anchor, hipStream_t st);
-// Slot attention: scores, softmax, mix for each active token.
-void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int ntok, hipStream_t st);
-// Damped RMS update and per-(token,slot) residual partials.
-void launch_update(const Dims &D, const SolveBuffers &b, int cur, int ntok, const float *anchor,
-                   const float *norm_scale, float beta, hipStream_t st);
-// Residual reduction, exit test, iteration counts and the next active list.
-void launch_converge(const Dims &D, const SolveBuffers &b, int cur, int ntok, int k, int max_iters,
-                     float eps, hipStream_t st);
+// Slot attention: scores, softmax, mix for each active token; also clears the next list's
+// count and records the active count of iteration k.
+void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok, hipStream_t st);
+// Damped RMS update, token residual, exit test, iteration counts and the next active list.
+void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps, int ntok,
+                   const float *anchor, const float *norm_scale, float beta, hipStream_t st);
 // Anderson store + mix for the tokens still active after iteration k.
 void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int k, int m,
                      hipStream_t st);
@@ -66,6 +72,9 @@ void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, f
                       float *pnorm, hipStream_t st);
 // argmax over each row of logits with the last-max tie rule.
 void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st);
+// final reduction of the per-tile arg-max partials written by the LM-head GEMM
+void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
+                          hipStream_t st);
 // S_in gather for the embedded-input path: x[t] = E[tok[t]] (for init/signal when tokens given)
 void launch_copy_tokens_from_argmax(const int32_t *argmax, int32_t *tokens, int32_t *out_seq,
                                     int B, int n_new, int j, hipStream_t st);
@@ -76,13 +85,19 @@ struct ScanBuffers {
     float *y;          // [ntok][H][d] pre-readout output (or final if no W_out)
     float *chunk_s;    // [B][nch][H][d][N]
     float *chunk_p;    // [B][nch][H][d]
+    float *gate_a;     // [ntok][H][d] per-element decay abar
+    float *gate_x;     // [ntok][H][d] per-element input (1 - abar) x
 };
 int scan_rec_len(const Dims &D);
-void launch_scan_prep(const Dims &D, const float *h, int ntok, const float *w_kw, const float *w_b,
-                      const float *w_c, float *rec, hipStream_t st);
-void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, const float *a_log,
-                 const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in,
-                 float *y, float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st);
+// rec[row*REC] = sqrt(mean(h_row^2) + 1e-6) for every (token, slot) row
+void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipStream_t st);
+// abar and (1-abar) x for every (token, slot, channel)
+void launch_scan_gate(const Dims &D, const float *h, const float *rec, int ntok, const float *a_log,
+                      const float *wx_diag, const float *b_delta, const float *w_vw, float *gate_a, float *gate_x,
+                      hipStream_t st);
+void launch_scan(const Dims &D, const float *gate_a, const float *gate_x, const float *rec, int B, int T,
+                 int has_bc, const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p,
+                 int nch, hipStream_t st);
 int scan_chunks(int B, int T, int H, int d);
 
 // ---- misc (misc.hip) ----------------------------------------------------------------------

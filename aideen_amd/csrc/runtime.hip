@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <vector>
 
@@ -42,6 +43,7 @@ struct adn_ctx {
     float *anchor = nullptr, *norm_scale = nullptr, *embed = nullptr, *lm_w = nullptr;
     float *lm_b = nullptr, *lm_g = nullptr, *a_log = nullptr, *wx_diag = nullptr, *w_out = nullptr;
     float *b_delta = nullptr, *w_kw = nullptr, *w_vw = nullptr, *w_b = nullptr, *w_c = nullptr;
+    float *w_cat = nullptr;  // [H][r + 2N][d] = [W_kw^T; W_B; W_C] per slot (carrier projections)
 
     // work buffers (capacity-sized)
     SolveBuffers sb{};
@@ -50,6 +52,8 @@ struct adn_ctx {
     float *pnorm = nullptr;
     float *logits_scratch = nullptr;  // lazy [cap_tok][V]
     int32_t *argmax_scratch = nullptr;
+    float *am_val = nullptr;      // [cap_tok][ceil(V/128)] LM-head tile arg-max partials
+    int32_t *am_idx = nullptr;
     unsigned *d_err = nullptr;
 
     // host-API staging (lazy, capacity-sized)
@@ -139,10 +143,48 @@ float *staging_f(adn_ctx *c, int slot, size_t bytes) {
     return (float *)b.p;
 }
 
+// Per-launch event pairs for adn_profile_forward (null when not profiling).
+struct Prof {
+    struct Rec {
+        int stage, k;
+        hipEvent_t e0, e1;
+    };
+    std::vector<Rec> recs;
+    std::vector<hipEvent_t> pool;
+    size_t used = 0;
+    hipEvent_t get() {
+        if (used == pool.size()) {
+            hipEvent_t e;
+            ADN_HIP(hipEventCreate(&e));
+            pool.push_back(e);
+        }
+        return pool[used++];
+    }
+    ~Prof() {
+        for (auto e : pool) (void)hipEventDestroy(e);
+    }
+};
+
+struct Span {
+    Prof *p;
+    hipStream_t st;
+    size_t idx;
+    Span(Prof *p_, int stage, int k, hipStream_t st_) : p(p_), st(st_), idx(0) {
+        if (!p) return;
+        Prof::Rec r{stage, k, p->get(), p->get()};
+        ADN_HIP(hipEventRecord(r.e0, st));
+        idx = p->recs.size();
+        p->recs.push_back(r);
+    }
+    ~Span() {
+        if (p) (void)hipEventRecord(p->recs[idx].e1, st);
+    }
+};
+
 // ---------------------------------------------------------------------------------------
 // the forward pipeline (device pointers; enqueue only)
 // ---------------------------------------------------------------------------------------
-void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
+void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
     const Dims &D = c->D;
     const int ntok = r.batch * r.seq;
     const int d = D.d, H = D.H;
@@ -154,6 +196,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
     // signal[t][s] = W_in[s] x_t   (x gathered from the embedding when tokens are given)
     {
         GemmParams g{};
+        g.role = ROLE_SIGNAL;
         g.A = r.tokens ? c->embed : r.s_in;
         g.a_idx = r.tokens;
         g.a_idx_max = D.V;
@@ -170,15 +213,20 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
         g.S = H;
         g.err = b.err;
         g.epi = EPI_NONE;
+        Span sp(prof, ADN_STAGE_SIGNAL_GEMM, -1, st);
         launch_gemm(g, st);
     }
-    launch_init(D, b, r.tokens ? c->embed : r.s_in, r.tokens, ntok, c->anchor, st);
+    {
+        Span sp(prof, ADN_STAGE_INIT, -1, st);
+        launch_init(D, b, r.tokens ? c->embed : r.s_in, r.tokens, ntok, c->anchor, st);
+    }
 
     const int m = c->cfg.anderson_m;
     for (int k = 0; k < r.max_iters; ++k) {
         const int cur = k & 1;
         {  // Q|K|V for every slot of every active token
             GemmParams g{};
+            g.role = ROLE_QKV;
             g.A = b.h;
             g.a_idx = b.act[cur];
             g.a_idx_max = ntok;
@@ -199,11 +247,16 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
             g.m_count = b.cnt + cur;
             g.err = b.err;
             g.epi = c->qk_bias ? EPI_BIAS : EPI_NONE;
+            Span sp(prof, ADN_STAGE_QKV_GEMM, k, st);
             launch_gemm(g, st);
         }
-        launch_attn(D, b, cur, ntok, st);
+        {
+            Span sp(prof, ADN_STAGE_ATTN, k, st);
+            launch_attn(D, b, cur, k, ntok, st);
+        }
         {  // o = W_o mix
             GemmParams g{};
+            g.role = ROLE_WO;
             g.A = b.mix;
             g.a_sm = (long)H * d;
             g.a_ss = d;
@@ -219,17 +272,25 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
             g.m_count = b.cnt + cur;
             g.err = b.err;
             g.epi = EPI_NONE;
+            Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
             launch_gemm(g, st);
         }
-        launch_update(D, b, cur, ntok, c->anchor, c->norm_scale, r.damping, st);
-        launch_converge(D, b, cur, ntok, k, r.max_iters, r.eps, st);
-        if (m > 0 && k + 1 < r.max_iters) launch_anderson(D, b, cur ^ 1, ntok, k, m, st);
+        {
+            Span sp(prof, ADN_STAGE_UPDATE, k, st);
+            launch_update(D, b, cur, k, r.max_iters, r.eps, ntok, c->anchor, c->norm_scale, r.damping, st);
+        }
+        if (m > 0 && k + 1 < r.max_iters) {
+            Span sp(prof, ADN_STAGE_ANDERSON, k, st);
+            launch_anderson(D, b, cur ^ 1, ntok, k, m, st);
+        }
     }
 
     // LM head
     const bool want_logits = o.logits || o.argmax;
-    if (o.pooled || want_logits)
+    if (o.pooled || want_logits) {
+        Span sp(prof, ADN_STAGE_POOL, -1, st);
         launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr, st);
+    }
     if (want_logits) {
         float *logits = o.logits;
         if (!logits) {
@@ -238,6 +299,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
             logits = c->logits_scratch;
         }
         GemmParams g{};
+        g.role = ROLE_LMHEAD;
         g.A = c->pnorm;
         g.a_sm = d;
         g.B = c->lm_w;
@@ -251,21 +313,59 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
         g.S = 1;
         g.err = b.err;
         g.epi = c->lm_b ? EPI_BIAS : EPI_NONE;
-        launch_gemm(g, st);
-        if (o.argmax) launch_argmax(logits, ntok, D.V, o.argmax, st);
+        const int ntiles = (D.V + GEMM_BN - 1) / GEMM_BN;
+        if (o.argmax) {
+            g.am_val = c->am_val;
+            g.am_idx = c->am_idx;
+        }
+        {
+            Span sp(prof, ADN_STAGE_LMHEAD_GEMM, -1, st);
+            launch_gemm(g, st);
+        }
+        if (o.argmax) {
+            Span sp(prof, ADN_STAGE_ARGMAX, -1, st);
+            launch_argmax_reduce(c->am_val, c->am_idx, ntok, ntiles, o.argmax, st);
+        }
     }
 
     // temporal carrier
     if (o.scan_y || o.scan_state) {
-        launch_scan_prep(D, b.h, ntok, c->w_kw, c->w_b, c->w_c, c->scb.rec, st);
+        const int REC = scan_rec_len(D);
+        {
+            Span sp(prof, ADN_STAGE_SCAN_PREP, -1, st);
+            launch_row_rms(b.h, (long)ntok * H, d, c->scb.rec, REC, st);
+            GemmParams g{};  // P[t][s] = W_cat[s] h[t][s] into rec[1 .. REC)
+            g.role = ROLE_SCAN_PROJ;
+            g.A = b.h;
+            g.a_sm = (long)H * d;
+            g.a_ss = d;
+            g.B = c->w_cat;
+            g.b_ss = (long)(REC - 1) * d;
+            g.C = c->scb.rec + 1;
+            g.c_sm = (long)H * REC;
+            g.c_ss = REC;
+            g.M = ntok;
+            g.N = REC - 1;
+            g.K = d;
+            g.S = H;
+            g.err = b.err;
+            g.epi = EPI_NONE;
+            launch_gemm(g, st);
+        }
         // chunk buffers hold max_batch * scan_nch_cap sequence-chunks
         const int nch_fit = std::max(1, (c->cfg.max_batch * c->scan_nch_cap) / r.batch);
         const int nch = std::min(std::min(scan_chunks(r.batch, r.seq, H, d), c->scan_nch_cap), nch_fit);
         float *y = (o.scan_y && !c->w_out) ? o.scan_y : c->scb.y;
-        launch_scan(D, b.h, c->scb.rec, r.batch, r.seq, c->a_log, c->wx_diag, c->b_delta, c->w_vw,
-                    r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch, st);
+        {
+            Span sp(prof, ADN_STAGE_SCAN, nch, st);
+            launch_scan_gate(D, b.h, c->scb.rec, ntok, c->a_log, c->wx_diag, c->b_delta, c->w_vw, c->scb.gate_a,
+                             c->scb.gate_x, st);
+            launch_scan(D, c->scb.gate_a, c->scb.gate_x, c->scb.rec, r.batch, r.seq, c->w_b != nullptr,
+                        r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch, st);
+        }
         if (o.scan_y && c->w_out) {
             GemmParams g{};
+            g.role = ROLE_READOUT;
             g.A = y;
             g.a_sm = (long)H * d;
             g.a_ss = d;
@@ -280,6 +380,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
             g.S = H;
             g.err = b.err;
             g.epi = EPI_ADD_A;
+            Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st);
             launch_gemm(g, st);
         }
     }
@@ -292,7 +393,8 @@ int check_run(adn_ctx *c, const adn_run *r) {
     if (r->batch < 1 || r->seq < 1) return fail(ADN_E_INVALID, "batch and seq must be >= 1");
     if ((long)r->batch * r->seq > c->cap_tok)
         return fail(ADN_E_CAPACITY, "batch*seq exceeds the context capacity");
-    if (r->max_iters < 1) return fail(ADN_E_INVALID, "max_iters must be >= 1");
+    if (r->max_iters < 1 || r->max_iters > ADN_PROFILE_MAX_ITERS)
+        return fail(ADN_E_INVALID, "max_iters must be in [1, 256]");
     if (!(r->damping > 0.0f && r->damping <= 1.0f)) return fail(ADN_E_INVALID, "damping must be in (0, 1]");
     if (!(r->eps >= 0.0f)) return fail(ADN_E_INVALID, "eps must be >= 0");
     if ((r->tokens == nullptr) == (r->s_in == nullptr))
@@ -356,19 +458,24 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         b.qkv = (float *)dmalloc(c, 3 * hd);
         b.mix = (float *)dmalloc(c, hd);
         b.o = (float *)dmalloc(c, hd);
-        b.res_part = (float *)dmalloc(c, (size_t)T * H * sizeof(float));
         b.act[0] = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
         b.act[1] = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
         b.cnt = (int32_t *)dmalloc(c, 4 * sizeof(int32_t));
         b.iters = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        b.cnt_hist = (int32_t *)dmalloc(c, ADN_PROFILE_MAX_ITERS * sizeof(int32_t));
         b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
         b.err = c->d_err;
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
         c->pnorm = (float *)dmalloc(c, (size_t)T * d * sizeof(float));
         c->argmax_scratch = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        const size_t ntiles = ((size_t)cfg->vocab + GEMM_BN - 1) / GEMM_BN;
+        c->am_val = (float *)dmalloc(c, (size_t)T * ntiles * sizeof(float));
+        c->am_idx = (int32_t *)dmalloc(c, (size_t)T * ntiles * sizeof(int32_t));
         c->scb.rec = (float *)dmalloc(c, (size_t)T * H * scan_rec_len(c->D) * sizeof(float));
         c->scb.y = (float *)dmalloc(c, hd);
+        c->scb.gate_a = (float *)dmalloc(c, hd);
+        c->scb.gate_x = (float *)dmalloc(c, hd);
         c->scan_nch_cap = 16;
         const size_t chunk_states = (size_t)cfg->max_batch * c->scan_nch_cap * H * d;
         c->scb.chunk_s = (float *)dmalloc(c, chunk_states * cfg->d_state * sizeof(float));
@@ -477,6 +584,25 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
         upload(c, &c->w_vw, w->w_vw, (size_t)H * r * d, "w_vw", false);
         upload(c, &c->w_b, w->w_b, (size_t)H * N * d, "w_b", false);
         upload(c, &c->w_c, w->w_c, (size_t)H * N * d, "w_c", false);
+        {  // W_cat[s] = [W_kw[s]^T (r rows); W_B[s] (N rows); W_C[s] (N rows)], zeros where absent
+            const size_t rows = (size_t)r + 2 * N;
+            if (!c->w_cat) c->w_cat = (float *)dmalloc(c, (size_t)H * rows * d * sizeof(float));
+            ADN_HIP(hipMemsetAsync(c->w_cat, 0, (size_t)H * rows * d * sizeof(float), c->stream));
+            if (c->w_kw) {
+                float *t2 = staging_f(c, 18, (size_t)H * r * d * sizeof(float));
+                launch_transpose(c->w_kw, d, r, H, t2, c->stream);
+                ADN_HIP(hipMemcpy2DAsync(c->w_cat, rows * d * sizeof(float), t2, (size_t)r * d * sizeof(float),
+                                         (size_t)r * d * sizeof(float), H, hipMemcpyDeviceToDevice, c->stream));
+            }
+            if (c->w_b) {
+                ADN_HIP(hipMemcpy2DAsync(c->w_cat + (size_t)r * d, rows * d * sizeof(float), c->w_b,
+                                         (size_t)N * d * sizeof(float), (size_t)N * d * sizeof(float), H,
+                                         hipMemcpyDeviceToDevice, c->stream));
+                ADN_HIP(hipMemcpy2DAsync(c->w_cat + (size_t)(r + N) * d, rows * d * sizeof(float), c->w_c,
+                                         (size_t)N * d * sizeof(float), (size_t)N * d * sizeof(float), H,
+                                         hipMemcpyDeviceToDevice, c->stream));
+            }
+        }
         ADN_HIP(hipStreamSynchronize(c->stream));
     } catch (const HipError &e) {
         return hip_fail(e);
@@ -708,6 +834,71 @@ int adn_ffn_forward(adn_ctx *c, int32_t w_id, int32_t in_id, int32_t out_dim, fl
         return hip_fail(e);
     }
     return ADN_OK;
+}
+
+int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_profile *prof) {
+    int rc = check_run(c, r);
+    if (rc) return rc;
+    if (!o || !prof) return fail(ADN_E_INVALID, "null argument");
+    try {
+        Prof P;
+        enqueue_forward(c, *r, *o, &P);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        int32_t hist[ADN_PROFILE_MAX_ITERS] = {0};
+        ADN_HIP(hipMemcpy(hist, c->sb.cnt_hist, r->max_iters * sizeof(int32_t), hipMemcpyDeviceToHost));
+        memset(prof, 0, sizeof(*prof));
+        prof->n_iters = r->max_iters;
+        for (int k = 0; k < r->max_iters; ++k) prof->active[k] = hist[k];
+        const double d = c->D.d, H = c->D.H, V = c->D.V, N = c->D.N, R = c->D.r;
+        const double ntok = (double)r->batch * r->seq, REC = 1 + R + 2 * N, f = 4.0;
+        const int m = c->cfg.anderson_m;
+        for (const auto &rec : P.recs) {
+            float ms = 0.0f;
+            ADN_HIP(hipEventElapsedTime(&ms, rec.e0, rec.e1));
+            const int st = rec.stage;
+            const double n = (rec.k >= 0 && st >= ADN_STAGE_QKV_GEMM && st <= ADN_STAGE_CONVERGE) ? hist[rec.k] : ntok;
+            double fl = 0, by = 0;
+            switch (st) {
+                case ADN_STAGE_SIGNAL_GEMM: fl = 2 * ntok * H * d * d; by = f * (ntok * d + H * d * d + ntok * H * d); break;
+                case ADN_STAGE_INIT: by = f * (ntok * d + ntok * H * d); break;
+                case ADN_STAGE_QKV_GEMM: fl = 6 * n * H * d * d; by = n > 0 ? f * (n * H * d + 3 * H * d * d + 3 * n * H * d) : 0; break;
+                case ADN_STAGE_ATTN: fl = 4 * n * H * H * d; by = f * 4 * n * H * d; break;
+                case ADN_STAGE_WO_GEMM: fl = 2 * n * H * d * d; by = n > 0 ? f * (2 * n * H * d + H * d * d) : 0; break;
+                case ADN_STAGE_UPDATE: fl = 10 * n * H * d; by = f * (4 * n * H * d + 3 * n); break;
+                case ADN_STAGE_CONVERGE: by = f * n * (H + 3); break;
+                case ADN_STAGE_ANDERSON: {
+                    const double nn = (rec.k + 1 < r->max_iters) ? hist[rec.k + 1] : 0;
+                    const int k = rec.k, n_res = k < m - 1 ? k : m - 1;
+                    const double nr = (k >= 2 && n_res >= 2) ? n_res : 0;
+                    fl = nn * H * d * (nr * (nr + 1) + 2 * nr);
+                    by = f * nn * H * d * (2 + (nr > 0 ? 2 * nr + 2 : 0));
+                    break;
+                }
+                case ADN_STAGE_POOL: fl = ntok * H * d; by = f * (ntok * H * d + 2 * ntok * d); break;
+                case ADN_STAGE_LMHEAD_GEMM: fl = 2 * ntok * V * d; by = f * (ntok * d + V * d + ntok * V); break;
+                case ADN_STAGE_ARGMAX: by = f * (2 * ntok * std::ceil(V / GEMM_BN) + ntok); break;  // tile partials
+                case ADN_STAGE_SCAN_PREP: fl = 2 * ntok * H * d * (R + 2 * N); by = f * (ntok * H * d + ntok * H * REC + H * d * (R + 2 * N)); break;
+                case ADN_STAGE_SCAN:  // compulsory: read h*, the record; write y
+                    fl = ntok * H * d * (2 * R + 4 * N + 10);
+                    by = f * (ntok * H * d + ntok * H * REC + ntok * H * d); break;
+                case ADN_STAGE_READOUT_GEMM: fl = 2 * ntok * H * d * d; by = f * (2 * ntok * H * d + H * d * d); break;
+                default: break;
+            }
+            prof->ms[st] += ms;
+            prof->flops[st] += fl;
+            prof->bytes[st] += by;
+            prof->launches[st] += 1;
+        }
+        if (!P.recs.empty()) {
+            float tot = 0.0f;
+            ADN_HIP(hipEventElapsedTime(&tot, P.recs.front().e0, P.recs.back().e1));
+            prof->total_ms = tot;
+        }
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
 }
 
 }  // extern "C"

@@ -9,12 +9,16 @@
 //   m_t[n] = abar m_{t-1}[n] + (1-abar) B_t[n] x,   y_t = sum_n C_t[n] m_t[n],
 //   Y_t = y_t + W_out y_t (readout GEMM, gemm.hip).
 //
-// k_scan_prep: one wave per (token, slot) computes the per-row record
-//   [rms, bn[0..r), B[0..N), C[0..N)]  (the rank-r bottleneck and the B/C projections).
-// k_scan: one thread per (sequence, slot, channel) carries the N states in registers; the
-//   record of each step is read with uniform (scalar) loads.  Long sequences are split into
-//   chunks: pass A (zero start) produces each chunk's end state and decay product, pass B
-//   carries the chunk starts sequentially, pass C re-runs every chunk from its start.
+// Pipeline: k_row_rms (rms of every (token, slot) row) and one MFMA GEMM against the per-slot
+//   W_cat[s] = [W_kw[s]^T; W_B[s]; W_C[s]]  (r + 2N rows of length d)
+// fill the per-row record [rms, P_bn[0..r), P_B[0..N), P_C[0..N)] with un-normalised
+// projections P = W_cat h; the scan divides them by rms as it stages them.
+// k_scan_gate: the per-element decay and input (all transcendental and rank-r work), fully
+//   parallel over (token, slot, channel).
+// k_scan: one thread per (sequence, slot, channel) carries the N states in registers; per chunk
+//   of TC steps the B/C values are staged in LDS and the gate values prefetched into registers.
+//   Long sequences are split into time chunks: pass A (zero start) produces each chunk's end
+//   state and decay product, pass B carries the chunk starts, pass C re-runs every chunk.
 #include "kernels.h"
 
 namespace adn {
@@ -23,131 +27,157 @@ namespace {
 
 constexpr int WPB = 4;
 
-__global__ __launch_bounds__(256) void k_scan_prep(Dims D, const float *h, int ntok,
-                                                   const float *w_kw, const float *w_b,
-                                                   const float *w_c, float *rec) {
-    const int row = blockIdx.x * WPB + (threadIdx.x >> 6);  // (t, s)
+__global__ __launch_bounds__(256) void k_row_rms(const float *h, long rows, int d, float *rec, int REC) {
+    const long row = (long)blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= ntok * D.H) return;
-    const int s = row % D.H;
-    const int d = D.d, r = D.r, N = D.N;
-    const int REC = 1 + r + 2 * N;
-    const float *hr = h + (long)row * d;
+    if (row >= rows) return;
+    const float *hr = h + row * d;
     float ss = 0.0f;
     for (int i = lane; i < d; i += 64) ss += hr[i] * hr[i];
     ss = wave_sum(ss);
-    const float rms = sqrtf(ss / (float)d + 1e-6f);
-    float *out = rec + (long)row * REC;
-    if (lane == 0) out[0] = rms;
-    if (D.flags & ADN_F_SCAN_SELECTIVE) {
-        const float *wk = w_kw + (long)s * d * r;
-        for (int j = 0; j < r; ++j) {
-            float p = 0.0f;
-            for (int i = lane; i < d; i += 64) p += wk[(long)i * r + j] * (hr[i] / rms);
-            p = wave_sum(p);
-            if (lane == 0) out[1 + j] = p;
-        }
-    }
-    for (int n = 0; n < N; ++n) {
-        float pb = 1.0f, pc = 1.0f;
-        if (w_b) {
-            const float *wb = w_b + ((long)s * N + n) * d;
-            const float *wc = w_c + ((long)s * N + n) * d;
-            pb = 0.0f;
-            pc = 0.0f;
-            for (int i = lane; i < d; i += 64) {
-                const float u = hr[i] / rms;
-                pb += wb[i] * u;
-                pc += wc[i] * u;
-            }
-            pb = wave_sum(pb);
-            pc = wave_sum(pc);
-        }
-        if (lane == 0) {
-            out[1 + r + n] = pb;
-            out[1 + r + N + n] = pc;
-        }
-    }
+    if (lane == 0) rec[row * REC] = sqrtf(ss / (float)d + 1e-6f);
 }
 
-// MODE 0: full scan from state_in, emit y and state_out (single chunk).
-// MODE 1: chunk pass A, zero start, emit chunk end state and decay product.
-// MODE 2: chunk pass C, start from chunk_s (carried), emit y; last chunk writes state_out.
-template <int NS, int RK, int MODE>
-__global__ __launch_bounds__(256) void k_scan(Dims D, const float *h, const float *rec, int T,
-                                              int nch, const float *a_log, const float *wx_diag,
-                                              const float *b_delta, const float *w_vw,
-                                              const float *state_in, float *y, float *state_out,
-                                              float *chunk_s, float *chunk_p) {
-    const int d = D.d, H = D.H, N = D.N, r = D.r;
-    const int dim = blockIdx.x * blockDim.x + threadIdx.x;
-    const int s = blockIdx.y;
-    const int bc = blockIdx.z;
-    const int b = bc / nch, c = bc - (bc / nch) * nch;
-    if (dim >= d) return;
-    const int REC = 1 + r + 2 * N;
-    const int Tc = (T + nch - 1) / nch;
-    const int t0 = c * Tc, t1 = min(T, t0 + Tc);
-    const bool selective = (D.flags & ADN_F_SCAN_SELECTIVE) != 0;
+constexpr int SCAN_NT = 256;
+constexpr int TC = 16;
+constexpr int GATE_ROWS = 16;
 
+// Gate: for every (token, slot, channel) the decay abar and the carrier input (1-abar) x,
+// fully parallel (the rank-r bottleneck comes from the record; W_vw's column for the channel
+// is held in registers across GATE_ROWS tokens of one slot).
+template <int RK, bool SEL>
+__global__ __launch_bounds__(SCAN_NT) void k_scan_gate(Dims D, const float *__restrict__ h,
+                                                       const float *__restrict__ rec, int ntok,
+                                                       const float *__restrict__ a_log,
+                                                       const float *__restrict__ wx_diag,
+                                                       const float *__restrict__ b_delta,
+                                                       const float *__restrict__ w_vw,
+                                                       float *__restrict__ gate_a, float *__restrict__ gate_x) {
+    const int d = D.d, H = D.H, r = D.r;
+    const int dim = blockIdx.x * SCAN_NT + threadIdx.x;
+    const int s = blockIdx.y;
+    const int t0 = blockIdx.z * GATE_ROWS;
+    if (dim >= d) return;
+    const int REC = 1 + D.r + 2 * D.N;
     const float al = a_log[(long)s * d + dim];
     const float abase = 1.0f / (1.0f + expf(al));
     const float ln_ab = logf(fmaxf(abase, 1.0e-6f));
     const float wx = 0.5f * tanhf(wx_diag[(long)s * d + dim]);
     const float bd = b_delta ? b_delta[(long)s * d + dim] : 0.0f;
-    float wv[RK];
-    if (selective) {
+    constexpr int RKA = RK > 0 ? RK : 1;
+    float wv[RKA];
 #pragma unroll
-        for (int j = 0; j < RK; ++j) wv[j] = j < r ? w_vw[((long)s * r + j) * d + dim] : 0.0f;
-    }
-    float m[NS];
-    const long st_off = (((long)b * H + s) * d + dim) * N;
-#pragma unroll
-    for (int n = 0; n < NS; ++n) {
-        m[n] = 0.0f;
-        if (n < N) {
-            if (MODE == 0 && state_in) m[n] = state_in[st_off + n];
-            if (MODE == 2) m[n] = chunk_s[((((long)b * nch + c) * H + s) * d + dim) * N + n];
-        }
-    }
-    float prod = 1.0f;
+    for (int q = 0; q < RKA; ++q) wv[q] = (SEL && q < r) ? w_vw[((long)s * r + q) * d + dim] : 0.0f;
+    const int t1 = min(ntok, t0 + GATE_ROWS);
     for (int t = t0; t < t1; ++t) {
-        const long row = ((long)b * T + t) * H + s;
+        const long row = (long)t * H + s;
         const float *rc = rec + row * REC;
-        const float u = h[row * d + dim] / rc[0];
+        const float rms = rc[0];
+        const float u = h[row * d + dim] / rms;
         const float x = u + wx * u;
         float abar;
-        if (selective) {
-            float pre = bd;
+        if (SEL) {
+            // W_vw^T (W_kw^T u) with u = h/rms: the record holds W_kw^T h, so divide once
+            float dot = 0.0f;
 #pragma unroll
-            for (int j = 0; j < RK; ++j)
-                if (j < r) pre += wv[j] * rc[1 + j];
+            for (int q = 0; q < RKA; ++q)
+                if (q < r) dot += wv[q] * rc[1 + q];
+            const float pre = bd + dot / rms;
             const float delta = logf(1.0f + expf(pre));
             const float acore = expf(delta * ln_ab);
             abar = 0.10f + (1.0f - 0.10f) * acore;
         } else {
             abar = abase;
         }
-        const float bb = 1.0f - abar;
-        float acc = 0.0f;
+        gate_a[row * d + dim] = abar;
+        gate_x[row * d + dim] = (1.0f - abar) * x;
+    }
+}
+
+// Recurrence over time for one (sequence, slot, channel) per thread, N states in registers:
+//   m[n] = abar m[n] + B[n] ((1-abar) x),  y = sum_n C[n] m[n].
+// MODE 0: full scan from state_in, emit y and state_out (single chunk).
+// MODE 1: chunk pass A, zero start, emit chunk end state and decay product.
+// MODE 2: chunk pass C, start from chunk_s (carried), emit y; last chunk writes state_out.
+// Per TC steps the B/C values (projection / rms) are staged in LDS and the gate values are
+// loaded into registers up front.  EXACT: NS == N (branch-free inner loops).
+template <int NS, int MODE, bool EXACT>
+__global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restrict__ gate_a,
+                                                  const float *__restrict__ gate_x,
+                                                  const float *__restrict__ rec, int T, int nch, int has_bc,
+                                                  const float *__restrict__ state_in, float *__restrict__ y,
+                                                  float *__restrict__ state_out, float *__restrict__ chunk_s,
+                                                  float *__restrict__ chunk_p) {
+    __shared__ float sbc[TC][2 * NS];
+    const int d = D.d, H = D.H;
+    const int N = EXACT ? NS : D.N;
+    const int tid = threadIdx.x;
+    const int dim = blockIdx.x * SCAN_NT + tid;
+    const int s = blockIdx.y;
+    const int bc = blockIdx.z;
+    const int b = bc / nch, c = bc - (bc / nch) * nch;
+    const bool active = dim < d;
+    const int REC = 1 + D.r + 2 * D.N;
+    const int boff = 1 + D.r;
+    const int Tc = (T + nch - 1) / nch;
+    const int t0 = c * Tc, t1 = min(T, t0 + Tc);
+    const int dd = active ? dim : 0;
+    float m[NS];
+    const long st_off = (((long)b * H + s) * d + dd) * D.N;
 #pragma unroll
-        for (int n = 0; n < NS; ++n) {
-            if (n < N) {
-                m[n] = abar * m[n] + bb * (rc[1 + r + n] * x);
-                acc += rc[1 + r + N + n] * m[n];
+    for (int n = 0; n < NS; ++n) {
+        m[n] = 0.0f;
+        if (n < N && active) {
+            if (MODE == 0 && state_in) m[n] = state_in[st_off + n];
+            if (MODE == 2) m[n] = chunk_s[((((long)b * nch + c) * H + s) * d + dd) * D.N + n];
+        }
+    }
+    float prod = 1.0f;
+    for (int tb = t0; tb < t1; tb += TC) {
+        const int nt = min(TC, t1 - tb);
+        if (has_bc) {
+            for (int idx = tid; idx < nt * 2 * N; idx += SCAN_NT) {
+                const int j = idx / (2 * N), q = idx - j * 2 * N;
+                const float *rc = rec + (((long)b * T + tb + j) * H + s) * REC;
+                sbc[j][q] = rc[boff + q] / rc[0];
             }
         }
-        if (MODE == 1)
-            prod *= abar;
-        else
-            y[row * d + dim] = acc;
+        float av[TC], xv[TC];
+#pragma unroll
+        for (int j = 0; j < TC; ++j) {
+            const long off = (((long)b * T + tb + j) * H + s) * d + dd;
+            av[j] = (j < nt && active) ? gate_a[off] : 1.0f;
+            xv[j] = (j < nt && active) ? gate_x[off] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TC; ++j) {
+            if (j < nt) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int n = 0; n < NS; ++n) {
+                    if (EXACT || n < N) {
+                        const float Bn = has_bc ? sbc[j][n] : 1.0f;
+                        const float Cn = has_bc ? sbc[j][N + n] : 1.0f;
+                        m[n] = av[j] * m[n] + Bn * xv[j];
+                        acc += Cn * m[n];
+                    }
+                }
+                if (MODE == 1)
+                    prod *= av[j];
+                else if (active)
+                    y[(((long)b * T + tb + j) * H + s) * d + dd] = acc;
+            }
+        }
+        __syncthreads();
     }
+    if (!active) return;
     if (MODE == 1) {
-        const long co = (((long)b * nch + c) * H + s) * d + dim;
+        const long co = (((long)b * nch + c) * H + s) * d + dd;
         chunk_p[co] = prod;
 #pragma unroll
         for (int n = 0; n < NS; ++n)
-            if (n < N) chunk_s[co * N + n] = m[n];
+            if (n < N) chunk_s[co * D.N + n] = m[n];
     } else if (state_out && (MODE == 0 || c == nch - 1)) {
 #pragma unroll
         for (int n = 0; n < NS; ++n)
@@ -178,25 +208,23 @@ __global__ void k_scan_carry(Dims D, int B, int nch, const float *state_in, floa
     }
 }
 
-template <int NS, int RK>
-void scan_modes(const Dims &D, const float *h, const float *rec, int B, int T, const float *a_log,
-                const float *wx_diag, const float *b_delta, const float *w_vw,
-                const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p,
-                int nch, hipStream_t st) {
-    const int bx = D.d < 256 ? D.d : 256;
-    const dim3 grid((unsigned)((D.d + bx - 1) / bx), (unsigned)D.H, (unsigned)(B * nch));
+template <int NS, bool EXACT>
+void scan_modes(const Dims &D, const float *ga, const float *gx, const float *rec, int B, int T, int has_bc,
+                const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p, int nch,
+                hipStream_t st) {
+    const dim3 grid((unsigned)((D.d + SCAN_NT - 1) / SCAN_NT), (unsigned)D.H, (unsigned)(B * nch));
     if (nch <= 1) {
-        hipLaunchKernelGGL((k_scan<NS, RK, 0>), grid, dim3(bx), 0, st, D, h, rec, T, 1, a_log, wx_diag,
-                           b_delta, w_vw, state_in, y, state_out, chunk_s, chunk_p);
+        hipLaunchKernelGGL((k_scan<NS, 0, EXACT>), grid, dim3(SCAN_NT), 0, st, D, ga, gx, rec, T, 1, has_bc,
+                           state_in, y, state_out, chunk_s, chunk_p);
         return;
     }
-    hipLaunchKernelGGL((k_scan<NS, RK, 1>), grid, dim3(bx), 0, st, D, h, rec, T, nch, a_log, wx_diag,
-                       b_delta, w_vw, state_in, y, state_out, chunk_s, chunk_p);
+    hipLaunchKernelGGL((k_scan<NS, 1, EXACT>), grid, dim3(SCAN_NT), 0, st, D, ga, gx, rec, T, nch, has_bc,
+                       state_in, y, state_out, chunk_s, chunk_p);
     const long total = (long)B * D.H * D.d * D.N;
     hipLaunchKernelGGL(k_scan_carry, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, D, B, nch,
                        state_in, chunk_s, chunk_p);
-    hipLaunchKernelGGL((k_scan<NS, RK, 2>), grid, dim3(bx), 0, st, D, h, rec, T, nch, a_log, wx_diag,
-                       b_delta, w_vw, state_in, y, state_out, chunk_s, chunk_p);
+    hipLaunchKernelGGL((k_scan<NS, 2, EXACT>), grid, dim3(SCAN_NT), 0, st, D, ga, gx, rec, T, nch, has_bc,
+                       state_in, y, state_out, chunk_s, chunk_p);
 }
 
 }  // namespace
@@ -204,38 +232,48 @@ void scan_modes(const Dims &D, const float *h, const float *rec, int B, int T, c
 int scan_rec_len(const Dims &D) { return 1 + D.r + 2 * D.N; }
 
 int scan_chunks(int B, int T, int H, int d) {
-    const long waves = (long)B * H * ((d + 63) / 64);
+    const long wgs = (long)B * H * ((d + SCAN_NT - 1) / SCAN_NT);
     int nch = 1;
-    while (waves * nch < 4096 && T / (nch * 2) >= 64) nch *= 2;
+    while (wgs * nch < 2048 && T / (nch * 2) >= 4 * TC) nch *= 2;
     return nch;
 }
 
-void launch_scan_prep(const Dims &D, const float *h, int ntok, const float *w_kw, const float *w_b,
-                      const float *w_c, float *rec, hipStream_t st) {
-    const long rows = (long)ntok * D.H;
-    hipLaunchKernelGGL(k_scan_prep, dim3((unsigned)((rows + WPB - 1) / WPB)), dim3(64 * WPB), 0, st, D, h,
-                       ntok, w_kw, w_b, w_c, rec);
+void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipStream_t st) {
+    hipLaunchKernelGGL(k_row_rms, dim3((unsigned)((rows + WPB - 1) / WPB)), dim3(64 * WPB), 0, st, h, rows, d,
+                       rec, REC);
 }
 
-void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, const float *a_log,
-                 const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in,
-                 float *y, float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st) {
-    // register budget: NS >= N states, RK >= r rank entries
-    if (D.N <= 16) {
-        if (D.r <= 32)
-            scan_modes<16, 32>(D, h, rec, B, T, a_log, wx_diag, b_delta, w_vw, state_in, y, state_out,
-                               chunk_s, chunk_p, nch, st);
-        else
-            scan_modes<16, 64>(D, h, rec, B, T, a_log, wx_diag, b_delta, w_vw, state_in, y, state_out,
-                               chunk_s, chunk_p, nch, st);
-    } else {
-        if (D.r <= 32)
-            scan_modes<32, 32>(D, h, rec, B, T, a_log, wx_diag, b_delta, w_vw, state_in, y, state_out,
-                               chunk_s, chunk_p, nch, st);
-        else
-            scan_modes<32, 64>(D, h, rec, B, T, a_log, wx_diag, b_delta, w_vw, state_in, y, state_out,
-                               chunk_s, chunk_p, nch, st);
-    }
+void launch_scan_gate(const Dims &D, const float *h, const float *rec, int ntok, const float *a_log,
+                      const float *wx_diag, const float *b_delta, const float *w_vw, float *gate_a, float *gate_x,
+                      hipStream_t st) {
+    const dim3 grid((unsigned)((D.d + SCAN_NT - 1) / SCAN_NT), (unsigned)D.H,
+                    (unsigned)((ntok + GATE_ROWS - 1) / GATE_ROWS));
+    const bool sel = (D.flags & ADN_F_SCAN_SELECTIVE) != 0;
+#define ADN_GATE_ARGS D, h, rec, ntok, a_log, wx_diag, b_delta, w_vw, gate_a, gate_x
+    if (!sel)
+        hipLaunchKernelGGL((k_scan_gate<0, false>), grid, dim3(SCAN_NT), 0, st, ADN_GATE_ARGS);
+    else if (D.r <= 32)
+        hipLaunchKernelGGL((k_scan_gate<32, true>), grid, dim3(SCAN_NT), 0, st, ADN_GATE_ARGS);
+    else
+        hipLaunchKernelGGL((k_scan_gate<64, true>), grid, dim3(SCAN_NT), 0, st, ADN_GATE_ARGS);
+#undef ADN_GATE_ARGS
+}
+
+void launch_scan(const Dims &D, const float *gate_a, const float *gate_x, const float *rec, int B, int T,
+                 int has_bc, const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p,
+                 int nch, hipStream_t st) {
+#define ADN_SCAN_ARGS D, gate_a, gate_x, rec, B, T, has_bc, state_in, y, state_out, chunk_s, chunk_p, nch, st
+    if (D.N == 16)
+        scan_modes<16, true>(ADN_SCAN_ARGS);
+    else if (D.N == 1)
+        scan_modes<1, true>(ADN_SCAN_ARGS);
+    else if (D.N == 32)
+        scan_modes<32, true>(ADN_SCAN_ARGS);
+    else if (D.N <= 8)
+        scan_modes<8, false>(ADN_SCAN_ARGS);
+    else
+        scan_modes<32, false>(ADN_SCAN_ARGS);
+#undef ADN_SCAN_ARGS
 }
 
 }  // namespace adn

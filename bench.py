@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""Forward throughput of the MI355X DEQ path at the north-star shape.
+
+Workload (BASELINE.json metric, configs[1] shape at batch 32): d_r=512, h_slots=8,
+vocab=50257, d_state=16, B=32 sequences x ctx=256 tokens, fp32, Xavier weights rescaled to
+spectral norm 0.5 (seed 0), Zipf(1.1) token ids (seed 1), Picard max 20 / tol 1e-4, no Anderson.
+
+A step is one full forward over the batch with inputs resident in HBM: embedding gather +
+W_in signal, the device-resident Picard solve (per-token exit), the selective carrier scan,
+the LM head (logits for every position) and the greedy arg-max.  K steps are timed between
+two device synchronisations; value = B*T*K / elapsed (tokens/s).
+
+Also reported: the roofline of the dominant kernel (from a profiled forward with HIP events
+on the kernel's own stream), per-stage figures, the Picard iteration statistics, and the
+same-run CPU baseline (the C oracle, OpenMP over tokens on this host, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "forward tokens/sec at d_r=512,h_slots=8,ctx=256,B=32; HBM GB/s & MFMA % of peak"
+PEAK_HBM_GBS = 8000.0
+PEAK_FP32_TFLOPS = 157.3
+MFMA_STAGES = ("signal_gemm", "qkv_gemm", "wo_gemm", "lmhead_gemm", "readout_gemm")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(mc, w, toks, seconds: float):
+    """The C oracle (a port of the reference's CPU forward) timed on whole sequences of the same
+    workload: one sequence calibrates, then as many sequences as fill about `seconds`."""
+    from oracle import pyoracle
+    pyoracle.build()
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    o = pyoracle.Oracle(mc, w).prepared()
+    B, T = toks.shape
+    t0 = time.perf_counter()
+    o.forward(toks[:1].copy(), nthreads=threads)
+    t1 = time.perf_counter() - t0
+    nseq = int(max(1, min(B, seconds / max(t1, 1e-6))))
+    t0 = time.perf_counter()
+    o.forward(toks[:nseq].copy(), nthreads=threads)
+    t2 = time.perf_counter() - t0
+    n = nseq * T
+    return dict(value=round(n / t2, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=(f"{nseq} of the {B} sequences ({n} tokens) of the same workload, same weights "
+                        f"and token ids: solve + LM-head logits + arg-max + carrier scan, "
+                        f"{threads} OpenMP threads over tokens, {t2:.1f} s"),
+                seconds=round(t2, 2))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="NS")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(one MI355X per box); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from aideen_amd import synth
+    from aideen_amd.backend import GpuDeqBackend
+
+    p = synth.PRESETS[args.config]
+    mc = p["model"]
+    B, T = p["B"], p["T"]
+    log(f"config {args.config}: d={mc.d} H={mc.H} V={mc.V} N={mc.N} B={B} T={T}")
+    w = synth.make_weights(mc, seed=0)
+    toks = synth.make_tokens(p["tokens"], B, T, mc.V, seed=1)
+
+    dev = torch.device("cuda:0")
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    # a dedicated (default-priority) stream: the library's kernels and the timing events share it
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    assert stream.cuda_stream != 0
+    tok_d = torch.from_numpy(toks).to(dev)
+    outs = dict(
+        h_star=torch.empty((B, T, mc.H, mc.d), dtype=torch.float32, device=dev),
+        iters=torch.empty((B, T), dtype=torch.int32, device=dev),
+        logits=torch.empty((B, T, mc.V), dtype=torch.float32, device=dev),
+        argmax=torch.empty((B, T), dtype=torch.int32, device=dev),
+        scan_y=torch.empty((B, T, mc.H, mc.d), dtype=torch.float32, device=dev),
+        scan_state=torch.empty((B, mc.H, mc.d, mc.N), dtype=torch.float32, device=dev),
+    )
+
+    for _ in range(args.warmup):
+        be.forward_async(tok_d, outputs=outs)
+    torch.cuda.synchronize()
+    be.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        be.forward_async(tok_d, outputs=outs)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    be.synchronize()
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / args.steps
+    tok_s = B * T * args.steps / (gpu_ms / 1e3)
+    log(f"{args.steps} steps: {gpu_ms:.2f} ms on the stream ({wall * 1e3:.2f} ms wall) "
+        f"-> {ms_per_step:.3f} ms/step, {tok_s:,.0f} tokens/s")
+
+    iters = outs["iters"].cpu().numpy()
+    prof = be.profile_forward(tok_d, outputs=outs)
+    stages = {}
+    for name, s in prof["stages"].items():
+        e = dict(ms=round(s["ms"], 4), launches=s["launches"])
+        if s["ms"] > 0:
+            if s["flops"] > 0:
+                e["tflops"] = round(s["flops"] / s["ms"] / 1e9, 2)
+            if s["bytes"] > 0:
+                e["gbs"] = round(s["bytes"] / s["ms"] / 1e6, 1)
+        stages[name] = e
+    dom = max((n for n in prof["stages"] if n in MFMA_STAGES), key=lambda n: prof["stages"][n]["ms"])
+    ds = prof["stages"][dom]
+    achieved = ds["flops"] / ds["ms"] / 1e9  # TFLOP/s
+    traffic = None
+    tf_path = os.path.join(ROOT, "profiles", f"{dom}_{args.config}_traffic.json")
+    if os.path.exists(tf_path):
+        traffic = json.load(open(tf_path)).get("bytes_per_launch")
+    roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 2), peak=PEAK_FP32_TFLOPS,
+                    unit="TFLOP/s", frac=round(achieved / PEAK_FP32_TFLOPS, 4), traffic=traffic,
+                    launches=ds["launches"], avg_launch_ms=round(ds["ms"] / ds["launches"], 4),
+                    flops_per_launch=ds["flops"] / ds["launches"])
+    hbm = {}
+    for n in ("attn", "update", "scan", "argmax", "pool"):
+        if n in prof["stages"] and prof["stages"][n]["ms"] > 0:
+            s = prof["stages"][n]
+            g = s["bytes"] / s["ms"] / 1e6
+            hbm[n] = dict(gbs=round(g, 1), frac=round(g / PEAK_HBM_GBS, 4))
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(mc, w, toks, args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']} tokens/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded Xavier weights at spectral norm 0.5, Zipf(1.1) token ids)",
+        "config": {"workload": f"{args.config}: DEQ forward d_r={mc.d} h_slots={mc.H} vocab={mc.V} "
+                               f"d_state={mc.N} B={B} ctx={T}, Picard max {mc.max_iters} tol {mc.eps}, "
+                               f"anderson m={mc.anderson_m}; logits for all positions + arg-max + scan",
+                   "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "picard": {"mean_iters": round(float(iters.mean()), 3), "max_iters": int(iters.max()),
+                   "hist": np.bincount(iters.ravel(), minlength=mc.max_iters + 1).tolist(),
+                   "active_per_iter": prof["active"]},
+        "hbm_kernels": hbm,
+        "stages": stages,
+        "profiled_forward_ms": round(prof["total_ms"], 3),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -177,6 +177,39 @@ int adn_load_tensor(adn_ctx *ctx, const float *data, int64_t n, int32_t *id);
  * in_dim = element count of the input tensor; y is host memory [out_dim]. */
 int adn_ffn_forward(adn_ctx *ctx, int32_t w_id, int32_t in_id, int32_t out_dim, float *y);
 
+/* --- measurement (the reference's AIDEEN_DEQ_FORWARD_PROFILE per-pass timing,
+ *     deq_bridge.rs:2234-2380, and GPU timestamp queries, gpu_deq.rs:490-570) ------------- */
+#define ADN_STAGE_SIGNAL_GEMM 0  /* signal = W_in x (embedding gather fused)          */
+#define ADN_STAGE_INIT 1         /* h0 and the first active list                      */
+#define ADN_STAGE_QKV_GEMM 2     /* per-slot Q|K|V projections of the active tokens    */
+#define ADN_STAGE_ATTN 3         /* slot scores, softmax, mix                          */
+#define ADN_STAGE_WO_GEMM 4      /* per-slot W_o projection                            */
+#define ADN_STAGE_UPDATE 5       /* RMS norm, damped update, residual partials         */
+#define ADN_STAGE_CONVERGE 6     /* exit test, iteration counts, compaction            */
+#define ADN_STAGE_ANDERSON 7     /* Anderson store + mix                               */
+#define ADN_STAGE_POOL 8         /* slot mean-pool + RMSNorm                           */
+#define ADN_STAGE_LMHEAD_GEMM 9  /* logits = W_lm x + b                                */
+#define ADN_STAGE_ARGMAX 10      /* greedy arg-max                                     */
+#define ADN_STAGE_SCAN_PREP 11   /* carrier prologue (rms, rank-r bottleneck, B/C)     */
+#define ADN_STAGE_SCAN 12        /* chunked selective scan                             */
+#define ADN_STAGE_READOUT_GEMM 13 /* Y = y + W_out y                                   */
+#define ADN_STAGE_COUNT 14
+#define ADN_PROFILE_MAX_ITERS 256
+
+typedef struct adn_profile {
+    double ms[ADN_STAGE_COUNT];       /* device time summed over the stage's launches   */
+    double flops[ADN_STAGE_COUNT];    /* algorithmic FLOPs summed over those launches   */
+    double bytes[ADN_STAGE_COUNT];    /* algorithmic (compulsory) HBM bytes             */
+    int32_t launches[ADN_STAGE_COUNT];
+    int32_t active[ADN_PROFILE_MAX_ITERS]; /* tokens entering Picard iteration k        */
+    int32_t n_iters;                  /* iterations enqueued (= max_iters)              */
+    double total_ms;                  /* first to last event                            */
+} adn_profile;
+
+/* Runs adn_forward_async with a HIP event pair around every kernel launch on the context
+ * stream, synchronises, and fills *prof.  Device-memory arguments as adn_forward_async. */
+int adn_profile_forward(adn_ctx *ctx, const adn_run *run, const adn_outputs *out, adn_profile *prof);
+
 #ifdef __cplusplus
 }
 #endif

@@ -652,22 +652,40 @@ void orc_scan_recirculate(const orc_cfg *c, const orc_weights *w, int T, const f
 /* whole forward                                                              */
 /* ------------------------------------------------------------------------- */
 
+/* A model with its weights laid out for the CPU loops (transposed once). */
+struct orc_model {
+    prep p;
+    float *lm_wt; /* [d][V] */
+};
+
+orc_model *orc_model_create(const orc_cfg *c, const orc_weights *w) {
+    orc_model *m = (orc_model *)calloc(1, sizeof(orc_model));
+    prep_init(&m->p, c, w);
+    m->lm_wt = (float *)malloc(sizeof(float) * (size_t)c->V * c->d);
+    transpose(w->lm_w, c->V, c->d, m->lm_wt);
+    return m;
+}
+
+void orc_model_free(orc_model *m) {
+    if (!m) return;
+    prep_free(&m->p);
+    free(m->lm_wt);
+    free(m);
+}
+
 /* Canonical forward (TRAINER:4677-4731 per-token structure with x_t = E[tok] as in the
  * fixed-history query, tokenizer.rs:117-119): solve every token independently, pool, LM head,
  * greedy argmax; then the carrier over each sequence. */
-void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
-                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
-                 float *scan_y, float *scan_state, int nthreads) {
+void orc_model_forward(orc_model *mdl, int B, int T, const int32_t *tokens, float *h_star,
+                       float *pooled, float *logits, int32_t *iters, int32_t *argmax,
+                       float *scan_y, float *scan_state, int nthreads) {
+    const orc_cfg *c = &mdl->p.c;
+    const orc_weights *w = mdl->p.w;
     const int d = c->d, H = c->H, V = c->V;
     const size_t hd = (size_t)H * d;
     const long ntok = (long)B * T;
-    prep p;
-    prep_init(&p, c, w);
-    float *lm_wt = NULL;
-    if (logits || argmax) {
-        lm_wt = (float *)malloc(sizeof(float) * (size_t)V * d);
-        transpose(w->lm_w, V, d, lm_wt);
-    }
+    const prep *p = &mdl->p;
+    const float *lm_wt = mdl->lm_wt;
     float *hs_all = h_star;
     int own_h = 0;
     if (!hs_all) {
@@ -689,7 +707,7 @@ void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int
         for (long t = 0; t < ntok; ++t) {
             const int32_t tok = tokens[t];
             float *h = hs_all + hd * t;
-            int it = solve_p(&p, &sc, w->embed + (size_t)tok * d, h, NULL);
+            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, h, NULL);
             if (iters) iters[t] = it;
             if (pooled || logits || argmax) {
                 float *lt = logits ? logits + (size_t)V * t : lg;
@@ -714,8 +732,15 @@ void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int
         if (!scan_y) free(ybuf);
     }
     if (own_h) free(hs_all);
-    free(lm_wt);
-    prep_free(&p);
+}
+
+void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
+                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
+                 float *scan_y, float *scan_state, int nthreads) {
+    orc_model *m = orc_model_create(c, w);
+    orc_model_forward(m, B, T, tokens, h_star, pooled, logits, iters, argmax, scan_y, scan_state,
+                      nthreads);
+    orc_model_free(m);
 }
 
 /* Greedy decode (TRAINER:4219-4431 loop with LmHead::sample at temperature <= 1e-4 =

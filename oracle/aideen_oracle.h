@@ -85,6 +85,13 @@ void orc_scan_recirculate(const orc_cfg *c, const orc_weights *w, int T, const f
 void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
                  float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
                  float *scan_y, float *scan_state, int nthreads);
+/* The same forward on a model prepared once (weights transposed for the CPU loops). */
+typedef struct orc_model orc_model;
+orc_model *orc_model_create(const orc_cfg *c, const orc_weights *w);
+void orc_model_forward(orc_model *m, int B, int T, const int32_t *tokens, float *h_star,
+                       float *pooled, float *logits, int32_t *iters, int32_t *argmax,
+                       float *scan_y, float *scan_state, int nthreads);
+void orc_model_free(orc_model *m);
 void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int32_t *start,
                        int n_new, int32_t *out_tokens, int nthreads);
 

@@ -66,6 +66,11 @@ def lib():
         L.orc_scan_recirculate.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, F32P, F32P, F32P]
         L.orc_forward.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, C.c_int, I32P,
                                   F32P, F32P, F32P, I32P, I32P, F32P, F32P, C.c_int]
+        L.orc_model_create.restype = C.c_void_p
+        L.orc_model_create.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights)]
+        L.orc_model_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, I32P, F32P, F32P, F32P, I32P,
+                                        I32P, F32P, F32P, C.c_int]
+        L.orc_model_free.argtypes = [C.c_void_p]
         L.orc_decode_greedy.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, I32P,
                                         C.c_int, I32P, C.c_int]
         L.orc_zoh_step.argtypes = [C.c_int, F32P, F32P, F32P, F32P, F32P, F32P]
@@ -174,12 +179,45 @@ class Oracle:
                            fp(out.get("scan_state")), nthreads)
         return out
 
+    def prepared(self):
+        """A model handle with the CPU-side weight layout done once (for timing)."""
+        return _Prepared(self)
+
     def decode_greedy(self, start, n_new, nthreads=0):
         start = np.ascontiguousarray(start, dtype=np.int32)
         out = np.zeros((start.shape[0], n_new), np.int32)
         self.L.orc_decode_greedy(C.byref(self.c), C.byref(self.w), start.shape[0], ip(start),
                                  n_new, ip(out), nthreads)
         return out
+
+
+class _Prepared:
+    def __init__(self, o: "Oracle"):
+        self.o = o
+        self.h = o.L.orc_model_create(C.byref(o.c), C.byref(o.w))
+
+    def forward(self, tokens, nthreads=0, want_logits=True, want_scan=True):
+        """Same outputs as Oracle.forward (logits/scan optional); returns the output dict."""
+        o, mc = self.o, self.o.mc
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, T = tokens.shape
+        out = dict(h_star=np.zeros((B, T, mc.H, mc.d), np.float32), iters=np.zeros((B, T), np.int32),
+                   argmax=np.zeros((B, T), np.int32))
+        if want_logits:
+            out["logits"] = np.zeros((B, T, mc.V), np.float32)
+        if want_scan:
+            out["scan_y"] = np.zeros((B, T, mc.H, mc.d), np.float32)
+            out["scan_state"] = np.zeros((B, mc.H, mc.d, mc.N), np.float32)
+        o.L.orc_model_forward(self.h, B, T, ip(tokens), fp(out["h_star"]), None, fp(out.get("logits")),
+                              ip(out["iters"]), ip(out["argmax"]), fp(out.get("scan_y")),
+                              fp(out.get("scan_state")), nthreads)
+        return out
+
+    def __del__(self):
+        try:
+            self.o.L.orc_model_free(self.h)
+        except Exception:
+            pass
 
 
 def spectral_norm(w: np.ndarray, n_iter: int = 20) -> float:
