@@ -12,30 +12,14 @@
 //   k order is a fixed permutation shared by A and B.
 //   Block order: slot-major, then groups of 8 m-tiles with n fastest inside a group, spread so
 //   each XCD (own L2) gets a contiguous range -> one slot's weights stay resident in one L2.
-#include "kernels.h"
+#include "gemm_common.h"
 
 namespace adn {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4, NT = 256, GROUP_M = 8, NXCD = 8;
-
-__device__ __forceinline__ void map_block(int bid, int total, int nM, int nN, int &s, int &mt,
-                                          int &nt) {
-    // XCD-contiguous remap: hardware sends workgroup i to XCD i % 8.
-    const int q = total / NXCD, rem = total % NXCD;
-    const int x = bid % NXCD, j = bid / NXCD;
-    const int logical = x * q + (x < rem ? x : rem) + j;
-    const int per_slot = nM * nN;
-    s = logical / per_slot;
-    const int l = logical - s * per_slot;
-    const int group = l / (GROUP_M * nN);
-    const int first_m = group * GROUP_M;
-    const int gsz = min(nM - first_m, GROUP_M);
-    const int within = l - group * GROUP_M * nN;
-    mt = first_m + within % gsz;
-    nt = within / gsz;
-}
+using namespace gemm;
+constexpr int BK = 32, LDK = BK + 4;
 
 template <int ROLE>
 __global__ __launch_bounds__(NT, 2) void k_gemm_nt(GemmParams p) {
@@ -130,88 +114,17 @@ __global__ __launch_bounds__(NT, 2) void k_gemm_nt(GemmParams p) {
         __syncthreads();
     }
 
-    // Epilogue.  Output layout of a 32x32 MFMA tile: lane holds column lane%32, register e holds
-    // row 8*(e/4) + 4*(lane/32) + e%4.  Each value is formed once (acc + bias[n], or A[m][n] +
-    // acc) and feeds both the store and the optional per-row arg-max.
-    float bj[2] = {0.0f, 0.0f};
-    bool nv[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn * 64 + j * 32 + r;
-        nv[j] = n < p.N;
-        if (p.epi == EPI_BIAS && nv[j] && n < p.bias_n) bj[j] = p.bias[(long)s * p.bias_ss + n];
-    }
-    const bool want_am = p.am_val != nullptr;
-    // arg-max partials reuse the A staging area once the k loop is done
-    float *am_v = &As[0][0][0];
-    int *am_i = reinterpret_cast<int *>(&Bs[0][0][0]);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int ml = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
-            const int m = m0 + ml;
-            const bool mv = m < M;
-            float *crow = p.C + (long)m * p.c_sm + (long)s * p.c_ss;
-            const float *res_row = p.A + (long)m * p.a_sm + (long)s * p.a_ss;
-            float bv = -INFINITY;
-            int bi = -1;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = n0 + wn * 64 + j * 32 + r;
-                float v = acc[i][j][e];
-                if (p.epi == EPI_BIAS)
-                    v += bj[j];
-                else if (p.epi == EPI_ADD_A && mv && nv[j])
-                    v = res_row[n] + v;
-                if (mv && nv[j]) {
-                    crow[n] = v;
-                    if (v > bv || (v == bv && n > bi)) {
-                        bv = v;
-                        bi = n;
-                    }
-                }
-            }
-            if (want_am) {
-#pragma unroll
-                for (int off = 16; off > 0; off >>= 1) {
-                    const float v2 = __shfl_xor(bv, off, 64);
-                    const int i2 = __shfl_xor(bi, off, 64);
-                    if (v2 > bv || (v2 == bv && i2 > bi)) {
-                        bv = v2;
-                        bi = i2;
-                    }
-                }
-                if (r == 0) {
-                    am_v[wn * BM + ml] = bv;
-                    am_i[wn * BM + ml] = bi;
-                }
-            }
-        }
-    }
-    if (want_am) {
-        __syncthreads();
-        if (tid < BM) {
-            const int m = m0 + tid;
-            if (m < M) {
-                float v = am_v[tid];
-                int ix = am_i[tid];
-                const float v2 = am_v[BM + tid];
-                const int i2 = am_i[BM + tid];
-                if (v2 > v || (v2 == v && i2 > ix)) {
-                    v = v2;
-                    ix = i2;
-                }
-                p.am_val[(long)nt * p.M + m] = v;  // [tile][row]: coalesced across rows
-                p.am_idx[(long)nt * p.M + m] = ix;
-            }
-        }
-    }
+    // the main loop ended with a barrier: its LDS is free for the arg-max partials
+    epilogue(p, acc, M, s, m0, n0, nt, nN, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0]));
 }
 
 }  // namespace
 
 void launch_gemm(const GemmParams &p, hipStream_t st) {
+    if (p.prec != PREC_FP32) {
+        launch_gemm_split(p, st);
+        return;
+    }
     const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
     const int total = nM * nN * p.S;
     if (total <= 0) return;

@@ -1,0 +1,117 @@
+// Pieces shared by the fp32 and the split-precision MFMA GEMMs: block ordering and the
+// epilogue (bias / residual add / per-row arg-max partials) of a 2x2 grid of 32x32 MFMA tiles
+// per wave, 64x64 per wave, 128x128 per workgroup.
+#pragma once
+
+#include "kernels.h"
+
+namespace adn {
+namespace gemm {
+
+constexpr int BM = 128, BN = 128, NT = 256, GROUP_M = 8, NXCD = 8;
+
+__device__ __forceinline__ void map_block(int bid, int total, int nM, int nN, int &s, int &mt,
+                                          int &nt) {
+    // XCD-contiguous remap: hardware sends workgroup i to XCD i % 8.
+    const int q = total / NXCD, rem = total % NXCD;
+    const int x = bid % NXCD, j = bid / NXCD;
+    const int logical = x * q + (x < rem ? x : rem) + j;
+    const int per_slot = nM * nN;
+    s = logical / per_slot;
+    const int l = logical - s * per_slot;
+    const int group = l / (GROUP_M * nN);
+    const int first_m = group * GROUP_M;
+    const int gsz = min(nM - first_m, GROUP_M);
+    const int within = l - group * GROUP_M * nN;
+    mt = first_m + within % gsz;
+    nt = within / gsz;
+}
+
+// Epilogue for one wave's 2x2 accumulators.  `scratch` is >= 2*BM floats of LDS no longer
+// needed by the main loop (ints are stored through the same space, second half).
+__device__ __forceinline__ void epilogue(const GemmParams &p, floatx16 (&acc)[2][2], int M, int s, int m0,
+                                         int n0, int nt, int nN, float *scratch_v, int *scratch_i) {
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r = lane & 31, hh = lane >> 5;
+    // Epilogue.  Output layout of a 32x32 MFMA tile: lane holds column lane%32, register e holds
+    // row 8*(e/4) + 4*(lane/32) + e%4.  Each value is formed once (acc + bias[n], or A[m][n] +
+    // acc) and feeds both the store and the optional per-row arg-max.
+    float bj[2] = {0.0f, 0.0f};
+    bool nv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + r;
+        nv[j] = n < p.N;
+        if (p.epi == EPI_BIAS && nv[j] && n < p.bias_n) bj[j] = p.bias[(long)s * p.bias_ss + n];
+    }
+    const bool want_am = p.am_val != nullptr;
+    float *am_v = scratch_v;
+    int *am_i = scratch_i;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int ml = wm * 64 + i * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
+            const int m = m0 + ml;
+            const bool mv = m < M;
+            float *crow = p.C + (long)m * p.c_sm + (long)s * p.c_ss;
+            const float *res_row = p.A + (long)m * p.a_sm + (long)s * p.a_ss;
+            float bv = -INFINITY;
+            int bi = -1;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 64 + j * 32 + r;
+                float v = acc[i][j][e];
+                if (p.epi == EPI_BIAS)
+                    v += bj[j];
+                else if (p.epi == EPI_ADD_A && mv && nv[j])
+                    v = res_row[n] + v;
+                if (mv && nv[j]) {
+                    crow[n] = v;
+                    if (v > bv || (v == bv && n > bi)) {
+                        bv = v;
+                        bi = n;
+                    }
+                }
+            }
+            if (want_am) {
+#pragma unroll
+                for (int off = 16; off > 0; off >>= 1) {
+                    const float v2 = __shfl_xor(bv, off, 64);
+                    const int i2 = __shfl_xor(bi, off, 64);
+                    if (v2 > bv || (v2 == bv && i2 > bi)) {
+                        bv = v2;
+                        bi = i2;
+                    }
+                }
+                if (r == 0) {
+                    am_v[wn * BM + ml] = bv;
+                    am_i[wn * BM + ml] = bi;
+                }
+            }
+        }
+    }
+    if (want_am) {
+        __syncthreads();
+        if (tid < BM) {
+            const int m = m0 + tid;
+            if (m < M) {
+                float v = am_v[tid];
+                int ix = am_i[tid];
+                const float v2 = am_v[BM + tid];
+                const int i2 = am_i[BM + tid];
+                if (v2 > v || (v2 == v && i2 > ix)) {
+                    v = v2;
+                    ix = i2;
+                }
+                p.am_val[(long)nt * p.M + m] = v;  // [tile][row]: coalesced across rows
+                p.am_idx[(long)nt * p.M + m] = ix;
+            }
+        }
+    }
+}
+
+}  // namespace gemm
+}  // namespace adn

@@ -10,6 +10,8 @@ enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS = 1, EPI_ADD_A = 2 };
 // 128-column tile into [ceil(N/128)][M] partials (LM head + greedy decode).
 // Each use of the GEMM is a separate kernel symbol so profilers report them apart.
 enum GemmRole { ROLE_SIGNAL = 0, ROLE_QKV, ROLE_WO, ROLE_LMHEAD, ROLE_READOUT, ROLE_SCAN_PROJ, ROLE_COUNT };
+// GEMM arithmetic: plain fp32 MFMA, or fp32 operands as hi+lo halves on the 16-bit MFMA.
+enum GemmPrec { PREC_F16X3 = 0, PREC_FP32 = 1, PREC_BF16X3 = 2, PREC_BF16X1 = 3 };
 
 // C[m][n] = sum_k A(m,s)[k] * B(s)[n][k] (+ epilogue), for m < M (or *m_count), n < N, s < S.
 //   A(m,s) = A + row(m)*a_sm + s*a_ss, row(m) = a_idx ? a_idx[m] : m   (a_idx checked < a_idx_max)
@@ -34,9 +36,17 @@ struct GemmParams {
     int role;
     float *am_val;
     int32_t *am_idx;
+    int prec;            // GemmPrec
+    const void *Bhi;     // split weights [S][N][K] (prec != PREC_FP32)
+    const void *Blo;
+    float a_scale;       // A scaled by this power of two before the split
+    float out_scale;     // accumulator scaled by this power of two (undoes both scales)
 };
 constexpr int GEMM_BN = 128;
 void launch_gemm(const GemmParams &p, hipStream_t st);
+void launch_gemm_split(const GemmParams &p, hipStream_t st);
+// hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16; lo may be null
+void launch_split_weights(const float *w, long n, float scale, int prec, void *hi, void *lo, hipStream_t st);
 
 // ---- DEQ solve kernels (deq.hip) ------------------------------------------------------
 struct SolveBuffers {

@@ -10,6 +10,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <initializer_list>
+#include <utility>
 #include <mutex>
 #include <vector>
 
@@ -44,6 +46,15 @@ struct adn_ctx {
     float *lm_b = nullptr, *lm_g = nullptr, *a_log = nullptr, *wx_diag = nullptr, *w_out = nullptr;
     float *b_delta = nullptr, *w_kw = nullptr, *w_vw = nullptr, *w_b = nullptr, *w_c = nullptr;
     float *w_cat = nullptr;  // [H][r + 2N][d] = [W_kw^T; W_B; W_C] per slot (carrier projections)
+
+    // split-precision copies of the GEMM weights (hi/lo halves of w * scale)
+    struct Split {
+        void *hi = nullptr, *lo = nullptr;
+        float scale = 1.0f;
+    };
+    int prec = PREC_F16X3;
+    Split sp_in, sp_qkv, sp_o, sp_out, sp_cat, sp_lm;
+    float embed_scale = 1.0f;  // A-side power-of-two scale of the signal GEMM (fp16 split)
 
     // work buffers (capacity-sized)
     SolveBuffers sb{};
@@ -105,7 +116,9 @@ std::string validate_config(const adn_config &c) {
     if (c.max_batch < 1 || c.max_seq < 1) return "max_batch and max_seq must be >= 1";
     if ((long)c.max_batch * c.max_seq > (1L << 24)) return "max_batch*max_seq must be <= 2^24";
     if (c.anderson_m < 0 || c.anderson_m > 5) return "anderson_m must be in [0, 5]";
-    if (c.flags & ~0x3Fu) return "unknown flag bits";
+    if (c.flags & ~0x1FFu) return "unknown flag bits";
+    const uint32_t g = c.flags & (ADN_F_GEMM_FP32 | ADN_F_GEMM_BF16X3 | ADN_F_GEMM_BF16);
+    if (g & (g - 1)) return "at most one ADN_F_GEMM_* flag";
     return "";
 }
 
@@ -181,6 +194,42 @@ struct Span {
     }
 };
 
+float host_maxabs(std::initializer_list<std::pair<const float *, size_t>> parts) {
+    float m = 0.0f;
+    for (const auto &pr : parts)
+        if (pr.first)
+            for (size_t i = 0; i < pr.second; ++i) m = std::max(m, std::fabs(pr.first[i]));
+    return m;
+}
+
+// Power-of-two scale putting max|x| in [2^(h-1), 2^h) for fp16 halves (keeps lo out of the
+// subnormal range and hi below 65504); 1 for bf16 (same exponent range as fp32).
+float split_scale(int prec, float maxabs, int headroom_log2 = 14) {
+    if (prec != PREC_F16X3 || !(maxabs > 0.0f) || !std::isfinite(maxabs)) return 1.0f;
+    int e = (int)std::floor(std::log2((double)(1 << headroom_log2) / maxabs));
+    e = std::max(-24, std::min(24, e));
+    return std::ldexp(1.0f, e);
+}
+
+void make_split(adn_ctx *c, adn_ctx::Split &sp, const float *dev_w, size_t n, float maxabs) {
+    if (c->prec == PREC_FP32) return;
+    const size_t bytes = n * 2;
+    if (!sp.hi) sp.hi = dmalloc(c, bytes);
+    if (c->prec != PREC_BF16X1 && !sp.lo) sp.lo = dmalloc(c, bytes);
+    sp.scale = split_scale(c->prec, maxabs);
+    launch_split_weights(dev_w, (long)n, sp.scale, c->prec, sp.hi, c->prec == PREC_BF16X1 ? nullptr : sp.lo,
+                         c->stream);
+}
+
+void set_split(const adn_ctx *c, GemmParams &g, const adn_ctx::Split &sp, float a_scale = 1.0f) {
+    g.prec = c->prec;
+    if (c->prec == PREC_FP32) return;
+    g.Bhi = sp.hi;
+    g.Blo = sp.lo ? sp.lo : sp.hi;
+    g.a_scale = a_scale;
+    g.out_scale = 1.0f / (sp.scale * a_scale);
+}
+
 // ---------------------------------------------------------------------------------------
 // the forward pipeline (device pointers; enqueue only)
 // ---------------------------------------------------------------------------------------
@@ -213,6 +262,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
         g.S = H;
         g.err = b.err;
         g.epi = EPI_NONE;
+        set_split(c, g, c->sp_in, c->embed_scale);
         Span sp(prof, ADN_STAGE_SIGNAL_GEMM, -1, st);
         launch_gemm(g, st);
     }
@@ -247,6 +297,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             g.m_count = b.cnt + cur;
             g.err = b.err;
             g.epi = c->qk_bias ? EPI_BIAS : EPI_NONE;
+            set_split(c, g, c->sp_qkv);
             Span sp(prof, ADN_STAGE_QKV_GEMM, k, st);
             launch_gemm(g, st);
         }
@@ -272,6 +323,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             g.m_count = b.cnt + cur;
             g.err = b.err;
             g.epi = EPI_NONE;
+            set_split(c, g, c->sp_o);
             Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
             launch_gemm(g, st);
         }
@@ -313,6 +365,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
         g.S = 1;
         g.err = b.err;
         g.epi = c->lm_b ? EPI_BIAS : EPI_NONE;
+        set_split(c, g, c->sp_lm);
         const int ntiles = (D.V + GEMM_BN - 1) / GEMM_BN;
         if (o.argmax) {
             g.am_val = c->am_val;
@@ -350,6 +403,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             g.S = H;
             g.err = b.err;
             g.epi = EPI_NONE;
+            set_split(c, g, c->sp_cat);
             launch_gemm(g, st);
         }
         // chunk buffers hold max_batch * scan_nch_cap sequence-chunks
@@ -380,6 +434,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             g.S = H;
             g.err = b.err;
             g.epi = EPI_ADD_A;
+            set_split(c, g, c->sp_out);
             Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st);
             launch_gemm(g, st);
         }
@@ -445,6 +500,10 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
     try {
         c->cfg = *cfg;
         c->D = Dims{cfg->d_r, cfg->h_slots, cfg->vocab, cfg->d_state, cfg->rank, cfg->flags};
+        c->prec = (cfg->flags & ADN_F_GEMM_FP32)     ? PREC_FP32
+                  : (cfg->flags & ADN_F_GEMM_BF16X3) ? PREC_BF16X3
+                  : (cfg->flags & ADN_F_GEMM_BF16)   ? PREC_BF16X1
+                                                     : PREC_F16X3;
         ADN_HIP(hipGetDevice(&c->device));
         ADN_HIP(hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking));
         c->stream = c->own_stream;
@@ -603,6 +662,22 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
                                          hipMemcpyDeviceToDevice, c->stream));
             }
         }
+        // split-precision copies of every GEMM weight (device-side, from the fp32 copies)
+        const size_t nmat = (size_t)H * mat;
+        make_split(c, c->sp_qkv, c->w_qkv, 3 * nmat,
+                   host_maxabs({{w->w_q, nmat}, {w->w_k, nmat}, {w->w_v, nmat}}));
+        make_split(c, c->sp_o, c->w_o, nmat, host_maxabs({{w->w_o, nmat}}));
+        make_split(c, c->sp_in, c->w_in, nmat, host_maxabs({{w->w_in, nmat}}));
+        if (c->w_out) make_split(c, c->sp_out, c->w_out, nmat, host_maxabs({{w->w_out, nmat}}));
+        make_split(c, c->sp_cat, c->w_cat, (size_t)H * (r + 2 * N) * d,
+                   host_maxabs({{w->w_kw, (size_t)H * d * r}, {w->w_b, (size_t)H * N * d},
+                                {w->w_c, (size_t)H * N * d}}));
+        make_split(c, c->sp_lm, c->lm_w, (size_t)V * d, host_maxabs({{w->lm_w, (size_t)V * d}}));
+        // The signal GEMM's A operand (gathered embedding rows, or s_in rows of the same
+        // scale) is scaled up too, with 6 bits of headroom: inputs up to 64x the table's
+        // maximum magnitude stay inside the fp16 range.
+        c->embed_scale = split_scale(c->prec, host_maxabs({{w->embed, (size_t)V * d}}), 10);
+        ADN_HIP(hipGetLastError());
         ADN_HIP(hipStreamSynchronize(c->stream));
     } catch (const HipError &e) {
         return hip_fail(e);

@@ -34,6 +34,9 @@ F_RMS_EXCL_ANCHOR = 1 << 2
 F_INIT_SIGNAL_RMS = 1 << 3
 F_RESID_L2 = 1 << 4
 F_SCAN_SELECTIVE = 1 << 5
+F_GEMM_FP32 = 1 << 6
+F_GEMM_BF16X3 = 1 << 7
+F_GEMM_BF16 = 1 << 8
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)

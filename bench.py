@@ -27,7 +27,15 @@ sys.path.insert(0, ROOT)
 
 METRIC = "forward tokens/sec at d_r=512,h_slots=8,ctx=256,B=32; HBM GB/s & MFMA % of peak"
 PEAK_HBM_GBS = 8000.0
-PEAK_FP32_TFLOPS = 157.3
+# MI355X published dense MFMA peaks (TFLOP/s).  The split-precision GEMMs execute 3 16-bit
+# products per fp32 product, so their algorithmic (fp32-equivalent) ceiling is the 16-bit
+# peak / 3; bf16 single-product GEMMs are priced at the full bf16 peak.
+GEMM_MODES = {
+    "f16x3": dict(flag=0, peak=2500.0 / 3, basis="fp16 dense MFMA 2500 TFLOP/s / 3 products per fp32 multiply"),
+    "bf16x3": dict(flag=1 << 7, peak=2500.0 / 3, basis="bf16 dense MFMA 2500 TFLOP/s / 3 products per fp32 multiply"),
+    "fp32": dict(flag=1 << 6, peak=157.3, basis="fp32 MFMA 157.3 TFLOP/s"),
+    "bf16": dict(flag=1 << 8, peak=2500.0, basis="bf16 dense MFMA 2500 TFLOP/s"),
+}
 MFMA_STAGES = ("signal_gemm", "qkv_gemm", "wo_gemm", "lmhead_gemm", "readout_gemm")
 
 
@@ -66,6 +74,9 @@ def main() -> int:
     ap.add_argument("--config", default="NS")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemm", choices=list(GEMM_MODES), default="f16x3",
+                    help="GEMM arithmetic (f16x3 / bf16x3 / fp32 are fp32-accurate; bf16 is the "
+                         "reduced-precision bf16-input variant)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -78,8 +89,10 @@ def main() -> int:
     from aideen_amd import synth
     from aideen_amd.backend import GpuDeqBackend
 
+    import dataclasses
     p = synth.PRESETS[args.config]
-    mc = p["model"]
+    gm = GEMM_MODES[args.gemm]
+    mc = dataclasses.replace(p["model"], flags=p["model"].flags | gm["flag"])
     B, T = p["B"], p["T"]
     log(f"config {args.config}: d={mc.d} H={mc.H} V={mc.V} N={mc.N} B={B} T={T}")
     w = synth.make_weights(mc, seed=0)
@@ -137,11 +150,12 @@ def main() -> int:
     ds = prof["stages"][dom]
     achieved = ds["flops"] / ds["ms"] / 1e9  # TFLOP/s
     traffic = None
-    tf_path = os.path.join(ROOT, "profiles", f"{dom}_{args.config}_traffic.json")
+    tf_path = os.path.join(ROOT, "profiles", f"{dom}_{args.config}_{args.gemm}_traffic.json")
     if os.path.exists(tf_path):
         traffic = json.load(open(tf_path)).get("bytes_per_launch")
-    roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 2), peak=PEAK_FP32_TFLOPS,
-                    unit="TFLOP/s", frac=round(achieved / PEAK_FP32_TFLOPS, 4), traffic=traffic,
+    roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 2), peak=round(gm["peak"], 1),
+                    unit="TFLOP/s", frac=round(achieved / gm["peak"], 4), traffic=traffic,
+                    peak_basis=gm["basis"], gemm=args.gemm,
                     launches=ds["launches"], avg_launch_ms=round(ds["ms"] / ds["launches"], 4),
                     flops_per_launch=ds["flops"] / ds["launches"])
     hbm = {}
@@ -160,11 +174,12 @@ def main() -> int:
     line = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32" if args.gemm != "bf16" else "bf16-in/f32-acc",
         "data": "synthetic (seeded Xavier weights at spectral norm 0.5, Zipf(1.1) token ids)",
         "config": {"workload": f"{args.config}: DEQ forward d_r={mc.d} h_slots={mc.H} vocab={mc.V} "
                                f"d_state={mc.N} B={B} ctx={T}, Picard max {mc.max_iters} tol {mc.eps}, "
-                               f"anderson m={mc.anderson_m}; logits for all positions + arg-max + scan",
+                               f"anderson m={mc.anderson_m}; logits for all positions + arg-max + scan; "
+                               f"GEMM {args.gemm}",
                    "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
         "roofline": roofline,
         "cpu_baseline": cpu,

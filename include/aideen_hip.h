@@ -56,6 +56,13 @@ extern "C" {
 #define ADN_F_RESID_L2 (1u << 4)        /* L2 exit residual (aideen-node/src/inference.rs:214-221)    */
 #define ADN_F_SCAN_SELECTIVE (1u << 5)  /* input-dependent carrier decay (gpu_deq.rs:6129-6214)      */
 
+/* GEMM arithmetic (adn_config.flags; at most one).  Default: fp32 operands carried as fp16
+ * hi+lo pairs on the 16-bit MFMA with three products per multiply (hi.hi + hi.lo + lo.hi),
+ * fp32 accumulation -- fp32-level accuracy at several times the fp32 MFMA rate. */
+#define ADN_F_GEMM_FP32 (1u << 6)   /* plain fp32 MFMA (v_mfma_f32_32x32x2f32)                      */
+#define ADN_F_GEMM_BF16X3 (1u << 7) /* bf16 hi+lo pairs, three products (~2^-16 relative)           */
+#define ADN_F_GEMM_BF16 (1u << 8)   /* bf16 inputs, fp32 accumulate (one product)                   */
+
 /* weight layouts for adn_upload_weights */
 #define ADN_LAYOUT_OUT_IN 0u /* W[s][out][in] row-major                                   */
 #define ADN_LAYOUT_IN_OUT 1u /* W[s][in][out]: the reference's GPU flat layout            */

@@ -22,7 +22,8 @@ def test_header_flag_values_match_oracle_and_synth():
     hdr = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define ADN_F_(\w+) \(1u << (\d+)\)", text)}
     orc = open(_lib.HEADER.replace("include/aideen_hip.h", "oracle/aideen_oracle.h")).read()
     ohd = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define ORC_F_(\w+)\s+\(1u << (\d+)\)", orc)}
-    assert hdr == ohd
+    # semantic switches are shared with the oracle; the GEMM arithmetic bits are product-only
+    assert {k: v for k, v in hdr.items() if not k.startswith("GEMM_")} == ohd
     for k, v in hdr.items():
         assert getattr(synth, "F_" + k) == 1 << v
 
@@ -39,7 +40,7 @@ def test_struct_layouts_match_header():
 
 @pytest.mark.parametrize("bad", [
     dict(d_r=100), dict(d_r=4096), dict(h_slots=3), dict(d_state=0), dict(d_state=64),
-    dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 9), dict(vocab=0),
+    dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 9), dict(vocab=0), dict(flags=(1 << 6) | (1 << 7)),
 ])
 def test_create_rejects_invalid_config_before_device(bad):
     L = _lib.lib()

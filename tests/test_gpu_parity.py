@@ -64,6 +64,38 @@ def test_c1_matches_golden(name):
     assert np.array_equal(got["argmax"], data["argmax"])
 
 
+PRECISIONS = {"f16x3": 0, "fp32": synth.F_GEMM_FP32, "bf16x3": synth.F_GEMM_BF16X3}
+
+
+@pytest.mark.parametrize("prec", list(PRECISIONS), ids=list(PRECISIONS))
+@pytest.mark.parametrize("name", ["c1_forward", "c1_anderson_m5"])
+def test_c1_matches_golden_every_gemm_precision(name, prec):
+    """Every fp32-accurate GEMM arithmetic meets the same bar against the golden fixtures."""
+    log(f"case {name} {prec}")
+    mc, w, data = golden_case(name)
+    mc = dataclasses.replace(mc, flags=mc.flags | PRECISIONS[prec])
+    be = make(mc, 1, 64)
+    be.upload_weights(w)
+    got = be.forward(data["tokens"])
+    assert_forward_parity(got, data, f"{name}/{prec}")
+
+
+def test_bf16_input_variant_close_to_fp32(oracle_lib):
+    """The bf16-input, fp32-accumulate GEMM (ADN_F_GEMM_BF16) is a reduced-precision variant:
+    its product noise (~2^-9 relative) is far above tol 1e-4, so it is checked at a tolerance
+    bf16 can meet (eps 5e-3 in both paths; h* and logits within 2e-2, iterations within 2)."""
+    mc, w, data = golden_case("c1_forward")
+    mc = dataclasses.replace(mc, eps=5e-3)
+    ref = oracle_lib.Oracle(mc, w).forward(data["tokens"])
+    mcb = dataclasses.replace(mc, flags=mc.flags | synth.F_GEMM_BF16)
+    be = make(mcb, 1, 64)
+    be.upload_weights(w)
+    got = be.forward(data["tokens"])
+    assert np.abs(got["iters"].astype(int) - ref["iters"]).max() <= 2
+    np.testing.assert_allclose(got["h_star"], ref["h_star"], rtol=0, atol=2e-2)
+    np.testing.assert_allclose(got["logits"], ref["logits"], rtol=0, atol=2e-2)
+
+
 def _small(d, H, V, N, flags=0, **kw):
     mc = synth.ModelConfig(d=d, H=H, V=V, N=N, r=32, flags=flags, **kw)
     return mc, synth.make_weights(mc, seed=3)
