@@ -113,5 +113,114 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, floatx16 (&acc)[2]
     }
 }
 
+
+// Generic epilogue: each wave holds WTM x WTN tiles of 32x32 (acc[i][j]); the workgroup is a
+// WGM x WGN grid of waves, block tile (WGM*WTM*32) x (WGN*WTN*32).  Per-row arg-max partials go
+// through `scratch_v/scratch_i` (>= WGN * block-rows entries of LDS free after the k loop).
+// The tile rows are walked by template recursion (I = 0..WTM-1) so that every accumulator index
+// is a compile-time constant: a runtime row loop leaves the accumulator array in scratch memory.
+struct EpiCtx {
+    int M, s, m0, n0, wm, wn, r, hh;
+    float osc;  // accumulator scale (undoes the power-of-two operand scaling)
+    bool want_am;
+    float *scratch_v;
+    int *scratch_i;
+};
+
+template <int I, int WTM, int WTN, int WGM>
+__device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c,
+                                         const float (&bj)[WTN], const bool (&nv)[WTN]) {
+    constexpr int BMt = WGM * WTM * 32;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int ml = (c.wm * WTM + I) * 32 + 8 * (e >> 2) + 4 * c.hh + (e & 3);
+        const int m = c.m0 + ml;
+        const bool mv = m < c.M;
+        float *crow = p.C + (long)m * p.c_sm + (long)c.s * p.c_ss;
+        const float *res_row = p.A + (long)m * p.a_sm + (long)c.s * p.a_ss;
+        float bv = -INFINITY;
+        int bi = -1;
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            const int n = c.n0 + (c.wn * WTN + j) * 32 + c.r;
+            float v = acc[I][j][e] * c.osc;
+            if (p.epi == EPI_BIAS)
+                v += bj[j];
+            else if (p.epi == EPI_ADD_A && mv && nv[j])
+                v = res_row[n] + v;
+            if (mv && nv[j]) {
+                crow[n] = v;
+                if (v > bv || (v == bv && n > bi)) {
+                    bv = v;
+                    bi = n;
+                }
+            }
+        }
+        if (c.want_am) {
+#pragma unroll
+            for (int off = 16; off > 0; off >>= 1) {
+                const float v2 = __shfl_xor(bv, off, 64);
+                const int i2 = __shfl_xor(bi, off, 64);
+                if (v2 > bv || (v2 == bv && i2 > bi)) {
+                    bv = v2;
+                    bi = i2;
+                }
+            }
+            if (c.r == 0) {
+                c.scratch_v[c.wn * BMt + ml] = bv;
+                c.scratch_i[c.wn * BMt + ml] = bi;
+            }
+        }
+    }
+    if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM>(p, acc, c, bj, nv);
+}
+
+template <int WTM, int WTN, int WGM, int WGN>
+__device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[WTM][WTN], int M, int s,
+                                           int m0, int n0, float osc, float *scratch_v, int *scratch_i) {
+    constexpr int BMt = WGM * WTM * 32;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    EpiCtx c{M, s, m0, n0, wave / WGN, wave % WGN, lane & 31, lane >> 5, osc, p.am_val != nullptr, scratch_v,
+             scratch_i};
+    float bj[WTN];
+    bool nv[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+        const int n = n0 + (c.wn * WTN + j) * 32 + c.r;
+        nv[j] = n < p.N;
+        bj[j] = (p.epi == EPI_BIAS && nv[j] && n < p.bias_n) ? p.bias[(long)s * p.bias_ss + n] : 0.0f;
+    }
+    epi_rows<0, WTM, WTN, WGM>(p, acc, c, bj, nv);
+    if (c.want_am) {
+        // partials are per 128 columns: waves covering 64 columns are combined in pairs
+        constexpr int CPW = WTN * 32;
+        static_assert(CPW == 64 || CPW == 128, "arg-max partials need 64 or 128 columns per wave");
+        constexpr int TPW = 128 / CPW;
+        constexpr int QT = WGN / TPW;  // 128-column tiles per block
+        __syncthreads();
+        for (int idx = tid; idx < BMt * QT; idx += 64 * WGM * WGN) {
+            const int ml = idx % BMt, q = idx / BMt;
+            const int m = m0 + ml;
+            const int tile = (n0 >> 7) + q;
+            if (m < M && tile * 128 < p.N) {
+                float v = scratch_v[q * TPW * BMt + ml];
+                int ix = scratch_i[q * TPW * BMt + ml];
+#pragma unroll
+                for (int w = 1; w < TPW; ++w) {
+                    const float v2 = scratch_v[(q * TPW + w) * BMt + ml];
+                    const int i2 = scratch_i[(q * TPW + w) * BMt + ml];
+                    if (v2 > v || (v2 == v && i2 > ix)) {
+                        v = v2;
+                        ix = i2;
+                    }
+                }
+                p.am_val[(long)tile * p.M + m] = v;  // [tile][row]: coalesced across rows
+                p.am_idx[(long)tile * p.M + m] = ix;
+            }
+        }
+    }
+}
+
 }  // namespace gemm
 }  // namespace adn

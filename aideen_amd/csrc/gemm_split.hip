@@ -10,11 +10,27 @@
 // With bf16 halves (no range issue) the error is ~2^-16; TERMS = 1 is the plain bf16-input,
 // fp32-accumulate product.
 //
-// Weights (B) are split once at upload ([S][N][K] hi and lo arrays); activations (A, fp32 in
-// HBM) are split while the tile is staged into LDS.  Tiling as the fp32 kernel: 256 threads,
-// 128x128 block tile, k-step 32, each wave 64x64 = 2x2 tiles of 32x32.  LDS rows are 64 bytes
-// (32 halves) with the 16-byte chunks XOR-swizzled by (row & 3), so the ds_read_b128 operand
-// fetches of 32 consecutive rows are bank-conflict free without padding.
+// Weights (B) are split once at upload ([S][N][K] hi and lo arrays).  Activations (A) stay fp32
+// in HBM and in LDS and are split when a wave reads its MFMA fragments.
+//
+// Data movement is gfx950's direct global->LDS load (global_load_lds_dwordx4: lane L of a wave
+// writes LDS bytes [16L, 16L+16) of a 1 KB block at the wave-uniform address in M0), so no
+// staging registers are needed and the k loop runs a STAGES-deep LDS ring of BK = 16 slices:
+// the loads for slice kt + STAGES - 1 are issued while slice kt is multiplied, which hides the
+// HBM latency of the A rows that miss in L2.  One barrier per slice; each wave waits only for
+// its own loads of the slice about to be read (s_waitcnt vmcnt(n) with n = loads still allowed
+// in flight), then the barrier makes every wave's part visible and frees the slot that the next
+// loads overwrite.
+//
+// LDS rows: A is 16 fp32 = 64 bytes (4 chunks of 16 B), B is 16 halves = 32 bytes (2 chunks).
+// The chunks are XOR-swizzled so that the ds_read_b128 fragment reads (32 consecutive rows, one
+// chunk each) are conflict-free for 32 and for 64 four-byte banks:
+//   A: chunk ^ (((row >> 1) ^ (row >> 2)) & 3)        B: chunk ^ (((row >> 2) ^ (row >> 3)) & 1)
+// The DMA writes an LDS block linearly, so the swizzle is applied on the global side: lane L
+// fetches the chunk that belongs at its LDS position.
+//
+// Each wave owns WTM x WTN MFMA tiles of 32x32 (v_mfma_f32_32x32x16), the workgroup a WGM x WGN
+// grid of waves.  Wide GEMMs use 256x256 blocks of 8 waves (64x128 each, 2 waves per SIMD).
 #include "gemm_common.h"
 
 namespace adn {
@@ -22,10 +38,11 @@ namespace adn {
 namespace {
 
 using namespace gemm;
-constexpr int BK = 32;
+constexpr int BK = 16;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T>
 struct Vec8;
@@ -38,6 +55,9 @@ struct Vec8<__bf16> {
     typedef bf8 type;
 };
 
+__device__ __forceinline__ int swz_a(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+__device__ __forceinline__ int swz_b(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
+
 __device__ __forceinline__ floatx16 mfma16(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -45,155 +65,152 @@ __device__ __forceinline__ floatx16 mfma16(bf8 a, bf8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int ROLE, typename T, int TERMS>
-__global__ __launch_bounds__(NT, 2) void k_gemm_split(GemmParams p) {
-    typedef typename Vec8<T>::type V8;
-    constexpr int PARTS = TERMS == 3 ? 2 : 1;
-    __shared__ __attribute__((aligned(16))) T As[2][PARTS][BM][BK];
-    __shared__ __attribute__((aligned(16))) T Bs[2][PARTS][BN][BK];
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
-    const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
+// Workgroup barrier without the memory fence of __syncthreads (which would drain every
+// outstanding LDS DMA): this wave's LDS reads are completed first (through the builtin, so that
+// the compiler's own wait-count tracking sees it), the memory clobber keeps the compiler from
+// moving LDS accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
+template <int ROLE, typename T, int TERMS, int WTM, int WTN, int WGM, int WGN, int STAGES>
+__global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_gemm_split(GemmParams p) {
+    typedef typename Vec8<T>::type V8;
+    constexpr int NW = WGM * WGN;
+    constexpr int BMt = WGM * WTM * 32, BNt = WGN * WTN * 32;
+    constexpr int PARTS = TERMS == 3 ? 2 : 1;
+    constexpr int A_BLK = BMt / 16;  // 1 KB DMA blocks per A slice (16 rows of 64 B)
+    constexpr int B_BLK = BNt / 32;  // 1 KB DMA blocks per B slice and part (32 rows of 32 B)
+    static_assert(A_BLK % NW == 0 && B_BLK % NW == 0, "DMA blocks must split evenly over waves");
+    constexpr int A_PW = A_BLK / NW, B_PW = B_BLK / NW;
+    constexpr int LOADS = A_PW + PARTS * B_PW;  // DMA instructions per wave per slice
+    static_assert(STAGES >= 2 && (STAGES - 2) * LOADS < 64, "pipeline depth");
+    __shared__ __attribute__((aligned(1024))) float As[STAGES][BMt][BK];
+    __shared__ __attribute__((aligned(1024))) T Bs[STAGES][PARTS][BNt][BK];
+
+    const int nM = (p.M + BMt - 1) / BMt, nN = (p.N + BNt - 1) / BNt;
     int s, mt, nt;
     map_block(blockIdx.x, nM * nN * p.S, nM, nN, s, mt, nt);
     const int M = p.m_count ? min(*p.m_count, p.M) : p.M;
-    const int m0 = mt * BM, n0 = nt * BN;
+    const int m0 = mt * BMt, n0 = nt * BNt;
     if (m0 >= M) return;
 
     const int tid = threadIdx.x;
-    const int lrow = tid >> 2;  // 0..63, and lrow + 64
-    const int lc = tid & 3;     // 16-byte chunk (8 k values) within the 32-wide k step
-    const float *arow[2];
-    const T *bhi[2];
-    const T *blo[2];
-    bool aval[2], bval[2];
-    const T *Bh = reinterpret_cast<const T *>(p.Bhi);
-    const T *Bl = reinterpret_cast<const T *>(p.Blo);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+
+    // Per-lane source pointers of this wave's DMA blocks.  Rows past M or N read row 0 of the
+    // operand (their products land in outputs that the epilogue does not store).
+    const float *asrc[A_PW];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int m = m0 + lrow + 64 * j;
-        aval[j] = m < M;
-        long r = 0;
-        if (aval[j]) {
-            r = p.a_idx ? (long)p.a_idx[m] : (long)m;
-            if (p.a_idx && (r < 0 || r >= p.a_idx_max)) {
+    for (int j = 0; j < A_PW; ++j) {
+        const int row = (wave + NW * j) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ swz_a(row);
+        const int m = m0 + row;
+        long ar = 0;
+        if (m < M) {
+            ar = p.a_idx ? (long)p.a_idx[m] : (long)m;
+            if (p.a_idx && (ar < 0 || ar >= p.a_idx_max)) {
                 if (p.err) atomicOr(p.err, ADN_DEVERR_TOKEN);
-                r = 0;
+                ar = 0;
             }
         }
-        arow[j] = p.A + r * p.a_sm + (long)s * p.a_ss;
-        const int n = n0 + lrow + 64 * j;
-        bval[j] = n < p.N;
-        const long boff = (long)s * p.b_ss + (long)(bval[j] ? n : 0) * p.K;
-        bhi[j] = Bh + boff;
-        blo[j] = Bl + boff;
+        asrc[j] = p.A + ar * p.a_sm + (long)s * p.a_ss + c * 4;
     }
-
-    floatx4 ga[2][2];
-    V8 gbh[2], gbl[2];
-    auto gload = [&](int kt) {
-        const int k = kt * BK + lc * 8;
+    const T *bsrc[B_PW][PARTS];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            if (aval[j]) {
-                ga[j][0] = *reinterpret_cast<const floatx4 *>(arow[j] + k);
-                ga[j][1] = *reinterpret_cast<const floatx4 *>(arow[j] + k + 4);
-            } else {
-                ga[j][0] = floatx4{0, 0, 0, 0};
-                ga[j][1] = floatx4{0, 0, 0, 0};
-            }
-            if (bval[j]) {
-                gbh[j] = *reinterpret_cast<const V8 *>(bhi[j] + k);
-                if (TERMS == 3) gbl[j] = *reinterpret_cast<const V8 *>(blo[j] + k);
-            } else {
+    for (int j = 0; j < B_PW; ++j) {
+        const int row = (wave + NW * j) * 32 + (lane >> 1);
+        const int c = (lane & 1) ^ swz_b(row);
+        const int n = n0 + row;
+        const long off = (long)s * p.b_ss + (long)(n < p.N ? n : 0) * p.K + c * 8;
+        bsrc[j][0] = reinterpret_cast<const T *>(p.Bhi) + off;
+        if constexpr (TERMS == 3) bsrc[j][1] = reinterpret_cast<const T *>(p.Blo) + off;
+    }
+    auto issue = [&](int kt, int st) {
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    gbh[j][q] = (T)0.0f;
-                    gbl[j][q] = (T)0.0f;
-                }
-            }
-        }
-    };
-    const float asc = p.a_scale;
-    auto lstore = [&](int buf) {
+        for (int j = 0; j < A_PW; ++j)
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[j] + kt * BK),
+                                             (lds_void *)&As[st][(wave + NW * j) * 16][0], 16, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int row = lrow + 64 * j;
-            const int pc = (lc ^ (row & 3)) * 8;
-            V8 h8, l8;
+        for (int j = 0; j < B_PW; ++j)
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float x = ga[j][q >> 2][q & 3] * asc;
-                const T hv = (T)x;
-                h8[q] = hv;
-                if (TERMS == 3) l8[q] = (T)(x - (float)hv);
-            }
-            *reinterpret_cast<V8 *>(&As[buf][0][row][pc]) = h8;
-            *reinterpret_cast<V8 *>(&Bs[buf][0][row][pc]) = gbh[j];
-            if constexpr (TERMS == 3) {
-                *reinterpret_cast<V8 *>(&As[buf][1][row][pc]) = l8;
-                *reinterpret_cast<V8 *>(&Bs[buf][1][row][pc]) = gbl[j];
-            }
-        }
+            for (int q = 0; q < PARTS; ++q)
+                __builtin_amdgcn_global_load_lds((const void *)(bsrc[j][q] + kt * BK),
+                                                 (lds_void *)&Bs[st][q][(wave + NW * j) * 32][0], 16, 0, 0);
     };
 
-    const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int r = lane & 31, hh = lane >> 5;
-    floatx16 acc[2][2];
+    // fragment chunk positions: rows r + 32t share swz(r) (the swizzles read row bits 1..3)
+    const int pa0 = ((2 * hh) ^ swz_a(r)) * 4, pa1 = ((2 * hh + 1) ^ swz_a(r)) * 4;
+    const int pb = (hh ^ swz_b(r)) * 8;
+    const float asc = p.a_scale;
+    floatx16 acc[WTM][WTN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WTM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WTN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int nk = p.K / BK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
+    auto compute = [&](int st) {
+        V8 bh[WTN], bl[WTN];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            // lane half hh takes chunk 2*kk + hh of each row (8 consecutive k); the physical
-            // chunk is swizzled by row & 3 == r & 3 (tile row bases are multiples of 32)
-            const int pc = ((2 * kk + hh) ^ (r & 3)) * 8;
-            V8 ah[2], al[2], bh[2], bl[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                ah[i] = *reinterpret_cast<const V8 *>(&As[buf][0][wm * 64 + i * 32 + r][pc]);
-                if constexpr (TERMS == 3) al[i] = *reinterpret_cast<const V8 *>(&As[buf][1][wm * 64 + i * 32 + r][pc]);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                bh[j] = *reinterpret_cast<const V8 *>(&Bs[buf][0][wn * 64 + j * 32 + r][pc]);
-                if constexpr (TERMS == 3) bl[j] = *reinterpret_cast<const V8 *>(&Bs[buf][1][wn * 64 + j * 32 + r][pc]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    if constexpr (TERMS == 3) {
-                        acc[i][j] = mfma16(al[i], bh[j], acc[i][j]);
-                        acc[i][j] = mfma16(ah[i], bl[j], acc[i][j]);
-                    }
-                    acc[i][j] = mfma16(ah[i], bh[j], acc[i][j]);
-                }
+        for (int j = 0; j < WTN; ++j) {
+            const int row = (wn * WTN + j) * 32 + r;
+            bh[j] = *reinterpret_cast<const V8 *>(&Bs[st][0][row][pb]);
+            if constexpr (TERMS == 3) bl[j] = *reinterpret_cast<const V8 *>(&Bs[st][PARTS - 1][row][pb]);
         }
-        if (kt + 1 < nk) lstore(buf ^ 1);
-        __syncthreads();
-    }
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+            const int row = (wm * WTM + i) * 32 + r;
+            const floatx4 x0 = *reinterpret_cast<const floatx4 *>(&As[st][row][pa0]);
+            const floatx4 x1 = *reinterpret_cast<const floatx4 *>(&As[st][row][pa1]);
+            V8 ah, al;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float x = (q < 4 ? x0[q] : x1[q - 4]) * asc;
+                const T hv = (T)x;
+                ah[q] = hv;
+                if constexpr (TERMS == 3) al[q] = (T)(x - (float)hv);
+            }
+#pragma unroll
+            for (int j = 0; j < WTN; ++j) {
+                if constexpr (TERMS == 3) {
+                    acc[i][j] = mfma16(al, bh[j], acc[i][j]);
+                    acc[i][j] = mfma16(ah, bl[j], acc[i][j]);
+                }
+                acc[i][j] = mfma16(ah, bh[j], acc[i][j]);
+            }
+        }
+    };
 
-    const float osc = p.out_scale;
+    const int nk = p.K / BK;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] *= osc;
-    epilogue(p, acc, M, s, m0, n0, nt, nN, reinterpret_cast<float *>(&As[0][0][0][0]),
-             reinterpret_cast<int *>(&Bs[0][0][0][0]));
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nk) issue(st, st);
+    for (int kt = 0; kt < nk; ++kt) {
+        // this wave's loads of slice kt are done once at most (STAGES-2) later slices are in flight
+        if (kt + STAGES - 2 < nk)
+            wait_vmcnt<(STAGES - 2) * LOADS>();
+        else
+            wait_vmcnt<0>();
+        lds_barrier();
+        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        compute(kt % STAGES);
+    }
+    lds_barrier();  // every wave is done with the ring before the epilogue reuses it
+
+    epilogue_t<WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, p.out_scale, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
 }
 
 // Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi).
@@ -207,29 +224,40 @@ __global__ void k_split(const float *w, long n, float scale, T *hi, T *lo) {
     }
 }
 
+// Tile configurations (WTM, WTN, WGM, WGN, STAGES): GEMMs that are wide in both M and N use
+// 256x256 blocks of 8 waves (one workgroup per CU, 128 KB of LDS ring); the rest 128x128 blocks
+// of 4 waves (two workgroups per CU) so that their grids still cover the chip.
+template <int ROLE, typename T, int TERMS>
+void launch_cfg(const GemmParams &p, hipStream_t st) {
+    const bool big = p.N >= 1024 && p.M >= 1024;
+    const int bm = big ? 256 : 128, bn = big ? 256 : 128;
+    const int total = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.S;
+    if (total <= 0) return;
+    if (big)
+        hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4>), dim3(total), dim3(512), 0, st, p);
+    else
+        hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 2, 2, 2, 4>), dim3(total), dim3(256), 0, st, p);
+}
+
 template <typename T, int TERMS>
-void launch_role(const GemmParams &p, int total, hipStream_t st) {
-    const dim3 g(total), b(NT);
+void launch_role(const GemmParams &p, hipStream_t st) {
     switch (p.role) {
-        case ROLE_QKV: hipLaunchKernelGGL((k_gemm_split<ROLE_QKV, T, TERMS>), g, b, 0, st, p); break;
-        case ROLE_WO: hipLaunchKernelGGL((k_gemm_split<ROLE_WO, T, TERMS>), g, b, 0, st, p); break;
-        case ROLE_LMHEAD: hipLaunchKernelGGL((k_gemm_split<ROLE_LMHEAD, T, TERMS>), g, b, 0, st, p); break;
-        case ROLE_READOUT: hipLaunchKernelGGL((k_gemm_split<ROLE_READOUT, T, TERMS>), g, b, 0, st, p); break;
-        case ROLE_SCAN_PROJ: hipLaunchKernelGGL((k_gemm_split<ROLE_SCAN_PROJ, T, TERMS>), g, b, 0, st, p); break;
-        default: hipLaunchKernelGGL((k_gemm_split<ROLE_SIGNAL, T, TERMS>), g, b, 0, st, p); break;
+        case ROLE_QKV: launch_cfg<ROLE_QKV, T, TERMS>(p, st); break;
+        case ROLE_WO: launch_cfg<ROLE_WO, T, TERMS>(p, st); break;
+        case ROLE_LMHEAD: launch_cfg<ROLE_LMHEAD, T, TERMS>(p, st); break;
+        case ROLE_READOUT: launch_cfg<ROLE_READOUT, T, TERMS>(p, st); break;
+        case ROLE_SCAN_PROJ: launch_cfg<ROLE_SCAN_PROJ, T, TERMS>(p, st); break;
+        default: launch_cfg<ROLE_SIGNAL, T, TERMS>(p, st); break;
     }
 }
 
 }  // namespace
 
 void launch_gemm_split(const GemmParams &p, hipStream_t st) {
-    const int nM = (p.M + BM - 1) / BM, nN = (p.N + BN - 1) / BN;
-    const int total = nM * nN * p.S;
-    if (total <= 0) return;
     switch (p.prec) {
-        case PREC_BF16X3: launch_role<__bf16, 3>(p, total, st); break;
-        case PREC_BF16X1: launch_role<__bf16, 1>(p, total, st); break;
-        default: launch_role<_Float16, 3>(p, total, st); break;
+        case PREC_BF16X3: launch_role<__bf16, 3>(p, st); break;
+        case PREC_BF16X1: launch_role<__bf16, 1>(p, st); break;
+        default: launch_role<_Float16, 3>(p, st); break;
     }
 }
 

@@ -74,6 +74,8 @@ def main() -> int:
     ap.add_argument("--config", default="NS")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this size (calibrates HBM byte counters)")
     ap.add_argument("--gemm", choices=list(GEMM_MODES), default="f16x3",
                     help="GEMM arithmetic (f16x3 / bf16x3 / fp32 are fp32-accurate; bf16 is the "
                          "reduced-precision bf16-input variant)")
@@ -116,6 +118,12 @@ def main() -> int:
         scan_state=torch.empty((B, mc.H, mc.d, mc.N), dtype=torch.float32, device=dev),
     )
 
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         be.forward_async(tok_d, outputs=outs)
     torch.cuda.synchronize()
