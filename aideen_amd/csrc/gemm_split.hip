@@ -153,7 +153,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     // fragment chunk positions: rows r + 32t share swz(r) (the swizzles read row bits 1..3)
     const int pa0 = ((2 * hh) ^ swz_a(r)) * 4, pa1 = ((2 * hh + 1) ^ swz_a(r)) * 4;
     const int pb = (hh ^ swz_b(r)) * 8;
-    const float asc = p.a_scale;
+    float asc = p.a_scale, osc = p.out_scale;
+    if (p.a_absmax) {  // data-dependent A scale (power of two, never above the static one)
+        const float mx = __uint_as_float(*p.a_absmax);
+        if (mx > 0.0f) {
+            const float dyn = exp2f(floorf(log2f(p.a_headroom / mx)));
+            if (dyn < asc) {
+                osc *= asc / dyn;
+                asc = dyn;
+            }
+        }
+    }
     floatx16 acc[WTM][WTN];
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
@@ -210,7 +220,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     }
     lds_barrier();  // every wave is done with the ring before the epilogue reuses it
 
-    epilogue_t<WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, p.out_scale, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
+    epilogue_t<WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, osc, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
 }
 
 // Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi).

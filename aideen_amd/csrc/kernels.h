@@ -41,6 +41,11 @@ struct GemmParams {
     const void *Blo;
     float a_scale;       // A scaled by this power of two before the split
     float out_scale;     // accumulator scaled by this power of two (undoes both scales)
+    // Optional data-dependent A scale: with a_absmax set (bit pattern of max |A|, written by
+    // launch_absmax), the kernel uses min(a_scale, 2^floor(log2(a_headroom / max|A|))) and
+    // adjusts out_scale to match, so caller-supplied rows of any magnitude stay in range.
+    const unsigned *a_absmax;
+    float a_headroom;
 };
 constexpr int GEMM_BN = 128;
 void launch_gemm(const GemmParams &p, hipStream_t st);
@@ -121,5 +126,7 @@ void launch_gemv_colmajor(const float *w, const float *x, int in_dim, int out_di
 void launch_transpose(const float *src, int rows, int cols, long batch, float *dst,
                       hipStream_t st);
 void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
+// *out = bit pattern of max |x[i]| over n floats (atomic max; *out must be zeroed first)
+void launch_absmax(const float *x, long n, unsigned *out, hipStream_t st);
 
 }  // namespace adn

@@ -166,6 +166,22 @@ void launch_transpose(const float *src, int rows, int cols, long batch, float *d
     hipLaunchKernelGGL(k_transpose, grid, dim3(32, 8), 0, st, src, rows, cols, dst);
 }
 
+// max |x| as the bit pattern of a non-negative float (which orders like the float), one atomic
+// per wave.  NaN inputs compare above every finite value and propagate into the scale.
+__global__ void k_absmax(const float *x, long n, unsigned *out) {
+    unsigned m = 0;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+        m = max(m, __float_as_uint(fabsf(x[i])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, off, 64));
+    if ((threadIdx.x & 63) == 0 && m) atomicMax(out, m);
+}
+
+void launch_absmax(const float *x, long n, unsigned *out, hipStream_t st) {
+    const long blocks = std::min<long>((n + 255) / 256, 2048);
+    hipLaunchKernelGGL(k_absmax, dim3((unsigned)(blocks > 0 ? blocks : 1)), dim3(256), 0, st, x, n, out);
+}
+
 void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st) {
     const long blocks = (n + 255) / 256;
     hipLaunchKernelGGL(k_fill_i32, dim3((unsigned)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096)),

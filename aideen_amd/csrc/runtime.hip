@@ -65,6 +65,7 @@ struct adn_ctx {
     int32_t *argmax_scratch = nullptr;
     float *am_val = nullptr;      // [cap_tok][ceil(V/128)] LM-head tile arg-max partials
     int32_t *am_idx = nullptr;
+    unsigned *absmax = nullptr;   // max |s_in| (float bits) for the signal GEMM's A scale
     unsigned *d_err = nullptr;
 
     // host-API staging (lazy, capacity-sized)
@@ -264,6 +265,15 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
         g.epi = EPI_NONE;
         set_split(c, g, c->sp_in, c->embed_scale);
         Span sp(prof, ADN_STAGE_SIGNAL_GEMM, -1, st);
+        if (r.s_in && c->prec == PREC_F16X3) {
+            // caller-supplied rows: the A scale also honours their actual magnitude, so rows of
+            // any size stay inside the fp16 range (rows no larger than the embedding table's
+            // entries keep the embedding's scale, and match the token path bit for bit)
+            launch_fill_i32(reinterpret_cast<int32_t *>(c->absmax), 0, 1, st);
+            launch_absmax(r.s_in, (long)ntok * d, c->absmax, st);
+            g.a_absmax = c->absmax;
+            g.a_headroom = 1024.0f;
+        }
         launch_gemm(g, st);
     }
     {
@@ -524,6 +534,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         b.cnt_hist = (int32_t *)dmalloc(c, ADN_PROFILE_MAX_ITERS * sizeof(int32_t));
         b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
+        c->absmax = (unsigned *)dmalloc(c, sizeof(unsigned));
         b.err = c->d_err;
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
         c->pnorm = (float *)dmalloc(c, (size_t)T * d * sizeof(float));

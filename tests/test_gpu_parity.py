@@ -157,6 +157,24 @@ def test_s_in_path_equals_token_path():
     assert np.array_equal(p, a["pooled"].reshape(-1))
 
 
+def test_s_in_beyond_embedding_range(oracle_lib):
+    """s_in rows 4096x larger than every embedding entry: the fp16-split GEMM must rescale them
+    (a fixed embedding-derived scale would overflow fp16).  The oracle sees the same rows
+    through a table scaled by 4096, which it only uses to gather them."""
+    mc, w = _small(d=128, H=4, V=400, N=4, flags=synth.F_SCAN_SELECTIVE)
+    toks = synth.make_tokens("uniform", 2, 9, mc.V, seed=5)
+    big = dict(w)
+    big["embed"] = (w["embed"] * np.float32(4096)).astype(np.float32)
+    be = make(mc, 2, 9)
+    be.upload_weights(w)
+    got = be.forward(s_in=np.ascontiguousarray(big["embed"][toks]))
+    for k, v in got.items():
+        if v.dtype.kind == "f":
+            assert np.isfinite(v).all(), k
+    ref = oracle_lib.Oracle(mc, big).forward(toks)
+    assert_forward_parity(got, ref, "s_in x4096")
+
+
 def test_scan_state_continuation():
     mc, w = _small(d=128, H=4, V=400, N=16, flags=synth.F_SCAN_SELECTIVE)
     toks = synth.make_tokens("uniform", 2, 40, mc.V, seed=8)
