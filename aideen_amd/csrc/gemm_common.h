@@ -117,46 +117,51 @@ __device__ __forceinline__ void epilogue(const GemmParams &p, floatx16 (&acc)[2]
 // Generic epilogue: each wave holds WTM x WTN tiles of 32x32 (acc[i][j]); the workgroup is a
 // WGM x WGN grid of waves, block tile (WGM*WTM*32) x (WGN*WTN*32).  Per-row arg-max partials go
 // through `scratch_v/scratch_i` (>= WGN * block-rows entries of LDS free after the k loop).
-// The tile rows are walked by template recursion (I = 0..WTM-1) so that every accumulator index
-// is a compile-time constant: a runtime row loop leaves the accumulator array in scratch memory.
+// The epilogue mode (EPI), the arg-max (AM) and the bounds checks (CHECK: only edge tiles need
+// them) are compile-time, so an interior tile's epilogue is straight-line code: scale, bias,
+// store.  The tile rows are walked by template recursion (I = 0..WTM-1) so that every
+// accumulator index is a compile-time constant: a runtime row loop leaves the accumulator
+// array in scratch memory.
 struct EpiCtx {
     int M, s, m0, n0, wm, wn, r, hh;
     float osc;  // accumulator scale (undoes the power-of-two operand scaling)
-    bool want_am;
     float *scratch_v;
     int *scratch_i;
 };
 
-template <int I, int WTM, int WTN, int WGM>
+template <int I, int WTM, int WTN, int WGM, int EPI, bool AM, bool CHECK>
 __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c,
                                          const float (&bj)[WTN], const bool (&nv)[WTN]) {
     constexpr int BMt = WGM * WTM * 32;
+    const int ncol0 = c.n0 + c.wn * WTN * 32 + c.r;  // column of j = 0
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int ml = (c.wm * WTM + I) * 32 + 8 * (e >> 2) + 4 * c.hh + (e & 3);
         const int m = c.m0 + ml;
-        const bool mv = m < c.M;
-        float *crow = p.C + (long)m * p.c_sm + (long)c.s * p.c_ss;
-        const float *res_row = p.A + (long)m * p.a_sm + (long)c.s * p.a_ss;
+        const bool mv = !CHECK || m < c.M;
+        float *crow = p.C + (long)m * p.c_sm + (long)c.s * p.c_ss + ncol0;
         float bv = -INFINITY;
         int bi = -1;
 #pragma unroll
         for (int j = 0; j < WTN; ++j) {
-            const int n = c.n0 + (c.wn * WTN + j) * 32 + c.r;
+            const bool ok = !CHECK || (mv && nv[j]);
             float v = acc[I][j][e] * c.osc;
-            if (p.epi == EPI_BIAS)
-                v += bj[j];
-            else if (p.epi == EPI_ADD_A && mv && nv[j])
-                v = res_row[n] + v;
-            if (mv && nv[j]) {
-                crow[n] = v;
-                if (v > bv || (v == bv && n > bi)) {
-                    bv = v;
-                    bi = n;
+            if constexpr (EPI == EPI_BIAS) v += bj[j];
+            if constexpr (EPI == EPI_ADD_A) {
+                if (ok) v = p.A[(long)m * p.a_sm + (long)c.s * p.a_ss + ncol0 + 32 * j] + v;
+            }
+            if (ok) {
+                crow[32 * j] = v;
+                if constexpr (AM) {
+                    const int n = ncol0 + 32 * j;
+                    if (v > bv || (v == bv && n > bi)) {
+                        bv = v;
+                        bi = n;
+                    }
                 }
             }
         }
-        if (c.want_am) {
+        if constexpr (AM) {
 #pragma unroll
             for (int off = 16; off > 0; off >>= 1) {
                 const float v2 = __shfl_xor(bv, off, 64);
@@ -172,44 +177,42 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
             }
         }
     }
-    if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM>(p, acc, c, bj, nv);
+    if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM, EPI, AM, CHECK>(p, acc, c, bj, nv);
 }
 
-template <int WTM, int WTN, int WGM, int WGN>
-__device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[WTM][WTN], int M, int s,
-                                           int m0, int n0, float osc, float *scratch_v, int *scratch_i) {
+template <int WTM, int WTN, int WGM, int WGN, int EPI, bool AM, bool CHECK>
+__device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c) {
     constexpr int BMt = WGM * WTM * 32;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    EpiCtx c{M, s, m0, n0, wave / WGN, wave % WGN, lane & 31, lane >> 5, osc, p.am_val != nullptr, scratch_v,
-             scratch_i};
     float bj[WTN];
     bool nv[WTN];
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
-        const int n = n0 + (c.wn * WTN + j) * 32 + c.r;
-        nv[j] = n < p.N;
-        bj[j] = (p.epi == EPI_BIAS && nv[j] && n < p.bias_n) ? p.bias[(long)s * p.bias_ss + n] : 0.0f;
+        const int n = c.n0 + (c.wn * WTN + j) * 32 + c.r;
+        nv[j] = !CHECK || n < p.N;
+        bj[j] = 0.0f;
+        if constexpr (EPI == EPI_BIAS)
+            if (nv[j] && n < p.bias_n) bj[j] = p.bias[(long)c.s * p.bias_ss + n];
     }
-    epi_rows<0, WTM, WTN, WGM>(p, acc, c, bj, nv);
-    if (c.want_am) {
+    epi_rows<0, WTM, WTN, WGM, EPI, AM, CHECK>(p, acc, c, bj, nv);
+    if constexpr (AM) {
         // partials are per 128 columns: waves covering 64 columns are combined in pairs
         constexpr int CPW = WTN * 32;
         static_assert(CPW == 64 || CPW == 128, "arg-max partials need 64 or 128 columns per wave");
         constexpr int TPW = 128 / CPW;
         constexpr int QT = WGN / TPW;  // 128-column tiles per block
         __syncthreads();
+        const int tid = threadIdx.x;
         for (int idx = tid; idx < BMt * QT; idx += 64 * WGM * WGN) {
             const int ml = idx % BMt, q = idx / BMt;
-            const int m = m0 + ml;
-            const int tile = (n0 >> 7) + q;
-            if (m < M && tile * 128 < p.N) {
-                float v = scratch_v[q * TPW * BMt + ml];
-                int ix = scratch_i[q * TPW * BMt + ml];
+            const int m = c.m0 + ml;
+            const int tile = (c.n0 >> 7) + q;
+            if (m < c.M && tile * 128 < p.N) {
+                float v = c.scratch_v[q * TPW * BMt + ml];
+                int ix = c.scratch_i[q * TPW * BMt + ml];
 #pragma unroll
                 for (int w = 1; w < TPW; ++w) {
-                    const float v2 = scratch_v[(q * TPW + w) * BMt + ml];
-                    const int i2 = scratch_i[(q * TPW + w) * BMt + ml];
+                    const float v2 = c.scratch_v[(q * TPW + w) * BMt + ml];
+                    const int i2 = c.scratch_i[(q * TPW + w) * BMt + ml];
                     if (v2 > v || (v2 == v && i2 > ix)) {
                         v = v2;
                         ix = i2;
@@ -218,6 +221,63 @@ __device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[
                 p.am_val[(long)tile * p.M + m] = v;  // [tile][row]: coalesced across rows
                 p.am_idx[(long)tile * p.M + m] = ix;
             }
+        }
+    }
+}
+
+// Epilogue dispatch for one GEMM role: the modes a role can use are compiled for it, each in a
+// checked (edge tile) and an unchecked (interior tile) form.
+template <int ROLE, int WTM, int WTN, int WGM, int WGN>
+__device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[WTM][WTN], int M, int s,
+                                           int m0, int n0, float osc, float *scratch_v, int *scratch_i) {
+    constexpr int BMt = WGM * WTM * 32, BNt = WGN * WTN * 32;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const EpiCtx c{M, s, m0, n0, wave / WGN, wave % WGN, lane & 31, lane >> 5, osc, scratch_v, scratch_i};
+    const bool interior = m0 + BMt <= M && n0 + BNt <= p.N;
+    if constexpr (ROLE == ROLE_READOUT) {
+        if (interior)
+            epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, false>(p, acc, c);
+        else
+            epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, true>(p, acc, c);
+    } else if constexpr (ROLE == ROLE_LMHEAD) {
+        // the arg-max branch and the bias branch are uniform over the grid
+        if (p.am_val) {
+            if (p.epi == EPI_BIAS) {
+                if (interior)
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, false>(p, acc, c);
+                else
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, true>(p, acc, c);
+            } else {
+                if (interior)
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, false>(p, acc, c);
+                else
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, true>(p, acc, c);
+            }
+        } else {
+            if (p.epi == EPI_BIAS) {
+                if (interior)
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false>(p, acc, c);
+                else
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, true>(p, acc, c);
+            } else {
+                if (interior)
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false>(p, acc, c);
+                else
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true>(p, acc, c);
+            }
+        }
+    } else {
+        if (p.epi == EPI_BIAS) {
+            if (interior)
+                epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false>(p, acc, c);
+            else
+                epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, true>(p, acc, c);
+        } else {
+            if (interior)
+                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false>(p, acc, c);
+            else
+                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true>(p, acc, c);
         }
     }
 }

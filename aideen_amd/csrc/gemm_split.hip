@@ -220,7 +220,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     }
     lds_barrier();  // every wave is done with the ring before the epilogue reuses it
 
-    epilogue_t<WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, osc, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
+    epilogue_t<ROLE, WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, osc, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
 }
 
 // Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi).
