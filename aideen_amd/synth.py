@@ -222,6 +222,27 @@ def make_weights(cfg: ModelConfig, seed: int = 0, gates_seed: int = 2,
     return w
 
 
+def make_hist_weights(cfg: ModelConfig, seed: int = 0, strong: bool = False) -> Dict[str, np.ndarray]:
+    """Weights of the memory-coupled solve, following the reference's initial values
+    (FPMR:279 w_hist_shared = 0.15 I + U(+-0.01); FPMR:312-318 hist_slot_scale = centred slot *
+    5e-5 + U(+-1e-4); FPMR:327-333 hist_gate_logit = -1.204 + centred slot * 0.02).  ``strong``
+    widens hist_slot_scale to U(+-0.5) and the gate logits to U(-2, 2) so that every term of
+    the history context matters in tests.  Kept apart from make_weights so that the digests of
+    existing fixtures do not change."""
+    d, H = cfg.d, cfg.H
+    centred = (np.arange(H, dtype=np.float32) - np.float32((H - 1) * 0.5))[:, None]
+    w_hist = (np.eye(d, dtype=np.float32) * np.float32(0.15)
+              + uniform(seed, "w_hist_shared", (d, d), -0.01, 0.01))
+    if strong:
+        scale = uniform(seed, "hist_slot_scale", (H, d), -0.5, 0.5)
+        gate = uniform(seed, "hist_gate_logit", (H,), -2.0, 2.0)
+    else:
+        scale = centred * np.float32(5e-5) + uniform(seed, "hist_slot_scale", (H, d), -1e-4, 1e-4)
+        gate = (np.float32(-1.204) + centred[:, 0] * np.float32(0.02)).astype(np.float32)
+    return {"w_hist": w_hist.astype(np.float32), "hist_slot_scale": scale.astype(np.float32),
+            "hist_gate_logit": gate.astype(np.float32)}
+
+
 def make_tokens(kind: str, B: int, T: int, vocab: int, seed: int = 1) -> np.ndarray:
     if kind == "zipf":
         return zipf_tokens(seed, "tokens", B * T, vocab).reshape(B, T)

@@ -225,9 +225,10 @@ static void init_p(const prep *p, const float *x, const float *signal, float *h0
 }
 
 /* FPMR:1397-1424 cross_slot_attn followed by FPMR:1372-1395 step_with_fixed_hist_ctx
- * (hist = 0, FPMR:1450-1453), FPMR:1300-1303 rms_norm and spectral_norm.rs:93 damped_update. */
-static void step_p(const prep *p, scratch *sc, const float *h, const float *signal, float *h_next,
-                   float *attn_out) {
+ * (hist = NULL is the zero context of FPMR:1450-1453), FPMR:1300-1303 rms_norm and
+ * spectral_norm.rs:93 damped_update. */
+static void step_p(const prep *p, scratch *sc, const float *h, const float *signal,
+                   const float *hist, float *h_next, float *attn_out) {
     const int d = p->c.d, H = p->c.H;
     const orc_weights *w = p->w;
     const size_t mat = (size_t)d * d;
@@ -268,16 +269,18 @@ static void step_p(const prep *p, scratch *sc, const float *h, const float *sign
         /* combined = attn + signal + hist(0) + anchor; f = g*c/rms (FPMR:1386-1391) */
         const float *sg = signal + (size_t)a * d;
         const float *an = w->anchor + (size_t)a * d;
+        const float *hc = hist ? hist + (size_t)a * d : NULL;
         float ss = 0.0f;
         if (p->c.flags & ORC_F_RMS_EXCL_ANCHOR) {
             for (int i = 0; i < d; ++i) {
-                const float as_ = sc->o[i] + sg[i];
+                const float as_ = (sc->o[i] + sg[i]) + (hc ? hc[i] : 0.0f);
                 ss += as_ * as_;
                 sc->comb[i] = as_ + an[i];
             }
         } else {
+            /* combined = attn + input_signal + hist_k, then + slot_bias (FPMR:1386-1389) */
             for (int i = 0; i < d; ++i) {
-                sc->comb[i] = ((sc->o[i] + sg[i]) + 0.0f) + an[i];
+                sc->comb[i] = ((sc->o[i] + sg[i]) + (hc ? hc[i] : 0.0f)) + an[i];
                 ss += sc->comb[i] * sc->comb[i];
             }
         }
@@ -380,7 +383,8 @@ void orc_anderson_coeffs(int n, const float *g_in, float *beta) {
  * of updates applied.  Converged tokens are frozen.  Optional Anderson mixing after each step
  * (staged_adjoint_picard_clean.wgsl:1012-1134, gpu_deq.rs:4278-4293): the ring stores the
  * un-mixed Picard iterate; mixing starts at k >= 2 with n_res = min(k, m-1) >= 2. */
-static int solve_p(const prep *p, scratch *sc, const float *x, float *h, float *resid_trace) {
+static int solve_p(const prep *p, scratch *sc, const float *x, const float *hist, float *h,
+                   float *resid_trace) {
     const orc_cfg *c = &p->c;
     const int d = c->d, H = c->H;
     const size_t hd = (size_t)H * d;
@@ -390,7 +394,7 @@ static int solve_p(const prep *p, scratch *sc, const float *x, float *h, float *
     int iters = 0;
     const int m = c->anderson_m;
     for (int k = 0; k < c->max_iters; ++k) {
-        step_p(p, sc, h, signal, sc->hn, NULL);
+        step_p(p, sc, h, signal, hist, sc->hn, NULL);
         const float r = residual(c, sc->hn, h);
         if (resid_trace) resid_trace[k] = r;
         iters = k + 1;
@@ -456,7 +460,7 @@ void orc_picard_step(const orc_cfg *c, const orc_weights *w, const float *h, con
     scratch sc;
     prep_init(&p, c, w);
     scratch_init(&sc, c);
-    step_p(&p, &sc, h, signal, h_next, attn);
+    step_p(&p, &sc, h, signal, NULL, h_next, attn);
     scratch_free(&sc);
     prep_free(&p);
 }
@@ -467,7 +471,7 @@ int orc_solve_token(const orc_cfg *c, const orc_weights *w, const float *x, floa
     scratch sc;
     prep_init(&p, c, w);
     scratch_init(&sc, c);
-    int it = solve_p(&p, &sc, x, h_star, resid_trace);
+    int it = solve_p(&p, &sc, x, NULL, h_star, resid_trace);
     scratch_free(&sc);
     prep_free(&p);
     return it;
@@ -707,7 +711,7 @@ void orc_model_forward(orc_model *mdl, int B, int T, const int32_t *tokens, floa
         for (long t = 0; t < ntok; ++t) {
             const int32_t tok = tokens[t];
             float *h = hs_all + hd * t;
-            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, h, NULL);
+            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, NULL, h, NULL);
             if (iters) iters[t] = it;
             if (pooled || logits || argmax) {
                 float *lt = logits ? logits + (size_t)V * t : lg;
@@ -741,6 +745,146 @@ void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int
     orc_model_forward(m, B, T, tokens, h_star, pooled, logits, iters, argmax, scan_y, scan_state,
                       nthreads);
     orc_model_free(m);
+}
+
+/* ------------------------------------------------------------------------- */
+/* memory-coupled solve (fixed history context)                               */
+/* ------------------------------------------------------------------------- */
+
+/* FPMR:1317-1329: alpha_k = 0.07 + (0.20 - 0.07) * sigmoid(hist_gate_logit[k]). */
+static float hist_gate_alpha(const orc_hist_weights *hw, int k) {
+    const float sigma = 1.0f / (1.0f + expf(-hw->gate_logit[k]));
+    return 0.070f + (0.20f - 0.070f) * sigma;
+}
+
+/* FPMR:1337-1370 fixed_hist_ctx, with the input-signal RMS taken per slot (the reference has one
+ * shared W_in, so its signal is the same for every slot; per-slot W_in generalises it).
+ *   u_k = W_hist m_k + slot_scale_k * m_k / rms(m_k);  hist_k = u_k * (alpha_k * min(1, rms(sig_k)/rms(u_k)))
+ * (scale 1 when rms(u_k) <= 1e-6).  m_prev == NULL gives the zero context. */
+void orc_hist_ctx(const orc_cfg *c, const orc_hist_weights *hw, const float *m_prev,
+                  const float *signal, float *hist) {
+    const int d = c->d, H = c->H;
+    if (!m_prev) {
+        memset(hist, 0, sizeof(float) * (size_t)H * d);
+        return;
+    }
+    float *u = (float *)malloc(sizeof(float) * d);
+    for (int k = 0; k < H; ++k) {
+        const float *sg = signal + (size_t)k * d;
+        const float *pm = m_prev + (size_t)k * d;
+        float ss = 0.0f;
+        for (int i = 0; i < d; ++i) ss += sg[i] * sg[i];
+        const float inj_rms = sqrtf(ss / (float)d + 1e-6f);
+        float sp = 0.0f;
+        for (int i = 0; i < d; ++i) sp += pm[i] * pm[i];
+        const float prev_rms = sqrtf(sp / (float)d + 1e-6f);
+        gemv_rm(hw->w_hist, d, d, pm, u);
+        const float *sc = hw->slot_scale + (size_t)k * d;
+        for (int i = 0; i < d; ++i) u[i] += sc[i] * (pm[i] / prev_rms);
+        float su = 0.0f;
+        for (int i = 0; i < d; ++i) su += u[i] * u[i];
+        const float u_rms = sqrtf(su / (float)d + 1e-6f);
+        const float scale = u_rms > 1e-6f ? fminf(inj_rms / u_rms, 1.0f) : 1.0f;
+        const float g = hist_gate_alpha(hw, k) * scale;
+        for (int i = 0; i < d; ++i) hist[(size_t)k * d + i] = u[i] * g;
+    }
+    free(u);
+}
+
+/* FPMR:1454-1485 temporal_step: m_next = (I + W_out)(abar m + (1 - abar) x), x = u(1 + 0.5 tanh wx),
+ * u = h/rms(h), abar = sigmoid(-a_log) (or the selective decay when the flag is set).
+ * m_prev == NULL is the zero state. */
+void orc_temporal_step(const orc_cfg *c, const orc_weights *w, const float *m_prev,
+                       const float *h_star, float *m_next) {
+    const int d = c->d, H = c->H, r = c->r > 0 ? c->r : 1;
+    float *x = (float *)malloc(sizeof(float) * d);
+    float *ab = (float *)malloc(sizeof(float) * d);
+    float *mn = (float *)malloc(sizeof(float) * d);
+    float *wy = (float *)malloc(sizeof(float) * d);
+    float *bn = (float *)malloc(sizeof(float) * r);
+    float Bv[1], Cv[1];
+    orc_cfg c1 = *c;
+    c1.N = 1;
+    orc_weights w1 = *w;
+    w1.w_b = NULL;
+    w1.w_c = NULL;
+    for (int s = 0; s < H; ++s) {
+        carrier_inputs(&c1, &w1, s, h_star + (size_t)s * d, x, ab, Bv, Cv, bn);
+        const float *m = m_prev ? m_prev + (size_t)s * d : NULL;
+        for (int i = 0; i < d; ++i) mn[i] = ab[i] * (m ? m[i] : 0.0f) + (1.0f - ab[i]) * x[i];
+        float *out = m_next + (size_t)s * d;
+        if (w->w_out) {
+            gemv_rm(w->w_out + (size_t)s * d * d, d, d, mn, wy);
+            for (int i = 0; i < d; ++i) out[i] = mn[i] + wy[i];
+        } else {
+            memcpy(out, mn, sizeof(float) * d);
+        }
+    }
+    free(x); free(ab); free(mn); free(wy); free(bn);
+}
+
+/* Memory-coupled forward, the fixed-history reference mode of the trainer (TRAINER:677-720):
+ * per sequence and token, hist = fixed_hist_ctx(m_{t-1}, signal_t) (zero at the first token
+ * unless m_in is given), h* = the Picard solve with hist added (FPMR:1372-1395), then
+ * m_t = temporal_step(m_{t-1}, h*).  The solve keeps this library's exit rule (eps = 0 runs
+ * exactly max_iters steps, as solve_query_with_fixed_history does).  m_seq [B][T][H][d] receives
+ * every m_t; pooled/logits/argmax as in the canonical forward. */
+void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B,
+                        int T, const int32_t *tokens, const float *m_in, float *h_star, float *pooled,
+                        float *logits, int32_t *iters, int32_t *argmax, float *m_seq, int nthreads) {
+    const int d = c->d, H = c->H, V = c->V;
+    const size_t hd = (size_t)H * d;
+    prep p;
+    prep_init(&p, c, w);
+    float *lm_wt = (float *)malloc(sizeof(float) * (size_t)V * d);
+    transpose(w->lm_w, V, d, lm_wt);
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        scratch sc;
+        scratch_init(&sc, c);
+        float *sig = (float *)malloc(sizeof(float) * hd);
+        float *hist = (float *)malloc(sizeof(float) * hd);
+        float *h = (float *)malloc(sizeof(float) * hd);
+        float *m = (float *)malloc(sizeof(float) * hd);
+        float *mn = (float *)malloc(sizeof(float) * hd);
+        float *tmp = (float *)malloc(sizeof(float) * d);
+        float *lg = (float *)malloc(sizeof(float) * V);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int b = 0; b < B; ++b) {
+            int have_m = 0;
+            if (m_in) {
+                memcpy(m, m_in + hd * b, sizeof(float) * hd);
+                have_m = 1;
+            }
+            for (int t = 0; t < T; ++t) {
+                const size_t row = (size_t)b * T + t;
+                const float *x = w->embed + (size_t)tokens[row] * d;
+                signal_p(&p, x, sig);
+                orc_hist_ctx(c, hw, have_m ? m : NULL, sig, hist);
+                const int it = solve_p(&p, &sc, x, hist, h, NULL);
+                if (iters) iters[row] = it;
+                if (h_star) memcpy(h_star + hd * row, h, sizeof(float) * hd);
+                orc_temporal_step(c, w, have_m ? m : NULL, h, mn);
+                memcpy(m, mn, sizeof(float) * hd);
+                have_m = 1;
+                if (m_seq) memcpy(m_seq + hd * row, m, sizeof(float) * hd);
+                if (pooled || logits || argmax) {
+                    float *lt = logits ? logits + (size_t)V * row : lg;
+                    lm_head_tok(c, w, lm_wt, h, pooled ? pooled + (size_t)d * row : NULL, lt, tmp);
+                    if (argmax) argmax[row] = orc_argmax(lt, V);
+                }
+            }
+        }
+        free(sig); free(hist); free(h); free(m); free(mn); free(tmp); free(lg);
+        scratch_free(&sc);
+    }
+    free(lm_wt);
+    prep_free(&p);
 }
 
 /* Greedy decode (TRAINER:4219-4431 loop with LmHead::sample at temperature <= 1e-4 =

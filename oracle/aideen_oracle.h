@@ -81,6 +81,21 @@ void orc_scan_seq(const orc_cfg *c, const orc_weights *w, int T, const float *h_
 void orc_scan_recirculate(const orc_cfg *c, const orc_weights *w, int T, const float *h_star,
                           const float *m_in, float *y);
 
+/* --- memory-coupled solve (FPMR:1317-1370, 1454-1485; TRAINER:677-720) ---- */
+typedef struct orc_hist_weights {
+    const float *w_hist;     /* [d][d] shared W_hist, row-major (u = W_hist m)  */
+    const float *slot_scale; /* [H][d] hist_slot_scale                          */
+    const float *gate_logit; /* [H]    hist_gate_logit                          */
+} orc_hist_weights;
+void orc_hist_ctx(const orc_cfg *c, const orc_hist_weights *hw, const float *m_prev /* [H][d] or NULL */,
+                  const float *signal /* [H][d] */, float *hist /* [H][d] */);
+void orc_temporal_step(const orc_cfg *c, const orc_weights *w, const float *m_prev /* or NULL */,
+                       const float *h_star, float *m_next);
+void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B,
+                        int T, const int32_t *tokens, const float *m_in /* [B][H][d] or NULL */,
+                        float *h_star, float *pooled, float *logits, int32_t *iters,
+                        int32_t *argmax, float *m_seq /* [B][T][H][d] */, int nthreads);
+
 /* --- whole forward and decode ----------------------------------------------- */
 void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
                  float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,

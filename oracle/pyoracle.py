@@ -34,6 +34,14 @@ class OrcWeights(C.Structure):
     _fields_ = [(n, F32P) for n in WEIGHT_FIELDS]
 
 
+# memory-coupled solve weights (FPMR w_hist_shared, hist_slot_scale, hist_gate_logit)
+HIST_FIELDS = [("w_hist", "w_hist"), ("slot_scale", "hist_slot_scale"), ("gate_logit", "hist_gate_logit")]
+
+
+class OrcHistWeights(C.Structure):
+    _fields_ = [(n, F32P) for n, _ in HIST_FIELDS]
+
+
 def build(quiet: bool = True) -> None:
     subprocess.run(["make", "-s", "-C", HERE], check=True,
                    stdout=subprocess.DEVNULL if quiet else None)
@@ -73,6 +81,11 @@ def lib():
         L.orc_model_free.argtypes = [C.c_void_p]
         L.orc_decode_greedy.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, I32P,
                                         C.c_int, I32P, C.c_int]
+        L.orc_hist_ctx.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcHistWeights), F32P, F32P, F32P]
+        L.orc_temporal_step.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
+        L.orc_forward_memory.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcHistWeights),
+                                         C.c_int, C.c_int, I32P, F32P, F32P, F32P, F32P, I32P, I32P,
+                                         F32P, C.c_int]
         L.orc_zoh_step.argtypes = [C.c_int, F32P, F32P, F32P, F32P, F32P, F32P]
         L.orc_gemv_colmajor.argtypes = [F32P, F32P, C.c_int, C.c_int, F32P]
         _lib = L
@@ -103,6 +116,7 @@ class Oracle:
         self._keep = {k: (None if v is None else np.ascontiguousarray(v, dtype=np.float32))
                       for k, v in weights.items()}
         self.w = OrcWeights(**{k: fp(self._keep.get(k)) for k in WEIGHT_FIELDS})
+        self.hw = OrcHistWeights(**{n: fp(self._keep.get(k)) for n, k in HIST_FIELDS})
         self.L = lib()
 
     # --- per-token pieces -------------------------------------------------
@@ -156,6 +170,38 @@ class Oracle:
                                     fp(None if m_in is None else np.ascontiguousarray(m_in, np.float32)),
                                     fp(y))
         return y
+
+    # --- memory-coupled solve ------------------------------------------------
+    def hist_ctx(self, m_prev, signal):
+        out = np.zeros((self.mc.H, self.mc.d), np.float32)
+        self.L.orc_hist_ctx(C.byref(self.c), C.byref(self.hw),
+                            fp(None if m_prev is None else np.ascontiguousarray(m_prev, np.float32)),
+                            fp(np.ascontiguousarray(signal, np.float32)), fp(out))
+        return out
+
+    def temporal_step(self, m_prev, h_star):
+        out = np.zeros((self.mc.H, self.mc.d), np.float32)
+        self.L.orc_temporal_step(C.byref(self.c), C.byref(self.w),
+                                 fp(None if m_prev is None else np.ascontiguousarray(m_prev, np.float32)),
+                                 fp(np.ascontiguousarray(h_star, np.float32)), fp(out))
+        return out
+
+    def forward_memory(self, tokens, m_in=None, nthreads=0):
+        """Memory-coupled forward; returns h_star, pooled, logits, argmax, iters and m_seq (every
+        carrier state m_t)."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, T = tokens.shape
+        mc = self.mc
+        out = dict(h_star=np.zeros((B, T, mc.H, mc.d), np.float32),
+                   pooled=np.zeros((B, T, mc.d), np.float32),
+                   logits=np.zeros((B, T, mc.V), np.float32),
+                   iters=np.zeros((B, T), np.int32), argmax=np.zeros((B, T), np.int32),
+                   m_seq=np.zeros((B, T, mc.H, mc.d), np.float32))
+        self.L.orc_forward_memory(C.byref(self.c), C.byref(self.w), C.byref(self.hw), B, T, ip(tokens),
+                                  fp(None if m_in is None else np.ascontiguousarray(m_in, np.float32)),
+                                  fp(out["h_star"]), fp(out["pooled"]), fp(out["logits"]),
+                                  ip(out["iters"]), ip(out["argmax"]), fp(out["m_seq"]), nthreads)
+        return out
 
     # --- whole forward ------------------------------------------------------
     def forward(self, tokens, want_logits=True, want_scan=True, nthreads=0):

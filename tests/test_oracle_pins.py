@@ -483,3 +483,120 @@ def test_forward_is_per_token_solve_plus_head(oracle_lib):
         assert np.array_equal(y, out["scan_y"][b]) and np.array_equal(st, out["scan_state"][b])
     dec = o.decode_greedy(toks[:, 0], 3)
     assert dec[0, 0] == out["argmax"][0, 0]
+
+
+# ------------------------------------------------------------------------------------------
+# memory-coupled solve: FPMR:1317-1370 fixed_hist_ctx, FPMR:1454-1485 temporal_step,
+# TRAINER:677-720 fixed-history driver
+# ------------------------------------------------------------------------------------------
+def _mem_model(d=16, H=3, V=40, strong=True, **kw):
+    mc, w = small_model(d=d, H=H, V=V, **kw)
+    w = dict(w)
+    w.update(synth.make_hist_weights(mc, seed=11, strong=strong))
+    return mc, w
+
+
+def _alpha(logit):
+    return 0.07 + 0.13 / (1.0 + np.exp(-np.float64(logit)))
+
+
+def test_hist_ctx_is_zero_without_memory(oracle_lib):
+    # FPMR:1534-1545 fixed_hist_ctx_is_zero_without_memory
+    mc, w = _mem_model()
+    o = oracle(oracle_lib, mc, w)
+    sig = np.random.default_rng(0).standard_normal((mc.H, mc.d)).astype(np.float32)
+    assert np.array_equal(o.hist_ctx(None, sig), np.zeros((mc.H, mc.d), np.float32))
+
+
+def test_hist_ctx_orientation_gate_and_clamp(oracle_lib):
+    """m_prev = a basis vector e_j per slot: u = W_hist[:, j] + scale[:, j]-weighted e_j/rms(e_j)
+    singles out column j (a transposed W_hist would give row j); the gate alpha and the
+    min(1, rms(signal)/rms(u)) clamp follow in closed form for a small and a large signal."""
+    d, H = 12, 3
+    mc, w = _mem_model(d=d, H=H)
+    rng = np.random.default_rng(3)
+    w["w_hist"] = rng.standard_normal((d, d)).astype(np.float32)  # asymmetric
+    o = oracle(oracle_lib, mc, w)
+    js = [1, 5, 9]
+    m = np.zeros((H, d), np.float32)
+    for k, j in enumerate(js):
+        m[k, j] = 2.0
+    for sig_amp in (1e-3, 1e3):
+        sig = (sig_amp * rng.standard_normal((H, d))).astype(np.float32)
+        got = o.hist_ctx(m, sig).astype(np.float64)
+        for k, j in enumerate(js):
+            prev_rms = np.sqrt(4.0 / d + 1e-6)
+            u = 2.0 * w["w_hist"][:, j].astype(np.float64)
+            u[j] += w["hist_slot_scale"][k, j] * 2.0 / prev_rms
+            u_rms = np.sqrt((u * u).mean() + 1e-6)
+            inj = np.sqrt((sig[k].astype(np.float64) ** 2).mean() + 1e-6)
+            ref = u * _alpha(w["hist_gate_logit"][k]) * min(inj / u_rms, 1.0)
+            np.testing.assert_allclose(got[k], ref, rtol=2e-5, atol=1e-7)
+            # the transposed operand would differ
+            assert not np.allclose(got[k], 2.0 * w["w_hist"][j] * _alpha(w["hist_gate_logit"][k]), rtol=1e-2)
+
+
+def test_zero_hist_step_and_first_token_match_the_plain_solve(oracle_lib):
+    """FPMR:1547-1562 zero_fixed_hist_ctx_matches_plain_step, through the whole driver: the first
+    token has no memory, so its solve is the canonical one even with nonzero history weights; with
+    W_hist = 0 and slot_scale = 0 every token's history is zero (u = 0, scale 1) and the memory
+    forward reduces to the canonical solve plus the recirculating carrier."""
+    mc, w = _mem_model(d=16, H=3, V=40, eps=0.0, max_iters=12)
+    o = oracle(oracle_lib, mc, w)
+    toks = synth.make_tokens("uniform", 2, 6, mc.V, seed=9)
+    out = o.forward_memory(toks)
+    for b in range(2):
+        h, it, _ = o.solve(w["embed"][toks[b, 0]])
+        assert it == out["iters"][b, 0] == mc.max_iters
+        assert np.array_equal(h, out["h_star"][b, 0])
+    # with history, later tokens differ from the canonical solve
+    h5, _, _ = o.solve(w["embed"][toks[0, 5]])
+    assert np.abs(h5 - out["h_star"][0, 5]).max() > 1e-4
+    w0 = dict(w)
+    w0["w_hist"] = np.zeros_like(w["w_hist"])
+    w0["hist_slot_scale"] = np.zeros_like(w["hist_slot_scale"])
+    o0 = oracle(oracle_lib, mc, w0)
+    out0 = o0.forward_memory(toks)
+    canon = o0.forward(toks)
+    assert np.array_equal(out0["h_star"], canon["h_star"])
+    assert np.array_equal(out0["logits"], canon["logits"])
+    for b in range(2):
+        assert np.array_equal(out0["m_seq"][b], o0.scan_recirculate(canon["h_star"][b]))
+
+
+def test_temporal_step_closed_form(oracle_lib):
+    """W_out = 0, W_x = 0: m' = abar m + (1 - abar) h/rms(h), abar = sigmoid(-a_log) (FPMR:1465-1479);
+    with W_out the output is (I + W_out) of that (FPMR:1481-1482)."""
+    mc, w = _mem_model(d=16, H=2)
+    rng = np.random.default_rng(5)
+    h = rng.standard_normal((mc.H, mc.d)).astype(np.float32)
+    m = rng.standard_normal((mc.H, mc.d)).astype(np.float32)
+    w0 = dict(w)
+    w0["w_out"] = None
+    w0["wx_diag"] = np.zeros_like(w["wx_diag"])
+    got = oracle(oracle_lib, mc, w0).temporal_step(m, h).astype(np.float64)
+    h64 = h.astype(np.float64)
+    u = h64 / np.sqrt((h64 * h64).mean(1, keepdims=True) + 1e-6)
+    a = 1 / (1 + np.exp(w["a_log"].astype(np.float64)))
+    inner = a * m + (1 - a) * u
+    np.testing.assert_allclose(got, inner, rtol=1e-5, atol=1e-6)
+    got2 = oracle(oracle_lib, mc, dict(w0, w_out=w["w_out"])).temporal_step(m, h).astype(np.float64)
+    ref2 = inner + np.einsum("sij,sj->si", w["w_out"].astype(np.float64), inner)
+    np.testing.assert_allclose(got2, ref2, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(oracle(oracle_lib, mc, w0).temporal_step(None, h),
+                          oracle(oracle_lib, mc, w0).temporal_step(np.zeros_like(m), h))
+
+
+def test_memory_forward_continuation_and_independence(oracle_lib):
+    """Splitting a sequence and passing the carrier state reproduces the whole run bit for bit;
+    sequences of a batch do not interact."""
+    mc, w = _mem_model(d=16, H=3, V=40, eps=1e-5, max_iters=15)
+    o = oracle(oracle_lib, mc, w)
+    toks = synth.make_tokens("uniform", 3, 9, mc.V, seed=2)
+    full = o.forward_memory(toks)
+    a = o.forward_memory(toks[:, :4])
+    b = o.forward_memory(toks[:, 4:], m_in=a["m_seq"][:, -1])
+    for k in ("h_star", "m_seq", "logits", "iters"):
+        assert np.array_equal(np.concatenate([a[k], b[k]], axis=1), full[k]), k
+    rev = o.forward_memory(toks[::-1].copy())
+    assert np.array_equal(rev["h_star"], full["h_star"][::-1])
