@@ -34,7 +34,7 @@ class AdnConfig(C.Structure):
 
 WEIGHT_FIELDS = ["w_q", "w_k", "w_v", "w_o", "w_in", "q_bias", "k_bias", "anchor", "norm_scale",
                  "embed", "lm_w", "lm_b", "lm_g", "a_log", "wx_diag", "w_out", "b_delta", "w_kw",
-                 "w_vw", "w_b", "w_c"]
+                 "w_vw", "w_b", "w_c", "w_hist", "hist_slot_scale", "hist_gate_logit"]
 
 
 class AdnWeights(C.Structure):

@@ -183,18 +183,21 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
         for (int e = 0; e < E; ++e) g[e] = norm_scale[lane + 64 * e];
         const float omb = 1.0f - beta;
         float rtok = 0.0f;
+        const float *hc_tok = b.mem_hist ? b.mem_hist + (long)(t / b.mem_T) * H * d : nullptr;
         for (int s = 0; s < H; ++s) {
             const float *o = b.o + ((long)i * H + s) * d;
             const float *sg = b.signal + ((long)t * H + s) * d;
             const float *an = anchor + (long)s * d;
+            const float *hc = hc_tok ? hc_tok + (long)s * d : nullptr;
             float *h = b.h + ((long)t * H + s) * d;
             float cval[E], hold[E];
             float ss = 0.0f;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const int idx = lane + 64 * e;
-                const float as_ = o[idx] + sg[idx];
-                const float c = (as_ + 0.0f) + an[idx];
+                // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389)
+                const float as_ = (o[idx] + sg[idx]) + (hc ? hc[idx] : 0.0f);
+                const float c = as_ + an[idx];
                 cval[e] = c;
                 hold[e] = h[idx];
                 ss += excl ? as_ * as_ : c * c;
@@ -410,11 +413,11 @@ void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max
 #undef ADN_UPD_ARGS
 }
 
-void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int k, int m,
+void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int rows, int k, int m,
                      hipStream_t st) {
     const int n_res = k < m - 1 ? k : m - 1;
     const int nres = (k >= 2 && n_res >= 2) ? n_res : 0;
-    const dim3 grid((unsigned)ntok), blk(AND_NT);
+    const dim3 grid((unsigned)rows), blk(AND_NT);
     switch (nres) {
         case 0: hipLaunchKernelGGL(k_anderson<0>, grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
         case 2: hipLaunchKernelGGL(k_anderson<2>, grid, blk, 0, st, D, b, nxt, ntok, k, m); break;

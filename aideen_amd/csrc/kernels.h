@@ -66,6 +66,10 @@ struct SolveBuffers {
     int32_t *cnt_hist;  // [ADN_PROFILE_MAX_ITERS] active tokens entering iteration k
     float *hist;        // Anderson ring [m][ntok][H][d] or null
     unsigned *err;
+    // memory-coupled solve: history context of the tokens being solved, [B][H][d] indexed by
+    // sequence (token / mem_T), added to the update's sum; null = none
+    const float *mem_hist;
+    int mem_T;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -77,8 +81,9 @@ void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok,
 // Damped RMS update, token residual, exit test, iteration counts and the next active list.
 void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps, int ntok,
                    const float *anchor, const float *norm_scale, float beta, hipStream_t st);
-// Anderson store + mix for the tokens still active after iteration k.
-void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int k, int m,
+// Anderson store + mix for the tokens still active after iteration k (at most `rows` of them;
+// ntok is the token stride of the ring).
+void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int rows, int k, int m,
                      hipStream_t st);
 
 // ---- LM head (head.hip) -----------------------------------------------------------------
@@ -126,6 +131,15 @@ void launch_gemv_colmajor(const float *w, const float *x, int in_dim, int out_di
 void launch_transpose(const float *src, int rows, int cols, long batch, float *dst,
                       hipStream_t st);
 void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
+// ---- memory-coupled solve (memory.hip) -----------------------------------------------------
+// act[0] = tokens (b, t) = b*T + t for b < B, cnt[0] = B, cnt[1] = 0.
+void launch_mem_begin(const SolveBuffers &b, int B, int T, int t, hipStream_t st);
+// hist [B][H][d] holds u = W_hist m_prev on entry; becomes the history context.
+void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm, const float *signal, int B,
+                     int T, int t, const float *slot_scale, const float *gate_logit, hipStream_t st);
+// out[b][s] = abar m_prev + (1 - abar) x for the tokens at position t (m_prev null = zeros).
+void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const float *m_prev, long m_sm,
+                     const float *a_log, const float *wx_diag, float *out, long out_sm, hipStream_t st);
 // *out = bit pattern of max |x[i]| over n floats (atomic max; *out must be zeroed first)
 void launch_absmax(const float *x, long n, unsigned *out, hipStream_t st);
 

@@ -1,0 +1,104 @@
+// Memory-coupled solve (the trainer's fixed-history mode, trainer.rs:677-720): tokens of a
+// sequence are solved one position at a time, all sequences of the batch together.  Per
+// position t:
+//   k_mem_begin   active list = the B tokens (b, t)
+//   GEMM          u = W_hist m_{t-1}                      (shared W_hist, rows = (b, slot))
+//   k_hist_ctx    hist = u' * alpha * min(1, rms(signal)/rms(u')),  u' = u + scale * m/rms(m)
+//                 (fixed_point_memory_reasoning.rs:1337-1370)
+//   Picard iterations over the B tokens with hist added to the update
+//   k_temporal    m_inner = abar m_{t-1} + (1 - abar) x,  x = u(1 + 0.5 tanh wx),  u = h*/rms(h*)
+//   GEMM          m_t = m_inner + W_out m_inner           (fixed_point_memory_reasoning.rs:1454-1485)
+// One wave per (sequence, slot) row in the elementwise kernels; the rows are d floats wide.
+#include "kernels.h"
+
+namespace adn {
+
+namespace {
+
+constexpr int MW = 4;  // waves per block
+
+__global__ void k_mem_begin(SolveBuffers b, int B, int T, int t) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < B) b.act[0][i] = i * T + t;
+    if (i == 0) {
+        b.cnt[0] = B;
+        b.cnt[1] = 0;
+    }
+}
+
+// hist holds u = W_hist m_prev on entry ([B][H][d]); m_prev rows are m_prev + b*m_sm + s*d.
+__global__ __launch_bounds__(64 * MW) void k_hist_ctx(Dims D, float *hist, const float *m_prev, long m_sm,
+                                                      const float *signal, int B, int T, int t,
+                                                      const float *slot_scale, const float *gate_logit) {
+    const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int H = D.H, d = D.d;
+    if (row >= B * H) return;
+    const int bb = row / H, s = row - bb * H;
+    float *u = hist + (long)row * d;
+    const float *pm = m_prev + (long)bb * m_sm + (long)s * d;
+    const float *sg = signal + ((long)(bb * T + t) * H + s) * d;
+    const float *sc = slot_scale + (long)s * d;
+    float ssg = 0.0f, spm = 0.0f;
+    for (int i = lane; i < d; i += 64) {
+        ssg += sg[i] * sg[i];
+        spm += pm[i] * pm[i];
+    }
+    const float inj_rms = sqrtf(wave_sum(ssg) / (float)d + 1e-6f);
+    const float prev_rms = sqrtf(wave_sum(spm) / (float)d + 1e-6f);
+    float su = 0.0f;
+    for (int i = lane; i < d; i += 64) {
+        const float v = u[i] + sc[i] * (pm[i] / prev_rms);
+        u[i] = v;
+        su += v * v;
+    }
+    const float u_rms = sqrtf(wave_sum(su) / (float)d + 1e-6f);
+    const float scale = u_rms > 1e-6f ? fminf(inj_rms / u_rms, 1.0f) : 1.0f;
+    const float sigma = 1.0f / (1.0f + expf(-gate_logit[s]));
+    const float g = (0.070f + (0.20f - 0.070f) * sigma) * scale;
+    for (int i = lane; i < d; i += 64) u[i] = u[i] * g;
+}
+
+// m_inner for the tokens at position t; m_prev == nullptr is the zero state.
+__global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, int B, int T, int t,
+                                                      const float *m_prev, long m_sm, const float *a_log,
+                                                      const float *wx_diag, float *out, long out_sm) {
+    const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int H = D.H, d = D.d;
+    if (row >= B * H) return;
+    const int bb = row / H, s = row - bb * H;
+    const float *hs = h + ((long)(bb * T + t) * H + s) * d;
+    float ss = 0.0f;
+    for (int i = lane; i < d; i += 64) ss += hs[i] * hs[i];
+    const float rms = sqrtf(wave_sum(ss) / (float)d + 1e-6f);
+    const float *pm = m_prev ? m_prev + (long)bb * m_sm + (long)s * d : nullptr;
+    float *o = out + (long)bb * out_sm + (long)s * d;
+    for (int i = lane; i < d; i += 64) {
+        const float u = hs[i] / rms;
+        const float wx = 0.5f * tanhf(wx_diag[(long)s * d + i]);
+        const float x = u + wx * u;
+        const float ab = 1.0f / (1.0f + expf(a_log[(long)s * d + i]));
+        o[i] = ab * (pm ? pm[i] : 0.0f) + (1.0f - ab) * x;
+    }
+}
+
+}  // namespace
+
+void launch_mem_begin(const SolveBuffers &b, int B, int T, int t, hipStream_t st) {
+    hipLaunchKernelGGL(k_mem_begin, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, b, B, T, t);
+}
+
+void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm, const float *signal, int B,
+                     int T, int t, const float *slot_scale, const float *gate_logit, hipStream_t st) {
+    const int rows = B * D.H;
+    hipLaunchKernelGGL(k_hist_ctx, dim3((unsigned)((rows + MW - 1) / MW)), dim3(64 * MW), 0, st, D, hist, m_prev,
+                       m_sm, signal, B, T, t, slot_scale, gate_logit);
+}
+
+void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const float *m_prev, long m_sm,
+                     const float *a_log, const float *wx_diag, float *out, long out_sm, hipStream_t st) {
+    const int rows = B * D.H;
+    hipLaunchKernelGGL(k_temporal, dim3((unsigned)((rows + MW - 1) / MW)), dim3(64 * MW), 0, st, D, h, B, T, t,
+                       m_prev, m_sm, a_log, wx_diag, out, out_sm);
+}
+
+}  // namespace adn

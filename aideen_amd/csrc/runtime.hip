@@ -46,6 +46,7 @@ struct adn_ctx {
     float *lm_b = nullptr, *lm_g = nullptr, *a_log = nullptr, *wx_diag = nullptr, *w_out = nullptr;
     float *b_delta = nullptr, *w_kw = nullptr, *w_vw = nullptr, *w_b = nullptr, *w_c = nullptr;
     float *w_cat = nullptr;  // [H][r + 2N][d] = [W_kw^T; W_B; W_C] per slot (carrier projections)
+    float *w_hist = nullptr, *hist_scale = nullptr, *hist_gate = nullptr;  // memory-coupled solve
 
     // split-precision copies of the GEMM weights (hi/lo halves of w * scale)
     struct Split {
@@ -53,7 +54,7 @@ struct adn_ctx {
         float scale = 1.0f;
     };
     int prec = PREC_F16X3;
-    Split sp_in, sp_qkv, sp_o, sp_out, sp_cat, sp_lm;
+    Split sp_in, sp_qkv, sp_o, sp_out, sp_cat, sp_lm, sp_hist;
     float embed_scale = 1.0f;  // A-side power-of-two scale of the signal GEMM (fp16 split)
 
     // work buffers (capacity-sized)
@@ -117,7 +118,10 @@ std::string validate_config(const adn_config &c) {
     if (c.max_batch < 1 || c.max_seq < 1) return "max_batch and max_seq must be >= 1";
     if ((long)c.max_batch * c.max_seq > (1L << 24)) return "max_batch*max_seq must be <= 2^24";
     if (c.anderson_m < 0 || c.anderson_m > 5) return "anderson_m must be in [0, 5]";
-    if (c.flags & ~0x1FFu) return "unknown flag bits";
+    if (c.flags & ~0x3FFu) return "unknown flag bits";
+    if ((c.flags & ADN_F_MEMORY) && c.d_state != 1) return "ADN_F_MEMORY needs d_state == 1";
+    if ((c.flags & ADN_F_MEMORY) && (c.flags & ADN_F_SCAN_SELECTIVE))
+        return "ADN_F_MEMORY uses the non-selective carrier";
     const uint32_t g = c.flags & (ADN_F_GEMM_FP32 | ADN_F_GEMM_BF16X3 | ADN_F_GEMM_BF16);
     if (g & (g - 1)) return "at most one ADN_F_GEMM_* flag";
     return "";
@@ -234,16 +238,12 @@ void set_split(const adn_ctx *c, GemmParams &g, const adn_ctx::Split &sp, float 
 // ---------------------------------------------------------------------------------------
 // the forward pipeline (device pointers; enqueue only)
 // ---------------------------------------------------------------------------------------
-void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
+// signal[t][s] = W_in[s] x_t for every token, h0 and the first active list (all tokens).
+void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int ntok, Prof *prof) {
     const Dims &D = c->D;
-    const int ntok = r.batch * r.seq;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
-    SolveBuffers b = c->sb;
-    if (o.h_star) b.h = o.h_star;
-    if (o.iters) b.iters = o.iters;
-
-    // signal[t][s] = W_in[s] x_t   (x gathered from the embedding when tokens are given)
+    // x gathered from the embedding when tokens are given
     {
         GemmParams g{};
         g.role = ROLE_SIGNAL;
@@ -280,7 +280,14 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
         Span sp(prof, ADN_STAGE_INIT, -1, st);
         launch_init(D, b, r.tokens ? c->embed : r.s_in, r.tokens, ntok, c->anchor, st);
     }
+}
 
+// max_iters Picard steps over the active list b.act[0] / b.cnt[0]: at most `rows` tokens are
+// active, token indices are < ntok (the row stride of h, signal and the Anderson ring).
+void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int rows, int ntok, Prof *prof) {
+    const Dims &D = c->D;
+    const int d = D.d, H = D.H;
+    hipStream_t st = c->stream;
     const int m = c->cfg.anderson_m;
     for (int k = 0; k < r.max_iters; ++k) {
         const int cur = k & 1;
@@ -300,7 +307,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             g.bias = c->qk_bias;
             g.bias_ss = 2L * d;
             g.bias_n = 2 * d;
-            g.M = ntok;
+            g.M = rows;
             g.N = 3 * d;
             g.K = d;
             g.S = H;
@@ -313,7 +320,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
         }
         {
             Span sp(prof, ADN_STAGE_ATTN, k, st);
-            launch_attn(D, b, cur, k, ntok, st);
+            launch_attn(D, b, cur, k, rows, st);
         }
         {  // o = W_o mix
             GemmParams g{};
@@ -326,7 +333,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             g.C = b.o;
             g.c_sm = (long)H * d;
             g.c_ss = d;
-            g.M = ntok;
+            g.M = rows;
             g.N = d;
             g.K = d;
             g.S = H;
@@ -339,15 +346,20 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
         }
         {
             Span sp(prof, ADN_STAGE_UPDATE, k, st);
-            launch_update(D, b, cur, k, r.max_iters, r.eps, ntok, c->anchor, c->norm_scale, r.damping, st);
+            launch_update(D, b, cur, k, r.max_iters, r.eps, rows, c->anchor, c->norm_scale, r.damping, st);
         }
         if (m > 0 && k + 1 < r.max_iters) {
             Span sp(prof, ADN_STAGE_ANDERSON, k, st);
-            launch_anderson(D, b, cur ^ 1, ntok, k, m, st);
+            launch_anderson(D, b, cur ^ 1, ntok, rows, k, m, st);
         }
     }
+}
 
-    // LM head
+// pooled rows, logits and arg-max of the solved h of all ntok tokens.
+void enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int ntok, Prof *prof) {
+    const Dims &D = c->D;
+    const int d = D.d;
+    hipStream_t st = c->stream;
     const bool want_logits = o.logits || o.argmax;
     if (o.pooled || want_logits) {
         Span sp(prof, ADN_STAGE_POOL, -1, st);
@@ -390,8 +402,14 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             launch_argmax_reduce(c->am_val, c->am_idx, ntok, ntiles, o.argmax, st);
         }
     }
+}
 
-    // temporal carrier
+// canonical carrier over each sequence's solved h (the readout scan).
+void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const SolveBuffers &b, Prof *prof) {
+    const Dims &D = c->D;
+    const int ntok = r.batch * r.seq;
+    const int d = D.d, H = D.H;
+    hipStream_t st = c->stream;
     if (o.scan_y || o.scan_state) {
         const int REC = scan_rec_len(D);
         {
@@ -449,6 +467,106 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
             launch_gemm(g, st);
         }
     }
+}
+
+void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
+    const int ntok = r.batch * r.seq;
+    SolveBuffers b = c->sb;
+    if (o.h_star) b.h = o.h_star;
+    if (o.iters) b.iters = o.iters;
+    b.mem_hist = nullptr;
+    enqueue_signal_init(c, r, b, ntok, prof);
+    enqueue_iterations(c, r, b, ntok, ntok, prof);
+    enqueue_head(c, o, b, ntok, prof);
+    enqueue_scan(c, r, o, b, prof);
+}
+
+// Memory-coupled forward (fixed-history mode, trainer.rs:677-720): position t of every sequence
+// is solved with the history context of m_{t-1} added to the update, then m_t = temporal_step(
+// m_{t-1}, h*_t) (fixed_point_memory_reasoning.rs:1317-1370, 1454-1485).  The B tokens of one
+// position form the active list; positions run in order.  m_t of every token lands in scan_y
+// (or scratch), the last one in scan_state; scan_state_in is m_{-1} (null = zero state, no
+// history context at t = 0).
+void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
+    const Dims &D = c->D;
+    const int B = r.batch, T = r.seq, ntok = B * T;
+    const int d = D.d, H = D.H;
+    const long hd = (long)H * d;
+    hipStream_t st = c->stream;
+    SolveBuffers b = c->sb;
+    if (o.h_star) b.h = o.h_star;
+    if (o.iters) b.iters = o.iters;
+    b.mem_hist = nullptr;
+    b.mem_T = T;
+    enqueue_signal_init(c, r, b, ntok, nullptr);
+    float *mseq = o.scan_y ? o.scan_y : c->scb.y;  // [B][T][H][d]
+    float *hist = c->scb.gate_x;                     // [B][H][d]
+    float *mn = c->scb.gate_a;                       // [B][H][d] state before W_out
+    for (int t = 0; t < T; ++t) {
+        launch_mem_begin(b, B, T, t, st);
+        const float *mprev = t > 0 ? mseq + (long)(t - 1) * hd : r.scan_state_in;
+        const long msm = t > 0 ? (long)T * hd : hd;
+        b.mem_hist = nullptr;
+        if (mprev) {
+            GemmParams g{};  // u[b][s] = W_hist m_prev[b][s]  (one W_hist for every slot)
+            g.role = ROLE_WO;
+            g.A = mprev;
+            g.a_sm = msm;
+            g.a_ss = d;
+            g.B = c->w_hist;
+            g.b_ss = 0;
+            g.C = hist;
+            g.c_sm = hd;
+            g.c_ss = d;
+            g.M = B;
+            g.N = d;
+            g.K = d;
+            g.S = H;
+            g.err = b.err;
+            g.epi = EPI_NONE;
+            set_split(c, g, c->sp_hist);
+            launch_gemm(g, st);
+            launch_hist_ctx(D, hist, mprev, msm, b.signal, B, T, t, c->hist_scale, c->hist_gate, st);
+            b.mem_hist = hist;
+        }
+        enqueue_iterations(c, r, b, B, ntok, nullptr);
+        float *mt = mseq + (long)t * hd;
+        if (c->w_out) {
+            launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mn, hd, st);
+            GemmParams g{};  // m_t = m_inner + W_out m_inner
+            g.role = ROLE_READOUT;
+            g.A = mn;
+            g.a_sm = hd;
+            g.a_ss = d;
+            g.B = c->w_out;
+            g.b_ss = (long)d * d;
+            g.C = mt;
+            g.c_sm = (long)T * hd;
+            g.c_ss = d;
+            g.M = B;
+            g.N = d;
+            g.K = d;
+            g.S = H;
+            g.err = b.err;
+            g.epi = EPI_ADD_A;
+            set_split(c, g, c->sp_out);
+            launch_gemm(g, st);
+        } else {
+            launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mt, (long)T * hd, st);
+        }
+    }
+    if (o.scan_state)
+        ADN_HIP(hipMemcpy2DAsync(o.scan_state, hd * sizeof(float), mseq + (long)(T - 1) * hd,
+                                 (size_t)T * hd * sizeof(float), hd * sizeof(float), B, hipMemcpyDeviceToDevice,
+                                 st));
+    enqueue_head(c, o, b, ntok, nullptr);
+}
+
+void enqueue_run(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
+    if (c->cfg.flags & ADN_F_MEMORY)
+        enqueue_forward_memory(c, r, o);
+    else
+        enqueue_forward(c, r, o);
 }
 
 int check_run(adn_ctx *c, const adn_run *r) {
@@ -649,6 +767,13 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
         } else {
             c->w_out = nullptr;
         }
+        if (cf.flags & ADN_F_MEMORY) {
+            // u = W_hist m with W_hist [out][in] row-major in either layout (the reference exports
+            // reasoning.w_hist_shared row-major, FPMR:656-659)
+            upload(c, &c->w_hist, w->w_hist, mat, "w_hist", true);
+            upload(c, &c->hist_scale, w->hist_slot_scale, (size_t)H * d, "hist_slot_scale", true);
+            upload(c, &c->hist_gate, w->hist_gate_logit, H, "hist_gate_logit", true);
+        }
         upload(c, &c->b_delta, w->b_delta, (size_t)H * d, "b_delta", false);
         upload(c, &c->w_kw, w->w_kw, (size_t)H * d * r, "w_kw", false);
         upload(c, &c->w_vw, w->w_vw, (size_t)H * r * d, "w_vw", false);
@@ -684,6 +809,7 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
                    host_maxabs({{w->w_kw, (size_t)H * d * r}, {w->w_b, (size_t)H * N * d},
                                 {w->w_c, (size_t)H * N * d}}));
         make_split(c, c->sp_lm, c->lm_w, (size_t)V * d, host_maxabs({{w->lm_w, (size_t)V * d}}));
+        if (c->w_hist) make_split(c, c->sp_hist, c->w_hist, mat, host_maxabs({{w->w_hist, mat}}));
         // The signal GEMM's A operand (gathered embedding rows, or s_in rows of the same
         // scale) is scaled up too, with 6 bits of headroom: inputs up to 64x the table's
         // maximum magnitude stay inside the fp16 range.
@@ -717,7 +843,7 @@ int adn_forward_async(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
     if (rc) return rc;
     if (!o) return fail(ADN_E_INVALID, "null outputs");
     try {
-        enqueue_forward(c, *r, *o);
+        enqueue_run(c, *r, *o);
         ADN_HIP(hipGetLastError());
     } catch (const HipError &e) {
         return hip_fail(e);
@@ -761,7 +887,7 @@ int adn_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
         if (o->iters) dout.iters = (int32_t *)staging_f(c, 4, (size_t)ntok * sizeof(int32_t));
         if (o->scan_y) dout.scan_y = staging_f(c, 5, hsz * sizeof(float));
         if (o->scan_state) dout.scan_state = staging_f(c, 6, stsz * sizeof(float));
-        enqueue_forward(c, dr, dout);
+        enqueue_run(c, dr, dout);
         ADN_HIP(hipGetLastError());
         auto d2h = [&](void *dst, const void *src, size_t bytes) {
             if (dst) ADN_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
@@ -788,6 +914,8 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, const int32_t *start, int32_t n
     if (batch > c->cap_tok) return fail(ADN_E_CAPACITY, "batch exceeds the context capacity");
     for (int b = 0; b < batch; ++b)
         if (start[b] < 0 || start[b] >= c->D.V) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
+    if (c->cfg.flags & ADN_F_MEMORY)
+        return fail(ADN_E_INVALID, "adn_decode_greedy runs the canonical forward; not available with ADN_F_MEMORY");
     if (n_new == 0) return ADN_OK;
     adn_run r{};
     r.batch = batch;
@@ -926,6 +1054,8 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
     int rc = check_run(c, r);
     if (rc) return rc;
     if (!o || !prof) return fail(ADN_E_INVALID, "null argument");
+    if (c->cfg.flags & ADN_F_MEMORY)
+        return fail(ADN_E_INVALID, "adn_profile_forward profiles the canonical forward; not available with ADN_F_MEMORY");
     try {
         Prof P;
         enqueue_forward(c, *r, *o, &P);

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define ADN_ABI_VERSION 1
+#define ADN_ABI_VERSION 2
 
 /* status codes */
 #define ADN_OK 0
@@ -55,6 +55,17 @@ extern "C" {
 #define ADN_F_INIT_SIGNAL_RMS (1u << 3) /* h0 = signal/rms(signal) (deq_slot_attn_unified_clean.wgsl:900-943) */
 #define ADN_F_RESID_L2 (1u << 4)        /* L2 exit residual (aideen-node/src/inference.rs:214-221)    */
 #define ADN_F_SCAN_SELECTIVE (1u << 5)  /* input-dependent carrier decay (gpu_deq.rs:6129-6214)      */
+
+/* Memory-coupled forward (the trainer's fixed-history mode, trainer.rs:677-720): per sequence,
+ * token t's solve adds the history context fixed_hist_ctx(m_{t-1}, signal_t)
+ * (fixed_point_memory_reasoning.rs:1337-1370, weights w_hist / hist_slot_scale /
+ * hist_gate_logit) and the carrier advances after each token, m_t = temporal_step(m_{t-1}, h*_t)
+ * (fixed_point_memory_reasoning.rs:1454-1485: non-selective decay, m_t = (I + W_out) m_inner).
+ * Tokens of a sequence are solved one after another.  Requires d_state == 1 and no
+ * ADN_F_SCAN_SELECTIVE; scan_y returns every m_t [B][T][H][d], scan_state the last one
+ * [B][H][d], scan_state_in the memory before the first token (NULL = none).  eps = 0 runs
+ * exactly max_iters steps per token, as the reference's fixed-history solve does. */
+#define ADN_F_MEMORY (1u << 9)
 
 /* GEMM arithmetic (adn_config.flags; at most one).  Default: fp32 operands carried as fp16
  * hi+lo pairs on the 16-bit MFMA with three products per multiply (hi.hi + hi.lo + lo.hi),
@@ -101,6 +112,12 @@ typedef struct adn_weights {
     const float *w_kw;                          /* [H][d][r] selective write down     */
     const float *w_vw;                          /* [H][r][d] selective write up       */
     const float *w_b, *w_c;                     /* [H][N][d] carrier B/C, NULL = 1    */
+    /* memory-coupled forward (ADN_F_MEMORY; ignored otherwise), fixed_point_memory_reasoning.rs:
+     * 279, 312-333 and the export names reasoning.w_hist_shared / hist_slot_scale /
+     * hist_gate_logit (:656-671) */
+    const float *w_hist;                        /* [d][d] shared, row-major (u = W m)  */
+    const float *hist_slot_scale;               /* [H][d]                             */
+    const float *hist_gate_logit;               /* [H]                                */
 } adn_weights;
 
 /* One forward call (reference: run_forward_deq(batch, seq, max_iters, eps, damping, s_in, ...),

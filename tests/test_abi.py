@@ -14,7 +14,7 @@ def test_library_loads_and_exports_every_header_symbol():
     assert len(names) >= 15
     for n in names:
         assert hasattr(L, n), f"{n} declared in include/aideen_hip.h but not exported"
-    assert L.adn_abi_version() == 1
+    assert L.adn_abi_version() == 2
 
 
 def test_header_flag_values_match_oracle_and_synth():
@@ -35,12 +35,13 @@ def test_struct_layouts_match_header():
     fields = re.findall(r"\*(\w+)", body)
     assert fields == _lib.WEIGHT_FIELDS
     assert C.sizeof(_lib.AdnConfig) == 9 * 4
-    assert C.sizeof(_lib.AdnWeights) == 21 * 8
+    assert C.sizeof(_lib.AdnWeights) == 24 * 8
 
 
 @pytest.mark.parametrize("bad", [
     dict(d_r=100), dict(d_r=4096), dict(h_slots=3), dict(d_state=0), dict(d_state=64),
-    dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 9), dict(vocab=0), dict(flags=(1 << 6) | (1 << 7)),
+    dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 10), dict(flags=1 << 9, d_state=4),
+    dict(flags=(1 << 9) | (1 << 5), d_state=1), dict(vocab=0), dict(flags=(1 << 6) | (1 << 7)),
 ])
 def test_create_rejects_invalid_config_before_device(bad):
     L = _lib.lib()
