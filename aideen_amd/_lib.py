@@ -53,7 +53,8 @@ class AdnOutputs(C.Structure):
 
 
 STAGES = ["signal_gemm", "init", "qkv_gemm", "attn", "wo_gemm", "update", "converge", "anderson",
-          "pool", "lmhead_gemm", "argmax", "scan_prep", "scan", "readout_gemm"]
+          "pool", "lmhead_gemm", "argmax", "scan_prep", "scan", "readout_gemm", "hist_gemm", "hist_ctx",
+          "temporal"]
 PROFILE_MAX_ITERS = 256
 
 

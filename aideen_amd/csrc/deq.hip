@@ -58,6 +58,8 @@ __global__ void k_init(Dims D, SolveBuffers b, const float *x_src, const int32_t
         b.cnt[0] = ntok;
         b.cnt[1] = 0;
     }
+    if (row == 0)
+        for (int q = lane; q < ADN_PROFILE_MAX_ITERS; q += 64) b.cnt_hist[q] = 0;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         // the update kernel of this iteration appends survivors to the other list
         b.cnt[cur ^ 1] = 0;
-        b.cnt_hist[k] = n;
+        b.cnt_hist[k] += n;  // summed over the positions of a memory-coupled forward
     }
     const int i = gw / NG, g = gw - (gw / NG) * NG;
     if (i >= n) return;
@@ -301,7 +303,70 @@ __device__ void anderson_coeffs(int n, const float *g, float *beta) {
     }
 }
 
+// Update for few tokens (one position of every sequence, a decode step): one block per token
+// and one wave per slot, so that the slots' row updates run side by side instead of one after
+// another in a single wave.  Same arithmetic as k_update (the token residual is combined over
+// the slots in slot order).
+template <int E>
+__global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int cur, int k, int max_iters,
+                                                     float eps, const float *anchor, const float *norm_scale,
+                                                     float beta) {
+    __shared__ float rs[16];
+    const int i = blockIdx.x;
+    if (i >= b.cnt[cur]) return;
+    const int s = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int H = D.H;
+    constexpr int d = 64 * E;
+    const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
+    const bool l2 = (D.flags & ADN_F_RESID_L2) != 0;
+    const int t = b.act[cur][i];
+    const float *o = b.o + ((long)i * H + s) * d;
+    const float *sg = b.signal + ((long)t * H + s) * d;
+    const float *an = anchor + (long)s * d;
+    const float *hc = b.mem_hist ? b.mem_hist + ((long)(t / b.mem_T) * H + s) * d : nullptr;
+    float *h = b.h + ((long)t * H + s) * d;
+    float cval[E], hold[E];
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int idx = lane + 64 * e;
+        const float as_ = (o[idx] + sg[idx]) + (hc ? hc[idx] : 0.0f);
+        const float c = as_ + an[idx];
+        cval[e] = c;
+        hold[e] = h[idx];
+        ss += excl ? as_ * as_ : c * c;
+    }
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / (float)d + 1e-6f);
+    const float omb = 1.0f - beta;
+    float r = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float f = norm_scale[lane + 64 * e] * cval[e] / rms;
+        const float hn = f * beta + hold[e] * omb;
+        h[lane + 64 * e] = hn;
+        const float df = hn - hold[e];
+        r = l2 ? r + df * df : fmaxf(r, fabsf(df));
+    }
+    r = l2 ? wave_sum(r) : wave_max(r);
+    if (lane == 0) rs[s] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float rtok = 0.0f;
+        for (int q = 0; q < H; ++q) rtok = l2 ? rtok + rs[q] : fmaxf(rtok, rs[q]);
+        if (l2) rtok = sqrtf(rtok);
+        if ((rtok < eps) || (k + 1 >= max_iters)) {
+            b.iters[t] = k + 1;
+        } else {
+            const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
+            b.act[cur ^ 1][pos] = t;
+        }
+    }
+}
+
 constexpr int AND_NT = 256;
+// at most this many tokens in flight: the few-token kernel shapes (more waves per token)
+constexpr int SMALL_ROWS = 512;
 
 // NRES = 0: store only; NRES in 2..4: store, Gram, solve, mix.
 template <int NRES>
@@ -387,6 +452,17 @@ void launch_init(const Dims &D, const SolveBuffers &b, const float *x_src, const
 }
 
 void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok, hipStream_t st) {
+    if (ntok <= SMALL_ROWS) {  // one wave per (token, query slot): the same scores, more waves
+        switch (D.H) {
+            case 1: attn_dispatch_vec<1, 1>(D, b, cur, k, ntok, st); break;
+            case 2: attn_dispatch_vec<2, 1>(D, b, cur, k, ntok, st); break;
+            case 4: attn_dispatch_vec<4, 1>(D, b, cur, k, ntok, st); break;
+            case 8: attn_dispatch_vec<8, 1>(D, b, cur, k, ntok, st); break;
+            case 16: attn_dispatch_vec<16, 1>(D, b, cur, k, ntok, st); break;
+            default: break;
+        }
+        return;
+    }
     switch (D.H) {
         case 1: attn_dispatch_vec<1, 1>(D, b, cur, k, ntok, st); break;
         case 2: attn_dispatch_vec<2, 2>(D, b, cur, k, ntok, st); break;
@@ -399,8 +475,21 @@ void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok,
 
 void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps, int ntok,
                    const float *anchor, const float *norm_scale, float beta, hipStream_t st) {
-    const dim3 grid((unsigned)((ntok + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), blk(64 * WAVES_PER_BLOCK);
 #define ADN_UPD_ARGS D, b, cur, k, max_iters, eps, anchor, norm_scale, beta
+    if (ntok <= SMALL_ROWS) {
+        const dim3 tgrid((unsigned)ntok), tblk(64 * D.H);
+        switch (D.d) {
+            case 64: hipLaunchKernelGGL(k_update_tok<1>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
+            case 128: hipLaunchKernelGGL(k_update_tok<2>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
+            case 256: hipLaunchKernelGGL(k_update_tok<4>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
+            case 512: hipLaunchKernelGGL(k_update_tok<8>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
+            case 1024: hipLaunchKernelGGL(k_update_tok<16>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
+            case 2048: hipLaunchKernelGGL(k_update_tok<32>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
+            default: break;  // rejected at context creation
+        }
+        return;
+    }
+    const dim3 grid((unsigned)((ntok + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), blk(64 * WAVES_PER_BLOCK);
     switch (D.d) {
         case 64: hipLaunchKernelGGL(k_update<1>, grid, blk, 0, st, ADN_UPD_ARGS); break;
         case 128: hipLaunchKernelGGL(k_update<2>, grid, blk, 0, st, ADN_UPD_ARGS); break;

@@ -223,6 +223,118 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     epilogue_t<ROLE, WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, osc, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
 }
 
+// Skinny GEMM (at most 32 rows: one position of every sequence, a decode step).  There the
+// ring kernel's serial k loop (one barrier per 16-K slice) is the whole cost, so here a
+// workgroup of KW waves owns a 32 x (32 WTN) output block and wave w multiplies its own K range
+// [w K/KW, (w+1) K/KW) straight from global memory into registers, 64 K values per step:
+// lane (q = lane & 31, g = lane >> 5) loads the 32 consecutive K values [64i + 32g, +32) of A
+// row q and of B row q (of each of the WTN column tiles), and MFMA step j (0..3) takes values
+// [8j, 8j + 8) of that run.  A and B use the same K order, so each MFMA still contracts
+// matching K indices.  The KW partial blocks are summed in LDS in wave order (deterministic)
+// and wave 0 runs the role's epilogue.
+template <int ROLE, typename T, int TERMS, int KW, int WTN>
+__global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
+    typedef typename Vec8<T>::type V8;
+    __shared__ float red[KW > 1 ? KW - 1 : 1][WTN * 16][64];  // [wave-1][element][lane]
+    constexpr int BNt = 32 * WTN;
+    const int nN = (p.N + BNt - 1) / BNt;
+    int s, mt, nt;
+    map_block(blockIdx.x, nN * p.S, 1, nN, s, mt, nt);
+    const int M = p.m_count ? min(*p.m_count, p.M) : p.M;
+    if (M <= 0) return;
+    const int n0 = nt * BNt;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int q = lane & 31, g = lane >> 5;
+
+    // rows past M read row 0, columns past N row 0 of B (their outputs are not stored)
+    long ar = 0;
+    if (q < M) {
+        ar = p.a_idx ? (long)p.a_idx[q] : (long)q;
+        if (p.a_idx && (ar < 0 || ar >= p.a_idx_max)) {
+            if (p.err) atomicOr(p.err, ADN_DEVERR_TOKEN);
+            ar = 0;
+        }
+    }
+    const float *ap = p.A + ar * p.a_sm + (long)s * p.a_ss;
+    const T *bhp[WTN], *blp[WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+        const int n = n0 + 32 * j + q;
+        const long boff = (long)s * p.b_ss + (long)(n < p.N ? n : 0) * p.K;
+        bhp[j] = reinterpret_cast<const T *>(p.Bhi) + boff;
+        blp[j] = reinterpret_cast<const T *>(TERMS == 3 ? p.Blo : p.Bhi) + boff;
+    }
+
+    float asc = p.a_scale, osc = p.out_scale;
+    if (p.a_absmax) {  // data-dependent A scale (power of two, never above the static one)
+        const float mx = __uint_as_float(*p.a_absmax);
+        if (mx > 0.0f) {
+            const float dyn = exp2f(floorf(log2f(p.a_headroom / mx)));
+            if (dyn < asc) {
+                osc *= asc / dyn;
+                asc = dyn;
+            }
+        }
+    }
+    floatx16 acc[1][WTN];
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[0][j][e] = 0.0f;
+
+    const int kw = p.K / KW;  // a multiple of 64 (checked by the launcher)
+    for (int k = wave * kw; k < (wave + 1) * kw; k += 64) {
+        const int ko = k + 32 * g;
+        floatx4 a[8];
+        V8 bh[WTN][4], bl[WTN][4];
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                bh[j][st] = *reinterpret_cast<const V8 *>(bhp[j] + ko + 8 * st);
+                if constexpr (TERMS == 3) bl[j][st] = *reinterpret_cast<const V8 *>(blp[j] + ko + 8 * st);
+            }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const floatx4 *>(ap + ko + 4 * i);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            V8 ah, al;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = a[2 * st + (e >> 2)][e & 3] * asc;
+                const T hv = (T)x;
+                ah[e] = hv;
+                if constexpr (TERMS == 3) al[e] = (T)(x - (float)hv);
+            }
+#pragma unroll
+            for (int j = 0; j < WTN; ++j) {
+                if constexpr (TERMS == 3) {
+                    acc[0][j] = mfma16(al, bh[j][st], acc[0][j]);
+                    acc[0][j] = mfma16(ah, bl[j][st], acc[0][j]);
+                }
+                acc[0][j] = mfma16(ah, bh[j][st], acc[0][j]);
+            }
+        }
+    }
+    if constexpr (KW > 1) {
+        if (wave > 0)
+#pragma unroll
+            for (int j = 0; j < WTN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) red[wave - 1][j * 16 + e][lane] = acc[0][j][e];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+            for (int j = 0; j < WTN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[0][j][e] += red[w][j * 16 + e][lane];
+    }
+    epilogue_t<ROLE, 1, WTN, 1, 1>(p, acc, M, s, 0, n0, osc, nullptr, nullptr);
+}
+
 // Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi).
 template <typename T>
 __global__ void k_split(const float *w, long n, float scale, T *hi, T *lo) {
@@ -234,11 +346,47 @@ __global__ void k_split(const float *w, long n, float scale, T *hi, T *lo) {
     }
 }
 
+template <int ROLE, typename T, int TERMS, int WTN>
+void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
+    const int total = ((p.N + 32 * WTN - 1) / (32 * WTN)) * p.S;
+    if (total <= 0) return;
+    switch (kw) {  // kw divides K / 64
+        case 8: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 8, WTN>), dim3(total), dim3(512), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 4, WTN>), dim3(total), dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 2, WTN>), dim3(total), dim3(128), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 1, WTN>), dim3(total), dim3(64), 0, st, p); break;
+    }
+}
+
 // Tile configurations (WTM, WTN, WGM, WGN, STAGES): GEMMs that are wide in both M and N use
 // 256x256 blocks of 8 waves (one workgroup per CU, 128 KB of LDS ring); the rest 128x128 blocks
 // of 4 waves (two workgroups per CU) so that their grids still cover the chip.
 template <int ROLE, typename T, int TERMS>
 void launch_cfg(const GemmParams &p, hipStream_t st) {
+    if constexpr (ROLE != ROLE_LMHEAD) {
+        if (p.M <= 32 && p.K % 64 == 0) {
+            // skinny: K split over the waves of a workgroup, about two 64-K steps per wave;
+            // wide outputs take two column tiles per wave (each A fragment feeds both)
+            const int steps = p.K / 64;
+            int kw = steps >= 16 ? 8 : steps >= 8 ? 4 : steps >= 4 ? 2 : 1;
+            while (steps % kw) kw >>= 1;  // each wave's K range is whole 64-K steps
+            if (p.N >= 1024)
+                launch_skinny<ROLE, T, TERMS, 2>(p, kw, st);
+            else
+                launch_skinny<ROLE, T, TERMS, 1>(p, kw, st);
+            return;
+        }
+        if (p.M <= 32) {
+            // skinny (at most 32 rows, e.g. one position of every sequence): 32x32 blocks of one
+            // wave, an 8-deep ring, so that the weight stream is spread over as many CUs as
+            // possible (the LM head keeps 128-column tiles: its arg-max partials are per 128
+            // columns)
+            const int total = ((p.N + 31) / 32) * p.S;
+            if (total > 0)
+                hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 1, 1, 1, 1, 8>), dim3(total), dim3(64), 0, st, p);
+            return;
+        }
+    }
     const bool big = p.N >= 1024 && p.M >= 1024;
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
     const int total = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.S;

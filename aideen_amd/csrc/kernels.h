@@ -63,7 +63,7 @@ struct SolveBuffers {
     int32_t *act[2];    // active token lists
     int32_t *cnt;       // [4]: counts of act[0], act[1]; cnt[2] unused; cnt[3] = total tokens
     int32_t *iters;     // [ntok]
-    int32_t *cnt_hist;  // [ADN_PROFILE_MAX_ITERS] active tokens entering iteration k
+    int32_t *cnt_hist;  // [ADN_PROFILE_MAX_ITERS] active tokens entering iteration k (summed over positions)
     float *hist;        // Anderson ring [m][ntok][H][d] or null
     unsigned *err;
     // memory-coupled solve: history context of the tokens being solved, [B][H][d] indexed by

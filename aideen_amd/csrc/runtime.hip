@@ -164,7 +164,7 @@ float *staging_f(adn_ctx *c, int slot, size_t bytes) {
 // Per-launch event pairs for adn_profile_forward (null when not profiling).
 struct Prof {
     struct Rec {
-        int stage, k;
+        int stage, k, n;  // n: rows of the launch (-1: every token of the forward)
         hipEvent_t e0, e1;
     };
     std::vector<Rec> recs;
@@ -187,9 +187,9 @@ struct Span {
     Prof *p;
     hipStream_t st;
     size_t idx;
-    Span(Prof *p_, int stage, int k, hipStream_t st_) : p(p_), st(st_), idx(0) {
+    Span(Prof *p_, int stage, int k, hipStream_t st_, int n = -1) : p(p_), st(st_), idx(0) {
         if (!p) return;
-        Prof::Rec r{stage, k, p->get(), p->get()};
+        Prof::Rec r{stage, k, n, p->get(), p->get()};
         ADN_HIP(hipEventRecord(r.e0, st));
         idx = p->recs.size();
         p->recs.push_back(r);
@@ -487,7 +487,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
 // position form the active list; positions run in order.  m_t of every token lands in scan_y
 // (or scratch), the last one in scan_state; scan_state_in is m_{-1} (null = zero state, no
 // history context at t = 0).
-void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
+void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
     const Dims &D = c->D;
     const int B = r.batch, T = r.seq, ntok = B * T;
     const int d = D.d, H = D.H;
@@ -498,12 +498,15 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o) 
     if (o.iters) b.iters = o.iters;
     b.mem_hist = nullptr;
     b.mem_T = T;
-    enqueue_signal_init(c, r, b, ntok, nullptr);
+    enqueue_signal_init(c, r, b, ntok, prof);
     float *mseq = o.scan_y ? o.scan_y : c->scb.y;  // [B][T][H][d]
     float *hist = c->scb.gate_x;                     // [B][H][d]
     float *mn = c->scb.gate_a;                       // [B][H][d] state before W_out
     for (int t = 0; t < T; ++t) {
-        launch_mem_begin(b, B, T, t, st);
+        {
+            Span sp(prof, ADN_STAGE_CONVERGE, -1, st, B);
+            launch_mem_begin(b, B, T, t, st);
+        }
         const float *mprev = t > 0 ? mseq + (long)(t - 1) * hd : r.scan_state_in;
         const long msm = t > 0 ? (long)T * hd : hd;
         b.mem_hist = nullptr;
@@ -525,14 +528,21 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o) 
             g.err = b.err;
             g.epi = EPI_NONE;
             set_split(c, g, c->sp_hist);
-            launch_gemm(g, st);
+            {
+                Span sp(prof, ADN_STAGE_HIST_GEMM, -1, st, B);
+                launch_gemm(g, st);
+            }
+            Span sp(prof, ADN_STAGE_HIST_CTX, -1, st, B);
             launch_hist_ctx(D, hist, mprev, msm, b.signal, B, T, t, c->hist_scale, c->hist_gate, st);
             b.mem_hist = hist;
         }
-        enqueue_iterations(c, r, b, B, ntok, nullptr);
+        enqueue_iterations(c, r, b, B, ntok, prof);
         float *mt = mseq + (long)t * hd;
         if (c->w_out) {
-            launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mn, hd, st);
+            {
+                Span sp(prof, ADN_STAGE_TEMPORAL, -1, st, B);
+                launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mn, hd, st);
+            }
             GemmParams g{};  // m_t = m_inner + W_out m_inner
             g.role = ROLE_READOUT;
             g.A = mn;
@@ -550,8 +560,10 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o) 
             g.err = b.err;
             g.epi = EPI_ADD_A;
             set_split(c, g, c->sp_out);
+            Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st, B);
             launch_gemm(g, st);
         } else {
+            Span sp(prof, ADN_STAGE_TEMPORAL, -1, st, B);
             launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mt, (long)T * hd, st);
         }
     }
@@ -559,14 +571,14 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o) 
         ADN_HIP(hipMemcpy2DAsync(o.scan_state, hd * sizeof(float), mseq + (long)(T - 1) * hd,
                                  (size_t)T * hd * sizeof(float), hd * sizeof(float), B, hipMemcpyDeviceToDevice,
                                  st));
-    enqueue_head(c, o, b, ntok, nullptr);
+    enqueue_head(c, o, b, ntok, prof);
 }
 
-void enqueue_run(adn_ctx *c, const adn_run &r, const adn_outputs &o) {
+void enqueue_run(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
     if (c->cfg.flags & ADN_F_MEMORY)
-        enqueue_forward_memory(c, r, o);
+        enqueue_forward_memory(c, r, o, prof);
     else
-        enqueue_forward(c, r, o);
+        enqueue_forward(c, r, o, prof);
 }
 
 int check_run(adn_ctx *c, const adn_run *r) {
@@ -1054,11 +1066,9 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
     int rc = check_run(c, r);
     if (rc) return rc;
     if (!o || !prof) return fail(ADN_E_INVALID, "null argument");
-    if (c->cfg.flags & ADN_F_MEMORY)
-        return fail(ADN_E_INVALID, "adn_profile_forward profiles the canonical forward; not available with ADN_F_MEMORY");
     try {
         Prof P;
-        enqueue_forward(c, *r, *o, &P);
+        enqueue_run(c, *r, *o, &P);
         ADN_HIP(hipGetLastError());
         ADN_HIP(hipStreamSynchronize(c->stream));
         int32_t hist[ADN_PROFILE_MAX_ITERS] = {0};
@@ -1069,11 +1079,21 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
         const double d = c->D.d, H = c->D.H, V = c->D.V, N = c->D.N, R = c->D.r;
         const double ntok = (double)r->batch * r->seq, REC = 1 + R + 2 * N, f = 4.0;
         const int m = c->cfg.anderson_m;
+        // hist[k] sums the active tokens of iteration k over every launch of it (one per
+        // position in memory mode): a launch's share is hist[k] / (launches of its stage at k)
+        std::vector<int> per_k((size_t)ADN_STAGE_COUNT * ADN_PROFILE_MAX_ITERS, 0);
+        for (const auto &rec : P.recs)
+            if (rec.k >= 0 && rec.k < ADN_PROFILE_MAX_ITERS) ++per_k[(size_t)rec.stage * ADN_PROFILE_MAX_ITERS + rec.k];
+        auto act = [&](int st, int k, int kk) {  // active tokens of launch (st, k) entering iteration kk
+            const int cnt = per_k[(size_t)st * ADN_PROFILE_MAX_ITERS + k];
+            return (kk < r->max_iters && cnt > 0) ? (double)hist[kk] / cnt : 0.0;
+        };
         for (const auto &rec : P.recs) {
             float ms = 0.0f;
             ADN_HIP(hipEventElapsedTime(&ms, rec.e0, rec.e1));
             const int st = rec.stage;
-            const double n = (rec.k >= 0 && st >= ADN_STAGE_QKV_GEMM && st <= ADN_STAGE_CONVERGE) ? hist[rec.k] : ntok;
+            const bool per_iter = rec.k >= 0 && st >= ADN_STAGE_QKV_GEMM && st <= ADN_STAGE_CONVERGE;
+            const double n = per_iter ? act(st, rec.k, rec.k) : (rec.n >= 0 ? rec.n : ntok);
             double fl = 0, by = 0;
             switch (st) {
                 case ADN_STAGE_SIGNAL_GEMM: fl = 2 * ntok * H * d * d; by = f * (ntok * d + H * d * d + ntok * H * d); break;
@@ -1082,9 +1102,9 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
                 case ADN_STAGE_ATTN: fl = 4 * n * H * H * d; by = f * 4 * n * H * d; break;
                 case ADN_STAGE_WO_GEMM: fl = 2 * n * H * d * d; by = n > 0 ? f * (2 * n * H * d + H * d * d) : 0; break;
                 case ADN_STAGE_UPDATE: fl = 10 * n * H * d; by = f * (4 * n * H * d + 3 * n); break;
-                case ADN_STAGE_CONVERGE: by = f * n * (H + 3); break;
+                case ADN_STAGE_CONVERGE: by = f * (n * (rec.k >= 0 ? H + 3 : 1) + 2); break;
                 case ADN_STAGE_ANDERSON: {
-                    const double nn = (rec.k + 1 < r->max_iters) ? hist[rec.k + 1] : 0;
+                    const double nn = act(st, rec.k, rec.k + 1);
                     const int k = rec.k, n_res = k < m - 1 ? k : m - 1;
                     const double nr = (k >= 2 && n_res >= 2) ? n_res : 0;
                     fl = nn * H * d * (nr * (nr + 1) + 2 * nr);
@@ -1098,7 +1118,10 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
                 case ADN_STAGE_SCAN:  // compulsory: read h*, the record; write y
                     fl = ntok * H * d * (2 * R + 4 * N + 10);
                     by = f * (ntok * H * d + ntok * H * REC + ntok * H * d); break;
-                case ADN_STAGE_READOUT_GEMM: fl = 2 * ntok * H * d * d; by = f * (2 * ntok * H * d + H * d * d); break;
+                case ADN_STAGE_READOUT_GEMM: fl = 2 * n * H * d * d; by = f * (2 * n * H * d + H * d * d); break;
+                case ADN_STAGE_HIST_GEMM: fl = 2 * n * H * d * d; by = f * (2 * n * H * d + d * d); break;
+                case ADN_STAGE_HIST_CTX: fl = 9 * n * H * d; by = f * (4 * n * H * d + H * d + H); break;
+                case ADN_STAGE_TEMPORAL: fl = 10 * n * H * d; by = f * (3 * n * H * d + 2 * H * d); break;
                 default: break;
             }
             prof->ms[st] += ms;

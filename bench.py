@@ -66,6 +66,32 @@ def cpu_baseline(mc, w, toks, seconds: float):
                 seconds=round(t2, 2))
 
 
+def cpu_baseline_memory(mc, w, toks, seconds: float):
+    """The C oracle's memory-coupled forward (sequential over positions, OpenMP over sequences)
+    timed on a prefix of as many sequences as there are threads: one short calibration run,
+    then a prefix length that fills about `seconds`."""
+    from oracle import pyoracle
+    pyoracle.build()
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    o = pyoracle.Oracle(mc, w)
+    B, T = toks.shape
+    nseq = min(B, threads)
+    t_cal = min(T, 8)
+    t0 = time.perf_counter()
+    o.forward_memory(toks[:nseq, :t_cal].copy(), nthreads=threads)
+    t1 = time.perf_counter() - t0
+    tp = int(max(1, min(T, t_cal * seconds / max(t1, 1e-6))))
+    t0 = time.perf_counter()
+    o.forward_memory(toks[:nseq, :tp].copy(), nthreads=threads)
+    t2 = time.perf_counter() - t0
+    n = nseq * tp
+    return dict(value=round(n / t2, 2), unit="tokens/s", cores=threads, kind="port",
+                sample=(f"the first {tp} of {T} positions of {nseq} of the {B} sequences ({n} tokens) of the "
+                        f"same workload, same weights and token ids: memory-coupled solve + carrier + "
+                        f"LM-head logits + arg-max, {threads} OpenMP threads over sequences, {t2:.1f} s"),
+                seconds=round(t2, 2))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -76,6 +102,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates HBM byte counters)")
+    ap.add_argument("--mode", choices=["forward", "memory"], default="forward",
+                    help="forward: the canonical (token-parallel) forward, the headline metric; memory: "
+                         "the memory-coupled forward (positions in order, history context and carrier "
+                         "state between them) on the same shape with a one-dimensional carrier state")
+    ap.add_argument("--eps", type=float, default=None, help="override the Picard tolerance")
     ap.add_argument("--gemm", choices=list(GEMM_MODES), default="f16x3",
                     help="GEMM arithmetic (f16x3 / bf16x3 / fp32 are fp32-accurate; bf16 is the "
                          "reduced-precision bf16-input variant)")
@@ -95,9 +126,17 @@ def main() -> int:
     p = synth.PRESETS[args.config]
     gm = GEMM_MODES[args.gemm]
     mc = dataclasses.replace(p["model"], flags=p["model"].flags | gm["flag"])
+    memory = args.mode == "memory"
+    if memory:  # the fixed-history mode's carrier: one state per (slot, dim), constant decay
+        mc = dataclasses.replace(mc, N=1, flags=(mc.flags & ~synth.F_SCAN_SELECTIVE) | synth.F_MEMORY)
+    if args.eps is not None:
+        mc = dataclasses.replace(mc, eps=args.eps)
     B, T = p["B"], p["T"]
-    log(f"config {args.config}: d={mc.d} H={mc.H} V={mc.V} N={mc.N} B={B} T={T}")
+    log(f"config {args.config} ({args.mode}): d={mc.d} H={mc.H} V={mc.V} N={mc.N} B={B} T={T} eps={mc.eps}")
     w = synth.make_weights(mc, seed=0)
+    if memory:
+        w = dict(w)
+        w.update(synth.make_hist_weights(mc, seed=0))
     toks = synth.make_tokens(p["tokens"], B, T, mc.V, seed=1)
 
     dev = torch.device("cuda:0")
@@ -156,18 +195,29 @@ def main() -> int:
         stages[name] = e
     dom = max((n for n in prof["stages"] if n in MFMA_STAGES), key=lambda n: prof["stages"][n]["ms"])
     ds = prof["stages"][dom]
-    achieved = ds["flops"] / ds["ms"] / 1e9  # TFLOP/s
     traffic = None
-    tf_path = os.path.join(ROOT, "profiles", f"{dom}_{args.config}_{args.gemm}_traffic.json")
+    tf_path = os.path.join(ROOT, "profiles", f"{dom}_{args.config}{'_memory' if memory else ''}_{args.gemm}_traffic.json")
     if os.path.exists(tf_path):
         traffic = json.load(open(tf_path)).get("bytes_per_launch")
-    roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 2), peak=round(gm["peak"], 1),
-                    unit="TFLOP/s", frac=round(achieved / gm["peak"], 4), traffic=traffic,
-                    peak_basis=gm["basis"], gemm=args.gemm,
-                    launches=ds["launches"], avg_launch_ms=round(ds["ms"] / ds["launches"], 4),
-                    flops_per_launch=ds["flops"] / ds["launches"])
+    tflops = ds["flops"] / ds["ms"] / 1e9
+    if memory:
+        # one position of every sequence per launch (B rows): 2*B flops per 4-byte weight, far
+        # below the f16x3 ridge (peak / HBM bandwidth), so the weight stream bounds the kernel
+        gbs = ds["bytes"] / ds["ms"] / 1e6
+        roofline = dict(kernel=dom, bound="hbm", achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                        frac=round(gbs / PEAK_HBM_GBS, 4), traffic=traffic,
+                        basis="algorithmic bytes: fp32-equivalent weights (hi + lo halves) + A rows + C rows",
+                        gemm=args.gemm, launches=ds["launches"], avg_launch_ms=round(ds["ms"] / ds["launches"], 4),
+                        bytes_per_launch=ds["bytes"] / ds["launches"],
+                        mfma_tflops=round(tflops, 2), mfma_frac=round(tflops / gm["peak"], 4))
+    else:
+        roofline = dict(kernel=dom, bound="mfma", achieved=round(tflops, 2), peak=round(gm["peak"], 1),
+                        unit="TFLOP/s", frac=round(tflops / gm["peak"], 4), traffic=traffic,
+                        peak_basis=gm["basis"], gemm=args.gemm,
+                        launches=ds["launches"], avg_launch_ms=round(ds["ms"] / ds["launches"], 4),
+                        flops_per_launch=ds["flops"] / ds["launches"])
     hbm = {}
-    for n in ("attn", "update", "scan", "argmax", "pool"):
+    for n in ("attn", "update", "scan", "argmax", "pool", "hist_ctx", "temporal"):
         if n in prof["stages"] and prof["stages"][n]["ms"] > 0:
             s = prof["stages"][n]
             g = s["bytes"] / s["ms"] / 1e6
@@ -176,18 +226,23 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
-        cpu = cpu_baseline(mc, w, toks, args.cpu_seconds)
+        cpu = (cpu_baseline_memory if memory else cpu_baseline)(mc, w, toks, args.cpu_seconds)
         log(f"cpu baseline {cpu['value']} tokens/s on {cpu['cores']} threads")
 
     line = {
-        "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "metric": METRIC if not memory else "memory-coupled forward tokens/sec at d_r=512,h_slots=8,ctx=256,B=32", "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32" if args.gemm != "bf16" else "bf16-in/f32-acc",
         "data": "synthetic (seeded Xavier weights at spectral norm 0.5, Zipf(1.1) token ids)",
-        "config": {"workload": f"{args.config}: DEQ forward d_r={mc.d} h_slots={mc.H} vocab={mc.V} "
-                               f"d_state={mc.N} B={B} ctx={T}, Picard max {mc.max_iters} tol {mc.eps}, "
-                               f"anderson m={mc.anderson_m}; logits for all positions + arg-max + scan; "
-                               f"GEMM {args.gemm}",
+        "config": {"workload": (f"{args.config}: DEQ forward d_r={mc.d} h_slots={mc.H} vocab={mc.V} "
+                                f"d_state={mc.N} B={B} ctx={T}, Picard max {mc.max_iters} tol {mc.eps}, "
+                                f"anderson m={mc.anderson_m}; logits for all positions + arg-max + scan; "
+                                f"GEMM {args.gemm}") if not memory else
+                               (f"{args.config}-memory: memory-coupled DEQ forward d_r={mc.d} h_slots={mc.H} "
+                                f"vocab={mc.V} B={B} ctx={T} (positions in order, B tokens per solve), "
+                                f"history context + carrier state d_state=1, Picard max {mc.max_iters} tol "
+                                f"{mc.eps}; logits for all positions + arg-max; GEMM {args.gemm}"),
+                   "mode": args.mode,
                    "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
         "roofline": roofline,
         "cpu_baseline": cpu,

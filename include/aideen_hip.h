@@ -216,8 +216,11 @@ int adn_ffn_forward(adn_ctx *ctx, int32_t w_id, int32_t in_id, int32_t out_dim, 
 #define ADN_STAGE_ARGMAX 10      /* greedy arg-max                                     */
 #define ADN_STAGE_SCAN_PREP 11   /* carrier prologue (rms, rank-r bottleneck, B/C)     */
 #define ADN_STAGE_SCAN 12        /* chunked selective scan                             */
-#define ADN_STAGE_READOUT_GEMM 13 /* Y = y + W_out y                                   */
-#define ADN_STAGE_COUNT 14
+#define ADN_STAGE_READOUT_GEMM 13 /* Y = y + W_out y (memory mode: m_t = m + W_out m)  */
+#define ADN_STAGE_HIST_GEMM 14   /* memory mode: u = W_hist m_{t-1}                    */
+#define ADN_STAGE_HIST_CTX 15    /* memory mode: history context gate and clamp        */
+#define ADN_STAGE_TEMPORAL 16    /* memory mode: m = abar m_{t-1} + (1 - abar) x      */
+#define ADN_STAGE_COUNT 17
 #define ADN_PROFILE_MAX_ITERS 256
 
 typedef struct adn_profile {
@@ -225,7 +228,8 @@ typedef struct adn_profile {
     double flops[ADN_STAGE_COUNT];    /* algorithmic FLOPs summed over those launches   */
     double bytes[ADN_STAGE_COUNT];    /* algorithmic (compulsory) HBM bytes             */
     int32_t launches[ADN_STAGE_COUNT];
-    int32_t active[ADN_PROFILE_MAX_ITERS]; /* tokens entering Picard iteration k        */
+    int32_t active[ADN_PROFILE_MAX_ITERS]; /* tokens entering Picard iteration k (memory
+                                           * mode: summed over the positions)            */
     int32_t n_iters;                  /* iterations enqueued (= max_iters)              */
     double total_ms;                  /* first to last event                            */
 } adn_profile;

@@ -10,6 +10,9 @@ import dataclasses
 
 import numpy as np
 import pytest
+# torch (device buffers for the profiled forward) brings its own HIP runtime: it is imported
+# before the library is first loaded so that one runtime serves both
+import torch
 
 from aideen_amd import synth
 from aideen_amd._lib import AdnError
@@ -141,3 +144,30 @@ def test_memory_errors():
     be.upload_weights(w)
     with pytest.raises(AdnError, match="ADN_F_MEMORY"):
         be.decode_greedy(np.array([1, 2], np.int32), 3)
+
+
+def test_memory_profile_counts():
+    """adn_profile_forward in memory mode: the active tokens per iteration, summed over the
+    positions, add up to every token's iteration count; one launch per position and iteration."""
+    log("memory profile")
+    mc, w = mem_model(128, 4, 500)
+    B, T = 3, 9
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=12)
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    dev = torch.device("cuda:0")
+    outs = dict(h_star=torch.empty((B, T, mc.H, mc.d), device=dev),
+                iters=torch.empty((B, T), dtype=torch.int32, device=dev),
+                logits=torch.empty((B, T, mc.V), device=dev),
+                argmax=torch.empty((B, T), dtype=torch.int32, device=dev),
+                scan_y=torch.empty((B, T, mc.H, mc.d), device=dev),
+                scan_state=torch.empty((B, mc.H, mc.d, 1), device=dev))
+    prof = be.profile_forward(torch.from_numpy(toks).to(dev), outputs=outs)
+    iters = outs["iters"].cpu().numpy()
+    assert sum(prof["active"]) == int(iters.sum())
+    assert prof["active"][0] == B * T
+    st = prof["stages"]
+    assert st["qkv_gemm"]["launches"] == T * mc.max_iters
+    assert st["temporal"]["launches"] == T and st["hist_gemm"]["launches"] == T - 1
+    ref = be.forward(toks)
+    np.testing.assert_array_equal(outs["argmax"].cpu().numpy(), ref["argmax"])
