@@ -118,7 +118,9 @@ std::string validate_config(const adn_config &c) {
     if (c.max_batch < 1 || c.max_seq < 1) return "max_batch and max_seq must be >= 1";
     if ((long)c.max_batch * c.max_seq > (1L << 24)) return "max_batch*max_seq must be <= 2^24";
     if (c.anderson_m < 0 || c.anderson_m > 5) return "anderson_m must be in [0, 5]";
-    if (c.flags & ~0x3FFu) return "unknown flag bits";
+    if (c.flags & ~0x7FFu) return "unknown flag bits";
+    if ((c.flags & ADN_F_TOKEN_CARRY) && !(c.flags & ADN_F_MEMORY))
+        return "ADN_F_TOKEN_CARRY needs ADN_F_MEMORY (positions solved in order)";
     if ((c.flags & ADN_F_MEMORY) && c.d_state != 1) return "ADN_F_MEMORY needs d_state == 1";
     if ((c.flags & ADN_F_MEMORY) && (c.flags & ADN_F_SCAN_SELECTIVE))
         return "ADN_F_MEMORY uses the non-selective carrier";
@@ -510,6 +512,10 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
         const float *mprev = t > 0 ? mseq + (long)(t - 1) * hd : r.scan_state_in;
         const long msm = t > 0 ? (long)T * hd : hd;
         b.mem_hist = nullptr;
+        if (t > 0 && (c->cfg.flags & ADN_F_TOKEN_CARRY))  // warm start from h*_{t-1}
+            ADN_HIP(hipMemcpy2DAsync(b.h + (long)t * hd, (size_t)T * hd * sizeof(float), b.h + (long)(t - 1) * hd,
+                                     (size_t)T * hd * sizeof(float), hd * sizeof(float), B, hipMemcpyDeviceToDevice,
+                                     st));
         if (mprev) {
             GemmParams g{};  // u[b][s] = W_hist m_prev[b][s]  (one W_hist for every slot)
             g.role = ROLE_WO;

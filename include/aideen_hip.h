@@ -66,6 +66,10 @@ extern "C" {
  * [B][H][d], scan_state_in the memory before the first token (NULL = none).  eps = 0 runs
  * exactly max_iters steps per token, as the reference's fixed-history solve does. */
 #define ADN_F_MEMORY (1u << 9)
+/* With ADN_F_MEMORY: the solve of position t > 0 starts from h* of position t - 1 of the same
+ * sequence instead of the init rule (token carry, the GPU reference's default warm start:
+ * deq_slot_attn_unified_clean.wgsl:898, deq_bridge.rs:167-173 AIDEEN_DEQ_TOKEN_CARRY). */
+#define ADN_F_TOKEN_CARRY (1u << 10)
 
 /* GEMM arithmetic (adn_config.flags; at most one).  Default: fp32 operands carried as fp16
  * hi+lo pairs on the 16-bit MFMA with three products per multiply (hi.hi + hi.lo + lo.hi),

@@ -383,14 +383,15 @@ void orc_anderson_coeffs(int n, const float *g_in, float *beta) {
  * of updates applied.  Converged tokens are frozen.  Optional Anderson mixing after each step
  * (staged_adjoint_picard_clean.wgsl:1012-1134, gpu_deq.rs:4278-4293): the ring stores the
  * un-mixed Picard iterate; mixing starts at k >= 2 with n_res = min(k, m-1) >= 2. */
+/* warm != 0: h already holds the starting iterate (token carry), init_p is skipped */
 static int solve_p(const prep *p, scratch *sc, const float *x, const float *hist, float *h,
-                   float *resid_trace) {
+                   float *resid_trace, int warm) {
     const orc_cfg *c = &p->c;
     const int d = c->d, H = c->H;
     const size_t hd = (size_t)H * d;
     float *signal = (float *)malloc(sizeof(float) * hd);
     signal_p(p, x, signal);
-    init_p(p, x, signal, h);
+    if (!warm) init_p(p, x, signal, h);
     int iters = 0;
     const int m = c->anderson_m;
     for (int k = 0; k < c->max_iters; ++k) {
@@ -471,7 +472,7 @@ int orc_solve_token(const orc_cfg *c, const orc_weights *w, const float *x, floa
     scratch sc;
     prep_init(&p, c, w);
     scratch_init(&sc, c);
-    int it = solve_p(&p, &sc, x, NULL, h_star, resid_trace);
+    int it = solve_p(&p, &sc, x, NULL, h_star, resid_trace, 0);
     scratch_free(&sc);
     prep_free(&p);
     return it;
@@ -711,7 +712,7 @@ void orc_model_forward(orc_model *mdl, int B, int T, const int32_t *tokens, floa
         for (long t = 0; t < ntok; ++t) {
             const int32_t tok = tokens[t];
             float *h = hs_all + hd * t;
-            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, NULL, h, NULL);
+            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, NULL, h, NULL, 0);
             if (iters) iters[t] = it;
             if (pooled || logits || argmax) {
                 float *lt = logits ? logits + (size_t)V * t : lg;
@@ -823,7 +824,9 @@ void orc_temporal_step(const orc_cfg *c, const orc_weights *w, const float *m_pr
     free(x); free(ab); free(mn); free(wy); free(bn);
 }
 
-/* Memory-coupled forward, the fixed-history reference mode of the trainer (TRAINER:677-720):
+/* Memory-coupled forward, the fixed-history reference mode of the trainer (TRAINER:677-720).
+ * With ORC_F_TOKEN_CARRY the solve of position t > 0 starts from h*_{t-1} of the same sequence
+ * instead of the init rule (the GPU reference's default warm start, UWGSL:898, BRIDGE:167-173):
  * per sequence and token, hist = fixed_hist_ctx(m_{t-1}, signal_t) (zero at the first token
  * unless m_in is given), h* = the Picard solve with hist added (FPMR:1372-1395), then
  * m_t = temporal_step(m_{t-1}, h*).  The solve keeps this library's exit rule (eps = 0 runs
@@ -866,7 +869,10 @@ void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_w
                 const float *x = w->embed + (size_t)tokens[row] * d;
                 signal_p(&p, x, sig);
                 orc_hist_ctx(c, hw, have_m ? m : NULL, sig, hist);
-                const int it = solve_p(&p, &sc, x, hist, h, NULL);
+                /* token carry: h still holds h*_{t-1} of this sequence (UWGSL:898
+                 * should_init_h = t == 0 || !ENABLE_TOKEN_CARRY) */
+                const int warm = (c->flags & ORC_F_TOKEN_CARRY) && t > 0;
+                const int it = solve_p(&p, &sc, x, hist, h, NULL, warm);
                 if (iters) iters[row] = it;
                 if (h_star) memcpy(h_star + hd * row, h, sizeof(float) * hd);
                 orc_temporal_step(c, w, have_m ? m : NULL, h, mn);

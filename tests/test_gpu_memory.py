@@ -67,6 +67,8 @@ MEM_VARIANTS = [
     dict(d=128, H=8, V=1000, qk_bias=True, flags=synth.F_SCORE_CLAMP4),
     dict(d=256, H=4, V=700, strong=False),  # the reference's initial history weights
     dict(d=128, H=4, V=500, sigma=0.7, anderson_m=3),
+    dict(d=128, H=4, V=500, flags=synth.F_TOKEN_CARRY),  # warm start from h*_{t-1}
+    dict(d=256, H=8, V=700, flags=synth.F_TOKEN_CARRY | synth.F_INIT_SIGNAL_RMS, anderson_m=2),
 ]
 
 
@@ -171,3 +173,16 @@ def test_memory_profile_counts():
     assert st["temporal"]["launches"] == T and st["hist_gemm"]["launches"] == T - 1
     ref = be.forward(toks)
     np.testing.assert_array_equal(outs["argmax"].cpu().numpy(), ref["argmax"])
+
+
+def test_token_carry_repeated_token_converges_at_once():
+    """With zero history and the same token at every position, a warm-started solve begins at
+    its own fixed point: one iteration per position after the first, as the oracle pins."""
+    log("token carry repeated token")
+    mc, w = mem_model(128, 4, 500, flags=synth.F_TOKEN_CARRY, eps=1e-5, max_iters=40)
+    w["w_hist"] = np.zeros_like(w["w_hist"])
+    w["hist_slot_scale"] = np.zeros_like(w["hist_slot_scale"])
+    toks = np.full((2, 6), 17, np.int32)
+    got = gpu_memory(mc, w, toks)
+    assert got["iters"][0, 0] > 3
+    assert np.all(got["iters"][:, 1:] == 1)

@@ -600,3 +600,36 @@ def test_memory_forward_continuation_and_independence(oracle_lib):
         assert np.array_equal(np.concatenate([a[k], b[k]], axis=1), full[k]), k
     rev = o.forward_memory(toks[::-1].copy())
     assert np.array_equal(rev["h_star"], full["h_star"][::-1])
+
+
+def test_token_carry_known_answers(oracle_lib):
+    """Token carry (UWGSL:898, BRIDGE:167-173): position t > 0 starts from h*_{t-1}.
+    - a repeated token with zero history starts at its own fixed point, so the first step's
+      residual is already below eps: exactly 1 iteration, and h* moves by less than eps;
+    - without carry the same positions take the cold-start count of position 0;
+    - one position is unaffected; the warm-started fixed point equals the cold one."""
+    mc, w = _mem_model(d=16, H=3, V=40, eps=1e-5, max_iters=60)
+    w0 = dict(w)
+    w0["w_hist"] = np.zeros_like(w["w_hist"])
+    w0["hist_slot_scale"] = np.zeros_like(w["hist_slot_scale"])
+    toks = np.full((2, 5), 7, np.int32)
+    toks[1] = 11
+    cold = oracle(oracle_lib, mc, w0).forward_memory(toks)
+    mcc = dataclasses.replace(mc, flags=mc.flags | synth.F_TOKEN_CARRY)
+    warm = oracle(oracle_lib, mcc, w0).forward_memory(toks)
+    assert np.all(cold["iters"] == cold["iters"][:, :1]) and cold["iters"][0, 0] > 3
+    assert np.array_equal(warm["iters"][:, 0], cold["iters"][:, 0])
+    assert np.all(warm["iters"][:, 1:] == 1)
+    assert np.abs(warm["h_star"][:, 1:] - warm["h_star"][:, :-1]).max() < mc.eps
+    assert np.array_equal(warm["h_star"][:, 0], cold["h_star"][:, 0])
+    # with history and distinct tokens: same fixed points within the contraction bound
+    mct = dataclasses.replace(mc, eps=2e-6, max_iters=200)  # above the fp32 residual floor
+    toks2 = synth.make_tokens("uniform", 2, 6, mc.V, seed=4)
+    a = oracle(oracle_lib, mct, w).forward_memory(toks2)
+    b = oracle(oracle_lib, dataclasses.replace(mct, flags=mct.flags | synth.F_TOKEN_CARRY), w).forward_memory(toks2)
+    assert a["iters"].max() < mct.max_iters and b["iters"].max() < mct.max_iters
+    np.testing.assert_allclose(b["h_star"], a["h_star"], rtol=0, atol=2e-5)
+    assert not np.array_equal(b["iters"], a["iters"])  # the warm start is in effect
+    one = oracle(oracle_lib, dataclasses.replace(mc, flags=mc.flags | synth.F_TOKEN_CARRY), w).forward_memory(toks2[:, :1])
+    ref = oracle(oracle_lib, mc, w).forward_memory(toks2[:, :1])
+    assert np.array_equal(one["h_star"], ref["h_star"])
