@@ -109,6 +109,8 @@ def lib():
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),
         "adn_load_tensor": (C.c_int, [ctx_p, F32P, C.c_int64, I32P]),
         "adn_ffn_forward": (C.c_int, [ctx_p, C.c_int32, C.c_int32, C.c_int32, F32P]),
+        "adn_embed_context": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
+        "adn_embed_context_async": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_profile_forward": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs),
                                           C.POINTER(AdnProfile)]),
     }

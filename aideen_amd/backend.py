@@ -174,6 +174,21 @@ class GpuDeqBackend:
                                     launches=prof.launches[i])
         return dict(stages=stages, active=list(prof.active[:prof.n_iters]), total_ms=prof.total_ms)
 
+    # input pipeline --------------------------------------------------------------------------
+    def embed_context(self, tokens: np.ndarray, max_ctx: int) -> np.ndarray:
+        """``Tokenizer::embed_context`` (tokenizer.rs:133-149) for the window ending at every
+        position (trainer.rs:4690-4696): tokens [B][T] -> queries [B][T][d], an ``s_in``."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        B, T = tokens.shape
+        out = np.zeros((B, T, self.model.d), np.float32)
+        check(lib().adn_embed_context(self._ctx, B, T, _ip(tokens), int(max_ctx), _fp(out)))
+        return out
+
+    def embed_context_async(self, tokens, max_ctx: int, out) -> None:
+        """Device-memory form (torch tensors): enqueue only."""
+        B, T = tokens.shape
+        check(lib().adn_embed_context_async(self._ctx, B, T, _dev_i(tokens), int(max_ctx), _dev_f(out)))
+
     # reference-named conveniences ---------------------------------------------------------
     def run_forward_deq(self, batch, seq, max_iters, eps, damping, s_in):
         """``run_forward_deq`` (gpu_deq.rs:3687-3727): H_next [B*T*H*d] and iteration counts."""

@@ -133,6 +133,11 @@ void launch_transpose(const float *src, int rows, int cols, long batch, float *d
 void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
 // ---- memory-coupled solve (memory.hip) -----------------------------------------------------
 // act[0] = tokens (b, t) = b*T + t for b < B, cnt[0] = B, cnt[1] = 0.
+// embed_context of the window ending at every position; tot0/tot1 hold
+// B * embed_context_chunks(T) * d doubles each.
+long embed_context_chunks(int T);
+void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
+                          double *tot1, float *out, unsigned *err, hipStream_t st);
 void launch_mem_begin(const SolveBuffers &b, int B, int T, int t, hipStream_t st);
 // hist [B][H][d] holds u = W_hist m_prev on entry; becomes the history context.
 void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm, const float *signal, int B,

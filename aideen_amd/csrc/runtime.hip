@@ -47,6 +47,8 @@ struct adn_ctx {
     float *b_delta = nullptr, *w_kw = nullptr, *w_vw = nullptr, *w_b = nullptr, *w_c = nullptr;
     float *w_cat = nullptr;  // [H][r + 2N][d] = [W_kw^T; W_B; W_C] per slot (carrier projections)
     float *w_hist = nullptr, *hist_scale = nullptr, *hist_gate = nullptr;  // memory-coupled solve
+    double *ctx_tot = nullptr;  // embed_context chunk totals (2 x ctx_tot_n doubles)
+    long ctx_tot_n = 0;
 
     // split-precision copies of the GEMM weights (hi/lo halves of w * scale)
     struct Split {
@@ -1066,6 +1068,68 @@ int adn_ffn_forward(adn_ctx *c, int32_t w_id, int32_t in_id, int32_t out_dim, fl
         return hip_fail(e);
     }
     return ADN_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int check_embed_context(adn_ctx *c, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
+                        const float *out) {
+    if (!c || !tokens || !out) return fail(ADN_E_INVALID, "null argument");
+    if (!c->has_weights) return fail(ADN_E_NO_WEIGHTS, "embed_context before adn_upload_weights");
+    if (batch < 1 || seq < 1) return fail(ADN_E_INVALID, "batch and seq must be >= 1");
+    if ((long)batch * seq > c->cap_tok) return fail(ADN_E_CAPACITY, "batch*seq exceeds the context capacity");
+    if (max_ctx < 1) return fail(ADN_E_INVALID, "max_ctx must be >= 1");
+    return ADN_OK;
+}
+
+void enqueue_embed_context(adn_ctx *c, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
+                           float *out) {
+    const long need = (long)batch * embed_context_chunks(seq) * c->D.d;
+    if (need > c->ctx_tot_n) {  // grows to the largest request (the old block is freed with the context)
+        c->ctx_tot = (double *)dmalloc(c, 2 * (size_t)need * sizeof(double));
+        c->ctx_tot_n = need;
+    }
+    launch_embed_context(c->embed, c->D.d, c->D.V, tokens, batch, seq, max_ctx, c->ctx_tot, c->ctx_tot + need, out,
+                         c->d_err, c->stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int adn_embed_context_async(adn_ctx *c, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
+                            float *out) {
+    int rc = check_embed_context(c, batch, seq, tokens, max_ctx, out);
+    if (rc) return rc;
+    try {
+        enqueue_embed_context(c, batch, seq, tokens, max_ctx, out);
+        ADN_HIP(hipGetLastError());
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_embed_context(adn_ctx *c, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx, float *out) {
+    int rc = check_embed_context(c, batch, seq, tokens, max_ctx, out);
+    if (rc) return rc;
+    const long n = (long)batch * seq;
+    for (long i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c->D.V) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
+    try {
+        if (!c->tok_dev) c->tok_dev = (int32_t *)dmalloc(c, (size_t)c->cap_tok * sizeof(int32_t));
+        ADN_HIP(hipMemcpyAsync(c->tok_dev, tokens, n * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+        float *dout = staging_f(c, 19, (size_t)n * c->D.d * sizeof(float));
+        enqueue_embed_context(c, batch, seq, c->tok_dev, max_ctx, dout);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(out, dout, (size_t)n * c->D.d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
 }
 
 int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_profile *prof) {

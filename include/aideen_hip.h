@@ -205,6 +205,19 @@ int adn_load_tensor(adn_ctx *ctx, const float *data, int64_t n, int32_t *id);
  * in_dim = element count of the input tensor; y is host memory [out_dim]. */
 int adn_ffn_forward(adn_ctx *ctx, int32_t w_id, int32_t in_id, int32_t out_dim, float *y);
 
+/* --- input pipeline ------------------------------------------------------------------
+ * Tokenizer::embed_context (tokenizer.rs:133-149) for the window ending at every position, as
+ * the trainer builds the query of position i (trainer.rs:4690-4696: context =
+ * tokens[max(0, i - max_ctx + 1) ..= i]): out[b][i] = r / |r| (r when |r| <= 1e-6),
+ * r = sum over the window of E[tok] * (pos + 1) / len.  tokens [B][T], out [B][T][d]; the
+ * result is an adn_run.s_in.  Needs uploaded weights (the embedding table); B * T within the
+ * context capacity; max_ctx >= 1.  adn_embed_context takes host memory and blocks;
+ * adn_embed_context_async takes device memory and only enqueues on the context stream. */
+int adn_embed_context(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
+                      float *out);
+int adn_embed_context_async(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
+                            float *out);
+
 /* --- measurement (the reference's AIDEEN_DEQ_FORWARD_PROFILE per-pass timing,
  *     deq_bridge.rs:2234-2380, and GPU timestamp queries, gpu_deq.rs:490-570) ------------- */
 #define ADN_STAGE_SIGNAL_GEMM 0  /* signal = W_in x (embedding gather fused)          */

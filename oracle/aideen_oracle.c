@@ -913,6 +913,35 @@ void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int3
 /* trait surfaces                                                             */
 /* ------------------------------------------------------------------------- */
 
+/* tokenizer.rs:133-149 embed_context, one window per position (TRAINER:4690-4696).  The reference
+ * evaluates result += emb * pos_weight in window order with pos_weight = (pos + 1) as f32 /
+ * len as f32 (f32 division), then divides by result.norm() when it exceeds 1e-6.  The norm's
+ * summation order (nalgebra) is restated as a sequential sum of squares: ulp-level, unpinned. */
+void orc_embed_context(int d, const float *embed, int B, int T, const int32_t *tokens, int ctx, float *out) {
+    float *r = (float *)malloc(sizeof(float) * d);
+    for (int b = 0; b < B; ++b) {
+        for (int i = 0; i < T; ++i) {
+            const int start = i + 1 > ctx ? i + 1 - ctx : 0;
+            const int len = i + 1 - start;
+            for (int j = 0; j < d; ++j) r[j] = 0.0f;
+            for (int pos = 0; pos < len; ++pos) {
+                const float w = (float)(pos + 1) / (float)len;
+                const float *e = embed + (size_t)tokens[(size_t)b * T + start + pos] * d;
+                for (int j = 0; j < d; ++j) {
+                    const float t = e[j] * w;
+                    r[j] = r[j] + t;
+                }
+            }
+            float ss = 0.0f;
+            for (int j = 0; j < d; ++j) ss += r[j] * r[j];
+            const float nrm = sqrtf(ss);
+            float *o = out + ((size_t)b * T + i) * d;
+            for (int j = 0; j < d; ++j) o[j] = nrm > 1e-6f ? r[j] / nrm : r[j];
+        }
+    }
+    free(r);
+}
+
 /* gpu_backend.rs:18-56 CpuBlockBackend::fpm_batch_step (ZOH, h_prev = 0). */
 void orc_zoh_step(int d, const float *x, const float *dt, const float *a, const float *b,
                   const float *c, float *y) {

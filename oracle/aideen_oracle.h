@@ -113,6 +113,10 @@ void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int3
                        int n_new, int32_t *out_tokens, int nthreads);
 
 /* --- other trait surfaces --------------------------------------------------- */
+/* tokenizer.rs:133-149 embed_context for the window ending at every position (TRAINER:4690-4696:
+ * context = tokens[max(0, i - ctx + 1) ..= i]): out[b][i] = r / |r| (r itself when |r| <= 1e-6),
+ * r = sum over the window of E[tok] * ((pos + 1) / len), pos = index in the window. */
+void orc_embed_context(int d, const float *embed, int B, int T, const int32_t *tokens, int ctx, float *out);
 void orc_zoh_step(int d, const float *x, const float *dt, const float *a, const float *b,
                   const float *c, float *y);
 void orc_gemv_colmajor(const float *w, const float *x, int in_dim, int out_dim, float *y);

@@ -87,6 +87,7 @@ def lib():
                                          C.c_int, C.c_int, I32P, F32P, F32P, F32P, F32P, I32P, I32P,
                                          F32P, C.c_int]
         L.orc_zoh_step.argtypes = [C.c_int, F32P, F32P, F32P, F32P, F32P, F32P]
+        L.orc_embed_context.argtypes = [C.c_int, F32P, C.c_int, C.c_int, I32P, C.c_int, F32P]
         L.orc_gemv_colmajor.argtypes = [F32P, F32P, C.c_int, C.c_int, F32P]
         _lib = L
     return _lib
@@ -316,3 +317,15 @@ def gemv_colmajor(w, x, out_dim):
     y = np.zeros(out_dim, np.float32)
     lib().orc_gemv_colmajor(fp(w), fp(x), x.size, out_dim, fp(y))
     return y
+
+
+def embed_context(embed: np.ndarray, tokens: np.ndarray, ctx: int) -> np.ndarray:
+    """tokenizer.rs:133-149 embed_context for the window ending at every position of every
+    sequence; tokens [B][T] -> [B][T][d]."""
+    embed = np.ascontiguousarray(embed, np.float32)
+    tokens = np.ascontiguousarray(tokens, np.int32)
+    B, T = tokens.shape
+    d = embed.shape[1]
+    out = np.zeros((B, T, d), np.float32)
+    lib().orc_embed_context(d, fp(embed), B, T, ip(tokens), ctx, fp(out))
+    return out

@@ -633,3 +633,61 @@ def test_token_carry_known_answers(oracle_lib):
     one = oracle(oracle_lib, dataclasses.replace(mc, flags=mc.flags | synth.F_TOKEN_CARRY), w).forward_memory(toks2[:, :1])
     ref = oracle(oracle_lib, mc, w).forward_memory(toks2[:, :1])
     assert np.array_equal(one["h_star"], ref["h_star"])
+
+
+# ------------------------------------------------------------------------------------------
+# embed_context (tokenizer.rs:133-149), one window per position (TRAINER:4690-4696)
+# ------------------------------------------------------------------------------------------
+def _embed_context_f64(E, toks, ctx):
+    B, T = toks.shape
+    out = np.zeros((B, T, E.shape[1]))
+    for b in range(B):
+        for i in range(T):
+            s = max(0, i - ctx + 1)
+            win = toks[b, s:i + 1]
+            w = np.arange(1, len(win) + 1, dtype=np.float64) / len(win)
+            r = (E[win].astype(np.float64) * w[:, None]).sum(0)
+            n = np.sqrt((r * r).sum())
+            out[b, i] = r / n if n > 1e-6 else r
+    return out
+
+
+def test_embed_context_closed_forms(oracle_lib):
+    rng = np.random.default_rng(0)
+    d, V = 24, 50
+    E = rng.standard_normal((V, d)).astype(np.float32)
+    # one token: the normalised embedding row
+    got = oracle_lib.embed_context(E, np.array([[7]], np.int32), 4)
+    np.testing.assert_allclose(got[0, 0], E[7] / np.linalg.norm(E[7].astype(np.float64)), rtol=1e-6, atol=1e-7)
+    # two tokens: weights 1/2 and 2/2 (the later token weighs more)
+    got = oracle_lib.embed_context(E, np.array([[3, 9]], np.int32), 4)
+    r = 0.5 * E[3].astype(np.float64) + E[9]
+    np.testing.assert_allclose(got[0, 1], r / np.linalg.norm(r), rtol=1e-6, atol=1e-7)
+    # ctx = 1: every position is its own normalised row
+    toks = rng.integers(0, V, (2, 9)).astype(np.int32)
+    got = oracle_lib.embed_context(E, toks, 1)
+    ref = E[toks] / np.linalg.norm(E[toks].astype(np.float64), axis=-1, keepdims=True)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
+    # a zero row stays below the 1e-6 norm threshold: returned unnormalised (zero)
+    E0 = E.copy()
+    E0[5] = 0
+    assert np.array_equal(oracle_lib.embed_context(E0, np.array([[5, 5]], np.int32), 4), np.zeros((1, 2, d), np.float32))
+
+
+def test_embed_context_windows_match_float64(oracle_lib):
+    """Prefix windows while i < ctx, sliding windows after; scale invariance of the output."""
+    rng = np.random.default_rng(1)
+    d, V = 32, 80
+    E = (0.01 * rng.standard_normal((V, d))).astype(np.float32)
+    toks = rng.integers(0, V, (3, 40)).astype(np.int32)
+    for ctx in (1, 5, 16, 40, 64):
+        got = oracle_lib.embed_context(E, toks, ctx)
+        np.testing.assert_allclose(got, _embed_context_f64(E, toks, ctx), rtol=0, atol=3e-6)
+    # the window ending at i depends only on tokens[i-ctx+1 ..= i]
+    t2 = toks.copy()
+    t2[:, :10] = (t2[:, :10] + 1) % V
+    a = oracle_lib.embed_context(E, toks, 8)
+    b2 = oracle_lib.embed_context(E, t2, 8)
+    assert np.array_equal(a[:, 17:], b2[:, 17:]) and not np.array_equal(a[:, :10], b2[:, :10])
+    # scaling E by a power of two leaves the normalised output unchanged (exactly)
+    assert np.array_equal(oracle_lib.embed_context(4 * E, toks, 8), a)
