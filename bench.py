@@ -92,6 +92,63 @@ def cpu_baseline_memory(mc, w, toks, seconds: float):
                 seconds=round(t2, 2))
 
 
+def bench_embed(args, be, mc, w, toks, dev, torch) -> int:
+    """embed_context for every position of the NS batch (window = ctx = T): the input pipeline's
+    GPU part.  HBM-bound: compulsory bytes are the token ids, one embedding row read and one
+    query row written per position."""
+    B, T = toks.shape
+    ctx = T
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    tok_d = torch.from_numpy(toks).to(dev)
+    out = torch.empty((B, T, mc.d), dtype=torch.float32, device=dev)
+    for _ in range(args.warmup):
+        be.embed_context_async(tok_d, ctx, out)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        be.embed_context_async(tok_d, ctx, out)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    tok_s = B * T / (ms / 1e3)
+    byts = B * T * (4 + 8 * mc.d)
+    gbs = byts / ms / 1e6
+    log(f"embed_context: {ms * 1e3:.1f} us per call, {tok_s:,.0f} positions/s, {gbs:.0f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import pyoracle
+        pyoracle.build()
+        n = max(1, min(B, int(args.cpu_seconds)))
+        t0 = time.perf_counter()
+        pyoracle.embed_context(w["embed"], toks[:1], ctx)
+        t1 = time.perf_counter() - t0
+        n = int(max(1, min(B, args.cpu_seconds / max(t1, 1e-6))))
+        t0 = time.perf_counter()
+        pyoracle.embed_context(w["embed"], toks[:n], ctx)
+        t2 = time.perf_counter() - t0
+        cpu = dict(value=round(n * T / t2, 1), unit="positions/s", cores=1, kind="port",
+                   sample=f"{n} of the {B} sequences ({n * T} positions), one thread, {t2:.1f} s")
+    line = {
+        "metric": f"embed_context positions/sec at d_r={mc.d},ctx={ctx},B={B}", "value": round(tok_s, 1),
+        "unit": "positions/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (f64 prefix sums)", "data": "synthetic (closed-form embedding table, Zipf(1.1) token ids)",
+        "config": {"workload": f"{args.config}-embed: embed_context of the window ending at every position, "
+                               f"B={B} T={T} ctx={ctx} d_r={mc.d} vocab={mc.V}", "mode": "embed",
+                   "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
+        "roofline": dict(kernel="k_ctx_chunks + k_ctx_window", bound="hbm", achieved=round(gbs, 1),
+                         peak=PEAK_HBM_GBS, unit="GB/s", frac=round(gbs / PEAK_HBM_GBS, 4), traffic=None,
+                         basis="token ids + one embedding row read + one query row written per position",
+                         bytes_per_call=byts),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,10 +159,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates HBM byte counters)")
-    ap.add_argument("--mode", choices=["forward", "memory"], default="forward",
+    ap.add_argument("--mode", choices=["forward", "memory", "embed"], default="forward",
                     help="forward: the canonical (token-parallel) forward, the headline metric; memory: "
                          "the memory-coupled forward (positions in order, history context and carrier "
-                         "state between them) on the same shape with a one-dimensional carrier state")
+                         "state between them) on the same shape with a one-dimensional carrier state; "
+                         "embed: embed_context queries for every position (window = ctx)")
     ap.add_argument("--eps", type=float, default=None, help="override the Picard tolerance")
     ap.add_argument("--gemm", choices=list(GEMM_MODES), default="f16x3",
                     help="GEMM arithmetic (f16x3 / bf16x3 / fp32 are fp32-accurate; bf16 is the "
@@ -142,6 +200,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     be = GpuDeqBackend(mc, B, T)
     be.upload_weights(w)
+    if args.mode == "embed":
+        return bench_embed(args, be, mc, w, toks, dev, torch)
     # a dedicated (default-priority) stream: the library's kernels and the timing events share it
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
