@@ -109,6 +109,15 @@ def lib():
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),
         "adn_load_tensor": (C.c_int, [ctx_p, F32P, C.c_int64, I32P]),
         "adn_ffn_forward": (C.c_int, [ctx_p, C.c_int32, C.c_int32, C.c_int32, F32P]),
+        "adn_aidn_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+        "adn_aidn_close": (None, [C.c_void_p]),
+        "adn_aidn_config_get": (C.c_int, [C.c_void_p, C.c_void_p]),
+        "adn_aidn_count": (C.c_int, [C.c_void_p, I32P, I32P]),
+        "adn_aidn_name": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_char_p)]),
+        "adn_aidn_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(F32P), C.POINTER(C.c_int64)]),
+        "adn_aidn_metadata": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+        "adn_aidn_weights": (C.c_int, [C.c_void_p, C.POINTER(AdnWeights), C.POINTER(AdnConfig),
+                                       C.POINTER(AdnRun)]),
         "adn_embed_context": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_embed_context_async": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_profile_forward": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs),

@@ -78,6 +78,25 @@ class GpuDeqBackend:
                 return None
             raise
 
+    @classmethod
+    def from_aidn(cls, path: str, max_batch: int = 1, max_seq: Optional[int] = None, flags: int = 0,
+                  anderson_m: int = 0) -> "GpuDeqBackend":
+        """A context for a reference checkpoint (the trainer's load_full, trainer.rs:6598-6680):
+        the library's loader maps the file onto its weights; the model's max_deq_iters,
+        deq_epsilon and damping become the run defaults."""
+        import dataclasses
+        from .aidn import AidnModel
+        from .synth import ModelConfig
+        m = AidnModel(path)
+        w, cfg, run = m.weights()
+        m.close()
+        mc = ModelConfig(d=cfg["d_r"], H=cfg["h_slots"], V=cfg["vocab"], N=cfg["d_state"], r=cfg["rank"],
+                         flags=flags, max_iters=run["max_iters"], eps=run["eps"], beta=run["damping"],
+                         anderson_m=anderson_m)
+        be = cls(mc, max_batch, max_seq or cfg["max_seq"])
+        be.upload_weights(w)
+        return be
+
     def close(self) -> None:
         if self._ctx:
             lib().adn_destroy(self._ctx)

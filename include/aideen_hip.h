@@ -218,6 +218,36 @@ int adn_embed_context(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *t
 int adn_embed_context_async(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
                             float *out);
 
+/* --- .aidn checkpoints (AidenModel::load, aideen-core/src/model.rs:39-47) ---------------------
+ * bincode 1.3 of { config: ArchitectureConfig, weights: name -> [f32], metadata: name -> string }.
+ * Host-only: no device is touched.  adn_aidn_weights maps the reference's exported names and
+ * layouts (FixedPointMemoryReasoning::export_weights, fixed_point_memory_reasoning.rs:626-784;
+ * LmHead::export_weights, lm_head.rs:169-188; Trainer::save_full, trainer.rs:6472-6530) onto
+ * adn_weights: the CPU model's shared matrices are replicated per slot, tokenizer.embeddings
+ * (nalgebra column-major) is transposed to [V][d], W_x gives its diagonal.  Its arrays stay valid
+ * until adn_aidn_close.  It also proposes an adn_config (d_r, h_slots, vocab, d_state = 1,
+ * rank = 32, max_seq = ctx_len, the CPU semantics flags = 0) and the run parameters
+ * (max_iters = max_deq_iters, eps = deq_epsilon, damping = reasoning.damping). */
+typedef struct adn_aidn adn_aidn;
+typedef struct adn_aidn_config { /* ArchitectureConfig, aideen-core/src/state.rs:7-35 */
+    int64_t d_m, d_r, d_c, d_e, d_sim, h_slots, vocab_size, ctx_len, max_deq_iters;
+    float deq_epsilon;
+    int64_t adj_iters;
+    int32_t train_deq;
+    float deq_grad_scale;
+    int64_t renorm_every_steps, num_samples;
+    float weight_decay;
+} adn_aidn_config;
+int adn_aidn_open(const char *path, adn_aidn **out);
+void adn_aidn_close(adn_aidn *model);
+int adn_aidn_config_get(const adn_aidn *model, adn_aidn_config *out);
+int adn_aidn_count(const adn_aidn *model, int32_t *n_weights, int32_t *n_metadata);
+int adn_aidn_name(const adn_aidn *model, int32_t i, const char **name); /* i-th weight, file order */
+/* AidenModel::get_weight (model.rs:55-57): *data = NULL and *count = 0 when absent */
+int adn_aidn_tensor(const adn_aidn *model, const char *name, const float **data, int64_t *count);
+int adn_aidn_metadata(const adn_aidn *model, const char *key, const char **value); /* NULL if absent */
+int adn_aidn_weights(adn_aidn *model, adn_weights *w, adn_config *cfg, adn_run *run);
+
 /* --- measurement (the reference's AIDEEN_DEQ_FORWARD_PROFILE per-pass timing,
  *     deq_bridge.rs:2234-2380, and GPU timestamp queries, gpu_deq.rs:490-570) ------------- */
 #define ADN_STAGE_SIGNAL_GEMM 0  /* signal = W_in x (embedding gather fused)          */
