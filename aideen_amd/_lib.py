@@ -109,6 +109,13 @@ def lib():
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),
         "adn_load_tensor": (C.c_int, [ctx_p, F32P, C.c_int64, I32P]),
         "adn_ffn_forward": (C.c_int, [ctx_p, C.c_int32, C.c_int32, C.c_int32, F32P]),
+        "adn_tokenizer_load": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+        "adn_tokenizer_free": (None, [C.c_void_p]),
+        "adn_tokenizer_vocab_size": (C.c_int32, [C.c_void_p]),
+        "adn_tokenizer_encode": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int64, I32P, C.c_int64,
+                                           C.POINTER(C.c_int64)]),
+        "adn_tokenizer_decode": (C.c_int, [C.c_void_p, I32P, C.c_int64, C.c_char_p, C.c_int64,
+                                           C.POINTER(C.c_int64)]),
         "adn_aidn_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
         "adn_aidn_close": (None, [C.c_void_p]),
         "adn_aidn_config_get": (C.c_int, [C.c_void_p, C.c_void_p]),

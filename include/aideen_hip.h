@@ -218,6 +218,23 @@ int adn_embed_context(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *t
 int adn_embed_context_async(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
                             float *out);
 
+/* --- byte-level BPE (Tokenizer::encode / decode, tokenizer.rs:94-116, which run the HF
+ *     `tokenizers` crate on aideen-backbone/tokenizer.json) --------------------------------------
+ * Host-only.  adn_tokenizer_load reads a tokenizer.json with a BPE model, the byte-level
+ * pre-tokenizer (no prefix space) and no normalizer; anything else is reported.  encode is
+ * encode(text, add_special_tokens = true): text is UTF-8 (len bytes; invalid UTF-8 is
+ * ADN_E_INVALID), *n receives the id count, ADN_E_CAPACITY when it exceeds cap.  decode is
+ * decode(ids, skip_special_tokens = true): ids without a token are skipped, invalid UTF-8 in the
+ * byte stream becomes U+FFFD, *len receives the byte length (not NUL-terminated),
+ * ADN_E_CAPACITY when it exceeds cap.  One tokenizer may be used from several threads. */
+typedef struct adn_tokenizer adn_tokenizer;
+int adn_tokenizer_load(const char *tokenizer_json_path, adn_tokenizer **out);
+void adn_tokenizer_free(adn_tokenizer *tok);
+int32_t adn_tokenizer_vocab_size(const adn_tokenizer *tok); /* get_vocab_size(true) */
+int adn_tokenizer_encode(adn_tokenizer *tok, const char *text, int64_t len, int32_t *ids, int64_t cap, int64_t *n);
+int adn_tokenizer_decode(const adn_tokenizer *tok, const int32_t *ids, int64_t count, char *text, int64_t cap,
+                         int64_t *len);
+
 /* --- .aidn checkpoints (AidenModel::load, aideen-core/src/model.rs:39-47) ---------------------
  * bincode 1.3 of { config: ArchitectureConfig, weights: name -> [f32], metadata: name -> string }.
  * Host-only: no device is touched.  adn_aidn_weights maps the reference's exported names and
