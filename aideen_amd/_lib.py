@@ -109,6 +109,8 @@ def lib():
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),
         "adn_load_tensor": (C.c_int, [ctx_p, F32P, C.c_int64, I32P]),
         "adn_ffn_forward": (C.c_int, [ctx_p, C.c_int32, C.c_int32, C.c_int32, F32P]),
+        "adn_adjoint": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, C.c_int32, C.c_float, F32P, F32P]),
+        "adn_adjoint_async": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, C.c_int32, C.c_float, F32P, F32P]),
         "adn_tokenizer_load": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
         "adn_tokenizer_free": (None, [C.c_void_p]),
         "adn_tokenizer_vocab_size": (C.c_int32, [C.c_void_p]),

@@ -208,6 +208,27 @@ class GpuDeqBackend:
         B, T = tokens.shape
         check(lib().adn_embed_context_async(self._ctx, B, T, _dev_i(tokens), int(max_ctx), _dev_f(out)))
 
+    # backward ----------------------------------------------------------------------------------
+    def adjoint(self, dl: np.ndarray, iters: int, damping: Optional[float] = None,
+                h_star: Optional[np.ndarray] = None):
+        """The clean adjoint Picard for the tokens of the most recent forward (gpu_deq.rs:4736-4975):
+        dl [B][T][d] = dL/d pooled h* -> (v [B][T][H][d], source gradient [B][T][d])."""
+        m = self.model
+        dl = np.ascontiguousarray(dl, np.float32)
+        lead = dl.shape[:-1]
+        ntok = int(np.prod(lead))
+        v = np.zeros(lead + (m.H, m.d), np.float32)
+        src = np.zeros(lead + (m.d,), np.float32)
+        hs = None if h_star is None else np.ascontiguousarray(h_star, np.float32)
+        check(lib().adn_adjoint(self._ctx, ntok, _fp(hs), _fp(dl), int(iters),
+                                m.beta if damping is None else float(damping), _fp(v), _fp(src)))
+        return v, src
+
+    def adjoint_async(self, ntok: int, dl, iters: int, damping: float, v_out=None, src_out=None,
+                      h_star=None) -> None:
+        check(lib().adn_adjoint_async(self._ctx, int(ntok), _dev_f(h_star), _dev_f(dl), int(iters), float(damping),
+                                      _dev_f(v_out), _dev_f(src_out)))
+
     # reference-named conveniences ---------------------------------------------------------
     def run_forward_deq(self, batch, seq, max_iters, eps, damping, s_in):
         """``run_forward_deq`` (gpu_deq.rs:3687-3727): H_next [B*T*H*d] and iteration counts."""

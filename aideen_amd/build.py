@@ -16,7 +16,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libaideen_hip.so")
-SOURCES = ["gemm.hip", "gemm_split.hip", "deq.hip", "memory.hip", "embed.hip", "head.hip", "scan.hip", "misc.hip",
+SOURCES = ["gemm.hip", "gemm_split.hip", "deq.hip", "memory.hip", "embed.hip", "adjoint.hip", "head.hip", "scan.hip", "misc.hip",
            "runtime.hip", "aidn.cpp", "bpe.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

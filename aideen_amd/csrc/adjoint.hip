@@ -1,0 +1,157 @@
+// Clean adjoint Picard, the reference's backward for the DEQ solve
+// (staged_adjoint_picard_clean.wgsl:143-337; driver gpu_deq.rs:4736-4975).  Per (token, slot) row,
+// with pre = signal + h* (the forward's stored signal and fixed point) and rhs = dl[t] / H
+// (dl = dL/d pooled h*):
+//   v_0 = rhs,   v_{k+1} = rhs + N^T(beta v_k) + (1 - beta) v_k,
+//   N^T(u)_i = (g_i / rms) u_i - pre_i (sum_j u_j g_j pre_j) / (d rms^3),  rms = sqrt(mean pre^2 + 1e-6)
+// (the RMSNorm vector-Jacobian product; attention is left out of this adjoint, as in the
+// reference), optionally Anderson-mixed per token after every step (the forward's mixing kernel);
+// then the source gradient src[t] = sum over slots of N^T(beta v*).
+//   k_adj_prep:   pre, the row's 1/rms and 1/(d rms^3), and v_0 (one wave per row)
+//   k_adj_step:   one Picard step (one wave per row; pre is reused, only the coefficient reduces)
+//   k_adj_source: per token, the slots' N^T(beta v*) summed in slot order
+#include "kernels.h"
+
+namespace adn {
+
+namespace {
+
+constexpr int AW = 4;  // waves per block
+
+template <int E>
+__global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, const float *signal, const float *h_star,
+                                                       const float *dl, int rows, float *pre, float *terms,
+                                                       float *v0) {
+    constexpr int d = 64 * E;
+    const int row = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int t = row / H;
+    const long o = (long)row * d;
+    const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        const float p = signal[o + i] + 1.0f * h_star[o + i];
+        pre[o + i] = p;
+        ss += p * p;
+        v0[o + i] = dl[(long)t * d + i] * rhs_scale;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) {
+        const float rms = sqrtf(ss * (1.0f / (float)d) + 1.0e-6f);
+        terms[2 * row] = 1.0f / fmaxf(rms, 1.0e-6f);
+        terms[2 * row + 1] = 1.0f / fmaxf((float)d * rms * rms * rms, 1.0e-6f);
+    }
+}
+
+template <int E>
+__global__ __launch_bounds__(64 * AW) void k_adj_step(int H, const float *pre, const float *terms,
+                                                       const float *g, const float *dl, int rows, float beta,
+                                                       const float *v, float *vn) {
+    constexpr int d = 64 * E;
+    const int row = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int t = row / H;
+    const long o = (long)row * d;
+    const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
+    float pv[E], vv[E], gv[E];
+    float cf = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        pv[e] = pre[o + i];
+        vv[e] = v[o + i];
+        gv[e] = g[i];
+        cf += beta * vv[e] * gv[e] * pv[e];
+    }
+    const float inv_rms = terms[2 * row];
+    const float cs = wave_sum(cf) * terms[2 * row + 1];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        const float ng = (gv[e] * inv_rms) * (beta * vv[e]) - pv[e] * cs;
+        vn[o + i] = dl[(long)t * d + i] * rhs_scale + (1.0f * ng + (1.0f - beta) * vv[e]);
+    }
+}
+
+template <int E>
+__global__ __launch_bounds__(64 * AW) void k_adj_source(int H, const float *pre, const float *terms,
+                                                         const float *g, int ntok, float beta, const float *v,
+                                                         float *src) {
+    constexpr int d = 64 * E;
+    const int t = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= ntok) return;
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = 0.0f;
+    for (int s = 0; s < H; ++s) {
+        const int row = t * H + s;
+        const long o = (long)row * d;
+        float pv[E], up[E];
+        float cf = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = lane + 64 * e;
+            pv[e] = pre[o + i];
+            up[e] = beta * v[o + i];
+            cf += up[e] * g[i] * pv[e];
+        }
+        const float inv_rms = terms[2 * row];
+        const float cs = wave_sum(cf) * terms[2 * row + 1];
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] = acc[e] + ((g[lane + 64 * e] * inv_rms) * up[e] - pv[e] * cs);
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) src[(long)t * d + lane + 64 * e] = acc[e];
+}
+
+__global__ void k_iota(int32_t *a, int n, int32_t *cnt) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) a[i] = i;
+    if (i == 0) cnt[0] = n;
+}
+
+template <int E>
+const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
+    const int rows = a.ntok * D.H;
+    const dim3 rg((unsigned)((rows + AW - 1) / AW)), blk(64 * AW);
+    float *v = a.v0, *vn = a.v1;
+    hipLaunchKernelGGL(k_adj_prep<E>, rg, blk, 0, st, D.H, a.signal, a.h_star, a.dl, rows, a.pre, a.terms, v);
+    SolveBuffers b = a.sb;
+    if (a.anderson_m > 0) {
+        b.act[0] = a.act;
+        b.cnt = a.cnt;
+        hipLaunchKernelGGL(k_iota, dim3((unsigned)((a.ntok + 255) / 256)), dim3(256), 0, st, a.act, a.ntok, a.cnt);
+    }
+    for (int k = 0; k < a.iters; ++k) {
+        hipLaunchKernelGGL(k_adj_step<E>, rg, blk, 0, st, D.H, a.pre, a.terms, a.g, a.dl, rows, a.beta, v, vn);
+        if (a.anderson_m > 0) {  // store the new iterate, mix from the third step (per token)
+            b.h = vn;
+            launch_anderson(D, b, 0, a.ntok, a.ntok, k, a.anderson_m, st);
+        }
+        float *sw = v;
+        v = vn;
+        vn = sw;
+    }
+    if (a.src)
+        hipLaunchKernelGGL(k_adj_source<E>, dim3((unsigned)((a.ntok + AW - 1) / AW)), blk, 0, st, D.H, a.pre,
+                           a.terms, a.g, a.ntok, a.beta, v, a.src);
+    return v;
+}
+
+}  // namespace
+
+const float *launch_adjoint(const Dims &D, const AdjointArgs &a, hipStream_t st) {
+    switch (D.d) {
+        case 64: return adj_run<1>(D, a, st);
+        case 128: return adj_run<2>(D, a, st);
+        case 256: return adj_run<4>(D, a, st);
+        case 512: return adj_run<8>(D, a, st);
+        case 1024: return adj_run<16>(D, a, st);
+        case 2048: return adj_run<32>(D, a, st);
+        default: return nullptr;  // rejected at context creation
+    }
+}
+
+}  // namespace adn

@@ -138,6 +138,18 @@ void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
 long embed_context_chunks(int T);
 void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
                           double *tot1, float *out, unsigned *err, hipStream_t st);
+// Clean adjoint Picard for ntok tokens (rows = ntok * H of d floats); scratch pre, v0, v1 hold
+// rows * d floats, terms 2 * rows.  Returns the buffer (v0 or v1) holding the final iterate.
+struct AdjointArgs {
+    int ntok, iters, anderson_m;
+    float beta;
+    const float *signal, *h_star, *dl, *g;  // [ntok][H][d], [ntok][H][d], [ntok][d], [d]
+    float *pre, *terms, *v0, *v1;
+    float *src;                             // [ntok][d] or null
+    SolveBuffers sb;                        // its Anderson ring
+    int32_t *act, *cnt;                     // token list and count for the Anderson kernel
+};
+const float *launch_adjoint(const Dims &D, const AdjointArgs &a, hipStream_t st);
 void launch_mem_begin(const SolveBuffers &b, int B, int T, int t, hipStream_t st);
 // hist [B][H][d] holds u = W_hist m_prev on entry; becomes the history context.
 void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm, const float *signal, int B,

@@ -47,6 +47,8 @@ struct adn_ctx {
     float *b_delta = nullptr, *w_kw = nullptr, *w_vw = nullptr, *w_b = nullptr, *w_c = nullptr;
     float *w_cat = nullptr;  // [H][r + 2N][d] = [W_kw^T; W_B; W_C] per slot (carrier projections)
     float *w_hist = nullptr, *hist_scale = nullptr, *hist_gate = nullptr;  // memory-coupled solve
+    const float *last_h = nullptr;  // h* of the most recent forward (its signal is sb.signal)
+    int last_ntok = 0;
     double *ctx_tot = nullptr;  // embed_context chunk totals (2 x ctx_tot_n doubles)
     long ctx_tot_n = 0;
 
@@ -479,6 +481,8 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     if (o.h_star) b.h = o.h_star;
     if (o.iters) b.iters = o.iters;
     b.mem_hist = nullptr;
+    c->last_h = b.h;  // the adjoint reads this forward's h* and signal
+    c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
     enqueue_iterations(c, r, b, ntok, ntok, prof);
     enqueue_head(c, o, b, ntok, prof);
@@ -502,6 +506,8 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
     if (o.iters) b.iters = o.iters;
     b.mem_hist = nullptr;
     b.mem_T = T;
+    c->last_h = b.h;
+    c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
     float *mseq = o.scan_y ? o.scan_y : c->scb.y;  // [B][T][H][d]
     float *hist = c->scb.gate_x;                     // [B][H][d]
@@ -1125,6 +1131,87 @@ int adn_embed_context(adn_ctx *c, int32_t batch, int32_t seq, const int32_t *tok
         enqueue_embed_context(c, batch, seq, c->tok_dev, max_ctx, dout);
         ADN_HIP(hipGetLastError());
         ADN_HIP(hipMemcpyAsync(out, dout, (size_t)n * c->D.d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+}
+
+}  // extern "C"
+
+namespace {
+
+int check_adjoint(adn_ctx *c, int32_t ntok, const float *dl, int32_t iters, float damping) {
+    if (!c || !dl) return fail(ADN_E_INVALID, "null argument");
+    if (!c->last_h || c->last_ntok < 1) return fail(ADN_E_INVALID, "adjoint before a forward on this context");
+    if (ntok != c->last_ntok) return fail(ADN_E_INVALID, "ntok differs from the most recent forward's token count");
+    if (iters < 0 || iters > ADN_PROFILE_MAX_ITERS) return fail(ADN_E_INVALID, "iters must be in [0, 256]");
+    if (!(damping > 0.0f && damping <= 1.0f)) return fail(ADN_E_INVALID, "damping must be in (0, 1]");
+    return ADN_OK;
+}
+
+void enqueue_adjoint(adn_ctx *c, int32_t ntok, const float *h_star, const float *dl, int32_t iters, float damping,
+                     float *v_out, float *src) {
+    const size_t n = (size_t)ntok * c->D.H * c->D.d;
+    AdjointArgs a{};
+    a.ntok = ntok;
+    a.iters = iters;
+    a.anderson_m = c->cfg.anderson_m;
+    a.beta = damping;
+    a.signal = c->sb.signal;
+    a.h_star = h_star ? h_star : c->last_h;
+    a.dl = dl;
+    a.g = c->norm_scale;
+    a.pre = c->sb.qkv;  // Q|K|V scratch is 3 * n floats: pre and the two iterates
+    a.v0 = c->sb.qkv + n;
+    a.v1 = c->sb.qkv + 2 * n;
+    a.terms = c->sb.mix;
+    a.src = src;
+    a.sb = c->sb;
+    a.act = c->sb.act[0];
+    a.cnt = c->sb.cnt;
+    const float *v = launch_adjoint(c->D, a, c->stream);
+    if (v_out && v) ADN_HIP(hipMemcpyAsync(v_out, v, n * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int adn_adjoint_async(adn_ctx *c, int32_t ntok, const float *h_star, const float *dl, int32_t iters, float damping,
+                      float *v_out, float *src) {
+    int rc = check_adjoint(c, ntok, dl, iters, damping);
+    if (rc) return rc;
+    try {
+        enqueue_adjoint(c, ntok, h_star, dl, iters, damping, v_out, src);
+        ADN_HIP(hipGetLastError());
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_adjoint(adn_ctx *c, int32_t ntok, const float *h_star, const float *dl, int32_t iters, float damping,
+                float *v_out, float *src) {
+    int rc = check_adjoint(c, ntok, dl, iters, damping);
+    if (rc) return rc;
+    try {
+        const size_t hd = (size_t)c->D.H * c->D.d, d = c->D.d;
+        const float *dh = nullptr;
+        if (h_star) {
+            float *t = staging_f(c, 20, (size_t)ntok * hd * sizeof(float));
+            ADN_HIP(hipMemcpyAsync(t, h_star, (size_t)ntok * hd * sizeof(float), hipMemcpyHostToDevice, c->stream));
+            dh = t;
+        }
+        float *ddl = staging_f(c, 21, (size_t)ntok * d * sizeof(float));
+        ADN_HIP(hipMemcpyAsync(ddl, dl, (size_t)ntok * d * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        float *dv = v_out ? staging_f(c, 22, (size_t)ntok * hd * sizeof(float)) : nullptr;
+        float *ds = src ? staging_f(c, 23, (size_t)ntok * d * sizeof(float)) : nullptr;
+        enqueue_adjoint(c, ntok, dh, ddl, iters, damping, dv, ds);
+        ADN_HIP(hipGetLastError());
+        if (v_out) ADN_HIP(hipMemcpyAsync(v_out, dv, (size_t)ntok * hd * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        if (src) ADN_HIP(hipMemcpyAsync(src, ds, (size_t)ntok * d * sizeof(float), hipMemcpyDeviceToHost, c->stream));
         ADN_HIP(hipStreamSynchronize(c->stream));
         return check_device_error(c);
     } catch (const HipError &e) {

@@ -205,6 +205,24 @@ int adn_load_tensor(adn_ctx *ctx, const float *data, int64_t n, int32_t *id);
  * in_dim = element count of the input tensor; y is host memory [out_dim]. */
 int adn_ffn_forward(adn_ctx *ctx, int32_t w_id, int32_t in_id, int32_t out_dim, float *y);
 
+/* --- backward: the clean adjoint Picard (GpuDeqBackend::run_staged_adjoint_picard_no_readback
+ *     -> run_clean_adjoint_picard_no_readback, gpu_deq.rs:4080-4920, and
+ *     reduce_clean_adjoint_to_source_grad_no_readback, :4922-4975; staged_adjoint_picard_clean.wgsl:
+ *     143-337) ----------------------------------------------------------------------------------
+ * For the ntok tokens of the most recent forward on this context (its signal; its h* unless
+ * h_star is given), per (token, slot) row with pre = signal + h* and rhs = dl[t] / H:
+ *   v_0 = rhs,  v_{k+1} = rhs + N^T(damping v_k) + (1 - damping) v_k   (iters steps),
+ * N^T the RMSNorm vector-Jacobian product at pre (attention is not part of this adjoint), each step
+ * Anderson-mixed per token when the context has anderson_m > 0 (from the third step).  v_out
+ * [ntok][H][d] receives v, src [ntok][d] the source gradient sum over slots of N^T(damping v);
+ * either may be NULL.  dl [ntok][d] is dL/d(pooled h*).  A forward (or greedy decode) in between
+ * replaces the state the adjoint reads.  adn_adjoint: host memory, blocking; adn_adjoint_async:
+ * device memory, enqueue only. */
+int adn_adjoint(adn_ctx *ctx, int32_t ntok, const float *h_star, const float *dl, int32_t iters, float damping,
+                float *v_out, float *src);
+int adn_adjoint_async(adn_ctx *ctx, int32_t ntok, const float *h_star, const float *dl, int32_t iters,
+                      float damping, float *v_out, float *src);
+
 /* --- input pipeline ------------------------------------------------------------------
  * Tokenizer::embed_context (tokenizer.rs:133-149) for the window ending at every position, as
  * the trainer builds the query of position i (trainer.rs:4690-4696: context =

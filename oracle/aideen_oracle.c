@@ -913,6 +913,117 @@ void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int3
 /* trait surfaces                                                             */
 /* ------------------------------------------------------------------------- */
 
+/* The shader's reduction order: each of 64 lanes sums x[lane], x[lane + 64], ... (or, with
+ * contiguous = 1, its own block of d/64 values), then a tree over the lanes with strides
+ * 32, 16, ..., 1 (staged_adjoint_picard_clean.wgsl:201-209, 301-309). */
+static float lane_tree_sum(const float *x, int d, int contiguous) {
+    float lanes[64];
+    for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        if (contiguous) {
+            const int per = d / 64;
+            for (int k = 0; k < per; ++k) acc = acc + x[l * per + k];
+        } else {
+            for (int i = l; i < d; i += 64) acc = acc + x[i];
+        }
+        lanes[l] = acc;
+    }
+    for (int stride = 32; stride > 0; stride >>= 1)
+        for (int l = 0; l < stride; ++l) lanes[l] = lanes[l] + lanes[l + stride];
+    return lanes[0];
+}
+
+/* one row's RMSNorm VJP terms: inv_rms and coeff_scale (:211-214), with up = beta v */
+static void adj_row_terms(int d, const float *pre, const float *v, const float *g, float beta, int contiguous,
+                          float *tmp, float *inv_rms, float *coeff_scale) {
+    for (int i = 0; i < d; ++i) tmp[i] = pre[i] * pre[i];
+    const float sumsq = lane_tree_sum(tmp, d, contiguous);
+    for (int i = 0; i < d; ++i) {
+        const float up = beta * v[i];
+        tmp[i] = up * g[i] * pre[i];
+    }
+    const float coeff = lane_tree_sum(tmp, d, contiguous);
+    const float inv_d = 1.0f / fmaxf(1.0f, (float)d);
+    const float rms = sqrtf(sumsq * inv_d + 1.0e-6f);
+    *inv_rms = 1.0f / fmaxf(rms, 1.0e-6f);
+    *coeff_scale = coeff / fmaxf((float)d * rms * rms * rms, 1.0e-6f);
+}
+
+void orc_adjoint(const orc_cfg *c, const float *norm_scale, int ntok, const float *signal, const float *h_star,
+                 const float *dl, int iters, float beta, float *v_out, float *src) {
+    const int d = c->d, H = c->H, m = c->anderson_m;
+    const size_t hd = (size_t)H * d, n = (size_t)ntok * hd;
+    float *pre = (float *)malloc(sizeof(float) * n);
+    float *v = (float *)malloc(sizeof(float) * n);
+    float *vn = (float *)malloc(sizeof(float) * n);
+    float *ring = m > 0 ? (float *)malloc(sizeof(float) * n * m) : NULL;
+    float *tmp = (float *)malloc(sizeof(float) * d);
+    const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
+    for (size_t e = 0; e < n; ++e) pre[e] = signal[e] + 1.0f * h_star[e];
+    for (int t = 0; t < ntok; ++t)
+        for (int s = 0; s < H; ++s)
+            for (int i = 0; i < d; ++i) v[((size_t)t * H + s) * d + i] = dl[(size_t)t * d + i] * rhs_scale;
+    for (int k = 0; k < iters; ++k) {
+        for (int t = 0; t < ntok; ++t)
+            for (int s = 0; s < H; ++s) {
+                const size_t o = ((size_t)t * H + s) * d;
+                float inv_rms, cs;
+                adj_row_terms(d, pre + o, v + o, norm_scale, beta, 0, tmp, &inv_rms, &cs);
+                for (int i = 0; i < d; ++i) {
+                    const float vp = v[o + i];
+                    const float ng = (norm_scale[i] * inv_rms) * (beta * vp) - pre[o + i] * cs;
+                    const float jac = 1.0f * ng + (1.0f - beta) * vp;
+                    vn[o + i] = dl[(size_t)t * d + i] * rhs_scale + jac;
+                }
+            }
+        if (m > 0) { /* store, then mix from k >= 2 (gpu_deq.rs:4893-4906; the shader's :1012-1134) */
+            memcpy(ring + (size_t)(k % m) * n, vn, sizeof(float) * n);
+            const int n_res = k < m - 1 ? k : m - 1;
+            if (k >= 2 && n_res >= 2) {
+                for (int t = 0; t < ntok; ++t) {
+                    float g[16], bt[4];
+                    for (int ri = 0; ri < n_res; ++ri)
+                        for (int rj = ri; rj < n_res; ++rj) {
+                            const float *xi = ring + (size_t)((k + m - ri) % m) * n + (size_t)t * hd;
+                            const float *xi1 = ring + (size_t)((k + m - ri - 1) % m) * n + (size_t)t * hd;
+                            const float *xj = ring + (size_t)((k + m - rj) % m) * n + (size_t)t * hd;
+                            const float *xj1 = ring + (size_t)((k + m - rj - 1) % m) * n + (size_t)t * hd;
+                            float acc = 0.0f;
+                            for (size_t e = 0; e < hd; ++e) acc += (xi[e] - xi1[e]) * (xj[e] - xj1[e]);
+                            g[ri * n_res + rj] = acc;
+                            g[rj * n_res + ri] = acc;
+                        }
+                    orc_anderson_coeffs(n_res, g, bt);
+                    for (size_t e = 0; e < hd; ++e) {
+                        float acc = 0.0f;
+                        for (int i = 0; i < n_res; ++i)
+                            acc += bt[i] * ring[(size_t)((k + m - i) % m) * n + (size_t)t * hd + e];
+                        vn[(size_t)t * hd + e] = acc;
+                    }
+                }
+            }
+        }
+        float *sw = v;
+        v = vn;
+        vn = sw;
+    }
+    if (v_out) memcpy(v_out, v, sizeof(float) * n);
+    if (src) { /* picard_source_grad_reduce_main (:252-336): slots summed in order */
+        for (int t = 0; t < ntok; ++t) {
+            float *o = src + (size_t)t * d;
+            for (int i = 0; i < d; ++i) o[i] = 0.0f;
+            for (int s = 0; s < H; ++s) {
+                const size_t r = ((size_t)t * H + s) * d;
+                float inv_rms, cs;
+                /* the shader gives each lane d/64 contiguous dims (d a multiple of 64 there) */
+                adj_row_terms(d, pre + r, v + r, norm_scale, beta, d % 64 == 0, tmp, &inv_rms, &cs);
+                for (int i = 0; i < d; ++i) o[i] = o[i] + ((norm_scale[i] * inv_rms) * (beta * v[r + i]) - pre[r + i] * cs);
+            }
+        }
+    }
+    free(pre); free(v); free(vn); free(ring); free(tmp);
+}
+
 /* tokenizer.rs:133-149 embed_context, one window per position (TRAINER:4690-4696).  The reference
  * evaluates result += emb * pos_weight in window order with pos_weight = (pos + 1) as f32 /
  * len as f32 (f32 division), then divides by result.norm() when it exceeds 1e-6.  The norm's

@@ -113,6 +113,14 @@ void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int3
                        int n_new, int32_t *out_tokens, int nthreads);
 
 /* --- other trait surfaces --------------------------------------------------- */
+/* Clean adjoint Picard (staged_adjoint_picard_clean.wgsl:143-337; driver gpu_deq.rs:4736-4975):
+ * per (token, slot) row, pre = signal + h*, rhs = dl[t] / H, v_0 = rhs and `iters` steps
+ * v_{k+1} = rhs + N^T(beta v_k) + (1 - beta) v_k, N^T the RMSNorm vector-Jacobian product at pre
+ * (attention is left out of the adjoint); Anderson(c->anderson_m) over each token's [H][d] iterate
+ * after every step (mixing from the third).  src[t] = sum over slots of N^T(beta v*).
+ * signal, h_star, v_out [ntok][H][d]; dl, src [ntok][d]; v_out / src may be NULL. */
+void orc_adjoint(const orc_cfg *c, const float *norm_scale, int ntok, const float *signal, const float *h_star,
+                 const float *dl, int iters, float beta, float *v_out, float *src);
 /* tokenizer.rs:133-149 embed_context for the window ending at every position (TRAINER:4690-4696:
  * context = tokens[max(0, i - ctx + 1) ..= i]): out[b][i] = r / |r| (r itself when |r| <= 1e-6),
  * r = sum over the window of E[tok] * ((pos + 1) / len), pos = index in the window. */

@@ -88,6 +88,7 @@ def lib():
                                          F32P, C.c_int]
         L.orc_zoh_step.argtypes = [C.c_int, F32P, F32P, F32P, F32P, F32P, F32P]
         L.orc_embed_context.argtypes = [C.c_int, F32P, C.c_int, C.c_int, I32P, C.c_int, F32P]
+        L.orc_adjoint.argtypes = [C.POINTER(OrcCfg), F32P, C.c_int, F32P, F32P, F32P, C.c_int, C.c_float, F32P, F32P]
         L.orc_gemv_colmajor.argtypes = [F32P, F32P, C.c_int, C.c_int, F32P]
         _lib = L
     return _lib
@@ -171,6 +172,18 @@ class Oracle:
                                     fp(None if m_in is None else np.ascontiguousarray(m_in, np.float32)),
                                     fp(y))
         return y
+
+    # --- clean adjoint ----------------------------------------------------------
+    def adjoint(self, signal, h_star, dl, iters, beta=None):
+        """signal, h_star [ntok][H][d], dl [ntok][d] -> (v [ntok][H][d], source grad [ntok][d])."""
+        signal = np.ascontiguousarray(signal, np.float32).reshape(-1, self.mc.H, self.mc.d)
+        ntok = signal.shape[0]
+        v = np.zeros((ntok, self.mc.H, self.mc.d), np.float32)
+        src = np.zeros((ntok, self.mc.d), np.float32)
+        self.L.orc_adjoint(C.byref(self.c), fp(self._keep["norm_scale"]), ntok, fp(signal),
+                           fp(np.ascontiguousarray(h_star, np.float32)), fp(np.ascontiguousarray(dl, np.float32)),
+                           iters, self.mc.beta if beta is None else beta, fp(v), fp(src))
+        return v, src
 
     # --- memory-coupled solve ------------------------------------------------
     def hist_ctx(self, m_prev, signal):

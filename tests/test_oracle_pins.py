@@ -691,3 +691,95 @@ def test_embed_context_windows_match_float64(oracle_lib):
     assert np.array_equal(a[:, 17:], b2[:, 17:]) and not np.array_equal(a[:, :10], b2[:, :10])
     # scaling E by a power of two leaves the normalised output unchanged (exactly)
     assert np.array_equal(oracle_lib.embed_context(4 * E, toks, 8), a)
+
+
+# ------------------------------------------------------------------------------------------
+# clean adjoint Picard (staged_adjoint_picard_clean.wgsl:143-337, gpu_deq.rs:4736-4975)
+# ------------------------------------------------------------------------------------------
+def _adj_setup(d=16, H=3, ntok=4, seed=0, anderson_m=0):
+    mc = synth.ModelConfig(d=d, H=H, V=40, N=1, r=32, flags=0, beta=0.7, anderson_m=anderson_m)
+    w = synth.make_weights(mc, seed=seed)
+    rng = np.random.default_rng(seed)
+    w = dict(w)
+    w["norm_scale"] = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    signal = (2.0 * rng.standard_normal((ntok, H, d))).astype(np.float32)
+    h = rng.standard_normal((ntok, H, d)).astype(np.float32)
+    dl = rng.standard_normal((ntok, d)).astype(np.float32)
+    return mc, w, signal, h, dl
+
+
+def _phi(x, g, beta, s):  # the map the adjoint linearises: beta * g*(s+h)/rms(s+h) + (1-beta) h
+    p = s + x
+    return beta * g * p / np.sqrt((p * p).mean() + 1e-6) + (1 - beta) * x
+
+
+def _norm(p, g):
+    return g * p / np.sqrt((p * p).mean() + 1e-6)
+
+
+def _fd_jac(f, x, eps=1e-5):
+    n = x.size
+    J = np.zeros((n, n))
+    for j in range(n):
+        e = np.zeros(n)
+        e[j] = eps
+        J[:, j] = (f(x + e) - f(x - e)) / (2 * eps)
+    return J
+
+
+def test_adjoint_step_is_the_transpose_jacobian(oracle_lib):
+    mc, w, signal, h, dl = _adj_setup()
+    o = oracle(oracle_lib, mc, w)
+    v0, _ = o.adjoint(signal, h, dl, 0)
+    # rhs = dl * (1 / H), the shader's fp32 reciprocal (:159-163)
+    np.testing.assert_array_equal(v0, np.repeat(dl[:, None, :] * (np.float32(1) / np.float32(mc.H)), mc.H, axis=1))
+    v1, _ = o.adjoint(signal, h, dl, 1)
+    g = w["norm_scale"].astype(np.float64)
+    for t in range(dl.shape[0]):
+        for s in range(mc.H):
+            J = _fd_jac(lambda x: _phi(x, g, mc.beta, signal[t, s].astype(np.float64)), h[t, s].astype(np.float64))
+            rhs = dl[t].astype(np.float64) / mc.H
+            np.testing.assert_allclose(v1[t, s], rhs + J.T @ rhs, rtol=1e-4, atol=2e-5)
+
+
+def test_adjoint_fixed_point_and_source_grad(oracle_lib):
+    mc, w, signal, h, dl = _adj_setup(d=64, H=2, ntok=2, seed=1)
+    o = oracle(oracle_lib, mc, w)
+    v, src = o.adjoint(signal, h, dl, 150)
+    g = w["norm_scale"].astype(np.float64)
+    for t in range(dl.shape[0]):
+        ref_src = np.zeros(mc.d)
+        for s in range(mc.H):
+            sg = signal[t, s].astype(np.float64)
+            J = _fd_jac(lambda x: _phi(x, g, mc.beta, sg), h[t, s].astype(np.float64))
+            rhs = dl[t].astype(np.float64) / mc.H
+            vstar = np.linalg.solve(np.eye(mc.d) - J.T, rhs)
+            np.testing.assert_allclose(v[t, s], vstar, rtol=1e-4, atol=2e-5)
+            JN = _fd_jac(lambda p: _norm(p, g), sg + h[t, s].astype(np.float64))
+            ref_src += JN.T @ (mc.beta * v[t, s].astype(np.float64))
+        np.testing.assert_allclose(src[t], ref_src, rtol=1e-4, atol=2e-5)
+
+
+def test_adjoint_anderson_bookkeeping(oracle_lib):
+    """The reference's mixing (store the new iterate in ring slot k % m, mix from k = 2 over the
+    last min(k, m-1) iterates, per token over its [H][d] state) is a heuristic: it is pinned step
+    by step, not by convergence.  m = 1, 2 never mix (equal to Picard bit for bit); for m >= 3
+    the third step's result is rebuilt from the stored iterates and the coefficient solve."""
+    mc0, w, signal, h, dl = _adj_setup(seed=2)
+    picard = oracle(oracle_lib, mc0, w)
+    for m in (1, 2):
+        om = oracle(oracle_lib, dataclasses.replace(mc0, anderson_m=m), w)
+        for it in (1, 3, 7):
+            assert np.array_equal(om.adjoint(signal, h, dl, it)[0], picard.adjoint(signal, h, dl, it)[0])
+    X = [picard.adjoint(signal, h, dl, it)[0] for it in (1, 2, 3)]  # unmixed iterates of steps 0, 1, 2
+    for m in (3, 4, 5):
+        om = oracle(oracle_lib, dataclasses.replace(mc0, anderson_m=m), w)
+        assert np.array_equal(om.adjoint(signal, h, dl, 2)[0], X[1])  # no mixing before k = 2
+        got = om.adjoint(signal, h, dl, 3)[0]
+        for t in range(dl.shape[0]):
+            d0 = (X[2][t] - X[1][t]).ravel()
+            d1 = (X[1][t] - X[0][t]).ravel()
+            g = np.array([[d0 @ d0, d0 @ d1], [d1 @ d0, d1 @ d1]], np.float32)
+            beta = np.zeros(2, np.float32)
+            oracle_lib.lib().orc_anderson_coeffs(2, oracle_lib.fp(np.ascontiguousarray(g.ravel())), oracle_lib.fp(beta))
+            np.testing.assert_allclose(got[t], beta[0] * X[2][t] + beta[1] * X[1][t], rtol=1e-5, atol=1e-6)
