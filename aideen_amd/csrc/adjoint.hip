@@ -7,8 +7,10 @@
 // (the RMSNorm vector-Jacobian product; attention is left out of this adjoint, as in the
 // reference), optionally Anderson-mixed per token after every step (the forward's mixing kernel);
 // then the source gradient src[t] = sum over slots of N^T(beta v*).
-//   k_adj_prep:   pre, the row's 1/rms and 1/(d rms^3), and v_0 (one wave per row)
+//   k_adj_first:  pre, the row's 1/rms and 1/(d rms^3), and the first step from v_0 = rhs
+//   k_adj_prep:   the same preparation with v_0 stored, when no step is asked for
 //   k_adj_step:   one Picard step (one wave per row; pre is reused, only the coefficient reduces)
+// The last step writes the caller's v_out directly.
 //   k_adj_source: per token, the slots' N^T(beta v*) summed in slot order
 #include "kernels.h"
 
@@ -42,6 +44,46 @@ __global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, const float *signal
         const float rms = sqrtf(ss * (1.0f / (float)d) + 1.0e-6f);
         terms[2 * row] = 1.0f / fmaxf(rms, 1.0e-6f);
         terms[2 * row + 1] = 1.0f / fmaxf((float)d * rms * rms * rms, 1.0e-6f);
+    }
+}
+
+// the first step fused with the preparation: v_0 = rhs is formed in registers (never stored)
+template <int E>
+__global__ __launch_bounds__(64 * AW) void k_adj_first(int H, const float *signal, const float *h_star,
+                                                        const float *g, const float *dl, int rows, float beta,
+                                                        float *pre, float *terms, float *vn) {
+    constexpr int d = 64 * E;
+    const int row = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int t = row / H;
+    const long o = (long)row * d;
+    const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
+    float pv[E], rv[E], gv[E];
+    float ss = 0.0f, cf = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        pv[e] = signal[o + i] + 1.0f * h_star[o + i];
+        pre[o + i] = pv[e];
+        rv[e] = dl[(long)t * d + i] * rhs_scale;
+        gv[e] = g[i];
+        ss += pv[e] * pv[e];
+        cf += beta * rv[e] * gv[e] * pv[e];
+    }
+    ss = wave_sum(ss);
+    cf = wave_sum(cf);
+    const float rms = sqrtf(ss * (1.0f / (float)d) + 1.0e-6f);
+    const float inv_rms = 1.0f / fmaxf(rms, 1.0e-6f);
+    const float cden = 1.0f / fmaxf((float)d * rms * rms * rms, 1.0e-6f);
+    if (lane == 0) {
+        terms[2 * row] = inv_rms;
+        terms[2 * row + 1] = cden;
+    }
+    const float cs = cf * cden;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float ng = (gv[e] * inv_rms) * (beta * rv[e]) - pv[e] * cs;
+        vn[o + lane + 64 * e] = rv[e] + (1.0f * ng + (1.0f - beta) * rv[e]);
     }
 }
 
@@ -116,8 +158,17 @@ template <int E>
 const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
     const int rows = a.ntok * D.H;
     const dim3 rg((unsigned)((rows + AW - 1) / AW)), blk(64 * AW);
-    float *v = a.v0, *vn = a.v1;
-    hipLaunchKernelGGL(k_adj_prep<E>, rg, blk, 0, st, D.H, a.signal, a.h_star, a.dl, rows, a.pre, a.terms, v);
+    // step k writes dst(k); the last one writes v_out directly when the caller asked for it
+    auto dst = [&](int k) { return (k == a.iters - 1 && a.v_out) ? a.v_out : ((k & 1) ? a.v1 : a.v0); };
+    float *v;
+    if (a.iters == 0) {
+        v = a.v_out ? a.v_out : a.v0;
+        hipLaunchKernelGGL(k_adj_prep<E>, rg, blk, 0, st, D.H, a.signal, a.h_star, a.dl, rows, a.pre, a.terms, v);
+    } else {
+        v = dst(0);
+        hipLaunchKernelGGL(k_adj_first<E>, rg, blk, 0, st, D.H, a.signal, a.h_star, a.g, a.dl, rows, a.beta, a.pre,
+                           a.terms, v);
+    }
     SolveBuffers b = a.sb;
     if (a.anderson_m > 0) {
         b.act[0] = a.act;
@@ -125,14 +176,14 @@ const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
         hipLaunchKernelGGL(k_iota, dim3((unsigned)((a.ntok + 255) / 256)), dim3(256), 0, st, a.act, a.ntok, a.cnt);
     }
     for (int k = 0; k < a.iters; ++k) {
-        hipLaunchKernelGGL(k_adj_step<E>, rg, blk, 0, st, D.H, a.pre, a.terms, a.g, a.dl, rows, a.beta, v, vn);
+        float *vn = dst(k);
+        if (k > 0)
+            hipLaunchKernelGGL(k_adj_step<E>, rg, blk, 0, st, D.H, a.pre, a.terms, a.g, a.dl, rows, a.beta, v, vn);
         if (a.anderson_m > 0) {  // store the new iterate, mix from the third step (per token)
             b.h = vn;
             launch_anderson(D, b, 0, a.ntok, a.ntok, k, a.anderson_m, st);
         }
-        float *sw = v;
         v = vn;
-        vn = sw;
     }
     if (a.src)
         hipLaunchKernelGGL(k_adj_source<E>, dim3((unsigned)((a.ntok + AW - 1) / AW)), blk, 0, st, D.H, a.pre,

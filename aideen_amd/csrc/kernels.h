@@ -139,13 +139,14 @@ long embed_context_chunks(int T);
 void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
                           double *tot1, float *out, unsigned *err, hipStream_t st);
 // Clean adjoint Picard for ntok tokens (rows = ntok * H of d floats); scratch pre, v0, v1 hold
-// rows * d floats, terms 2 * rows.  Returns the buffer (v0 or v1) holding the final iterate.
+// rows * d floats, terms 2 * rows.  Returns the buffer holding the final iterate (v_out when given).
 struct AdjointArgs {
     int ntok, iters, anderson_m;
     float beta;
     const float *signal, *h_star, *dl, *g;  // [ntok][H][d], [ntok][H][d], [ntok][d], [d]
     float *pre, *terms, *v0, *v1;
     float *src;                             // [ntok][d] or null
+    float *v_out;                           // [ntok][H][d] or null: receives the final iterate
     SolveBuffers sb;                        // its Anderson ring
     int32_t *act, *cnt;                     // token list and count for the Anderson kernel
 };

@@ -1168,11 +1168,13 @@ void enqueue_adjoint(adn_ctx *c, int32_t ntok, const float *h_star, const float 
     a.v1 = c->sb.qkv + 2 * n;
     a.terms = c->sb.mix;
     a.src = src;
+    a.v_out = v_out;
     a.sb = c->sb;
     a.act = c->sb.act[0];
     a.cnt = c->sb.cnt;
     const float *v = launch_adjoint(c->D, a, c->stream);
-    if (v_out && v) ADN_HIP(hipMemcpyAsync(v_out, v, n * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    if (v_out && v && v != v_out)
+        ADN_HIP(hipMemcpyAsync(v_out, v, n * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
 }
 
 }  // namespace

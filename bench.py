@@ -149,6 +149,73 @@ def bench_embed(args, be, mc, w, toks, dev, torch) -> int:
     return 0
 
 
+def bench_adjoint(args, be, mc, w, toks, dev, torch) -> int:
+    """The clean adjoint backward for the NS forward's 8192 tokens: adj_iters Picard steps on the
+    adjoint state plus the source gradient.  HBM-bound: the first step reads signal and h* and
+    writes pre and v; every further step reads pre and v and writes v (d floats per row each, plus
+    the token's dL/dpool row); the source gradient reads pre and v."""
+    import numpy as np
+    B, T = toks.shape
+    n = B * T
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    tok_d = torch.from_numpy(toks).to(dev)
+    h = torch.empty((B, T, mc.H, mc.d), dtype=torch.float32, device=dev)
+    be.forward_async(tok_d, outputs=dict(h_star=h))
+    dl = torch.from_numpy(np.random.default_rng(3).standard_normal((B, T, mc.d)).astype(np.float32)).to(dev)
+    v = torch.empty((B, T, mc.H, mc.d), dtype=torch.float32, device=dev)
+    src = torch.empty((B, T, mc.d), dtype=torch.float32, device=dev)
+    K = args.adj_iters
+    for _ in range(args.warmup):
+        be.adjoint_async(n, dl, K, mc.beta, v, src)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        be.adjoint_async(n, dl, K, mc.beta, v, src)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    tok_s = n / (ms / 1e3)
+    rows = n * mc.H
+    # first step: read signal, h*, dl; write pre, v.  each further step: read pre, v, dl; write v.
+    # source gradient: read pre, v; write src.  (K = 0: the preparation alone, v_0 written.)
+    first = rows * mc.d * 4 + n * mc.d
+    byts = 4 * (first + max(K - 1, 0) * (rows * mc.d * 3 + n * mc.d) + rows * mc.d * 2 + n * mc.d)
+    gbs = byts / ms / 1e6
+    log(f"adjoint ({K} steps): {ms * 1e3:.1f} us per call, {tok_s:,.0f} tokens/s, {gbs:.0f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import pyoracle
+        pyoracle.build()
+        o = pyoracle.Oracle(mc, w)
+        hs = h.cpu().numpy().reshape(n, mc.H, mc.d)
+        ns = max(1, min(n, 512))
+        sig = np.stack([o.signal(w["embed"][t]) for t in toks.reshape(-1)[:ns]])
+        dls = dl.cpu().numpy().reshape(n, mc.d)[:ns]
+        t0 = time.perf_counter()
+        o.adjoint(sig, hs[:ns], dls, K)
+        t1 = time.perf_counter() - t0
+        cpu = dict(value=round(ns / t1, 1), unit="tokens/s", cores=1, kind="port",
+                   sample=f"the first {ns} of the {n} tokens, {K} steps + source gradient, one thread, {t1:.2f} s")
+    line = {
+        "metric": f"adjoint backward tokens/sec at d_r={mc.d},h_slots={mc.H},B={B},ctx={T}", "value": round(tok_s, 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (NS weights and tokens; dL/dpool ~ N(0,1))",
+        "config": {"workload": f"{args.config}-adjoint: clean adjoint Picard, {K} steps + source gradient, "
+                               f"B={B} T={T} d_r={mc.d} h_slots={mc.H}", "mode": "adjoint",
+                   "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)"},
+        "roofline": dict(kernel="k_adj_prep + k_adj_step x iters + k_adj_source", bound="hbm",
+                         achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s", frac=round(gbs / PEAK_HBM_GBS, 4),
+                         traffic=None, bytes_per_call=byts),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,11 +226,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates HBM byte counters)")
-    ap.add_argument("--mode", choices=["forward", "memory", "embed"], default="forward",
+    ap.add_argument("--mode", choices=["forward", "memory", "embed", "adjoint"], default="forward",
                     help="forward: the canonical (token-parallel) forward, the headline metric; memory: "
                          "the memory-coupled forward (positions in order, history context and carrier "
                          "state between them) on the same shape with a one-dimensional carrier state; "
-                         "embed: embed_context queries for every position (window = ctx)")
+                         "embed: embed_context queries for every position (window = ctx); adjoint: the "
+                         "clean adjoint Picard backward of the NS forward")
+    ap.add_argument("--adj-iters", type=int, default=2,
+                    help="adjoint steps (ArchitectureConfig::adj_iters defaults to 2)")
     ap.add_argument("--eps", type=float, default=None, help="override the Picard tolerance")
     ap.add_argument("--gemm", choices=list(GEMM_MODES), default="f16x3",
                     help="GEMM arithmetic (f16x3 / bf16x3 / fp32 are fp32-accurate; bf16 is the "
@@ -202,6 +272,8 @@ def main() -> int:
     be.upload_weights(w)
     if args.mode == "embed":
         return bench_embed(args, be, mc, w, toks, dev, torch)
+    if args.mode == "adjoint":
+        return bench_adjoint(args, be, mc, w, toks, dev, torch)
     # a dedicated (default-priority) stream: the library's kernels and the timing events share it
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
