@@ -282,3 +282,55 @@ def test_ns_shape_sampled_parity_and_fixed_point(oracle_lib):
         else:
             first[tk] = i
     assert pairs >= 50
+
+
+def _sampled_preset(oracle_lib, name, idx, n_fixed=3):
+    """A BASELINE preset at full size on the GPU: sampled tokens against the oracle (including the
+    logits' arg-max) and, over every token, pooled = slot mean of h*, iterations below the cap, and
+    solved tokens being fixed points of the oracle's step."""
+    p = synth.PRESETS[name]
+    mc = p["model"]
+    w = synth.make_weights(mc, seed=0)
+    toks = synth.make_tokens(p["tokens"], p["B"], p["T"], mc.V, seed=1)
+    be = make(mc, p["B"], p["T"])
+    be.upload_weights(w)
+    log(f"{name} forward: d={mc.d} H={mc.H} N={mc.N} B={p['B']} T={p['T']} anderson={mc.anderson_m}")
+    got = be.forward(toks, want=("h_star", "iters", "argmax", "pooled"))
+    be.close()
+    log(f"{name} iterations: mean {got['iters'].mean():.2f}, max {got['iters'].max()}")
+    o = oracle_lib.Oracle(mc, w)
+    sub = np.array([[toks[b, t] for b, t in idx]], np.int32)
+    ref = o.forward(sub, want_scan=False, nthreads=16)
+    gsub = {k: np.stack([got[k][b, t] for b, t in idx])[None] for k in ("h_star", "iters", "argmax", "pooled")}
+    rsub = {k: ref[k].copy() for k in ("h_star", "iters", "argmax", "pooled")}
+    # With Anderson mixing (this build's forward extension; the reference's forward is plain Picard,
+    # whose counts the +-1 bar is about) the residual is not monotone: a crossing of eps decided
+    # by rounding can move the exit by more than one iteration.  Such a token is accepted only if
+    # the oracle's residual at the earlier of the two exits lies within 10% of eps.
+    for j, (b, t) in enumerate(idx):
+        ig, ir = int(gsub["iters"][0, j]), int(rsub["iters"][0, j])
+        if abs(ig - ir) > 1:
+            assert mc.anderson_m > 0, f"{name} ({b},{t}): iterations {ig} vs {ir}"
+            _, _, trace = o.solve(w["embed"][toks[b, t]])
+            r = trace[min(ig, ir) - 1]
+            assert 0.9 * mc.eps <= r <= 1.1 * mc.eps, f"{name} ({b},{t}): {ig} vs {ir}, residual {r:.3e}"
+            rsub["iters"][0, j] = ig
+    assert_forward_parity(gsub, rsub, f"{name} sample")
+    np.testing.assert_allclose(got["pooled"], got["h_star"].mean(axis=2), rtol=1e-5, atol=1e-6)
+    for b, t in idx[:n_fixed]:
+        x = w["embed"][toks[b, t]]
+        hn, _ = o.step(got["h_star"][b, t], o.signal(x))
+        assert np.abs(hn - got["h_star"][b, t]).max() < 4 * mc.eps
+    return got
+
+
+def test_c3_shape_sampled_parity(oracle_lib):
+    """C3: B=32, T=1024 (32768 tokens), sigma 0.7, Anderson m=5."""
+    got = _sampled_preset(oracle_lib, "C3", [(0, 0), (31, 1023), (7, 512), (19, 77), (25, 900), (3, 333)])
+    assert got["iters"].max() <= synth.PRESETS["C3"]["model"].max_iters
+
+
+def test_c5_shape_sampled_parity(oracle_lib):
+    """C5, the largest preset: d=2048, H=16, N=32, B=16, T=2048 (32768 tokens), sigma 0.8, Anderson
+    m=5 -- the widest rows and the most slots every kernel supports."""
+    _sampled_preset(oracle_lib, "C5", [(0, 0), (15, 2047), (8, 1024), (3, 5)], n_fixed=2)
