@@ -109,26 +109,49 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
         }
     }
     const float scale = 1.0f / sqrtf((float)d);
-    float attn[QA][H];
+    // Wave totals of the P = QA*H partial dot products with wave_sum's offsets (32, 16, ..., 1),
+    // so that every total is bit-identical to wave_sum's.  Offsets >= P add all P values; below
+    // P the lanes also split the indices still held (a transposing butterfly): at offset `off`
+    // the lanes with that bit set keep the upper half of the range, the others the lower half,
+    // and each adds its partner's partial for the indices it keeps.  Lane L ends with the total
+    // of index L % P = a * H + c: 2P - 1 shuffles instead of 6P.
+    constexpr int P = QA * H;
+    float t[P];
 #pragma unroll
-    for (int a = 0; a < QA; ++a) {
-        float mx = -INFINITY;
+    for (int a = 0; a < QA; ++a)
 #pragma unroll
-        for (int c = 0; c < H; ++c) {
-            float sc = wave_sum(part[a][c]) * scale;
-            if (D.flags & ADN_F_SCORE_CLAMP4) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
-            attn[a][c] = sc;
-            mx = fmaxf(mx, sc);
+        for (int c = 0; c < H; ++c) t[a * H + c] = part[a][c];
+#pragma unroll
+    for (int off = 32; off >= P; off >>= 1)
+#pragma unroll
+        for (int j = 0; j < P; ++j) t[j] += __shfl_xor(t[j], off, 64);
+#pragma unroll
+    for (int off = (P < 64 ? P : 64) / 2; off > 0; off >>= 1) {
+        const bool up = (lane & off) != 0;
+#pragma unroll
+        for (int j = 0; j < off; ++j) {
+            const float send = up ? t[j] : t[j + off];
+            const float keep = up ? t[j + off] : t[j];
+            t[j] = keep + __shfl_xor(send, off, 64);
         }
-        float sum = 0.0f;
-#pragma unroll
-        for (int c = 0; c < H; ++c) {
-            attn[a][c] = expf(attn[a][c] - mx);
-            sum += attn[a][c];
-        }
-#pragma unroll
-        for (int c = 0; c < H; ++c) attn[a][c] = attn[a][c] / sum;
     }
+    float sc = t[0] * scale;
+    if (D.flags & ADN_F_SCORE_CLAMP4) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
+    // softmax over the key slots of this lane's query (lanes gb .. gb + H - 1), max and sum
+    // taken in key order as in the sequential form
+    const int gb = lane & ~(H - 1);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < H; ++c) mx = fmaxf(mx, __shfl(sc, gb + c, 64));
+    const float ex = expf(sc - mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < H; ++c) sum += __shfl(ex, gb + c, 64);
+    const float w_own = ex / sum;
+    // every weight to every lane as a wave-uniform value (lane i holds index i)
+    float w[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) w[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_own), q));
 
     float *mixbase = b.mix + (long)i * H * d;
     for (int off = lane * VEC; off < d; off += 64 * VEC) {
@@ -145,7 +168,7 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
 #pragma unroll
             for (int a = 0; a < QA; ++a)
 #pragma unroll
-                for (int v = 0; v < VEC; ++v) acc[a][v] = acc[a][v] + vv[v] * attn[a][c];
+                for (int v = 0; v < VEC; ++v) acc[a][v] = acc[a][v] + vv[v] * w[a * H + c];
         }
 #pragma unroll
         for (int a = 0; a < QA; ++a)
