@@ -58,6 +58,12 @@ struct Vec8<__bf16> {
 __device__ __forceinline__ int swz_a(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 __device__ __forceinline__ int swz_b(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
 
+// Slot stride of the split weights (blocked layout, rows padded to a multiple of 32); b_ss only
+// says whether the slots have matrices of their own (non-zero) or share one (zero).
+__device__ __forceinline__ long split_slot_stride(const GemmParams &p) {
+    return p.b_ss ? (long)((p.N + 31) / 32 * 32) * p.K : 0;
+}
+
 __device__ __forceinline__ floatx16 mfma16(half8 a, half8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
@@ -93,7 +99,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     static_assert(A_BLK % NW == 0 && B_BLK % NW == 0, "DMA blocks must split evenly over waves");
     constexpr int A_PW = A_BLK / NW, B_PW = B_BLK / NW;
     constexpr int LOADS = A_PW + PARTS * B_PW;  // DMA instructions per wave per slice
-    static_assert(STAGES >= 2 && (STAGES - 2) * LOADS < 64, "pipeline depth");
+    static_assert(STAGES >= 3 && (STAGES - 2) * LOADS < 64, "pipeline depth");
     __shared__ __attribute__((aligned(1024))) float As[STAGES][BMt][BK];
     __shared__ __attribute__((aligned(1024))) T Bs[STAGES][PARTS][BNt][BK];
 
@@ -125,13 +131,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
         }
         asrc[j] = p.A + ar * p.a_sm + (long)s * p.a_ss + c * 4;
     }
+    // B in the blocked layout (one contiguous 1 KB block per 32 rows x 16 K, see k_split): each
+    // DMA block is one such block; lane L takes the chunk its LDS position holds.  Row groups
+    // past N read group 0 (their products land in outputs that are not stored).
     const T *bsrc[B_PW][PARTS];
 #pragma unroll
     for (int j = 0; j < B_PW; ++j) {
         const int row = (wave + NW * j) * 32 + (lane >> 1);
         const int c = (lane & 1) ^ swz_b(row);
-        const int n = n0 + row;
-        const long off = (long)s * p.b_ss + (long)(n < p.N ? n : 0) * p.K + c * 8;
+        const long grp = (n0 >> 5) + wave + NW * j;
+        const long off = (long)s * split_slot_stride(p) + (grp * 32 < p.N ? grp : 0) * (p.K / BK) * 512 +
+                         (lane >> 1) * 16 + c * 8;
         bsrc[j][0] = reinterpret_cast<const T *>(p.Bhi) + off;
         if constexpr (TERMS == 3) bsrc[j][1] = reinterpret_cast<const T *>(p.Blo) + off;
     }
@@ -144,7 +154,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
         for (int j = 0; j < B_PW; ++j)
 #pragma unroll
             for (int q = 0; q < PARTS; ++q)
-                __builtin_amdgcn_global_load_lds((const void *)(bsrc[j][q] + kt * BK),
+                __builtin_amdgcn_global_load_lds((const void *)(bsrc[j][q] + kt * 512),
                                                  (lds_void *)&Bs[st][q][(wave + NW * j) * 32][0], 16, 0, 0);
     };
 
@@ -172,35 +182,45 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    auto compute = [&](int st) {
-        V8 bh[WTN], bl[WTN];
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-            const int row = (wn * WTN + j) * 32 + r;
-            bh[j] = *reinterpret_cast<const V8 *>(&Bs[st][0][row][pb]);
-            if constexpr (TERMS == 3) bl[j] = *reinterpret_cast<const V8 *>(&Bs[st][PARTS - 1][row][pb]);
-        }
+    // Fragments in registers: A of a slice is read raw (fp32) one step ahead and split just
+    // before its slice is multiplied; B is streamed one 32-column tile at a time through two
+    // buffers, tile j + 1 (or the next slice's tile 0) being read while tile j's MFMAs run, so
+    // that the LDS reads are spread over the MFMA phase instead of preceding it.
+    floatx4 anx[WTM][2];
+    V8 ah[WTM], al[WTM];
+    V8 bq[2][PARTS];
+    auto read_a = [&](int st) {
 #pragma unroll
         for (int i = 0; i < WTM; ++i) {
             const int row = (wm * WTM + i) * 32 + r;
-            const floatx4 x0 = *reinterpret_cast<const floatx4 *>(&As[st][row][pa0]);
-            const floatx4 x1 = *reinterpret_cast<const floatx4 *>(&As[st][row][pa1]);
-            V8 ah, al;
+            anx[i][0] = *reinterpret_cast<const floatx4 *>(&As[st][row][pa0]);
+            anx[i][1] = *reinterpret_cast<const floatx4 *>(&As[st][row][pa1]);
+        }
+    };
+    auto split_a = [&]() {
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const float x = (q < 4 ? x0[q] : x1[q - 4]) * asc;
+                const float x = anx[i][q >> 2][q & 3] * asc;
                 const T hv = (T)x;
-                ah[q] = hv;
-                if constexpr (TERMS == 3) al[q] = (T)(x - (float)hv);
+                ah[i][q] = hv;
+                if constexpr (TERMS == 3) al[i][q] = (T)(x - (float)hv);
             }
+    };
+    auto read_b = [&](int st, int j, V8 (&bb)[PARTS]) {
+        const int row = (wn * WTN + j) * 32 + r;
 #pragma unroll
-            for (int j = 0; j < WTN; ++j) {
-                if constexpr (TERMS == 3) {
-                    acc[i][j] = mfma16(al, bh[j], acc[i][j]);
-                    acc[i][j] = mfma16(ah, bl[j], acc[i][j]);
-                }
-                acc[i][j] = mfma16(ah, bh[j], acc[i][j]);
+        for (int q = 0; q < PARTS; ++q) bb[q] = *reinterpret_cast<const V8 *>(&Bs[st][q][row][pb]);
+    };
+    auto mfma_tile = [&](int j, const V8 (&bb)[PARTS]) {
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+            if constexpr (TERMS == 3) {
+                acc[i][j] = mfma16(al[i], bb[0], acc[i][j]);
+                acc[i][j] = mfma16(ah[i], bb[1], acc[i][j]);
             }
+            acc[i][j] = mfma16(ah[i], bb[0], acc[i][j]);
         }
     };
 
@@ -208,15 +228,44 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
         if (st < nk) issue(st, st);
+    if (STAGES - 2 < nk)  // this wave's loads of slice 0 are done
+        wait_vmcnt<(STAGES - 2) * LOADS>();
+    else
+        wait_vmcnt<0>();
+    lds_barrier();
+    read_a(0);
+    read_b(0, 0, bq[0]);
+    split_a();
     for (int kt = 0; kt < nk; ++kt) {
-        // this wave's loads of slice kt are done once at most (STAGES-2) later slices are in flight
-        if (kt + STAGES - 2 < nk)
-            wait_vmcnt<(STAGES - 2) * LOADS>();
-        else
-            wait_vmcnt<0>();
-        lds_barrier();
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        compute(kt % STAGES);
+        const int cs = kt % STAGES, ns = (kt + 1) % STAGES;
+        if (kt + 1 < nk) {
+            // slice kt+1 visible: this wave's loads of it are done once at most STAGES-3 later
+            // slices are in flight; the barrier covers the other waves' loads and their reads of
+            // the slot about to be refilled (slice kt-1's, last read in the previous step)
+            if (kt + STAGES - 2 < nk)
+                wait_vmcnt<(STAGES - 3) * LOADS>();
+            else
+                wait_vmcnt<0>();
+            lds_barrier();
+            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        }
+        // The reads below are unconditional so that the wait counts stay exact: after the last
+        // slice they read a slot no load writes any more, and the values are not used.
+        // sched_barrier keeps each tile's reads ahead of the previous tile's MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(ns);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            read_b(j + 1 < WTN ? cs : ns, (j + 1) % WTN, bq[(j + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_tile(j, bq[j & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (WTN & 1) {  // the next slice's tile 0 went to buffer 1
+#pragma unroll
+            for (int q = 0; q < PARTS; ++q) bq[0][q] = bq[1][q];
+        }
+        split_a();
     }
     lds_barrier();  // every wave is done with the ring before the epilogue reuses it
 
@@ -257,11 +306,13 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
         }
     }
     const float *ap = p.A + ar * p.a_sm + (long)s * p.a_ss;
+    // B row n in the blocked layout: K values [16b, 16b + 16) at block b of its 32-row group
     const T *bhp[WTN], *blp[WTN];
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
         const int n = n0 + 32 * j + q;
-        const long boff = (long)s * p.b_ss + (long)(n < p.N ? n : 0) * p.K;
+        const long nn = n < p.N ? n : 0;
+        const long boff = (long)s * split_slot_stride(p) + (nn >> 5) * (p.K / 16) * 512 + (nn & 31) * 16;
         bhp[j] = reinterpret_cast<const T *>(p.Bhi) + boff;
         blp[j] = reinterpret_cast<const T *>(TERMS == 3 ? p.Blo : p.Bhi) + boff;
     }
@@ -292,8 +343,9 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
         for (int j = 0; j < WTN; ++j)
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                bh[j][st] = *reinterpret_cast<const V8 *>(bhp[j] + ko + 8 * st);
-                if constexpr (TERMS == 3) bl[j][st] = *reinterpret_cast<const V8 *>(blp[j] + ko + 8 * st);
+                const long e = (long)((ko >> 4) + (st >> 1)) * 512 + (st & 1) * 8;
+                bh[j][st] = *reinterpret_cast<const V8 *>(bhp[j] + e);
+                if constexpr (TERMS == 3) bl[j][st] = *reinterpret_cast<const V8 *>(blp[j] + e);
             }
 #pragma unroll
         for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const floatx4 *>(ap + ko + 4 * i);
@@ -335,14 +387,22 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     epilogue_t<ROLE, 1, WTN, 1, 1>(p, acc, M, s, 0, n0, osc, nullptr, nullptr);
 }
 
-// Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi).
+// Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi), from [S][N][K] fp32 into
+// the blocked layout: per slot, rows in groups of 32 (N padded to a multiple of 32 with zeros),
+// each group's K in blocks of 16, a block (32 rows x 16 halves, 1 KB) contiguous and row-major:
+//   (s, n, k) -> s * split_slot_stride + ((n / 32) * (K / 16) + k / 16) * 512 + (n % 32) * 16 + k % 16
+// so that a GEMM's 32-row x 16-K load is one contiguous kilobyte.
 template <typename T>
-__global__ void k_split(const float *w, long n, float scale, T *hi, T *lo) {
-    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
-        const float x = w[i] * scale;
+__global__ void k_split(const float *w, int S, int N, int K, float scale, T *hi, T *lo) {
+    const long np = ((long)N + 31) / 32 * 32, total = (long)S * np * K, kb = K / 16;
+    for (long o = (long)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (long)gridDim.x * blockDim.x) {
+        const long sl = o / (np * K), ro = o - sl * np * K;
+        const long blk = ro >> 9, in = ro & 511;
+        const long n = (blk / kb) * 32 + (in >> 4), k = (blk % kb) * 16 + (in & 15);
+        const float x = n < N ? w[(sl * N + n) * K + k] * scale : 0.0f;
         const T h = (T)x;
-        hi[i] = h;
-        if (lo) lo[i] = (T)(x - (float)h);
+        hi[o] = h;
+        if (lo) lo[o] = (T)(x - (float)h);
     }
 }
 
@@ -419,13 +479,17 @@ void launch_gemm_split(const GemmParams &p, hipStream_t st) {
     }
 }
 
-void launch_split_weights(const float *w, long n, float scale, int prec, void *hi, void *lo, hipStream_t st) {
+long split_weight_elems(int S, int N, int K) { return (long)S * ((N + 31) / 32 * 32) * K; }
+
+void launch_split_weights(const float *w, int S, int N, int K, float scale, int prec, void *hi, void *lo,
+                          hipStream_t st) {
+    const long n = split_weight_elems(S, N, K);
     const long blocks = std::min<long>((n + 255) / 256, 8192);
     if (prec == PREC_F16X3)
-        hipLaunchKernelGGL(k_split<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st, w, n, scale,
+        hipLaunchKernelGGL(k_split<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st, w, S, N, K, scale,
                            (_Float16 *)hi, (_Float16 *)lo);
     else
-        hipLaunchKernelGGL(k_split<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st, w, n, scale,
+        hipLaunchKernelGGL(k_split<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st, w, S, N, K, scale,
                            (__bf16 *)hi, (__bf16 *)lo);
 }
 

@@ -50,8 +50,13 @@ struct GemmParams {
 constexpr int GEMM_BN = 128;
 void launch_gemm(const GemmParams &p, hipStream_t st);
 void launch_gemm_split(const GemmParams &p, hipStream_t st);
-// hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16; lo may be null
-void launch_split_weights(const float *w, long n, float scale, int prec, void *hi, void *lo, hipStream_t st);
+// hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16, from [S][N][K]
+// fp32 weights into the split GEMM's blocked layout (split_weight_elems halves each, N padded to
+// a multiple of 32); lo may be null.  The GEMMs' b_ss is then 0 (one matrix for every slot) or
+// non-zero (a matrix per slot, N x K).
+long split_weight_elems(int S, int N, int K);
+void launch_split_weights(const float *w, int S, int N, int K, float scale, int prec, void *hi, void *lo,
+                          hipStream_t st);
 
 // ---- DEQ solve kernels (deq.hip) ------------------------------------------------------
 struct SolveBuffers {

@@ -222,13 +222,14 @@ float split_scale(int prec, float maxabs, int headroom_log2 = 14) {
     return std::ldexp(1.0f, e);
 }
 
-void make_split(adn_ctx *c, adn_ctx::Split &sp, const float *dev_w, size_t n, float maxabs) {
+// split copies of S matrices [N][K] (the GEMMs' B operand) in the blocked layout
+void make_split(adn_ctx *c, adn_ctx::Split &sp, const float *dev_w, int S, int N, int K, float maxabs) {
     if (c->prec == PREC_FP32) return;
-    const size_t bytes = n * 2;
+    const size_t bytes = (size_t)split_weight_elems(S, N, K) * 2;
     if (!sp.hi) sp.hi = dmalloc(c, bytes);
     if (c->prec != PREC_BF16X1 && !sp.lo) sp.lo = dmalloc(c, bytes);
     sp.scale = split_scale(c->prec, maxabs);
-    launch_split_weights(dev_w, (long)n, sp.scale, c->prec, sp.hi, c->prec == PREC_BF16X1 ? nullptr : sp.lo,
+    launch_split_weights(dev_w, S, N, K, sp.scale, c->prec, sp.hi, c->prec == PREC_BF16X1 ? nullptr : sp.lo,
                          c->stream);
 }
 
@@ -826,16 +827,16 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
         }
         // split-precision copies of every GEMM weight (device-side, from the fp32 copies)
         const size_t nmat = (size_t)H * mat;
-        make_split(c, c->sp_qkv, c->w_qkv, 3 * nmat,
+        make_split(c, c->sp_qkv, c->w_qkv, H, 3 * d, d,
                    host_maxabs({{w->w_q, nmat}, {w->w_k, nmat}, {w->w_v, nmat}}));
-        make_split(c, c->sp_o, c->w_o, nmat, host_maxabs({{w->w_o, nmat}}));
-        make_split(c, c->sp_in, c->w_in, nmat, host_maxabs({{w->w_in, nmat}}));
-        if (c->w_out) make_split(c, c->sp_out, c->w_out, nmat, host_maxabs({{w->w_out, nmat}}));
-        make_split(c, c->sp_cat, c->w_cat, (size_t)H * (r + 2 * N) * d,
+        make_split(c, c->sp_o, c->w_o, H, d, d, host_maxabs({{w->w_o, nmat}}));
+        make_split(c, c->sp_in, c->w_in, H, d, d, host_maxabs({{w->w_in, nmat}}));
+        if (c->w_out) make_split(c, c->sp_out, c->w_out, H, d, d, host_maxabs({{w->w_out, nmat}}));
+        make_split(c, c->sp_cat, c->w_cat, H, r + 2 * N, d,
                    host_maxabs({{w->w_kw, (size_t)H * d * r}, {w->w_b, (size_t)H * N * d},
                                 {w->w_c, (size_t)H * N * d}}));
-        make_split(c, c->sp_lm, c->lm_w, (size_t)V * d, host_maxabs({{w->lm_w, (size_t)V * d}}));
-        if (c->w_hist) make_split(c, c->sp_hist, c->w_hist, mat, host_maxabs({{w->w_hist, mat}}));
+        make_split(c, c->sp_lm, c->lm_w, 1, V, d, host_maxabs({{w->lm_w, (size_t)V * d}}));
+        if (c->w_hist) make_split(c, c->sp_hist, c->w_hist, 1, d, d, host_maxabs({{w->w_hist, mat}}));
         // The signal GEMM's A operand (gathered embedding rows, or s_in rows of the same
         // scale) is scaled up too, with 6 bits of headroom: inputs up to 64x the table's
         // maximum magnitude stay inside the fp16 range.
