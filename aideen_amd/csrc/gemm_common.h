@@ -129,7 +129,7 @@ struct EpiCtx {
     int *scratch_i;
 };
 
-template <int I, int WTM, int WTN, int WGM, int EPI, bool AM, bool CHECK>
+template <int I, int WTM, int WTN, int WGM, int EPI, bool AM, bool CHECK, bool STREAM>
 __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c,
                                          const float (&bj)[WTN], const bool (&nv)[WTN]) {
     constexpr int BMt = WGM * WTM * 32;
@@ -151,7 +151,10 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
                 if (ok) v = p.A[(long)m * p.a_sm + (long)c.s * p.a_ss + ncol0 + 32 * j] + v;
             }
             if (ok) {
-                crow[32 * j] = v;
+                if constexpr (STREAM)
+                    __builtin_nontemporal_store(v, crow + 32 * j);
+                else
+                    crow[32 * j] = v;
                 if constexpr (AM) {
                     const int n = ncol0 + 32 * j;
                     if (v > bv || (v == bv && n > bi)) {
@@ -177,10 +180,10 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
             }
         }
     }
-    if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM, EPI, AM, CHECK>(p, acc, c, bj, nv);
+    if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM, EPI, AM, CHECK, STREAM>(p, acc, c, bj, nv);
 }
 
-template <int WTM, int WTN, int WGM, int WGN, int EPI, bool AM, bool CHECK>
+template <int WTM, int WTN, int WGM, int WGN, int EPI, bool AM, bool CHECK, bool STREAM = false>
 __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c) {
     constexpr int BMt = WGM * WTM * 32;
     float bj[WTN];
@@ -193,7 +196,7 @@ __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WT
         if constexpr (EPI == EPI_BIAS)
             if (nv[j] && n < p.bias_n) bj[j] = p.bias[(long)c.s * p.bias_ss + n];
     }
-    epi_rows<0, WTM, WTN, WGM, EPI, AM, CHECK>(p, acc, c, bj, nv);
+    epi_rows<0, WTM, WTN, WGM, EPI, AM, CHECK, STREAM>(p, acc, c, bj, nv);
     if constexpr (AM) {
         // partials are per 128 columns: waves covering 64 columns are combined in pairs
         constexpr int CPW = WTN * 32;
@@ -268,16 +271,20 @@ __device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[
             }
         }
     } else {
+        // Q|K|V and W_o outputs are read by the very next kernel (attention, update): stored
+        // non-temporally they stream past L2, which keeps the operands of the tiles still being
+        // multiplied in L2 and leaves the outputs to the consumer in the memory-side cache.
+        constexpr bool ST = ROLE == ROLE_QKV || ROLE == ROLE_WO;
         if (p.epi == EPI_BIAS) {
             if (interior)
-                epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false>(p, acc, c);
+                epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false, ST>(p, acc, c);
             else
-                epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, true>(p, acc, c);
+                epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, true, ST>(p, acc, c);
         } else {
             if (interior)
-                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false>(p, acc, c);
+                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false, ST>(p, acc, c);
             else
-                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true>(p, acc, c);
+                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true, ST>(p, acc, c);
         }
     }
 }
