@@ -83,6 +83,7 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
     if (i >= n) return;
     const int d = D.d;
     const long rowstride = 3L * d;
+    // Q|K|V rows are read once: non-temporal loads keep them from displacing cached data
     const float *base = b.qkv + (long)i * H * rowstride;
 
     float part[QA][H];
@@ -96,12 +97,12 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
 #pragma unroll
         for (int a = 0; a < QA; ++a)
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) q[a][v] = base[(long)(g * QA + a) * rowstride + off + v];
+            for (int v = 0; v < VEC; ++v) q[a][v] = __builtin_nontemporal_load(base + (long)(g * QA + a) * rowstride + off + v);
 #pragma unroll
         for (int c = 0; c < H; ++c) {
             float kk[VEC];
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) kk[v] = base[(long)c * rowstride + d + off + v];
+            for (int v = 0; v < VEC; ++v) kk[v] = __builtin_nontemporal_load(base + (long)c * rowstride + d + off + v);
 #pragma unroll
             for (int a = 0; a < QA; ++a)
 #pragma unroll
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
         for (int c = 0; c < H; ++c) {
             float vv[VEC];
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) vv[v] = base[(long)c * rowstride + 2 * d + off + v];
+            for (int v = 0; v < VEC; ++v) vv[v] = __builtin_nontemporal_load(base + (long)c * rowstride + 2 * d + off + v);
 #pragma unroll
             for (int a = 0; a < QA; ++a)
 #pragma unroll

@@ -104,47 +104,64 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     __shared__ __attribute__((aligned(1024))) T Bs[STAGES][PARTS][BNt][BK];
 
     const int nM = (p.M + BMt - 1) / BMt, nN = (p.N + BNt - 1) / BNt;
-    int s, mt, nt;
-    map_block(blockIdx.x, nM * nN * p.S, nM, nN, s, mt, nt);
+    const int total = nM * nN * p.S;
     const int M = p.m_count ? min(*p.m_count, p.M) : p.M;
-    const int m0 = mt * BMt, n0 = nt * BNt;
-    if (m0 >= M) return;
-
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
 
-    // Per-lane source pointers of this wave's DMA blocks.  Rows past M or N read row 0 of the
-    // operand (their products land in outputs that the epilogue does not store).
-    const float *asrc[A_PW];
-#pragma unroll
-    for (int j = 0; j < A_PW; ++j) {
-        const int row = (wave + NW * j) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ swz_a(row);
-        const int m = m0 + row;
-        long ar = 0;
-        if (m < M) {
-            ar = p.a_idx ? (long)p.a_idx[m] : (long)m;
-            if (p.a_idx && (ar < 0 || ar >= p.a_idx_max)) {
-                if (p.err) atomicOr(p.err, ADN_DEVERR_TOKEN);
-                ar = 0;
-            }
+    // Persistent: workgroup b takes tiles b, b + gridDim.x, ... (the grid is a multiple of the
+    // XCD count, so each tile stays on the XCD the block order assigns it to); tiles without
+    // rows (m0 >= M, converged tokens) are skipped.
+    auto next_tile = [&](int t) {
+        for (; t < total; t += gridDim.x) {
+            int s2, mt2, nt2;
+            map_block(t, total, nM, nN, s2, mt2, nt2);
+            if (mt2 * BMt < M) return t;
         }
-        asrc[j] = p.A + ar * p.a_sm + (long)s * p.a_ss + c * 4;
-    }
-    // B in the blocked layout (one contiguous 1 KB block per 32 rows x 16 K, see k_split): each
-    // DMA block is one such block; lane L takes the chunk its LDS position holds.  Row groups
-    // past N read group 0 (their products land in outputs that are not stored).
+        return total;
+    };
+    int t = next_tile(blockIdx.x);
+    if (t >= total) return;
+
+    // Per-lane source pointers of this wave's DMA blocks for the current tile.  Rows past M or N
+    // read row 0 of the operand (their products land in outputs that the epilogue does not
+    // store).  B is in the blocked layout (one contiguous 1 KB block per 32 rows x 16 K, see
+    // k_split): each DMA block is one such block, lane L taking the chunk its LDS position
+    // holds; row groups past N read group 0.
+    int s = 0, m0 = 0, n0 = 0;
+    const float *asrc[A_PW];
     const T *bsrc[B_PW][PARTS];
+    auto set_tile = [&](int tt) {
+        int mt, nt;
+        map_block(tt, total, nM, nN, s, mt, nt);
+        m0 = mt * BMt;
+        n0 = nt * BNt;
 #pragma unroll
-    for (int j = 0; j < B_PW; ++j) {
-        const int row = (wave + NW * j) * 32 + (lane >> 1);
-        const int c = (lane & 1) ^ swz_b(row);
-        const long grp = (n0 >> 5) + wave + NW * j;
-        const long off = (long)s * split_slot_stride(p) + (grp * 32 < p.N ? grp : 0) * (p.K / BK) * 512 +
-                         (lane >> 1) * 16 + c * 8;
-        bsrc[j][0] = reinterpret_cast<const T *>(p.Bhi) + off;
-        if constexpr (TERMS == 3) bsrc[j][1] = reinterpret_cast<const T *>(p.Blo) + off;
-    }
+        for (int j = 0; j < A_PW; ++j) {
+            const int row = (wave + NW * j) * 16 + (lane >> 2);
+            const int c = (lane & 3) ^ swz_a(row);
+            const int m = m0 + row;
+            long ar = 0;
+            if (m < M) {
+                ar = p.a_idx ? (long)p.a_idx[m] : (long)m;
+                if (p.a_idx && (ar < 0 || ar >= p.a_idx_max)) {
+                    if (p.err) atomicOr(p.err, ADN_DEVERR_TOKEN);
+                    ar = 0;
+                }
+            }
+            asrc[j] = p.A + ar * p.a_sm + (long)s * p.a_ss + c * 4;
+        }
+#pragma unroll
+        for (int j = 0; j < B_PW; ++j) {
+            const int row = (wave + NW * j) * 32 + (lane >> 1);
+            const int c = (lane & 1) ^ swz_b(row);
+            const long grp = (n0 >> 5) + wave + NW * j;
+            const long off = (long)s * split_slot_stride(p) + (grp * 32 < p.N ? grp : 0) * (p.K / BK) * 512 +
+                             (lane >> 1) * 16 + c * 8;
+            bsrc[j][0] = reinterpret_cast<const T *>(p.Bhi) + off;
+            if constexpr (TERMS == 3) bsrc[j][1] = reinterpret_cast<const T *>(p.Blo) + off;
+        }
+    };
     auto issue = [&](int kt, int st) {
 #pragma unroll
         for (int j = 0; j < A_PW; ++j)
@@ -175,12 +192,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
         }
     }
     floatx16 acc[WTM][WTN];
-#pragma unroll
-    for (int i = 0; i < WTM; ++i)
-#pragma unroll
-        for (int j = 0; j < WTN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     // Fragments in registers: A of a slice is read raw (fp32) one step ahead and split just
     // before its slice is multiplied; B is streamed one 32-column tile at a time through two
@@ -225,13 +236,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     };
 
     const int nk = p.K / BK;
+    auto prologue = [&]() {
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
-        if (st < nk) issue(st, st);
-    if (STAGES - 2 < nk)  // this wave's loads of slice 0 are done
+        for (int st = 0; st < STAGES - 1; ++st)
+            if (st < nk) issue(st, st);
+    };
+    set_tile(t);
+    prologue();
+    bool first = true;
+    while (true) {
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    // this wave's loads of the tile's first slice are complete: in a workgroup's first tile at
+    // most STAGES-2 later slices are in flight; after an epilogue, whose stores the
+    // vector-memory counter also counts, everything is waited for
+    if (first && STAGES - 2 < nk)
         wait_vmcnt<(STAGES - 2) * LOADS>();
     else
         wait_vmcnt<0>();
+    first = false;
     lds_barrier();
     read_a(0);
     read_b(0, 0, bq[0]);
@@ -267,9 +294,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
         }
         split_a();
     }
-    lds_barrier();  // every wave is done with the ring before the epilogue reuses it
-
-    epilogue_t<ROLE, WTM, WTN, WGM, WGN>(p, acc, M, s, m0, n0, osc, &As[0][0][0], reinterpret_cast<int *>(&Bs[0][0][0][0]));
+    lds_barrier();  // every wave is done with the ring
+    // The next tile's first slices are loaded into ring slots 0..STAGES-2 while this tile's
+    // results are stored; the epilogue's LDS scratch (arg-max partials) is slot STAGES-1.
+    const int es = s, em0 = m0, en0 = n0;
+    const int tn = next_tile(t + gridDim.x);
+    if (tn < total) {
+        set_tile(tn);
+        prologue();
+    }
+    epilogue_t<ROLE, WTM, WTN, WGM, WGN>(p, acc, M, es, em0, en0, osc, &As[STAGES - 1][0][0],
+                                         reinterpret_cast<int *>(&Bs[STAGES - 1][0][0][0]));
+    if (tn >= total) break;
+    t = tn;
+    }
 }
 
 // Skinny GEMM (at most 32 rows: one position of every sequence, a decode step).  There the
@@ -406,6 +444,19 @@ __global__ void k_split(const float *w, int S, int N, int K, float scale, T *hi,
     }
 }
 
+// Grid of the persistent ring kernel: at most `per_cu` resident workgroups on every CU, a
+// multiple of the XCD count (block i runs on XCD i % 8), never more than the tiles.
+int ring_grid(int total, int per_cu) {
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+        return total;
+    long g = (long)ncu * per_cu;
+    g -= g % NXCD;
+    if (g < NXCD) g = NXCD;
+    return (int)std::min<long>(total, g);
+}
+
 template <int ROLE, typename T, int TERMS, int WTN>
 void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
     const int total = ((p.N + 32 * WTN - 1) / (32 * WTN)) * p.S;
@@ -420,7 +471,10 @@ void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
 
 // Tile configurations (WTM, WTN, WGM, WGN, STAGES): GEMMs that are wide in both M and N use
 // 256x256 blocks of 8 waves (one workgroup per CU, 128 KB of LDS ring); the rest 128x128 blocks
-// of 4 waves (two workgroups per CU) so that their grids still cover the chip.
+// of 4 waves (two workgroups per CU) so that their grids still cover the chip.  The 256x256
+// configuration runs persistent (one resident workgroup per CU walking its share of tiles, the
+// next tile's first slices loaded during the epilogue); the smaller ones launch a workgroup per
+// tile, whose short k loops would otherwise wait on the previous tile's stores.
 template <int ROLE, typename T, int TERMS>
 void launch_cfg(const GemmParams &p, hipStream_t st) {
     if constexpr (ROLE != ROLE_LMHEAD) {
@@ -452,7 +506,8 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
     const int total = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.S;
     if (total <= 0) return;
     if (big)
-        hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4>), dim3(total), dim3(512), 0, st, p);
+        hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4>), dim3(ring_grid(total, 1)), dim3(512), 0, st,
+                           p);
     else
         hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 2, 2, 2, 4>), dim3(total), dim3(256), 0, st, p);
 }
