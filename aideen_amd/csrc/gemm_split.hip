@@ -469,7 +469,7 @@ void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
     }
 }
 
-// Tile configurations (WTM, WTN, WGM, WGN, STAGES): GEMMs that are wide in both M and N use
+// Tile configurations (WTM, WTN, WGM, WGN, STAGES): GEMMs with M >= 1024 and N >= 512 use
 // 256x256 blocks of 8 waves (one workgroup per CU, 128 KB of LDS ring); the rest 128x128 blocks
 // of 4 waves (two workgroups per CU) so that their grids still cover the chip.  The 256x256
 // configuration runs persistent (one resident workgroup per CU walking its share of tiles, the
@@ -501,7 +501,7 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
             return;
         }
     }
-    const bool big = p.N >= 1024 && p.M >= 1024;
+    const bool big = p.N >= 512 && p.M >= 1024;
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
     const int total = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.S;
     if (total <= 0) return;
