@@ -221,8 +221,9 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const int idx = lane + 64 * e;
-                // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389)
-                const float as_ = (o[idx] + sg[idx]) + (hc ? hc[idx] : 0.0f);
+                // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389);
+                // o is read once (non-temporal), signal and h again next iteration
+                const float as_ = (__builtin_nontemporal_load(o + idx) + sg[idx]) + (hc ? hc[idx] : 0.0f);
                 const float c = as_ + an[idx];
                 cval[e] = c;
                 hold[e] = h[idx];
