@@ -10,6 +10,16 @@ namespace gemm {
 
 constexpr int BM = 128, BN = 128, NT = 256, GROUP_M = 8, NXCD = 8;
 
+// Workgroup barrier without the memory fence of __syncthreads (which would drain every
+// outstanding global load and store, LDS DMA included): this wave's LDS operations are completed
+// first (through the builtin, so that the compiler's own wait-count tracking sees it), the memory
+// clobber keeps the compiler from moving LDS accesses across the barrier.  For exchanges through
+// LDS only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ void map_block(int bid, int total, int nM, int nN, int &s, int &mt,
                                           int &nt) {
     // XCD-contiguous remap: hardware sends workgroup i to XCD i % 8.
@@ -129,11 +139,33 @@ struct EpiCtx {
     int *scratch_i;
 };
 
+// One transposing step of the arg-max butterfly at lane offset OFF (< 32, within a half-wave):
+// of the 2 OFF candidates held in cv/ci[0 .. 2 OFF), a lane keeps the upper half if bit OFF of
+// its lane index is set and the lower half otherwise, combined with its partner's candidates for
+// the same rows, into cv/ci[0 .. OFF).
+template <int OFF, typename F>
+__device__ __forceinline__ void butterfly_step(float (&cv)[16], int (&ci)[16], int r, F better) {
+    const bool up = (r & OFF) != 0;
+#pragma unroll
+    for (int j = 0; j < OFF; ++j) {
+        const float sv = up ? cv[j] : cv[j + OFF];
+        const int si = up ? ci[j] : ci[j + OFF];
+        float kv = up ? cv[j + OFF] : cv[j];
+        int ki = up ? ci[j + OFF] : ci[j];
+        better(__int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(sv), (OFF << 10) | 0x1F)),
+               __builtin_amdgcn_ds_swizzle(si, (OFF << 10) | 0x1F), kv, ki);
+        cv[j] = kv;
+        ci[j] = ki;
+    }
+}
+
 template <int I, int WTM, int WTN, int WGM, int EPI, bool AM, bool CHECK, bool STREAM>
 __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c,
                                          const float (&bj)[WTN], const bool (&nv)[WTN]) {
     constexpr int BMt = WGM * WTM * 32;
     const int ncol0 = c.n0 + c.wn * WTN * 32 + c.r;  // column of j = 0
+    float cv[16];  // per row e: this lane's (max, last arg-max) over its WTN columns
+    int ci[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int ml = (c.wm * WTM + I) * 32 + 8 * (e >> 2) + 4 * c.hh + (e & 3);
@@ -165,19 +197,36 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
             }
         }
         if constexpr (AM) {
+            cv[e] = bv;
+            ci[e] = bi;
+        }
+    }
+    if constexpr (AM) {
+        // (max, last arg-max) of each of the 16 rows over the 32 lanes of a half-wave, by a
+        // transposing butterfly: offset 16 combines all 16 candidates with the partner's, then at
+        // offsets 8, 4, 2, 1 each lane keeps half of the rows it still holds (the upper half if
+        // that offset bit is set) and combines its partner's candidates for them.  Lane r ends
+        // with row e = r % 16.  The combination is a maximum with ties to the larger index, so
+        // the order of combination does not change the result.
+        auto better = [](float v2, int i2, float &v, int &i) {
+            if (v2 > v || (v2 == v && i2 > i)) {
+                v = v2;
+                i = i2;
+            }
+        };
 #pragma unroll
-            for (int off = 16; off > 0; off >>= 1) {
-                const float v2 = __shfl_xor(bv, off, 64);
-                const int i2 = __shfl_xor(bi, off, 64);
-                if (v2 > bv || (v2 == bv && i2 > bi)) {
-                    bv = v2;
-                    bi = i2;
-                }
-            }
-            if (c.r == 0) {
-                c.scratch_v[c.wn * BMt + ml] = bv;
-                c.scratch_i[c.wn * BMt + ml] = bi;
-            }
+        for (int e = 0; e < 16; ++e)
+            better(__int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(cv[e]), (16 << 10) | 0x1F)),
+                   __builtin_amdgcn_ds_swizzle(ci[e], (16 << 10) | 0x1F), cv[e], ci[e]);
+        butterfly_step<8>(cv, ci, c.r, better);
+        butterfly_step<4>(cv, ci, c.r, better);
+        butterfly_step<2>(cv, ci, c.r, better);
+        butterfly_step<1>(cv, ci, c.r, better);
+        if (c.r < 16) {
+            const int e = c.r;
+            const int ml = (c.wm * WTM + I) * 32 + 8 * (e >> 2) + 4 * c.hh + (e & 3);
+            c.scratch_v[c.wn * BMt + ml] = cv[0];
+            c.scratch_i[c.wn * BMt + ml] = ci[0];
         }
     }
     if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM, EPI, AM, CHECK, STREAM>(p, acc, c, bj, nv);
@@ -193,8 +242,10 @@ __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WT
         const int n = c.n0 + (c.wn * WTN + j) * 32 + c.r;
         nv[j] = !CHECK || n < p.N;
         bj[j] = 0.0f;
-        if constexpr (EPI == EPI_BIAS)
-            if (nv[j] && n < p.bias_n) bj[j] = p.bias[(long)c.s * p.bias_ss + n];
+        if constexpr (EPI == EPI_BIAS) {
+            if (nv[j] && n < p.bias_n)
+                bj[j] = p.bias[(long)c.s * p.bias_ss + n];
+        }
     }
     epi_rows<0, WTM, WTN, WGM, EPI, AM, CHECK, STREAM>(p, acc, c, bj, nv);
     if constexpr (AM) {
@@ -203,7 +254,7 @@ __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WT
         static_assert(CPW == 64 || CPW == 128, "arg-max partials need 64 or 128 columns per wave");
         constexpr int TPW = 128 / CPW;
         constexpr int QT = WGN / TPW;  // 128-column tiles per block
-        __syncthreads();
+        lds_barrier();  // the partials are exchanged through LDS; the logits stores need not wait
         const int tid = threadIdx.x;
         for (int idx = tid; idx < BMt * QT; idx += 64 * WGM * WGN) {
             const int ml = idx % BMt, q = idx / BMt;

@@ -79,14 +79,6 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier without the memory fence of __syncthreads (which would drain every
-// outstanding LDS DMA): this wave's LDS reads are completed first (through the builtin, so that
-// the compiler's own wait-count tracking sees it), the memory clobber keeps the compiler from
-// moving LDS accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
-}
 
 template <int ROLE, typename T, int TERMS, int WTM, int WTN, int WGM, int WGN, int STAGES>
 __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_gemm_split(GemmParams p) {
