@@ -188,10 +188,11 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
                 else
                     crow[32 * j] = v;
                 if constexpr (AM) {
-                    const int n = ncol0 + 32 * j;
-                    if (v > bv || (v == bv && n > bi)) {
+                    // this lane's columns grow with j, so "larger, or equal at a larger index"
+                    // is v >= bv here (false for NaN either way)
+                    if (v >= bv) {
                         bv = v;
-                        bi = n;
+                        bi = ncol0 + 32 * j;
                     }
                 }
             }
