@@ -78,10 +78,12 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_gate(Dims D, const float *__re
         float abar;
         if (SEL) {
             // W_vw^T (W_kw^T u) with u = h/rms: the record holds W_kw^T h, so divide once
+            // unconditional loads (index clamped into the row's r values; the weights past r are
+            // zero) so that the row's projections are fetched together instead of one load,
+            // wait and branch per term
             float dot = 0.0f;
 #pragma unroll
-            for (int q = 0; q < RKA; ++q)
-                if (q < r) dot += wv[q] * rc[1 + q];
+            for (int q = 0; q < RKA; ++q) dot += wv[q] * rc[1 + min(q, r - 1)];
             const float pre = bd + dot / rms;
             const float delta = logf(1.0f + expf(pre));
             const float acore = expf(delta * ln_ab);
