@@ -10,8 +10,9 @@
 // With bf16 halves (no range issue) the error is ~2^-16; TERMS = 1 is the plain bf16-input,
 // fp32-accumulate product.
 //
-// Weights (B) are split once at upload ([S][N][K] hi and lo arrays).  Activations (A) stay fp32
-// in HBM and in LDS and are split when a wave reads its MFMA fragments.
+// Weights (B) are split once at upload into hi and lo arrays in a blocked layout (k_split: each
+// 32-row x 16-K block one contiguous kilobyte).  Activations (A) stay fp32 in HBM and in LDS and
+// are split when a wave reads its MFMA fragments.
 //
 // Data movement is gfx950's direct global->LDS load (global_load_lds_dwordx4: lane L of a wave
 // writes LDS bytes [16L, 16L+16) of a 1 KB block at the wave-uniform address in M0), so no
@@ -20,7 +21,8 @@
 // HBM latency of the A rows that miss in L2.  One barrier per slice; each wave waits only for
 // its own loads of the slice about to be read (s_waitcnt vmcnt(n) with n = loads still allowed
 // in flight), then the barrier makes every wave's part visible and frees the slot that the next
-// loads overwrite.
+// loads overwrite.  The fragments of the next slice are read from LDS while the current one is
+// multiplied (A one step ahead, B one 32-column tile ahead).
 //
 // LDS rows: A is 16 fp32 = 64 bytes (4 chunks of 16 B), B is 16 halves = 32 bytes (2 chunks).
 // The chunks are XOR-swizzled so that the ds_read_b128 fragment reads (32 consecutive rows, one
@@ -30,7 +32,9 @@
 // fetches the chunk that belongs at its LDS position.
 //
 // Each wave owns WTM x WTN MFMA tiles of 32x32 (v_mfma_f32_32x32x16), the workgroup a WGM x WGN
-// grid of waves.  Wide GEMMs use 256x256 blocks of 8 waves (64x128 each, 2 waves per SIMD).
+// grid of waves.  Wide GEMMs use 256x256 blocks of 8 waves (64x128 each, 2 waves per SIMD), run
+// persistent: a resident workgroup per CU walks its share of the tiles, loading the next tile's
+// first slices while the current tile's results are stored.
 #include "gemm_common.h"
 
 namespace adn {
