@@ -53,6 +53,7 @@ __global__ void k_init(Dims D, SolveBuffers b, const float *x_src, const int32_t
     if (s == 0 && lane == 0) {
         b.act[0][t] = t;
         b.iters[t] = 0;
+        if (b.rprev) b.rprev[t] = 1.0f;
     }
     if (row == 0 && lane == 0) {
         b.cnt[0] = ntok;
@@ -178,6 +179,30 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
     }
 }
 
+// Token residual modes: max-abs over [H][d] (default), L2 over [H][d] (ADN_F_RESID_L2), or the
+// largest per-slot relative RMS change (ADN_F_RESID_RELRMS).  Per slot, `acc` is the max |dh|
+// (mode 0) or the sum of dh^2 (modes 1, 2) after the wave reduction; `rms` the slot's RMSNorm
+// denominator.
+__device__ __forceinline__ float slot_resid(int mode, float acc, float rms, int d) {
+    return mode == 2 ? sqrtf(acc / (float)d + 1e-12f) / fmaxf(rms, 1e-6f) : acc;
+}
+__device__ __forceinline__ float combine_resid(int mode, float tok, float slot) {
+    return mode == 1 ? tok + slot : fmaxf(tok, slot);
+}
+// Exit test after update k (0-based) of a token with residual r: below eps, the iteration cap,
+// or (with rprev) the homeostatic plateau of deq_slot_attn_unified_clean.wgsl:1786-1793
+// (k+1 >= 4, r <= max(eps, 0.15 * 0.2), |r - r_prev| <= 0.10 max(r_prev, eps)); r_prev is the
+// previous update's residual (1 before the first), replaced by r here (`store`: this lane writes).
+__device__ __forceinline__ bool token_done(float r, float eps, int k, int max_iters, float *rprev, bool store) {
+    bool done = (r < eps) || (k + 1 >= max_iters);
+    if (rprev) {
+        const float rp = *rprev;
+        if (k + 1 >= 4 && r <= fmaxf(eps, 0.15f * 0.2f) && fabsf(r - rp) / fmaxf(rp, eps) <= 0.10f) done = true;
+        if (store) *rprev = r;
+    }
+    return done;
+}
+
 // ---------------------------------------------------------------------------------------
 // Damped update and exit test of one active token (one wave; FPMR:1386-1393): per slot
 // c = o + signal + anchor, f = g*c/sqrt(mean(c^2)+1e-6), h' = f*beta + h*(1-beta); the token's
@@ -199,7 +224,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
     const int H = D.H;
     constexpr int d = 64 * E;
     const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
-    const bool l2 = (D.flags & ADN_F_RESID_L2) != 0;
+    const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
     bool keep = false;
     int t = -1;
     if (i < n) {
@@ -238,13 +263,13 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
                 const float hn = f * beta + hold[e] * omb;
                 h[lane + 64 * e] = hn;
                 const float df = hn - hold[e];
-                r = l2 ? r + df * df : fmaxf(r, fabsf(df));
+                r = rmode ? r + df * df : fmaxf(r, fabsf(df));
             }
-            r = l2 ? wave_sum(r) : wave_max(r);
-            rtok = l2 ? rtok + r : fmaxf(rtok, r);
+            r = rmode ? wave_sum(r) : wave_max(r);
+            rtok = combine_resid(rmode, rtok, slot_resid(rmode, r, rms, d));
         }
-        if (l2) rtok = sqrtf(rtok);
-        const bool done = (rtok < eps) || (k + 1 >= max_iters);
+        if (rmode == 1) rtok = sqrtf(rtok);
+        const bool done = token_done(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, lane == 0);
         if (done && lane == 0) b.iters[t] = k + 1;
         keep = !done;
     }
@@ -343,7 +368,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     const int H = D.H;
     constexpr int d = 64 * E;
     const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
-    const bool l2 = (D.flags & ADN_F_RESID_L2) != 0;
+    const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
     const int t = b.act[cur][i];
     const float *o = b.o + ((long)i * H + s) * d;
     const float *sg = b.signal + ((long)t * H + s) * d;
@@ -371,16 +396,16 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
         const float hn = f * beta + hold[e] * omb;
         h[lane + 64 * e] = hn;
         const float df = hn - hold[e];
-        r = l2 ? r + df * df : fmaxf(r, fabsf(df));
+        r = rmode ? r + df * df : fmaxf(r, fabsf(df));
     }
-    r = l2 ? wave_sum(r) : wave_max(r);
-    if (lane == 0) rs[s] = r;
+    r = rmode ? wave_sum(r) : wave_max(r);
+    if (lane == 0) rs[s] = slot_resid(rmode, r, rms, d);
     __syncthreads();
     if (threadIdx.x == 0) {
         float rtok = 0.0f;
-        for (int q = 0; q < H; ++q) rtok = l2 ? rtok + rs[q] : fmaxf(rtok, rs[q]);
-        if (l2) rtok = sqrtf(rtok);
-        if ((rtok < eps) || (k + 1 >= max_iters)) {
+        for (int q = 0; q < H; ++q) rtok = combine_resid(rmode, rtok, rs[q]);
+        if (rmode == 1) rtok = sqrtf(rtok);
+        if (token_done(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, true)) {
             b.iters[t] = k + 1;
         } else {
             const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);

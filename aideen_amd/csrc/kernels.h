@@ -68,6 +68,7 @@ struct SolveBuffers {
     int32_t *act[2];    // active token lists
     int32_t *cnt;       // [4]: counts of act[0], act[1]; cnt[2] unused; cnt[3] = total tokens
     int32_t *iters;     // [ntok]
+    float *rprev;       // [ntok] previous iteration's token residual (homeostatic exit) or null
     int32_t *cnt_hist;  // [ADN_PROFILE_MAX_ITERS] active tokens entering iteration k (summed over positions)
     float *hist;        // Anderson ring [m][ntok][H][d] or null
     unsigned *err;

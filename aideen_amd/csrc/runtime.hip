@@ -122,7 +122,9 @@ std::string validate_config(const adn_config &c) {
     if (c.max_batch < 1 || c.max_seq < 1) return "max_batch and max_seq must be >= 1";
     if ((long)c.max_batch * c.max_seq > (1L << 24)) return "max_batch*max_seq must be <= 2^24";
     if (c.anderson_m < 0 || c.anderson_m > 5) return "anderson_m must be in [0, 5]";
-    if (c.flags & ~0x7FFu) return "unknown flag bits";
+    if (c.flags & ~0x1FFFu) return "unknown flag bits";
+    if ((c.flags & ADN_F_RESID_L2) && (c.flags & ADN_F_RESID_RELRMS))
+        return "at most one of ADN_F_RESID_L2 and ADN_F_RESID_RELRMS";
     if ((c.flags & ADN_F_TOKEN_CARRY) && !(c.flags & ADN_F_MEMORY))
         return "ADN_F_TOKEN_CARRY needs ADN_F_MEMORY (positions solved in order)";
     if ((c.flags & ADN_F_MEMORY) && c.d_state != 1) return "ADN_F_MEMORY needs d_state == 1";
@@ -676,6 +678,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         b.act[1] = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
         b.cnt = (int32_t *)dmalloc(c, 4 * sizeof(int32_t));
         b.iters = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        b.rprev = (cfg->flags & ADN_F_HOMEOSTATIC_EXIT) ? (float *)dmalloc(c, (size_t)T * sizeof(float)) : nullptr;
         b.cnt_hist = (int32_t *)dmalloc(c, ADN_PROFILE_MAX_ITERS * sizeof(int32_t));
         b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));

@@ -39,6 +39,8 @@ F_GEMM_BF16X3 = 1 << 7
 F_GEMM_BF16 = 1 << 8
 F_MEMORY = 1 << 9
 F_TOKEN_CARRY = 1 << 10
+F_RESID_RELRMS = 1 << 11
+F_HOMEOSTATIC_EXIT = 1 << 12
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)

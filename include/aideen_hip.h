@@ -55,6 +55,15 @@ extern "C" {
 #define ADN_F_INIT_SIGNAL_RMS (1u << 3) /* h0 = signal/rms(signal) (deq_slot_attn_unified_clean.wgsl:900-943) */
 #define ADN_F_RESID_L2 (1u << 4)        /* L2 exit residual (aideen-node/src/inference.rs:214-221)    */
 #define ADN_F_SCAN_SELECTIVE (1u << 5)  /* input-dependent carrier decay (gpu_deq.rs:6129-6214)      */
+/* Relative-RMS exit residual (the GPU reference's err_h, deq_slot_attn_unified_clean.wgsl:1654-1695):
+ * per slot sqrt(mean_i (h'_i - h_i)^2 + 1e-12) / max(rms, 1e-6), rms the slot's RMSNorm
+ * denominator sqrt(mean c^2 + 1e-6); the token's residual is the largest over its slots (the
+ * joint-slot analogue of the max-abs default).  Excludes ADN_F_RESID_L2. */
+#define ADN_F_RESID_RELRMS (1u << 11)
+/* Homeostatic plateau exit as well (deq_slot_attn_unified_clean.wgsl:277-279,1786-1793): a token
+ * also stops after update k when k+1 >= 4, r_k <= max(eps, 0.15*0.2) and
+ * |r_k - r_{k-1}| <= 0.10 max(r_{k-1}, eps), with r_{-1} = 1 and r the token's residual. */
+#define ADN_F_HOMEOSTATIC_EXIT (1u << 12)
 
 /* Memory-coupled forward (the trainer's fixed-history mode, trainer.rs:677-720): per sequence,
  * token t's solve adds the history context fixed_hist_ctx(m_{t-1}, signal_t)

@@ -177,6 +177,7 @@ static void prep_free(prep *p) {
 typedef struct scratch {
     float *q, *k, *v, *mix, *o, *comb, *hn, *hist; /* hist: Anderson ring [m][H*d] */
     float *scores, *attn;
+    float *rms; /* [H] each slot's RMSNorm denominator in the last step (relative residual) */
 } scratch;
 
 static void scratch_init(scratch *s, const orc_cfg *c) {
@@ -192,11 +193,12 @@ static void scratch_init(scratch *s, const orc_cfg *c) {
     s->hist = (float *)malloc(sizeof(float) * hd * m);
     s->scores = (float *)malloc(sizeof(float) * c->H);
     s->attn = (float *)malloc(sizeof(float) * c->H * c->H);
+    s->rms = (float *)malloc(sizeof(float) * c->H);
 }
 
 static void scratch_free(scratch *s) {
     free(s->q); free(s->k); free(s->v); free(s->mix); free(s->o); free(s->comb); free(s->hn);
-    free(s->hist); free(s->scores); free(s->attn);
+    free(s->hist); free(s->scores); free(s->attn); free(s->rms);
 }
 
 /* FPMR:1305-1315 project_input_signal (per slot: signal_s = W_in[s] x). */
@@ -285,6 +287,7 @@ static void step_p(const prep *p, scratch *sc, const float *h, const float *sign
             }
         }
         const float rms = sqrtf(ss / (float)d + 1e-6f);
+        sc->rms[a] = rms;
         const float beta = p->c.beta, omb = 1.0f - p->c.beta;
         const float *ha = h + (size_t)a * d;
         float *hn = h_next + (size_t)a * d;
@@ -296,10 +299,26 @@ static void step_p(const prep *p, scratch *sc, const float *h, const float *sign
     if (attn_out) memcpy(attn_out, sc->attn, sizeof(float) * H * H);
 }
 
-/* Residual between consecutive iterates: max-abs (ARCHITECTURE.md:178-185) or L2 over the
- * token's flat [H*d] state (aideen-node/src/inference.rs:214-221). */
-static float residual(const orc_cfg *c, const float *a, const float *b) {
+/* Residual between consecutive iterates: max-abs (ARCHITECTURE.md:178-185), L2 over the
+ * token's flat [H*d] state (aideen-node/src/inference.rs:214-221), or the largest per-slot
+ * relative RMS change sqrt(mean (a-b)^2 + 1e-12) / max(rms, 1e-6) with rms the slot's RMSNorm
+ * denominator of the step that produced a (the GPU reference's err_h,
+ * deq_slot_attn_unified_clean.wgsl:1654-1695). */
+static float residual(const orc_cfg *c, const float *rms, const float *a, const float *b) {
     const int n = c->H * c->d;
+    if (c->flags & ORC_F_RESID_RELRMS) {
+        const int d = c->d;
+        float mx = 0.0f;
+        for (int s = 0; s < c->H; ++s) {
+            float acc = 0.0f;
+            for (int i = 0; i < d; ++i) {
+                const float df = a[(size_t)s * d + i] - b[(size_t)s * d + i];
+                acc += df * df;
+            }
+            mx = fmaxf(mx, sqrtf(acc / (float)d + 1e-12f) / fmaxf(rms[s], 1e-6f));
+        }
+        return mx;
+    }
     if (c->flags & ORC_F_RESID_L2) {
         float acc = 0.0f;
         for (int i = 0; i < n; ++i) {
@@ -394,14 +413,23 @@ static int solve_p(const prep *p, scratch *sc, const float *x, const float *hist
     if (!warm) init_p(p, x, signal, h);
     int iters = 0;
     const int m = c->anderson_m;
+    float r_prev = 1.0f; /* homeostatic exit: the previous update's residual (1 before the first) */
     for (int k = 0; k < c->max_iters; ++k) {
         step_p(p, sc, h, signal, hist, sc->hn, NULL);
-        const float r = residual(c, sc->hn, h);
+        const float r = residual(c, sc->rms, sc->hn, h);
         if (resid_trace) resid_trace[k] = r;
         iters = k + 1;
-        if (r < c->eps || m <= 0) {
+        /* exit below eps, or (ORC_F_HOMEOSTATIC_EXIT) on the plateau of
+         * deq_slot_attn_unified_clean.wgsl:1786-1793: k+1 >= 4, r <= max(eps, 0.15 * 0.2) and
+         * |r - r_prev| <= 0.10 max(r_prev, eps) */
+        int stop = r < c->eps;
+        if ((c->flags & ORC_F_HOMEOSTATIC_EXIT) && k + 1 >= 4 && r <= fmaxf(c->eps, 0.15f * 0.2f) &&
+            fabsf(r - r_prev) / fmaxf(r_prev, c->eps) <= 0.10f)
+            stop = 1;
+        r_prev = r;
+        if (stop || m <= 0) {
             memcpy(h, sc->hn, sizeof(float) * hd);
-            if (r < c->eps) break;
+            if (stop) break;
             continue;
         }
         /* Anderson: store g into ring slot k % m, then mix */

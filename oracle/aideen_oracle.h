@@ -28,6 +28,8 @@ extern "C" {
 #define ORC_F_SCAN_SELECTIVE   (1u << 5) /* input-dependent decay    (gpu_deq.rs:6129-6214)          */
 #define ORC_F_MEMORY           (1u << 9) /* memory-coupled forward   (orc_forward_memory; TRAINER:677-720) */
 #define ORC_F_TOKEN_CARRY      (1u << 10) /* memory mode: position t starts from h*_{t-1} (UWGSL:898, BRIDGE:167-173) */
+#define ORC_F_RESID_RELRMS     (1u << 11) /* largest per-slot relative RMS residual (UWGSL:1654-1695) */
+#define ORC_F_HOMEOSTATIC_EXIT (1u << 12) /* plateau exit as well (UWGSL:277-279,1786-1793)         */
 
 typedef struct orc_cfg {
     int32_t d, H, V, N, r;     /* d_r, h_slots, vocab, d_state, write rank (FPMR:290 RETAIN_RANK=32) */

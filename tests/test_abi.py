@@ -40,7 +40,8 @@ def test_struct_layouts_match_header():
 
 @pytest.mark.parametrize("bad", [
     dict(d_r=100), dict(d_r=4096), dict(h_slots=3), dict(d_state=0), dict(d_state=64),
-    dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 11), dict(flags=1 << 10, d_state=1),
+    dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 13), dict(flags=(1 << 4) | (1 << 11)),
+    dict(flags=1 << 10, d_state=1),
     dict(flags=1 << 9, d_state=4),
     dict(flags=(1 << 9) | (1 << 5), d_state=1), dict(vocab=0), dict(flags=(1 << 6) | (1 << 7)),
 ])

@@ -110,6 +110,12 @@ VARIANTS = [
     dict(d=128, H=4, V=500, N=2, flags=synth.F_INIT_SIGNAL_RMS | synth.F_RESID_L2 | synth.F_SCAN_SELECTIVE),
     dict(d=128, H=4, V=500, N=16, flags=synth.F_SCAN_SELECTIVE, sigma=0.7, anderson_m=3),
     dict(d=128, H=8, V=500, N=16, flags=synth.F_SCAN_SELECTIVE, sigma=0.7, anderson_m=5),
+    dict(d=128, H=4, V=500, N=4, flags=synth.F_RESID_RELRMS | synth.F_SCAN_SELECTIVE),
+    # damping 0.1: the residual shrinks ~5% per update, so the plateau rule ends most solves
+    # (r <= 0.03 with eps 1e-4) with both thresholds far from the fp32 rounding
+    dict(d=128, H=4, V=500, N=4, flags=synth.F_RESID_RELRMS | synth.F_HOMEOSTATIC_EXIT, beta=0.1, max_iters=40),
+    dict(d=64, H=8, V=300, N=1, flags=synth.F_RESID_RELRMS | synth.F_HOMEOSTATIC_EXIT, beta=0.1, max_iters=40,
+         anderson_m=3),
 ]
 
 
@@ -124,6 +130,25 @@ def test_variants_match_oracle(oracle_lib, var):
     be.upload_weights(w)
     got = be.forward(toks)
     assert_forward_parity(got, ref, str(var))
+
+
+def test_homeostatic_exit_shortens_the_solve(oracle_lib):
+    """With damping 0.1 the relative residual shrinks slowly; the plateau rule stops the tokens
+    well before the tolerance would (GPU and oracle agree on every count), and without the flag
+    the same model runs longer."""
+    log("homeostatic exit")
+    base = dict(d=128, H=4, V=500, N=4, beta=0.1, max_iters=60)
+    mc_h, w = _small(flags=synth.F_RESID_RELRMS | synth.F_HOMEOSTATIC_EXIT, **base)
+    mc_s, _ = _small(flags=synth.F_RESID_RELRMS, **base)
+    toks = synth.make_tokens("uniform", 2, 24, mc_h.V, seed=8)
+    be = make(mc_h, 2, 24)
+    be.upload_weights(w)
+    got = be.forward(toks, want=("iters", "h_star"))
+    ref = oracle_lib.Oracle(mc_h, w).forward(toks)
+    plain = oracle_lib.Oracle(mc_s, w).forward(toks)
+    assert np.array_equal(got["iters"], ref["iters"])
+    np.testing.assert_allclose(got["h_star"], ref["h_star"], rtol=RTOL, atol=ATOL)
+    assert (ref["iters"] < plain["iters"]).all() and ref["iters"].max() < 60
 
 
 def test_reference_gpu_layout_upload(oracle_lib):

@@ -161,6 +161,46 @@ def test_zero_attention_iteration_count_closed_form(oracle_lib, beta, eps):
     assert np.allclose(h, hk, atol=2e-6)
 
 
+@pytest.mark.parametrize("beta,eps,homeo", [(0.7, 1e-4, False), (0.35, 3e-5, False), (0.1, 1e-4, True),
+                                           (0.05, 1e-5, True), (0.3, 1e-4, True)])
+def test_zero_attention_relrms_and_homeostatic_closed_form(oracle_lib, beta, eps, homeo):
+    """Relative-RMS residual (and the homeostatic plateau exit) on the zero-attention model:
+    c_s = W_in[s] x + anchor_s is constant, so h_k = F + (1-beta)^k (h0 - F) and update k changes
+    slot s by beta (1-beta)^(k-1) (F - h0)_s; its residual is the largest over slots of
+    sqrt(mean of that squared + 1e-12) / rms(c_s).  The plateau ratio is then exactly beta from
+    the second update on, so the homeostatic rule (k >= 4, r <= max(eps, 0.03), ratio <= 0.1)
+    fires for beta <= 0.1 and never for beta = 0.3 (which must exit as without the flag)."""
+    flags = synth.F_RESID_RELRMS | (synth.F_HOMEOSTATIC_EXIT if homeo else 0)
+    mc, w = small_model(d=16, H=3, V=40, flags=flags, beta=beta, eps=eps, max_iters=200)
+    w = _zero_attention(w)
+    rng = np.random.default_rng(11)
+    w["norm_scale"] = rng.uniform(0.5, 1.5, 16).astype(np.float32)
+    o = oracle(oracle_lib, mc, w)
+    x = w["embed"][7].astype(np.float64)
+    c = np.einsum("sij,j->si", w["w_in"].astype(np.float64), x) + w["anchor"]
+    rms = np.sqrt((c * c).mean(1) + 1e-6)
+    Fh = w["norm_scale"] * c / rms[:, None]
+    h0 = x[None, :] + w["anchor"]
+    ks = np.arange(1, 201)
+    dh = beta * (1 - beta) ** (ks[:, None, None] - 1) * (Fh - h0)[None]
+    res = (np.sqrt((dh * dh).mean(2) + 1e-12) / np.maximum(rms, 1e-6)[None]).max(1)
+    stop = res < eps
+    if homeo:
+        prev = np.concatenate([[1.0], res[:-1]])
+        stop |= (ks >= 4) & (res <= max(eps, 0.15 * 0.2)) & (np.abs(res - prev) / np.maximum(prev, eps) <= 0.10)
+    k_exp = int(ks[np.argmax(stop)])
+    assert stop.any() and k_exp < 200
+    h, it, trace = o.solve(w["embed"][7])
+    assert it == k_exp
+    assert np.allclose(trace, res[:it], rtol=2e-4, atol=1e-7)
+    if homeo and beta <= 0.1:
+        assert res[it - 1] >= eps  # the plateau rule, not the tolerance, ended the solve
+    if homeo and beta == 0.3:  # never a plateau: the same exit as the plain relative residual
+        assert it == int(ks[np.argmax(res < eps)])
+    hk = Fh + (1 - beta) ** it * (h0 - Fh)
+    assert np.allclose(h, hk, atol=2e-6)
+
+
 def test_h1_attention_is_identity_weight(oracle_lib):
     """H=1: softmax over one key is 1, so o = W_o W_v h (orientation pinned by asymmetric W)."""
     mc, w = small_model(d=16, H=1, V=40)
