@@ -10,30 +10,35 @@ namespace {
 
 constexpr int WPB = 4;
 
-// pooled = fold(0, acc + h_s)/H (slot order kept); pnorm = (pooled/rms) * g, eps 1e-5.
+// pooled = fold(0, acc + h_s)/H (slot order kept); pnorm = (pooled/rms) * g, eps 1e-5.  One wave
+// per token; each lane keeps its E = d/64 pooled values in registers between the two passes.
+template <int E>
 __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int ntok, const float *g,
                                                    float *pooled, float *pnorm) {
     const int t = blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (t >= ntok) return;
-    const int d = D.d, H = D.H;
+    constexpr int d = 64 * E;
+    const int H = D.H;
     const float *ht = h + (long)t * H * d;
+    float pv[E];
     float ss = 0.0f;
-    for (int i = lane; i < d; i += 64) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
         float acc = 0.0f;
         for (int s = 0; s < H; ++s) acc = acc + ht[(long)s * d + i];
-        const float p = acc / (float)H;
-        if (pooled) pooled[(long)t * d + i] = p;
-        ss += p * p;
+        pv[e] = acc / (float)H;
+        if (pooled) pooled[(long)t * d + i] = pv[e];
+        ss += pv[e] * pv[e];
     }
     if (!pnorm) return;
     ss = wave_sum(ss);
     const float rms = sqrtf(ss / (float)d + 1e-5f);
-    for (int i = lane; i < d; i += 64) {
-        float acc = 0.0f;
-        for (int s = 0; s < H; ++s) acc = acc + ht[(long)s * d + i];
-        const float p = acc / (float)H;
-        pnorm[(long)t * d + i] = (p / rms) * (g ? g[i] : 1.0f);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        pnorm[(long)t * d + i] = (pv[e] / rms) * (g ? g[i] : 1.0f);
     }
 }
 
@@ -83,24 +88,29 @@ __global__ __launch_bounds__(AM_NT) void k_argmax(const float *logits, int V, in
 }
 
 // Reduce the LM-head tile partials of one row (one wave per row), same tie rule.
-__global__ __launch_bounds__(256) void k_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok,
-                                                       int ntiles, int32_t *out) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= ntok) return;
+// A block takes 64 rows (one per lane: the [tile][row] partials are read coalesced) and its
+// AR_W waves split the tiles; the waves' candidates are combined through LDS (the combination is
+// a maximum with ties to the larger index, so its order does not change the result).
+constexpr int AR_W = 16;
+
+__global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val, const int32_t *am_idx,
+                                                            int ntok, int ntiles, int32_t *out) {
+    __shared__ float sv[AR_W][64];
+    __shared__ int si[AR_W][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 64 + lane;
     float bv = -INFINITY;
     int bi = -1;
-    for (int t = lane; t < ntiles; t += 64) {
-        const float v = am_val[(long)t * ntok + row];
-        const int i = am_idx[(long)t * ntok + row];
-        am_combine(bv, bi, v, i);
+    if (row < ntok)
+        for (int t = w; t < ntiles; t += AR_W)
+            am_combine(bv, bi, am_val[(long)t * ntok + row], am_idx[(long)t * ntok + row]);
+    sv[w][lane] = bv;
+    si[w][lane] = bi;
+    __syncthreads();
+    if (w == 0 && row < ntok) {
+        for (int q = 1; q < AR_W; ++q) am_combine(bv, bi, sv[q][lane], si[q][lane]);
+        out[row] = bi < 0 ? 0 : bi;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-        const float v2 = __shfl_xor(bv, off, 64);
-        const int i2 = __shfl_xor(bi, off, 64);
-        am_combine(bv, bi, v2, i2);
-    }
-    if (lane == 0) out[row] = bi < 0 ? 0 : bi;
 }
 
 // Greedy decode bookkeeping: tokens[b] = argmax[b]; out_seq[b][j] = argmax[b].
@@ -117,8 +127,16 @@ __global__ void k_decode_step(const int32_t *argmax, int32_t *tokens, int32_t *o
 
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
                       float *pnorm, hipStream_t st) {
-    hipLaunchKernelGGL(k_pool_norm, dim3((unsigned)((ntok + WPB - 1) / WPB)), dim3(64 * WPB), 0, st, D,
-                       h, ntok, g, pooled, pnorm);
+    const dim3 grid((unsigned)((ntok + WPB - 1) / WPB)), blk(64 * WPB);
+    switch (D.d) {
+        case 64: hipLaunchKernelGGL(k_pool_norm<1>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        case 128: hipLaunchKernelGGL(k_pool_norm<2>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        case 256: hipLaunchKernelGGL(k_pool_norm<4>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        case 512: hipLaunchKernelGGL(k_pool_norm<8>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        case 1024: hipLaunchKernelGGL(k_pool_norm<16>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        case 2048: hipLaunchKernelGGL(k_pool_norm<32>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        default: break;  // rejected at context creation
+    }
 }
 
 void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st) {
@@ -127,7 +145,7 @@ void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream
 
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
                           hipStream_t st) {
-    hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 3) / 4)), dim3(256), 0, st, am_val, am_idx, ntok,
+    hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 63) / 64)), dim3(64 * AR_W), 0, st, am_val, am_idx, ntok,
                        ntiles, out);
 }
 
