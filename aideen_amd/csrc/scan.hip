@@ -27,13 +27,20 @@ namespace {
 
 constexpr int WPB = 4;
 
-__global__ __launch_bounds__(256) void k_row_rms(const float *h, long rows, int d, float *rec, int REC) {
+// E = d/64 values per lane, all loaded before the sum (in the same order as a strided loop)
+template <int E>
+__global__ __launch_bounds__(256) void k_row_rms(const float *h, long rows, float *rec, int REC) {
+    constexpr int d = 64 * E;
     const long row = (long)blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *hr = h + row * d;
+    float x[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[e] = hr[lane + 64 * e];
     float ss = 0.0f;
-    for (int i = lane; i < d; i += 64) ss += hr[i] * hr[i];
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss += x[e] * x[e];
     ss = wave_sum(ss);
     if (lane == 0) rec[row * REC] = sqrtf(ss / (float)d + 1e-6f);
 }
@@ -241,8 +248,16 @@ int scan_chunks(int B, int T, int H, int d) {
 }
 
 void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipStream_t st) {
-    hipLaunchKernelGGL(k_row_rms, dim3((unsigned)((rows + WPB - 1) / WPB)), dim3(64 * WPB), 0, st, h, rows, d,
-                       rec, REC);
+    const dim3 grid((unsigned)((rows + WPB - 1) / WPB)), blk(64 * WPB);
+    switch (d) {
+        case 64: hipLaunchKernelGGL(k_row_rms<1>, grid, blk, 0, st, h, rows, rec, REC); break;
+        case 128: hipLaunchKernelGGL(k_row_rms<2>, grid, blk, 0, st, h, rows, rec, REC); break;
+        case 256: hipLaunchKernelGGL(k_row_rms<4>, grid, blk, 0, st, h, rows, rec, REC); break;
+        case 512: hipLaunchKernelGGL(k_row_rms<8>, grid, blk, 0, st, h, rows, rec, REC); break;
+        case 1024: hipLaunchKernelGGL(k_row_rms<16>, grid, blk, 0, st, h, rows, rec, REC); break;
+        case 2048: hipLaunchKernelGGL(k_row_rms<32>, grid, blk, 0, st, h, rows, rec, REC); break;
+        default: break;  // rejected at context creation
+    }
 }
 
 void launch_scan_gate(const Dims &D, const float *h, const float *rec, int ntok, const float *a_log,
