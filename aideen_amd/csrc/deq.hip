@@ -69,6 +69,15 @@ __global__ void k_init(Dims D, SolveBuffers b, const float *x_src, const int32_t
 // folded in slot order.  One wave per (token, group of QA query slots); P = QA*H <= 64 partial
 // dot products per lane, all-reduced across the wave so every lane holds every score.
 // ---------------------------------------------------------------------------------------
+// *p, loaded non-temporally if NT
+template <bool NT>
+__device__ __forceinline__ float qkv_load(const float *p) {
+    if constexpr (NT)
+        return __builtin_nontemporal_load(p);
+    else
+        return *p;
+}
+
 template <int H, int QA, int VEC>
 __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, int k) {
     constexpr int NG = H / QA;
@@ -84,7 +93,9 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
     if (i >= n) return;
     const int d = D.d;
     const long rowstride = 3L * d;
-    // Q|K|V rows are read once: non-temporal loads keep them from displacing cached data
+    // With one wave per token (QA == H) the Q|K|V rows are read once: non-temporal loads keep
+    // them from displacing cached data.  With several, the waves of a token share K and V.
+    constexpr bool NT = QA == H;
     const float *base = b.qkv + (long)i * H * rowstride;
 
     float part[QA][H];
@@ -98,12 +109,12 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
 #pragma unroll
         for (int a = 0; a < QA; ++a)
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) q[a][v] = __builtin_nontemporal_load(base + (long)(g * QA + a) * rowstride + off + v);
+            for (int v = 0; v < VEC; ++v) q[a][v] = qkv_load<NT>(base + (long)(g * QA + a) * rowstride + off + v);
 #pragma unroll
         for (int c = 0; c < H; ++c) {
             float kk[VEC];
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) kk[v] = __builtin_nontemporal_load(base + (long)c * rowstride + d + off + v);
+            for (int v = 0; v < VEC; ++v) kk[v] = qkv_load<NT>(base + (long)c * rowstride + d + off + v);
 #pragma unroll
             for (int a = 0; a < QA; ++a)
 #pragma unroll
@@ -111,49 +122,73 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
         }
     }
     const float scale = 1.0f / sqrtf((float)d);
-    // Wave totals of the P = QA*H partial dot products with wave_sum's offsets (32, 16, ..., 1),
-    // so that every total is bit-identical to wave_sum's.  Offsets >= P add all P values; below
-    // P the lanes also split the indices still held (a transposing butterfly): at offset `off`
-    // the lanes with that bit set keep the upper half of the range, the others the lower half,
-    // and each adds its partner's partial for the indices it keeps.  Lane L ends with the total
-    // of index L % P = a * H + c: 2P - 1 shuffles instead of 6P.
     constexpr int P = QA * H;
-    float t[P];
+    float w[P];  // the attention weights, index a * H + c, the same in every lane
+    if constexpr (P >= 16) {
+        // Wave totals of the P = QA*H partial dot products with wave_sum's offsets (32, 16, ..., 1),
+        // so that every total is bit-identical to wave_sum's.  Offsets >= P add all P values; below
+        // P the lanes also split the indices still held (a transposing butterfly): at offset `off`
+        // the lanes with that bit set keep the upper half of the range, the others the lower half,
+        // and each adds its partner's partial for the indices it keeps.  Lane L ends with the total
+        // of index L % P = a * H + c: 2P - 1 shuffles instead of 6P.
+        float t[P];
 #pragma unroll
-    for (int a = 0; a < QA; ++a)
+        for (int a = 0; a < QA; ++a)
 #pragma unroll
-        for (int c = 0; c < H; ++c) t[a * H + c] = part[a][c];
+            for (int c = 0; c < H; ++c) t[a * H + c] = part[a][c];
 #pragma unroll
-    for (int off = 32; off >= P; off >>= 1)
+        for (int off = 32; off >= P; off >>= 1)
 #pragma unroll
-        for (int j = 0; j < P; ++j) t[j] += __shfl_xor(t[j], off, 64);
+            for (int j = 0; j < P; ++j) t[j] += __shfl_xor(t[j], off, 64);
 #pragma unroll
-    for (int off = (P < 64 ? P : 64) / 2; off > 0; off >>= 1) {
-        const bool up = (lane & off) != 0;
+        for (int off = (P < 64 ? P : 64) / 2; off > 0; off >>= 1) {
+            const bool up = (lane & off) != 0;
 #pragma unroll
-        for (int j = 0; j < off; ++j) {
-            const float send = up ? t[j] : t[j + off];
-            const float keep = up ? t[j + off] : t[j];
-            t[j] = keep + __shfl_xor(send, off, 64);
+            for (int j = 0; j < off; ++j) {
+                const float send = up ? t[j] : t[j + off];
+                const float keep = up ? t[j + off] : t[j];
+                t[j] = keep + __shfl_xor(send, off, 64);
+            }
+        }
+        float sc = t[0] * scale;
+        if (D.flags & ADN_F_SCORE_CLAMP4) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
+        // softmax over the key slots of this lane's query (lanes gb .. gb + H - 1), max and sum
+        // taken in key order as in the sequential form
+        const int gb = lane & ~(H - 1);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < H; ++c) mx = fmaxf(mx, __shfl(sc, gb + c, 64));
+        const float ex = expf(sc - mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < H; ++c) sum += __shfl(ex, gb + c, 64);
+        const float w_own = ex / sum;
+        // every weight to every lane as a wave-uniform value (lane i holds index i)
+#pragma unroll
+        for (int q = 0; q < P; ++q) w[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_own), q));
+    } else {
+        // few scores: one wave_sum each and the softmax in every lane (the same totals)
+#pragma unroll
+        for (int a = 0; a < QA; ++a) {
+            float mx = -INFINITY;
+            float e[H];
+#pragma unroll
+            for (int c = 0; c < H; ++c) {
+                float sc = wave_sum(part[a][c]) * scale;
+                if (D.flags & ADN_F_SCORE_CLAMP4) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
+                e[c] = sc;
+                mx = fmaxf(mx, sc);
+            }
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < H; ++c) {
+                e[c] = expf(e[c] - mx);
+                sum += e[c];
+            }
+#pragma unroll
+            for (int c = 0; c < H; ++c) w[a * H + c] = e[c] / sum;
         }
     }
-    float sc = t[0] * scale;
-    if (D.flags & ADN_F_SCORE_CLAMP4) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
-    // softmax over the key slots of this lane's query (lanes gb .. gb + H - 1), max and sum
-    // taken in key order as in the sequential form
-    const int gb = lane & ~(H - 1);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < H; ++c) mx = fmaxf(mx, __shfl(sc, gb + c, 64));
-    const float ex = expf(sc - mx);
-    float sum = 0.0f;
-#pragma unroll
-    for (int c = 0; c < H; ++c) sum += __shfl(ex, gb + c, 64);
-    const float w_own = ex / sum;
-    // every weight to every lane as a wave-uniform value (lane i holds index i)
-    float w[P];
-#pragma unroll
-    for (int q = 0; q < P; ++q) w[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_own), q));
 
     float *mixbase = b.mix + (long)i * H * d;
     for (int off = lane * VEC; off < d; off += 64 * VEC) {
@@ -166,7 +201,7 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
         for (int c = 0; c < H; ++c) {
             float vv[VEC];
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) vv[v] = __builtin_nontemporal_load(base + (long)c * rowstride + 2 * d + off + v);
+            for (int v = 0; v < VEC; ++v) vv[v] = qkv_load<NT>(base + (long)c * rowstride + 2 * d + off + v);
 #pragma unroll
             for (int a = 0; a < QA; ++a)
 #pragma unroll
