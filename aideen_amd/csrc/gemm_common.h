@@ -166,8 +166,26 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
     const int ncol0 = c.n0 + c.wn * WTN * 32 + c.r;  // column of j = 0
     float cv[16];  // per row e: this lane's (max, last arg-max) over its WTN columns
     int ci[16];
+    // The residual operand is loaded EB rows at a time before their stores: a load issued after
+    // stores is waited for behind them (the vector-memory counter retires in issue order).
+    constexpr int EB = EPI == EPI_ADD_A ? 8 : 16;
+    float av[EPI == EPI_ADD_A ? EB : 1][EPI == EPI_ADD_A ? WTN : 1];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
+        if constexpr (EPI == EPI_ADD_A) {
+            if (e % EB == 0) {
+#pragma unroll
+                for (int q = 0; q < EB; ++q) {
+                    const int m = c.m0 + (c.wm * WTM + I) * 32 + 8 * ((e + q) >> 2) + 4 * c.hh + ((e + q) & 3);
+                    const bool mv = !CHECK || m < c.M;
+#pragma unroll
+                    for (int j = 0; j < WTN; ++j)
+                        av[q][j] = (!CHECK || (mv && nv[j]))
+                                       ? p.A[(long)m * p.a_sm + (long)c.s * p.a_ss + ncol0 + 32 * j]
+                                       : 0.0f;
+                }
+            }
+        }
         const int ml = (c.wm * WTM + I) * 32 + 8 * (e >> 2) + 4 * c.hh + (e & 3);
         const int m = c.m0 + ml;
         const bool mv = !CHECK || m < c.M;
@@ -179,9 +197,7 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
             const bool ok = !CHECK || (mv && nv[j]);
             float v = acc[I][j][e] * c.osc;
             if constexpr (EPI == EPI_BIAS) v += bj[j];
-            if constexpr (EPI == EPI_ADD_A) {
-                if (ok) v = p.A[(long)m * p.a_sm + (long)c.s * p.a_ss + ncol0 + 32 * j] + v;
-            }
+            if constexpr (EPI == EPI_ADD_A) v = av[e % EB][j] + v;
             if (ok) {
                 if constexpr (STREAM)
                     __builtin_nontemporal_store(v, crow + 32 * j);

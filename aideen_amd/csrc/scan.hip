@@ -51,7 +51,10 @@ constexpr int GATE_ROWS = 16;
 
 // Gate: for every (token, slot, channel) the decay abar and the carrier input (1-abar) x,
 // fully parallel (the rank-r bottleneck comes from the record; W_vw's column for the channel
-// is held in registers across GATE_ROWS tokens of one slot).
+// is held in registers across GATE_ROWS tokens of one slot).  The block's GATE_ROWS records
+// (rms and the r projections) are staged in LDS, and a thread loads all of its h values before
+// its first store: a load issued after stores would be waited for behind them (the
+// vector-memory counter retires in issue order).
 template <int RK, bool SEL>
 __global__ __launch_bounds__(SCAN_NT) void k_scan_gate(Dims D, const float *__restrict__ h,
                                                        const float *__restrict__ rec, int ntok,
@@ -60,37 +63,54 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_gate(Dims D, const float *__re
                                                        const float *__restrict__ b_delta,
                                                        const float *__restrict__ w_vw,
                                                        float *__restrict__ gate_a, float *__restrict__ gate_x) {
+    constexpr int RKA = RK > 0 ? RK : 1;
+    constexpr int RS = 4 + RKA;  // [0] rms, [4 + q] projection q (16-byte aligned for broadcast reads)
+    __shared__ __attribute__((aligned(16))) float srec[GATE_ROWS][RS];
     const int d = D.d, H = D.H, r = D.r;
     const int dim = blockIdx.x * SCAN_NT + threadIdx.x;
     const int s = blockIdx.y;
     const int t0 = blockIdx.z * GATE_ROWS;
-    if (dim >= d) return;
     const int REC = 1 + D.r + 2 * D.N;
+    const int nrow = min(ntok - t0, GATE_ROWS);
+    for (int idx = threadIdx.x; idx < GATE_ROWS * RS; idx += SCAN_NT) {
+        const int j = idx / RS, q = idx - j * RS;
+        float v = 0.0f;
+        if (j < nrow) {
+            const float *rc = rec + ((long)(t0 + j) * H + s) * REC;
+            if (q == 0)
+                v = rc[0];
+            else if (SEL && q >= 4 && q - 4 < r)
+                v = rc[1 + (q - 4)];
+        }
+        srec[j][q] = v;
+    }
+    __syncthreads();
+    if (dim >= d) return;
+    float hv[GATE_ROWS];
+#pragma unroll
+    for (int j = 0; j < GATE_ROWS; ++j) hv[j] = j < nrow ? h[((long)(t0 + j) * H + s) * d + dim] : 0.0f;
     const float al = a_log[(long)s * d + dim];
     const float abase = 1.0f / (1.0f + expf(al));
     const float ln_ab = logf(fmaxf(abase, 1.0e-6f));
     const float wx = 0.5f * tanhf(wx_diag[(long)s * d + dim]);
     const float bd = b_delta ? b_delta[(long)s * d + dim] : 0.0f;
-    constexpr int RKA = RK > 0 ? RK : 1;
     float wv[RKA];
 #pragma unroll
     for (int q = 0; q < RKA; ++q) wv[q] = (SEL && q < r) ? w_vw[((long)s * r + q) * d + dim] : 0.0f;
-    const int t1 = min(ntok, t0 + GATE_ROWS);
-    for (int t = t0; t < t1; ++t) {
-        const long row = (long)t * H + s;
-        const float *rc = rec + row * REC;
-        const float rms = rc[0];
-        const float u = h[row * d + dim] / rms;
+#pragma unroll
+    for (int j = 0; j < GATE_ROWS; ++j) {
+        if (j >= nrow) continue;
+        const long row = (long)(t0 + j) * H + s;
+        const float rms = srec[j][0];
+        const float u = hv[j] / rms;
         const float x = u + wx * u;
         float abar;
         if (SEL) {
-            // W_vw^T (W_kw^T u) with u = h/rms: the record holds W_kw^T h, so divide once
-            // unconditional loads (index clamped into the row's r values; the weights past r are
-            // zero) so that the row's projections are fetched together instead of one load,
-            // wait and branch per term
+            // W_vw^T (W_kw^T u) with u = h/rms: the record holds W_kw^T h, so divide once (the
+            // weights and the staged projections past r are zero)
             float dot = 0.0f;
 #pragma unroll
-            for (int q = 0; q < RKA; ++q) dot += wv[q] * rc[1 + min(q, r - 1)];
+            for (int q = 0; q < RKA; ++q) dot += wv[q] * srec[j][4 + q];
             const float pre = bd + dot / rms;
             const float delta = logf(1.0f + expf(pre));
             const float acore = expf(delta * ln_ab);
@@ -142,21 +162,48 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restric
         }
     }
     float prod = 1.0f;
-    for (int tb = t0; tb < t1; tb += TC) {
-        const int nt = min(TC, t1 - tb);
-        if (has_bc) {
-            for (int idx = tid; idx < nt * 2 * N; idx += SCAN_NT) {
-                const int j = idx / (2 * N), q = idx - j * 2 * N;
-                const float *rc = rec + (((long)b * T + tb + j) * H + s) * REC;
-                sbc[j][q] = rc[boff + q] / rc[0];
-            }
-        }
-        float av[TC], xv[TC];
+    // Per chunk of TC steps the B/C values (projection / rms) are staged in LDS and the gate
+    // values held in registers.  Two register sets alternate (the chunk loop is unrolled by two)
+    // so that the next chunk's loads are issued before this chunk's y stores: a load issued
+    // after stores is waited for behind them (the vector-memory counter retires in issue order).
+    // The loads are unconditional, at addresses clamped into the chunk (steps past its end are
+    // not used), so that the compiler can count them exactly.
+    constexpr int BCP = (TC * 2 * NS + SCAN_NT - 1) / SCAN_NT;  // staged B/C values per thread
+    struct Chunk {
+        float a[TC], x[TC], bv[BCP], rv[BCP];
+    };
+    const long tstride = (long)H * d;                          // one time step of (b, s, dim)
+    const long gbase = (long)b * T * tstride + (long)s * d + dd;  // (b, t = 0, s, dd)
+    const int last = t1 - 1;
+    auto fetch = [&](Chunk &k, int tb) {
 #pragma unroll
         for (int j = 0; j < TC; ++j) {
-            const long off = (((long)b * T + tb + j) * H + s) * d + dd;
-            av[j] = (j < nt && active) ? gate_a[off] : 1.0f;
-            xv[j] = (j < nt && active) ? gate_x[off] : 0.0f;
+            const long off = gbase + (long)min(tb + j, last) * tstride;
+            k.a[j] = gate_a[off];
+            k.x[j] = gate_x[off];
+        }
+        if (has_bc) {
+#pragma unroll
+            for (int q2 = 0; q2 < BCP; ++q2) {
+                const int idx = min(tid + q2 * SCAN_NT, TC * 2 * N - 1);
+                const int j = idx / (2 * N), q = idx - j * 2 * N;
+                const float *rc = rec + (((long)b * T + min(tb + j, last)) * H + s) * REC;
+                k.bv[q2] = rc[boff + q];
+                k.rv[q2] = rc[0];
+            }
+        }
+    };
+    auto process = [&](const Chunk &k, int tb) {
+        const int nt = min(TC, t1 - tb);
+        if (has_bc) {
+#pragma unroll
+            for (int q2 = 0; q2 < BCP; ++q2) {
+                const int idx = tid + q2 * SCAN_NT;
+                if (idx < nt * 2 * N) {
+                    const int j = idx / (2 * N), q = idx - j * 2 * N;
+                    sbc[j][q] = k.bv[q2] / k.rv[q2];
+                }
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -168,17 +215,27 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restric
                     if (EXACT || n < N) {
                         const float Bn = has_bc ? sbc[j][n] : 1.0f;
                         const float Cn = has_bc ? sbc[j][N + n] : 1.0f;
-                        m[n] = av[j] * m[n] + Bn * xv[j];
+                        m[n] = k.a[j] * m[n] + Bn * k.x[j];
                         acc += Cn * m[n];
                     }
                 }
                 if (MODE == 1)
-                    prod *= av[j];
+                    prod *= k.a[j];
                 else if (active)
-                    y[(((long)b * T + tb + j) * H + s) * d + dd] = acc;
+                    y[gbase + (long)(tb + j) * tstride] = acc;
             }
         }
         __syncthreads();
+    };
+    // (the fetches are unconditional too: past the end they re-read the last step, unused)
+    Chunk ca, cb;
+    if (t0 < t1) fetch(ca, t0);
+    for (int tb = t0; tb < t1; tb += 2 * TC) {
+        fetch(cb, tb + TC);
+        process(ca, tb);
+        if (tb + TC >= t1) break;
+        fetch(ca, tb + 2 * TC);
+        process(cb, tb + TC);
     }
     if (!active) return;
     if (MODE == 1) {
