@@ -246,7 +246,12 @@ __device__ __forceinline__ bool token_done(float r, float eps, int k, int max_it
 // The list order is not deterministic, which is harmless: every token's arithmetic is
 // independent of its position.
 // ---------------------------------------------------------------------------------------
-template <int E>
+// With the slot count HT known at compile time (and d <= 1024) the slots are walked with the
+// next slot's rows loaded into a second register set before this slot's h is stored: a load
+// issued after stores is waited for behind them (the vector-memory counter retires in issue
+// order), and a fully unrolled walk lets the compiler count the loads exactly.  HT = 0: the
+// slot count is read at run time (one slot at a time).  HIST: the memory-coupled history term.
+template <int E, int HT, bool HIST>
 __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur, int k, int max_iters,
                                                 float eps, const float *anchor, const float *norm_scale,
                                                 float beta) {
@@ -256,7 +261,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
     const int n = b.cnt[cur];
     if (blockIdx.x * WAVES_PER_BLOCK >= n) return;
     const int i = blockIdx.x * WAVES_PER_BLOCK + wave;
-    const int H = D.H;
+    const int H = HT > 0 ? HT : D.H;
     constexpr int d = 64 * E;
     const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
     const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
@@ -269,24 +274,36 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
         for (int e = 0; e < E; ++e) g[e] = norm_scale[lane + 64 * e];
         const float omb = 1.0f - beta;
         float rtok = 0.0f;
-        const float *hc_tok = b.mem_hist ? b.mem_hist + (long)(t / b.mem_T) * H * d : nullptr;
-        for (int s = 0; s < H; ++s) {
+        const float *hc_tok = HIST ? b.mem_hist + (long)(t / b.mem_T) * H * d : nullptr;
+        struct SlotIn {
+            float o[E], sg[E], an[E], h[E], hc[HIST ? E : 1];
+        };
+        // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389); o is
+        // read once (non-temporal), signal and h again next iteration
+        auto load = [&](int s, SlotIn &q) {
             const float *o = b.o + ((long)i * H + s) * d;
             const float *sg = b.signal + ((long)t * H + s) * d;
             const float *an = anchor + (long)s * d;
-            const float *hc = hc_tok ? hc_tok + (long)s * d : nullptr;
-            float *h = b.h + ((long)t * H + s) * d;
-            float cval[E], hold[E];
-            float ss = 0.0f;
+            const float *h = b.h + ((long)t * H + s) * d;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const int idx = lane + 64 * e;
-                // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389);
-                // o is read once (non-temporal), signal and h again next iteration
-                const float as_ = (__builtin_nontemporal_load(o + idx) + sg[idx]) + (hc ? hc[idx] : 0.0f);
-                const float c = as_ + an[idx];
+                q.o[e] = __builtin_nontemporal_load(o + idx);
+                q.sg[e] = sg[idx];
+                q.an[e] = an[idx];
+                q.h[e] = h[idx];
+                if constexpr (HIST) q.hc[e] = hc_tok[(long)s * d + idx];
+            }
+        };
+        auto step = [&](int s, const SlotIn &q) {
+            float *h = b.h + ((long)t * H + s) * d;
+            float cval[E];
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const float as_ = (q.o[e] + q.sg[e]) + (HIST ? q.hc[e] : 0.0f);
+                const float c = as_ + q.an[e];
                 cval[e] = c;
-                hold[e] = h[idx];
                 ss += excl ? as_ * as_ : c * c;
             }
             ss = wave_sum(ss);
@@ -295,15 +312,31 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const float f = g[e] * cval[e] / rms;
-                const float hn = f * beta + hold[e] * omb;
+                const float hn = f * beta + q.h[e] * omb;
                 h[lane + 64 * e] = hn;
-                const float df = hn - hold[e];
+                const float df = hn - q.h[e];
                 r = rmode ? r + df * df : fmaxf(r, fabsf(df));
             }
             r = rmode ? wave_sum(r) : wave_max(r);
             rtok = combine_resid(rmode, rtok, slot_resid(rmode, r, rms, d));
+        };
+        if constexpr (HT > 0) {
+            static_assert(E <= 16, "two register sets of slot rows");
+            SlotIn q[2];
+            load(0, q[0]);
+#pragma unroll
+            for (int s = 0; s < HT; ++s) {
+                if (s + 1 < HT) load(s + 1, q[(s + 1) & 1]);
+                step(s, q[s & 1]);
+            }
+        } else {
+            for (int s = 0; s < H; ++s) {
+                SlotIn q;
+                load(s, q);
+                step(s, q);
+            }
         }
-        if (rmode == 1) rtok = sqrtf(rtok);
+    if (rmode == 1) rtok = sqrtf(rtok);
         const bool done = token_done(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, lane == 0);
         if (done && lane == 0) b.iters[t] = k + 1;
         keep = !done;
@@ -558,6 +591,31 @@ void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok,
     }
 }
 
+// k_update for d = 64 E: the slot count as a template argument (1, 2, 4, 8, 16) up to d = 1024
+// without the history term, read at run time otherwise.
+template <int E>
+void launch_update_e(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps,
+                     const float *anchor, const float *norm_scale, float beta, dim3 grid, dim3 blk,
+                     hipStream_t st) {
+#define ADN_UPD_ARGS D, b, cur, k, max_iters, eps, anchor, norm_scale, beta
+    if (b.mem_hist) {
+        hipLaunchKernelGGL((k_update<E, 0, true>), grid, blk, 0, st, ADN_UPD_ARGS);
+        return;
+    }
+    if constexpr (E <= 16) {
+        switch (D.H) {
+            case 1: hipLaunchKernelGGL((k_update<E, 1, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 2: hipLaunchKernelGGL((k_update<E, 2, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 4: hipLaunchKernelGGL((k_update<E, 4, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 8: hipLaunchKernelGGL((k_update<E, 8, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 16: hipLaunchKernelGGL((k_update<E, 16, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            default: break;
+        }
+    }
+    hipLaunchKernelGGL((k_update<E, 0, false>), grid, blk, 0, st, ADN_UPD_ARGS);
+#undef ADN_UPD_ARGS
+}
+
 void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps, int ntok,
                    const float *anchor, const float *norm_scale, float beta, hipStream_t st) {
 #define ADN_UPD_ARGS D, b, cur, k, max_iters, eps, anchor, norm_scale, beta
@@ -576,12 +634,12 @@ void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max
     }
     const dim3 grid((unsigned)((ntok + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), blk(64 * WAVES_PER_BLOCK);
     switch (D.d) {
-        case 64: hipLaunchKernelGGL(k_update<1>, grid, blk, 0, st, ADN_UPD_ARGS); break;
-        case 128: hipLaunchKernelGGL(k_update<2>, grid, blk, 0, st, ADN_UPD_ARGS); break;
-        case 256: hipLaunchKernelGGL(k_update<4>, grid, blk, 0, st, ADN_UPD_ARGS); break;
-        case 512: hipLaunchKernelGGL(k_update<8>, grid, blk, 0, st, ADN_UPD_ARGS); break;
-        case 1024: hipLaunchKernelGGL(k_update<16>, grid, blk, 0, st, ADN_UPD_ARGS); break;
-        case 2048: hipLaunchKernelGGL(k_update<32>, grid, blk, 0, st, ADN_UPD_ARGS); break;
+        case 64: launch_update_e<1>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
+        case 128: launch_update_e<2>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
+        case 256: launch_update_e<4>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
+        case 512: launch_update_e<8>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
+        case 1024: launch_update_e<16>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
+        case 2048: launch_update_e<32>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
         default: break;  // rejected at context creation
     }
 #undef ADN_UPD_ARGS
