@@ -163,7 +163,8 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restric
     }
     float prod = 1.0f;
     // Per chunk of TC steps the B/C values (projection / rms) are staged in LDS and the gate
-    // values held in registers.  Two register sets alternate (the chunk loop is unrolled by two)
+    // values held in registers.  Where y is stored (passes 0 and C) two register sets alternate
+    // (the chunk loop is unrolled by two)
     // so that the next chunk's loads are issued before this chunk's y stores: a load issued
     // after stores is waited for behind them (the vector-memory counter retires in issue order).
     // The loads are unconditional, at addresses clamped into the chunk (steps past its end are
@@ -227,15 +228,24 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restric
         }
         __syncthreads();
     };
-    // (the fetches are unconditional too: past the end they re-read the last step, unused)
-    Chunk ca, cb;
-    if (t0 < t1) fetch(ca, t0);
-    for (int tb = t0; tb < t1; tb += 2 * TC) {
-        fetch(cb, tb + TC);
-        process(ca, tb);
-        if (tb + TC >= t1) break;
-        fetch(ca, tb + 2 * TC);
-        process(cb, tb + TC);
+    // (the fetches are unconditional too: past the end they re-read the last step, unused).
+    // Pass A stores nothing in the loop, so there one register set serves.
+    Chunk ca;
+    if constexpr (MODE == 1) {
+        for (int tb = t0; tb < t1; tb += TC) {
+            fetch(ca, tb);
+            process(ca, tb);
+        }
+    } else {
+        Chunk cb;
+        if (t0 < t1) fetch(ca, t0);
+        for (int tb = t0; tb < t1; tb += 2 * TC) {
+            fetch(cb, tb + TC);
+            process(ca, tb);
+            if (tb + TC >= t1) break;
+            fetch(ca, tb + 2 * TC);
+            process(cb, tb + TC);
+        }
     }
     if (!active) return;
     if (MODE == 1) {
