@@ -500,7 +500,23 @@ __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int
     float *h = b.h + (long)t * hd;
     auto X = [&](int j) { return b.hist + ((long)(j % m) * ntok + t) * hd; };
     float *slot = X(k);
-    for (long e = tid; e < hd; e += AND_NT) slot[e] = h[e];
+    // Copies and the final mix go AB elements per thread at a time, loads before stores: a load
+    // issued after stores is waited for behind them (the vector-memory counter retires in issue
+    // order).
+    constexpr int AB = 8;
+    for (long e0 = tid; e0 < hd; e0 += AB * AND_NT) {
+        float v[AB];
+#pragma unroll
+        for (int q = 0; q < AB; ++q) {
+            const long e = e0 + (long)q * AND_NT;
+            v[q] = e < hd ? h[e] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < AB; ++q) {
+            const long e = e0 + (long)q * AND_NT;
+            if (e < hd) slot[e] = v[q];
+        }
+    }
     if constexpr (NRES >= 2) {
         constexpr int NPK = NRES * (NRES + 1) / 2;
         float gp[NPK];
@@ -538,11 +554,22 @@ __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int
             for (int q2 = 0; q2 < NRES; ++q2) beta_s[q2] = bt[q2];
         }
         __syncthreads();
-        for (long e = tid; e < hd; e += AND_NT) {
-            float acc = 0.0f;
+        for (long e0 = tid; e0 < hd; e0 += AB * AND_NT) {
+            float acc[AB];
 #pragma unroll
-            for (int ri = 0; ri < NRES; ++ri) acc += beta_s[ri] * X(k + m - ri)[e];
-            h[e] = acc;
+            for (int q = 0; q < AB; ++q) {
+                const long e = e0 + (long)q * AND_NT;
+                acc[q] = 0.0f;
+                if (e < hd) {
+#pragma unroll
+                    for (int ri = 0; ri < NRES; ++ri) acc[q] += beta_s[ri] * X(k + m - ri)[e];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < AB; ++q) {
+                const long e = e0 + (long)q * AND_NT;
+                if (e < hd) h[e] = acc[q];
+            }
         }
     }
 }

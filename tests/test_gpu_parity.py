@@ -132,6 +132,29 @@ def test_variants_match_oracle(oracle_lib, var):
     assert_forward_parity(got, ref, str(var))
 
 
+# More than 512 tokens in flight: the many-token update kernel, whose slot walk is compiled per
+# slot count (1, 2, 4, 8, 16 at d <= 1024; read at run time at d = 2048).
+MANY = [
+    dict(d=64, H=1, V=300, N=1),
+    dict(d=64, H=2, V=300, N=4, flags=synth.F_SCAN_SELECTIVE),
+    dict(d=128, H=16, V=300, N=4, flags=synth.F_SCAN_SELECTIVE | synth.F_RESID_L2),
+    dict(d=1024, H=2, V=300, N=1, flags=synth.F_RESID_RELRMS),
+]
+
+
+@pytest.mark.parametrize("var", MANY, ids=lambda v: "-".join(f"{k}{v[k]}" for k in v))
+def test_many_token_update_matches_oracle(oracle_lib, var):
+    log(f"many-token variant {var}")
+    mc, w = _small(**var)
+    B, T = 5, 131  # 655 tokens, ragged
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=6)
+    ref = oracle_lib.Oracle(mc, w).forward(toks)
+    be = make(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks)
+    assert_forward_parity(got, ref, str(var))
+
+
 def test_homeostatic_exit_shortens_the_solve(oracle_lib):
     """With damping 0.1 the relative residual shrinks slowly; the plateau rule stops the tokens
     well before the tolerance would (GPU and oracle agree on every count), and without the flag
