@@ -14,21 +14,41 @@ constexpr int WPB = 4;
 // per token; each lane keeps its E = d/64 pooled values in registers between the two passes.
 template <int E>
 __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int ntok, const float *g,
-                                                   float *pooled, float *pnorm) {
+                                                   float *pooled, float *pnorm, float *rec, int REC) {
     const int t = blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (t >= ntok) return;
     constexpr int d = 64 * E;
     const int H = D.H;
     const float *ht = h + (long)t * H * d;
+    // slot by slot: the pooled sums add the slots in order; with `rec` each slot row's RMS
+    // sqrt(mean h^2 + 1e-6) (the carrier's record, summed as k_row_rms does) is formed from the
+    // same loads, lane s keeping slot s's, and stored after the loop
     float pv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) pv[e] = 0.0f;
+    float my_rms = 0.0f;
+    for (int s = 0; s < H; ++s) {
+        float x[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = ht[(long)s * d + lane + 64 * e];
+#pragma unroll
+        for (int e = 0; e < E; ++e) pv[e] = pv[e] + x[e];
+        if (rec) {
+            float sr = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) sr += x[e] * x[e];
+            sr = wave_sum(sr);
+            const float rr = sqrtf(sr / (float)d + 1e-6f);
+            if (lane == s) my_rms = rr;
+        }
+    }
+    if (rec && lane < H) rec[((long)t * H + lane) * REC] = my_rms;
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        float acc = 0.0f;
-        for (int s = 0; s < H; ++s) acc = acc + ht[(long)s * d + i];
-        pv[e] = acc / (float)H;
+        pv[e] = pv[e] / (float)H;
         if (pooled) pooled[(long)t * d + i] = pv[e];
         ss += pv[e] * pv[e];
     }
@@ -126,15 +146,15 @@ __global__ void k_decode_step(const int32_t *argmax, int32_t *tokens, int32_t *o
 }  // namespace
 
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
-                      float *pnorm, hipStream_t st) {
+                      float *pnorm, float *rec, int REC, hipStream_t st) {
     const dim3 grid((unsigned)((ntok + WPB - 1) / WPB)), blk(64 * WPB);
     switch (D.d) {
-        case 64: hipLaunchKernelGGL(k_pool_norm<1>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
-        case 128: hipLaunchKernelGGL(k_pool_norm<2>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
-        case 256: hipLaunchKernelGGL(k_pool_norm<4>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
-        case 512: hipLaunchKernelGGL(k_pool_norm<8>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
-        case 1024: hipLaunchKernelGGL(k_pool_norm<16>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
-        case 2048: hipLaunchKernelGGL(k_pool_norm<32>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm); break;
+        case 64: hipLaunchKernelGGL(k_pool_norm<1>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
+        case 128: hipLaunchKernelGGL(k_pool_norm<2>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
+        case 256: hipLaunchKernelGGL(k_pool_norm<4>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
+        case 512: hipLaunchKernelGGL(k_pool_norm<8>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
+        case 1024: hipLaunchKernelGGL(k_pool_norm<16>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
+        case 2048: hipLaunchKernelGGL(k_pool_norm<32>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
         default: break;  // rejected at context creation
     }
 }

@@ -94,8 +94,9 @@ void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, in
 
 // ---- LM head (head.hip) -----------------------------------------------------------------
 // pooled = mean_s h*, pnorm = (pooled/rms(pooled, 1e-5)) * g
+// rec: when non-null, also each (token, slot) row's RMS into rec[row * REC] (the carrier record).
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
-                      float *pnorm, hipStream_t st);
+                      float *pnorm, float *rec, int REC, hipStream_t st);
 // argmax over each row of logits with the last-max tie rule.
 void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st);
 // final reduction of the per-tile arg-max partials written by the LM-head GEMM

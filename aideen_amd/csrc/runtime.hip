@@ -364,15 +364,20 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
     }
 }
 
-// pooled rows, logits and arg-max of the solved h of all ntok tokens.
-void enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int ntok, Prof *prof) {
+// pooled rows, logits and arg-max of the solved h of all ntok tokens.  scan_rms: the pooling
+// pass also writes every row's RMS into the carrier record (the scan then skips k_row_rms).
+// Returns whether it did.
+bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int ntok, Prof *prof,
+                  bool scan_rms = false) {
     const Dims &D = c->D;
     const int d = D.d;
     hipStream_t st = c->stream;
     const bool want_logits = o.logits || o.argmax;
-    if (o.pooled || want_logits) {
+    const bool pool = o.pooled || want_logits;
+    if (pool) {
         Span sp(prof, ADN_STAGE_POOL, -1, st);
-        launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr, st);
+        launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr,
+                         scan_rms ? c->scb.rec : nullptr, scan_rec_len(D), st);
     }
     if (want_logits) {
         float *logits = o.logits;
@@ -411,10 +416,12 @@ void enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
             launch_argmax_reduce(c->am_val, c->am_idx, ntok, ntiles, o.argmax, st);
         }
     }
+    return pool && scan_rms;
 }
 
 // canonical carrier over each sequence's solved h (the readout scan).
-void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const SolveBuffers &b, Prof *prof) {
+void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const SolveBuffers &b, Prof *prof,
+                  bool rms_done = false) {
     const Dims &D = c->D;
     const int ntok = r.batch * r.seq;
     const int d = D.d, H = D.H;
@@ -423,7 +430,7 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
         const int REC = scan_rec_len(D);
         {
             Span sp(prof, ADN_STAGE_SCAN_PREP, -1, st);
-            launch_row_rms(b.h, (long)ntok * H, d, c->scb.rec, REC, st);
+            if (!rms_done) launch_row_rms(b.h, (long)ntok * H, d, c->scb.rec, REC, st);
             GemmParams g{};  // P[t][s] = W_cat[s] h[t][s] into rec[1 .. REC)
             g.role = ROLE_SCAN_PROJ;
             g.A = b.h;
@@ -488,8 +495,8 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
     enqueue_iterations(c, r, b, ntok, ntok, prof);
-    enqueue_head(c, o, b, ntok, prof);
-    enqueue_scan(c, r, o, b, prof);
+    const bool rms_done = enqueue_head(c, o, b, ntok, prof, o.scan_y || o.scan_state);
+    enqueue_scan(c, r, o, b, prof, rms_done);
 }
 
 // Memory-coupled forward (fixed-history mode, trainer.rs:677-720): position t of every sequence
