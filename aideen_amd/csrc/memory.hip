@@ -27,57 +27,86 @@ __global__ void k_mem_begin(SolveBuffers b, int B, int T, int t) {
 }
 
 // hist holds u = W_hist m_prev on entry ([B][H][d]); m_prev rows are m_prev + b*m_sm + s*d.
+// E = d/64 values per lane, held in registers: every load of the row is issued before the
+// first store (a load issued after stores is waited for behind them), and u is not re-read.
+template <int E>
 __global__ __launch_bounds__(64 * MW) void k_hist_ctx(Dims D, float *hist, const float *m_prev, long m_sm,
                                                       const float *signal, int B, int T, int t,
                                                       const float *slot_scale, const float *gate_logit) {
+    constexpr int d = 64 * E;
     const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int H = D.H, d = D.d;
+    const int H = D.H;
     if (row >= B * H) return;
     const int bb = row / H, s = row - bb * H;
     float *u = hist + (long)row * d;
     const float *pm = m_prev + (long)bb * m_sm + (long)s * d;
     const float *sg = signal + ((long)(bb * T + t) * H + s) * d;
     const float *sc = slot_scale + (long)s * d;
+    float vs[E], vp[E], vu[E], vc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        vs[e] = sg[i];
+        vp[e] = pm[i];
+        vu[e] = u[i];
+        vc[e] = sc[i];
+    }
     float ssg = 0.0f, spm = 0.0f;
-    for (int i = lane; i < d; i += 64) {
-        ssg += sg[i] * sg[i];
-        spm += pm[i] * pm[i];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        ssg += vs[e] * vs[e];
+        spm += vp[e] * vp[e];
     }
     const float inj_rms = sqrtf(wave_sum(ssg) / (float)d + 1e-6f);
     const float prev_rms = sqrtf(wave_sum(spm) / (float)d + 1e-6f);
     float su = 0.0f;
-    for (int i = lane; i < d; i += 64) {
-        const float v = u[i] + sc[i] * (pm[i] / prev_rms);
-        u[i] = v;
-        su += v * v;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        vu[e] = vu[e] + vc[e] * (vp[e] / prev_rms);
+        su += vu[e] * vu[e];
     }
     const float u_rms = sqrtf(wave_sum(su) / (float)d + 1e-6f);
     const float scale = u_rms > 1e-6f ? fminf(inj_rms / u_rms, 1.0f) : 1.0f;
     const float sigma = 1.0f / (1.0f + expf(-gate_logit[s]));
     const float g = (0.070f + (0.20f - 0.070f) * sigma) * scale;
-    for (int i = lane; i < d; i += 64) u[i] = u[i] * g;
+#pragma unroll
+    for (int e = 0; e < E; ++e) u[lane + 64 * e] = vu[e] * g;
 }
 
-// m_inner for the tokens at position t; m_prev == nullptr is the zero state.
+// m_inner for the tokens at position t; m_prev == nullptr is the zero state.  E = d/64 values
+// per lane in registers, all loads before the stores.
+template <int E>
 __global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, int B, int T, int t,
                                                       const float *m_prev, long m_sm, const float *a_log,
                                                       const float *wx_diag, float *out, long out_sm) {
+    constexpr int d = 64 * E;
     const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int H = D.H, d = D.d;
+    const int H = D.H;
     if (row >= B * H) return;
     const int bb = row / H, s = row - bb * H;
     const float *hs = h + ((long)(bb * T + t) * H + s) * d;
-    float ss = 0.0f;
-    for (int i = lane; i < d; i += 64) ss += hs[i] * hs[i];
-    const float rms = sqrtf(wave_sum(ss) / (float)d + 1e-6f);
     const float *pm = m_prev ? m_prev + (long)bb * m_sm + (long)s * d : nullptr;
+    float vh[E], vw[E], va[E], vp[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        vh[e] = hs[i];
+        vw[e] = wx_diag[(long)s * d + i];
+        va[e] = a_log[(long)s * d + i];
+        vp[e] = pm ? pm[i] : 0.0f;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss += vh[e] * vh[e];
+    const float rms = sqrtf(wave_sum(ss) / (float)d + 1e-6f);
     float *o = out + (long)bb * out_sm + (long)s * d;
-    for (int i = lane; i < d; i += 64) {
-        const float u = hs[i] / rms;
-        const float wx = 0.5f * tanhf(wx_diag[(long)s * d + i]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float u = vh[e] / rms;
+        const float wx = 0.5f * tanhf(vw[e]);
         const float x = u + wx * u;
-        const float ab = 1.0f / (1.0f + expf(a_log[(long)s * d + i]));
-        o[i] = ab * (pm ? pm[i] : 0.0f) + (1.0f - ab) * x;
+        const float ab = 1.0f / (1.0f + expf(va[e]));
+        o[lane + 64 * e] = ab * vp[e] + (1.0f - ab) * x;
     }
 }
 
@@ -90,15 +119,37 @@ void launch_mem_begin(const SolveBuffers &b, int B, int T, int t, hipStream_t st
 void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm, const float *signal, int B,
                      int T, int t, const float *slot_scale, const float *gate_logit, hipStream_t st) {
     const int rows = B * D.H;
-    hipLaunchKernelGGL(k_hist_ctx, dim3((unsigned)((rows + MW - 1) / MW)), dim3(64 * MW), 0, st, D, hist, m_prev,
-                       m_sm, signal, B, T, t, slot_scale, gate_logit);
+    const dim3 grid((unsigned)((rows + MW - 1) / MW)), blk(64 * MW);
+#define ADN_HC(E) hipLaunchKernelGGL(k_hist_ctx<E>, grid, blk, 0, st, D, hist, m_prev, m_sm, signal, B, T, t, \
+                                     slot_scale, gate_logit)
+    switch (D.d) {
+        case 64: ADN_HC(1); break;
+        case 128: ADN_HC(2); break;
+        case 256: ADN_HC(4); break;
+        case 512: ADN_HC(8); break;
+        case 1024: ADN_HC(16); break;
+        case 2048: ADN_HC(32); break;
+        default: break;  // rejected at context creation
+    }
+#undef ADN_HC
 }
 
 void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const float *m_prev, long m_sm,
                      const float *a_log, const float *wx_diag, float *out, long out_sm, hipStream_t st) {
     const int rows = B * D.H;
-    hipLaunchKernelGGL(k_temporal, dim3((unsigned)((rows + MW - 1) / MW)), dim3(64 * MW), 0, st, D, h, B, T, t,
-                       m_prev, m_sm, a_log, wx_diag, out, out_sm);
+    const dim3 grid((unsigned)((rows + MW - 1) / MW)), blk(64 * MW);
+#define ADN_TP(E) hipLaunchKernelGGL(k_temporal<E>, grid, blk, 0, st, D, h, B, T, t, m_prev, m_sm, a_log, wx_diag, \
+                                     out, out_sm)
+    switch (D.d) {
+        case 64: ADN_TP(1); break;
+        case 128: ADN_TP(2); break;
+        case 256: ADN_TP(4); break;
+        case 512: ADN_TP(8); break;
+        case 1024: ADN_TP(16); break;
+        case 2048: ADN_TP(32); break;
+        default: break;  // rejected at context creation
+    }
+#undef ADN_TP
 }
 
 }  // namespace adn
