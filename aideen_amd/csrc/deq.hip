@@ -443,7 +443,9 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     const float *an = anchor + (long)s * d;
     const float *hc = b.mem_hist ? b.mem_hist + ((long)(t / b.mem_T) * H + s) * d : nullptr;
     float *h = b.h + ((long)t * H + s) * d;
-    float cval[E], hold[E];
+    // every load (the norm scale too) before the first store of h: a load issued after stores
+    // is waited for behind them (the vector-memory counter retires in issue order)
+    float cval[E], hold[E], gs[E];
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -452,6 +454,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
         const float c = as_ + an[idx];
         cval[e] = c;
         hold[e] = h[idx];
+        gs[e] = norm_scale[idx];
         ss += excl ? as_ * as_ : c * c;
     }
     ss = wave_sum(ss);
@@ -460,7 +463,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     float r = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const float f = norm_scale[lane + 64 * e] * cval[e] / rms;
+        const float f = gs[e] * cval[e] / rms;
         const float hn = f * beta + hold[e] * omb;
         h[lane + 64 * e] = hn;
         const float df = hn - hold[e];
