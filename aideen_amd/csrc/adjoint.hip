@@ -30,14 +30,21 @@ __global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, const float *signal
     const int t = row / H;
     const long o = (long)row * d;
     const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
+    // every load before the first store (a load issued after stores is waited for behind them)
+    float pv[E], rv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        pv[e] = signal[o + i] + 1.0f * h_star[o + i];
+        rv[e] = dl[(long)t * d + i];
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        const float p = signal[o + i] + 1.0f * h_star[o + i];
-        pre[o + i] = p;
-        ss += p * p;
-        v0[o + i] = dl[(long)t * d + i] * rhs_scale;
+        pre[o + i] = pv[e];
+        ss += pv[e] * pv[e];
+        v0[o + i] = rv[e] * rhs_scale;
     }
     ss = wave_sum(ss);
     if (lane == 0) {
@@ -59,14 +66,18 @@ __global__ __launch_bounds__(64 * AW) void k_adj_first(int H, const float *signa
     const long o = (long)row * d;
     const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
     float pv[E], rv[E], gv[E];
-    float ss = 0.0f, cf = 0.0f;
+    // every load before the first store (a load issued after stores is waited for behind them)
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
         pv[e] = signal[o + i] + 1.0f * h_star[o + i];
-        pre[o + i] = pv[e];
         rv[e] = dl[(long)t * d + i] * rhs_scale;
         gv[e] = g[i];
+    }
+    float ss = 0.0f, cf = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        pre[o + lane + 64 * e] = pv[e];
         ss += pv[e] * pv[e];
         cf += beta * rv[e] * gv[e] * pv[e];
     }
@@ -97,14 +108,17 @@ __global__ __launch_bounds__(64 * AW) void k_adj_step(int H, const float *pre, c
     const int t = row / H;
     const long o = (long)row * d;
     const float rhs_scale = 1.0f / fmaxf(1.0f, (float)H);
-    float pv[E], vv[E], gv[E];
+    float pv[E], vv[E], gv[E], rv[E];
     float cf = 0.0f;
+    // every load (dl too) before the first store: a load issued after stores is waited for
+    // behind them
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
         pv[e] = pre[o + i];
         vv[e] = v[o + i];
         gv[e] = g[i];
+        rv[e] = dl[(long)t * d + i];
         cf += beta * vv[e] * gv[e] * pv[e];
     }
     const float inv_rms = terms[2 * row];
@@ -113,7 +127,7 @@ __global__ __launch_bounds__(64 * AW) void k_adj_step(int H, const float *pre, c
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
         const float ng = (gv[e] * inv_rms) * (beta * vv[e]) - pv[e] * cs;
-        vn[o + i] = dl[(long)t * d + i] * rhs_scale + (1.0f * ng + (1.0f - beta) * vv[e]);
+        vn[o + i] = rv[e] * rhs_scale + (1.0f * ng + (1.0f - beta) * vv[e]);
     }
 }
 
