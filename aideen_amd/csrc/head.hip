@@ -115,20 +115,38 @@ constexpr int AR_W = 16;
 
 __global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val, const int32_t *am_idx,
                                                             int ntok, int ntiles, int32_t *out) {
-    __shared__ float sv[AR_W][64];
-    __shared__ int si[AR_W][64];
+    // 32 rows per block: half-wave hw of wave w takes tiles 2w + hw, 2w + hw + 2 AR_W, ... (the
+    // combination is a maximum with ties to the larger index, so its order does not matter), four
+    // tiles' loads in flight at a time
+    __shared__ float sv[2 * AR_W][32];
+    __shared__ int si[2 * AR_W][32];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 64 + lane;
+    const int hw = lane >> 5, rl = lane & 31;
+    const int row = blockIdx.x * 32 + rl;
+    const int q0 = 2 * w + hw;
+    constexpr int QS = 2 * AR_W;
     float bv = -INFINITY;
     int bi = -1;
-    if (row < ntok)
-        for (int t = w; t < ntiles; t += AR_W)
-            am_combine(bv, bi, am_val[(long)t * ntok + row], am_idx[(long)t * ntok + row]);
-    sv[w][lane] = bv;
-    si[w][lane] = bi;
+    if (row < ntok) {
+        int t = q0;
+        for (; t + 3 * QS < ntiles; t += 4 * QS) {
+            float v[4];
+            int ix[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v[u] = am_val[(long)(t + u * QS) * ntok + row];
+                ix[u] = am_idx[(long)(t + u * QS) * ntok + row];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) am_combine(bv, bi, v[u], ix[u]);
+        }
+        for (; t < ntiles; t += QS) am_combine(bv, bi, am_val[(long)t * ntok + row], am_idx[(long)t * ntok + row]);
+    }
+    sv[q0][rl] = bv;
+    si[q0][rl] = bi;
     __syncthreads();
-    if (w == 0 && row < ntok) {
-        for (int q = 1; q < AR_W; ++q) am_combine(bv, bi, sv[q][lane], si[q][lane]);
+    if (threadIdx.x < 32 && row < ntok) {
+        for (int q = 1; q < QS; ++q) am_combine(bv, bi, sv[q][rl], si[q][rl]);
         out[row] = bi < 0 ? 0 : bi;
     }
 }
@@ -165,7 +183,7 @@ void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream
 
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
                           hipStream_t st) {
-    hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 63) / 64)), dim3(64 * AR_W), 0, st, am_val, am_idx, ntok,
+    hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 31) / 32)), dim3(64 * AR_W), 0, st, am_val, am_idx, ntok,
                        ntiles, out);
 }
 
