@@ -278,8 +278,10 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
         struct SlotIn {
             float o[E], sg[E], an[E], h[E], hc[HIST ? E : 1];
         };
-        // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389); o is
-        // read once (non-temporal), signal and h again next iteration
+        // combined = attn + input signal + history, then + slot anchor (FPMR:1386-1389); o and
+        // the signal are loaded non-temporally (o is read once; an iteration's working set is
+        // larger than the caches, so keeping the signal cached only displaces h, which the next
+        // Q|K|V product reads)
         auto load = [&](int s, SlotIn &q) {
             const float *o = b.o + ((long)i * H + s) * d;
             const float *sg = b.signal + ((long)t * H + s) * d;
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
             for (int e = 0; e < E; ++e) {
                 const int idx = lane + 64 * e;
                 q.o[e] = __builtin_nontemporal_load(o + idx);
-                q.sg[e] = sg[idx];
+                q.sg[e] = __builtin_nontemporal_load(sg + idx);
                 q.an[e] = an[idx];
                 q.h[e] = h[idx];
                 if constexpr (HIST) q.hc[e] = hc_tok[(long)s * d + idx];
