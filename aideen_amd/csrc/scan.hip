@@ -86,9 +86,10 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_gate(Dims D, const float *__re
     }
     __syncthreads();
     if (dim >= d) return;
+    // h* is not read again after the gate: non-temporal loads keep it from displacing cached data
     float hv[GATE_ROWS];
 #pragma unroll
-    for (int j = 0; j < GATE_ROWS; ++j) hv[j] = j < nrow ? h[((long)(t0 + j) * H + s) * d + dim] : 0.0f;
+    for (int j = 0; j < GATE_ROWS; ++j) hv[j] = j < nrow ? __builtin_nontemporal_load(h + ((long)(t0 + j) * H + s) * d + dim) : 0.0f;
     const float al = a_log[(long)s * d + dim];
     const float abase = 1.0f / (1.0f + expf(al));
     const float ln_ab = logf(fmaxf(abase, 1.0e-6f));
@@ -176,12 +177,13 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restric
     const long tstride = (long)H * d;                          // one time step of (b, s, dim)
     const long gbase = (long)b * T * tstride + (long)s * d + dd;  // (b, t = 0, s, dd)
     const int last = t1 - 1;
+    // pass C is the gate values' last use: loaded non-temporally there
     auto fetch = [&](Chunk &k, int tb) {
 #pragma unroll
         for (int j = 0; j < TC; ++j) {
             const long off = gbase + (long)min(tb + j, last) * tstride;
-            k.a[j] = gate_a[off];
-            k.x[j] = gate_x[off];
+            k.a[j] = MODE == 2 ? __builtin_nontemporal_load(gate_a + off) : gate_a[off];
+            k.x[j] = MODE == 2 ? __builtin_nontemporal_load(gate_x + off) : gate_x[off];
         }
         if (has_bc) {
 #pragma unroll
