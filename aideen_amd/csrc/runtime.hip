@@ -364,9 +364,39 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
     }
 }
 
+// The carrier's per-row record: rms (unless the pooling pass wrote it: rms_done) and the
+// projections P[t][s] = W_cat[s] h[t][s] into rec[1 .. REC).
+void enqueue_scan_prep(adn_ctx *c, int ntok, const SolveBuffers &b, Prof *prof, bool rms_done) {
+    const Dims &D = c->D;
+    const int d = D.d, H = D.H;
+    const int REC = scan_rec_len(D);
+    hipStream_t st = c->stream;
+    Span sp(prof, ADN_STAGE_SCAN_PREP, -1, st);
+    if (!rms_done) launch_row_rms(b.h, (long)ntok * H, d, c->scb.rec, REC, st);
+    GemmParams g{};
+    g.role = ROLE_SCAN_PROJ;
+    g.A = b.h;
+    g.a_sm = (long)H * d;
+    g.a_ss = d;
+    g.B = c->w_cat;
+    g.b_ss = (long)(REC - 1) * d;
+    g.C = c->scb.rec + 1;
+    g.c_sm = (long)H * REC;
+    g.c_ss = REC;
+    g.M = ntok;
+    g.N = REC - 1;
+    g.K = d;
+    g.S = H;
+    g.err = b.err;
+    g.epi = EPI_NONE;
+    set_split(c, g, c->sp_cat);
+    launch_gemm(g, st);
+}
+
 // pooled rows, logits and arg-max of the solved h of all ntok tokens.  scan_rms: the pooling
-// pass also writes every row's RMS into the carrier record (the scan then skips k_row_rms).
-// Returns whether it did.
+// pass also writes every row's RMS into the carrier record, and the carrier's projections
+// follow it at once, before the LM head, while h* is still in the caches (the LM head's logits
+// stream would evict it).  Returns whether it did (the scan then skips its preparation).
 bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int ntok, Prof *prof,
                   bool scan_rms = false) {
     const Dims &D = c->D;
@@ -379,6 +409,7 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
         launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr,
                          scan_rms ? c->scb.rec : nullptr, scan_rec_len(D), st);
     }
+    if (pool && scan_rms) enqueue_scan_prep(c, ntok, b, prof, true);
     if (want_logits) {
         float *logits = o.logits;
         if (!logits) {
@@ -421,35 +452,13 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
 
 // canonical carrier over each sequence's solved h (the readout scan).
 void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const SolveBuffers &b, Prof *prof,
-                  bool rms_done = false) {
+                  bool prep_done = false) {
     const Dims &D = c->D;
     const int ntok = r.batch * r.seq;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
     if (o.scan_y || o.scan_state) {
-        const int REC = scan_rec_len(D);
-        {
-            Span sp(prof, ADN_STAGE_SCAN_PREP, -1, st);
-            if (!rms_done) launch_row_rms(b.h, (long)ntok * H, d, c->scb.rec, REC, st);
-            GemmParams g{};  // P[t][s] = W_cat[s] h[t][s] into rec[1 .. REC)
-            g.role = ROLE_SCAN_PROJ;
-            g.A = b.h;
-            g.a_sm = (long)H * d;
-            g.a_ss = d;
-            g.B = c->w_cat;
-            g.b_ss = (long)(REC - 1) * d;
-            g.C = c->scb.rec + 1;
-            g.c_sm = (long)H * REC;
-            g.c_ss = REC;
-            g.M = ntok;
-            g.N = REC - 1;
-            g.K = d;
-            g.S = H;
-            g.err = b.err;
-            g.epi = EPI_NONE;
-            set_split(c, g, c->sp_cat);
-            launch_gemm(g, st);
-        }
+        if (!prep_done) enqueue_scan_prep(c, ntok, b, prof, false);
         // chunk buffers hold max_batch * scan_nch_cap sequence-chunks
         const int nch_fit = std::max(1, (c->cfg.max_batch * c->scan_nch_cap) / r.batch);
         const int nch = std::min(std::min(scan_chunks(r.batch, r.seq, H, d), c->scan_nch_cap), nch_fit);
@@ -495,8 +504,8 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
     enqueue_iterations(c, r, b, ntok, ntok, prof);
-    const bool rms_done = enqueue_head(c, o, b, ntok, prof, o.scan_y || o.scan_state);
-    enqueue_scan(c, r, o, b, prof, rms_done);
+    const bool prep_done = enqueue_head(c, o, b, ntok, prof, o.scan_y || o.scan_state);
+    enqueue_scan(c, r, o, b, prof, prep_done);
 }
 
 // Memory-coupled forward (fixed-history mode, trainer.rs:677-720): position t of every sequence
