@@ -129,6 +129,7 @@ def lib():
                                        C.POINTER(AdnRun)]),
         "adn_embed_context": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_embed_context_async": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
+        "adn_embed_context_noalloc": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_profile_forward": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs),
                                           C.POINTER(AdnProfile)]),
     }

@@ -208,6 +208,12 @@ class GpuDeqBackend:
         B, T = tokens.shape
         check(lib().adn_embed_context_async(self._ctx, B, T, _dev_i(tokens), int(max_ctx), _dev_f(out)))
 
+    def embed_context_noalloc(self, tokens, max_ctx: int, out) -> None:
+        """Device-memory form that allocates nothing (a fixed per-device buffer; concurrent calls
+        on one GPU race): enqueue only."""
+        B, T = tokens.shape
+        check(lib().adn_embed_context_noalloc(self._ctx, B, T, _dev_i(tokens), int(max_ctx), _dev_f(out)))
+
     # backward ----------------------------------------------------------------------------------
     def adjoint(self, dl: np.ndarray, iters: int, damping: Optional[float] = None,
                 h_star: Optional[np.ndarray] = None):

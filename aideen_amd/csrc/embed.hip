@@ -216,9 +216,20 @@ void launch_ctx(const float *E, int d, int V, const int32_t *tokens, int B, int 
 // chunk count for the smallest chunk (d > 1024: 4 positions)
 long embed_context_chunks(int T) { return (T + 3) / 4; }
 
+// values per thread of a row: the launch's template bucket for d
+static int ctx_dpt(int d) {
+    const int dpt = (d + ENT - 1) / ENT;
+    return dpt <= 1 ? 1 : dpt <= 2 ? 2 : dpt <= 4 ? 4 : 8;
+}
+
+long embed_context_total_doubles(int d, int B, int T) {
+    const int chk = 32 / ctx_dpt(d);
+    return (long)B * ((T + chk - 1) / chk) * d;
+}
+
 void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
                           double *tot1, float *out, unsigned *err, hipStream_t st) {
-    const int dpt = (d + ENT - 1) / ENT;
+    const int dpt = ctx_dpt(d);
     if (dpt <= 1)
         launch_ctx<1>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, st);
     else if (dpt <= 2)

@@ -143,6 +143,9 @@ void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
 // embed_context of the window ending at every position; tot0/tot1 hold
 // B * embed_context_chunks(T) * d doubles each.
 long embed_context_chunks(int T);
+// doubles each of tot0 / tot1 that launch_embed_context writes for B sequences of T positions
+// at width d (B * its chunk count * d; never more than B * embed_context_chunks(T) * d)
+long embed_context_total_doubles(int d, int B, int T);
 void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
                           double *tot1, float *out, unsigned *err, hipStream_t st);
 // Clean adjoint Picard for ntok tokens (rows = ntok * H of d floats); scratch pre, v0, v1 hold

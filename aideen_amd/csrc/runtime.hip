@@ -24,6 +24,15 @@ static thread_local std::string g_last_error;
 void set_error(const std::string &msg) { g_last_error = msg; }
 }  // namespace adn
 
+// Chunk totals of adn_embed_context_noalloc: a fixed array per device (32 MiB), held until the
+// process ends.  Host code never passes the symbol itself to a kernel (on the host it names a
+// stand-in, not device memory): the device address is looked up once per device, with that
+// device current, when the first context on it is created, and only that address is used.
+constexpr long NOALLOC_MAX_DOUBLES = 1L << 22;
+static __device__ __align__(256) double scratch[NOALLOC_MAX_DOUBLES];
+static std::mutex g_scratch_mu;
+static double *g_scratch_ptr[256];  // by device ordinal; null until looked up
+
 struct DevBuf {
     void *p = nullptr;
     size_t bytes = 0;
@@ -678,6 +687,15 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
                   : (cfg->flags & ADN_F_GEMM_BF16)   ? PREC_BF16X1
                                                      : PREC_F16X3;
         ADN_HIP(hipGetDevice(&c->device));
+        if (c->device < 0 || c->device >= 256) throw HipError{hipErrorInvalidDevice, "adn_create: device ordinal"};
+        {  // the allocation-free entry point's per-device array (once per device)
+            std::lock_guard<std::mutex> lk(g_scratch_mu);
+            if (!g_scratch_ptr[c->device]) {
+                void *p = nullptr;
+                ADN_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+                g_scratch_ptr[c->device] = (double *)p;
+            }
+        }
         ADN_HIP(hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking));
         c->stream = c->own_stream;
         const long T = (long)cfg->max_batch * cfg->max_seq;
@@ -1131,6 +1149,28 @@ int adn_embed_context_async(adn_ctx *c, int32_t batch, int32_t seq, const int32_
     if (rc) return rc;
     try {
         enqueue_embed_context(c, batch, seq, tokens, max_ctx, out);
+        ADN_HIP(hipGetLastError());
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_embed_context_noalloc(adn_ctx *c, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
+                              float *out) {
+    int rc = check_embed_context(c, batch, seq, tokens, max_ctx, out);
+    if (rc) return rc;
+    const long half = embed_context_total_doubles(c->D.d, batch, seq);
+    if (2 * half > NOALLOC_MAX_DOUBLES)
+        return fail(ADN_E_CAPACITY, "adn_embed_context_noalloc: 2 * batch * chunks * d_r exceeds the fixed "
+                                    "buffer of 4194304 doubles");
+    double *p = g_scratch_ptr[c->device];
+    if (!p) return fail(ADN_E_HIP, "adn_embed_context_noalloc: no device buffer for this device");
+    try {
+        // every total the window kernel reads is written by the chunk kernel of this call first,
+        // so the buffer needs no clearing
+        launch_embed_context(c->embed, c->D.d, c->D.V, tokens, batch, seq, max_ctx, p, p + half, out, c->d_err,
+                             c->stream);
         ADN_HIP(hipGetLastError());
     } catch (const HipError &e) {
         return hip_fail(e);

@@ -244,6 +244,18 @@ int adn_embed_context(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *t
                       float *out);
 int adn_embed_context_async(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens, int32_t max_ctx,
                             float *out);
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): adn_embed_context_async
+ * with the same arguments, kernels and results, that allocates nothing.  Its per-chunk prefix totals
+ * live in a fixed per-device array of ADN_EMBED_NOALLOC_MAX_DOUBLES doubles (32 MiB, held until the
+ * process ends) instead of context memory grown on demand; a request needing more than that
+ * (2 * batch * ceil(seq / chunk) * d_r doubles, chunk = 32, 16, 8 or 4 positions for d_r up to
+ * 256, 512, 1024, 2048) fails with ADN_E_CAPACITY.  Every call on one GPU, from any context, shares
+ * that array: calls that overlap on one GPU (other streams, other threads) race.  The context's
+ * uploaded embedding table is read; device memory, enqueue only. */
+#define ADN_EMBED_NOALLOC_MAX_DOUBLES 4194304
+int adn_embed_context_noalloc(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens,
+                              int32_t max_ctx, float *out);
 
 /* --- byte-level BPE (Tokenizer::encode / decode, tokenizer.rs:94-116, which run the HF
  *     `tokenizers` crate on aideen-backbone/tokenizer.json) --------------------------------------
