@@ -49,7 +49,7 @@ class AdnRun(C.Structure):
 
 class AdnOutputs(C.Structure):
     _fields_ = [("h_star", F32P), ("pooled", F32P), ("logits", F32P), ("argmax", I32P),
-                ("iters", I32P), ("scan_y", F32P), ("scan_state", F32P)]
+                ("iters", I32P), ("scan_y", F32P), ("scan_state", F32P), ("converged", I32P)]
 
 
 STAGES = ["signal_gemm", "init", "qkv_gemm", "attn", "wo_gemm", "update", "converge", "anderson",
@@ -102,8 +102,8 @@ def lib():
         "adn_reset_state": (C.c_int, [ctx_p]),
         "adn_forward": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs)]),
         "adn_forward_async": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs)]),
-        "adn_decode_greedy": (C.c_int, [ctx_p, C.c_int32, I32P, C.c_int32, C.c_int32, C.c_float,
-                                        C.c_float, I32P]),
+        "adn_decode_greedy": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, C.c_int32, C.c_int32,
+                                        C.c_float, C.c_float, C.c_float, I32P]),
         "adn_spectral_norm": (C.c_int, [ctx_p, F32P, C.c_int32, C.c_int32, C.c_int32, F32P]),
         "adn_normalize_if_needed": (C.c_int, [ctx_p, F32P, C.c_int32, C.c_int32, C.c_float, C.c_int32]),
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),

@@ -145,7 +145,7 @@ class GpuDeqBackend:
         shapes = dict(h_star=((B, T, m.H, m.d), np.float32), pooled=((B, T, m.d), np.float32),
                       logits=((B, T, m.V), np.float32), argmax=((B, T), np.int32),
                       iters=((B, T), np.int32), scan_y=((B, T, m.H, m.d), np.float32),
-                      scan_state=((B, m.H, m.d, m.N), np.float32))
+                      scan_state=((B, m.H, m.d, m.N), np.float32), converged=((B, T), np.int32))
         outs = {k: np.zeros(*shapes[k]) for k in want}
         co = AdnOutputs(**{k: (_fp(v) if v.dtype == np.float32 else _ip(v)) for k, v in outs.items()})
         check(lib().adn_forward(self._ctx, C.byref(run), C.byref(co)))
@@ -167,7 +167,8 @@ class GpuDeqBackend:
         co = AdnOutputs(h_star=_dev_f(outputs.get("h_star")), pooled=_dev_f(outputs.get("pooled")),
                         logits=_dev_f(outputs.get("logits")), argmax=_dev_i(outputs.get("argmax")),
                         iters=_dev_i(outputs.get("iters")), scan_y=_dev_f(outputs.get("scan_y")),
-                        scan_state=_dev_f(outputs.get("scan_state")))
+                        scan_state=_dev_f(outputs.get("scan_state")),
+                        converged=_dev_i(outputs.get("converged")))
         check(lib().adn_forward_async(self._ctx, C.byref(run), C.byref(co)))
 
     def profile_forward(self, tokens=None, s_in=None, *, outputs: Dict[str, object],
@@ -183,7 +184,8 @@ class GpuDeqBackend:
         co = AdnOutputs(h_star=_dev_f(outputs.get("h_star")), pooled=_dev_f(outputs.get("pooled")),
                         logits=_dev_f(outputs.get("logits")), argmax=_dev_i(outputs.get("argmax")),
                         iters=_dev_i(outputs.get("iters")), scan_y=_dev_f(outputs.get("scan_y")),
-                        scan_state=_dev_f(outputs.get("scan_state")))
+                        scan_state=_dev_f(outputs.get("scan_state")),
+                        converged=_dev_i(outputs.get("converged")))
         prof = _lib.AdnProfile()
         check(lib().adn_profile_forward(self._ctx, C.byref(run), C.byref(co), C.byref(prof)))
         stages = {}
@@ -248,14 +250,19 @@ class GpuDeqBackend:
         o = self.forward(s_in=s, max_iters=max_iters, eps=eps, damping=damping, want=("pooled", "iters"))
         return o["pooled"].reshape(-1), o["iters"].reshape(-1).astype(np.uint32)
 
-    def decode_greedy(self, start_tokens, n_new: int, *, max_iters=None, eps=None, damping=None):
-        m = self.model
-        start = np.ascontiguousarray(start_tokens, dtype=np.int32).reshape(-1)
-        out = np.zeros((start.size, n_new), np.int32)
-        check(lib().adn_decode_greedy(self._ctx, start.size, _ip(start), n_new,
-                                      m.max_iters if max_iters is None else max_iters,
-                                      m.eps if eps is None else eps, m.beta if damping is None else damping,
-                                      _ip(out)))
+    def decode_greedy(self, prompt, n_new: int, ctx_len: int, *, max_iters: int = 10, eps: float = 0.0,
+                      damping: Optional[float] = None, repetition_penalty: float = 1.0) -> np.ndarray:
+        """``Trainer::generate`` with greedy sampling (trainer.rs:4219-4431): prompt [B][T0] ->
+        the n_new appended token ids [B][n_new].  The defaults are generate's own solve (10 Picard
+        steps, no early exit); ``ctx_len`` is ``ArchitectureConfig::ctx_len``."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        if prompt.ndim == 1:
+            prompt = prompt[:, None]
+        B, T0 = prompt.shape
+        out = np.zeros((B, n_new), np.int32)
+        check(lib().adn_decode_greedy(self._ctx, B, T0, _ip(prompt), int(n_new), int(ctx_len), int(max_iters),
+                                      float(eps), self.model.beta if damping is None else float(damping),
+                                      float(repetition_penalty), _ip(out)))
         return out
 
     # weight preparation --------------------------------------------------------------------

@@ -218,24 +218,30 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
 // largest per-slot relative RMS change (ADN_F_RESID_RELRMS).  Per slot, `acc` is the max |dh|
 // (mode 0) or the sum of dh^2 (modes 1, 2) after the wave reduction; `rms` the slot's RMSNorm
 // denominator.
+// A non-finite difference (a state that turned NaN or inf) counts as an infinite residual, so
+// such a token never passes the exit test and runs to the iteration cap unconverged (the
+// reference guards its state the same way, finite_or in deq_slot_attn_unified_clean.wgsl:99-108;
+// fmaxf alone would drop a NaN and report the token converged).
+__device__ __forceinline__ float nan_to_inf(float v) { return v == v ? v : INFINITY; }
 __device__ __forceinline__ float slot_resid(int mode, float acc, float rms, int d) {
-    return mode == 2 ? sqrtf(acc / (float)d + 1e-12f) / fmaxf(rms, 1e-6f) : acc;
+    return nan_to_inf(mode == 2 ? sqrtf(acc / (float)d + 1e-12f) / fmaxf(rms, 1e-6f) : acc);
 }
 __device__ __forceinline__ float combine_resid(int mode, float tok, float slot) {
     return mode == 1 ? tok + slot : fmaxf(tok, slot);
 }
-// Exit test after update k (0-based) of a token with residual r: below eps, the iteration cap,
-// or (with rprev) the homeostatic plateau of deq_slot_attn_unified_clean.wgsl:1786-1793
+// Exit test after update k (0-based) of a token with residual r: converged when below eps or
+// (with rprev) on the homeostatic plateau of deq_slot_attn_unified_clean.wgsl:1786-1793
 // (k+1 >= 4, r <= max(eps, 0.15 * 0.2), |r - r_prev| <= 0.10 max(r_prev, eps)); r_prev is the
-// previous update's residual (1 before the first), replaced by r here (`store`: this lane writes).
-__device__ __forceinline__ bool token_done(float r, float eps, int k, int max_iters, float *rprev, bool store) {
-    bool done = (r < eps) || (k + 1 >= max_iters);
+// previous update's residual (1 before the first), replaced by r here (`store`: this lane
+// writes).  Returns 1 (converged), 2 (unconverged at the iteration cap) or 0 (continue).
+__device__ __forceinline__ int token_exit(float r, float eps, int k, int max_iters, float *rprev, bool store) {
+    bool conv = r < eps;
     if (rprev) {
         const float rp = *rprev;
-        if (k + 1 >= 4 && r <= fmaxf(eps, 0.15f * 0.2f) && fabsf(r - rp) / fmaxf(rp, eps) <= 0.10f) done = true;
+        if (k + 1 >= 4 && r <= fmaxf(eps, 0.15f * 0.2f) && fabsf(r - rp) / fmaxf(rp, eps) <= 0.10f) conv = true;
         if (store) *rprev = r;
     }
-    return done;
+    return conv ? 1 : (k + 1 >= max_iters ? 2 : 0);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -317,7 +323,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
                 const float hn = f * beta + q.h[e] * omb;
                 h[lane + 64 * e] = hn;
                 const float df = hn - q.h[e];
-                r = rmode ? r + df * df : fmaxf(r, fabsf(df));
+                r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
             }
             r = rmode ? wave_sum(r) : wave_max(r);
             rtok = combine_resid(rmode, rtok, slot_resid(rmode, r, rms, d));
@@ -338,10 +344,13 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
                 step(s, q);
             }
         }
-    if (rmode == 1) rtok = sqrtf(rtok);
-        const bool done = token_done(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, lane == 0);
-        if (done && lane == 0) b.iters[t] = k + 1;
-        keep = !done;
+        if (rmode == 1) rtok = nan_to_inf(sqrtf(rtok));
+        const int ex = token_exit(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, lane == 0);
+        if (ex && lane == 0) {
+            b.iters[t] = k + 1;
+            if (b.conv) b.conv[t] = ex == 1;
+        }
+        keep = !ex;
     }
     if (lane == 0) {
         keep_s[wave] = keep;
@@ -469,7 +478,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
         const float hn = f * beta + hold[e] * omb;
         h[lane + 64 * e] = hn;
         const float df = hn - hold[e];
-        r = rmode ? r + df * df : fmaxf(r, fabsf(df));
+        r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
     }
     r = rmode ? wave_sum(r) : wave_max(r);
     if (lane == 0) rs[s] = slot_resid(rmode, r, rms, d);
@@ -477,9 +486,11 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     if (threadIdx.x == 0) {
         float rtok = 0.0f;
         for (int q = 0; q < H; ++q) rtok = combine_resid(rmode, rtok, rs[q]);
-        if (rmode == 1) rtok = sqrtf(rtok);
-        if (token_done(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, true)) {
+        if (rmode == 1) rtok = nan_to_inf(sqrtf(rtok));
+        const int ex = token_exit(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, true);
+        if (ex) {
             b.iters[t] = k + 1;
+            if (b.conv) b.conv[t] = ex == 1;
         } else {
             const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
             b.act[cur ^ 1][pos] = t;

@@ -151,14 +151,93 @@ __global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val
     }
 }
 
-// Greedy decode bookkeeping: tokens[b] = argmax[b]; out_seq[b][j] = argmax[b].
-__global__ void k_decode_step(const int32_t *argmax, int32_t *tokens, int32_t *out_seq, int B,
-                              int n_new, int j) {
+// ---------------------------------------------------------------------------------------
+// Greedy decode (Trainer::generate, trainer.rs:4219-4431).  seq [B][stride] holds each
+// sequence's tokens so far (the prompt, then the appended arg-maxes); step j works on the first
+// len = T0 + j of them, its context being the last ctx of those (trainer.rs:4248-4249).
+// ---------------------------------------------------------------------------------------
+constexpr int DQ_W = 8;  // waves per decode-query block
+
+// The context query embed_context(context, ctx) (tokenizer.rs:133-149) of every sequence, one
+// block per sequence: v = sum_{p < L} (p + 1) E[tok_p] over the window in fp64 (wave w takes the
+// positions p = w mod DQ_W, combined in wave order), q = v / |v| -- r = v / L itself when
+// |r| <= 1e-6, as embed_context keeps a near-zero sum unnormalised.  The same quantity as
+// k_ctx_window's at the last position, formed directly for one window per sequence.
+__global__ __launch_bounds__(64 * DQ_W) void k_decode_query(const float *E, int d, const int32_t *seq, int stride,
+                                                            int len, int ctx, float *q) {
+    __shared__ double part[DQ_W][64];
+    __shared__ double vbuf[2048];
+    __shared__ double red[DQ_W];
+    const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int start = len > ctx ? len - ctx : 0, L = len - start;
+    const int32_t *tk = seq + (long)b * stride + start;
+    for (int j0 = 0; j0 < d; j0 += 64) {
+        const int j = j0 + lane;
+        double acc = 0.0;
+        int p = wave;
+        for (; p + 3 * DQ_W < L; p += 4 * DQ_W) {  // four rows in flight
+            float x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = E[(long)tk[p + u * DQ_W] * d + j];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += (double)(p + u * DQ_W + 1) * (double)x[u];
+        }
+        for (; p < L; p += DQ_W) acc += (double)(p + 1) * (double)E[(long)tk[p] * d + j];
+        part[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            double v = 0.0;
+            for (int w = 0; w < DQ_W; ++w) v += part[w][lane];
+            vbuf[j] = v;
+        }
+        __syncthreads();
+    }
+    double ss = 0.0;
+    for (int j = threadIdx.x; j < d; j += 64 * DQ_W) ss += vbuf[j] * vbuf[j];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    double n2 = 0.0;
+    for (int w = 0; w < DQ_W; ++w) n2 += red[w];
+    const double nv = sqrt(n2);
+    const double inv = 1.0 / (nv > 1e-6 * (double)L ? nv : (double)L);
+    for (int j = threadIdx.x; j < d; j += 64 * DQ_W) q[(long)b * d + j] = (float)(vbuf[j] * inv);
+}
+
+// LmHead::sample's repetition penalty (lm_head.rs:81-99) on each sequence's logits row: every
+// distinct token of the context (the thread holding its first occurrence) has its logit
+// multiplied by pen when negative, divided by it otherwise.
+__global__ __launch_bounds__(256) void k_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len,
+                                                     int ctx, float pen) {
+    const int b = blockIdx.x;
+    const int start = len > ctx ? len - ctx : 0, L = len - start;
+    const int32_t *tk = seq + (long)b * stride + start;
+    float *lg = logits + (long)b * V;
+    for (int p = threadIdx.x; p < L; p += blockDim.x) {
+        const int tok = tk[p];
+        bool seen = false;
+        for (int u = 0; u < p && !seen; ++u) seen = tk[u] == tok;
+        if (seen || tok < 0 || tok >= V) continue;
+        const float sc = lg[tok];
+        lg[tok] = sc < 0.0f ? sc * pen : sc / pen;
+    }
+}
+
+// seq[b][len] = out[b][j] = tok[b]
+__global__ void k_decode_append(const int32_t *tok, int32_t *seq, int stride, int len, int32_t *out, int n_new, int j,
+                                int B) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= B) return;
-    const int32_t v = argmax[b];
-    tokens[b] = v;
-    out_seq[(long)b * n_new + j] = v;
+    const int32_t v = tok[b];
+    seq[(long)b * stride + len] = v;
+    out[(long)b * n_new + j] = v;
+}
+
+// last[b] = seq[b][len - 1]
+__global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) last[b] = seq[(long)b * stride + len - 1];
 }
 
 }  // namespace
@@ -187,10 +266,24 @@ void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, 
                        ntiles, out);
 }
 
-void launch_copy_tokens_from_argmax(const int32_t *argmax, int32_t *tokens, int32_t *out_seq,
-                                    int B, int n_new, int j, hipStream_t st) {
-    hipLaunchKernelGGL(k_decode_step, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, argmax,
-                       tokens, out_seq, B, n_new, j);
+void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
+                         hipStream_t st) {
+    hipLaunchKernelGGL(k_decode_query, dim3((unsigned)B), dim3(64 * DQ_W), 0, st, E, d, seq, stride, len, ctx, q);
+}
+
+void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
+                        hipStream_t st) {
+    hipLaunchKernelGGL(k_rep_penalty, dim3((unsigned)B), dim3(256), 0, st, logits, V, seq, stride, len, ctx, pen);
+}
+
+void launch_decode_append(const int32_t *tok, int32_t *seq, int stride, int len, int32_t *out, int n_new, int j, int B,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_decode_append, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, tok, seq, stride, len,
+                       out, n_new, j, B);
+}
+
+void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {
+    hipLaunchKernelGGL(k_decode_last, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, seq, stride, len, last, B);
 }
 
 }  // namespace adn

@@ -68,6 +68,7 @@ struct SolveBuffers {
     int32_t *act[2];    // active token lists
     int32_t *cnt;       // [4]: counts of act[0], act[1]; cnt[2] unused; cnt[3] = total tokens
     int32_t *iters;     // [ntok]
+    int32_t *conv;      // [ntok] 1 = exit by the tolerance (or plateau), 0 = stopped unconverged at the cap; or null
     float *rprev;       // [ntok] previous iteration's token residual (homeostatic exit) or null
     int32_t *cnt_hist;  // [ADN_PROFILE_MAX_ITERS] active tokens entering iteration k (summed over positions)
     float *hist;        // Anderson ring [m][ntok][H][d] or null
@@ -102,9 +103,18 @@ void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream
 // final reduction of the per-tile arg-max partials written by the LM-head GEMM
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
                           hipStream_t st);
-// S_in gather for the embedded-input path: x[t] = E[tok[t]] (for init/signal when tokens given)
-void launch_copy_tokens_from_argmax(const int32_t *argmax, int32_t *tokens, int32_t *out_seq,
-                                    int B, int n_new, int j, hipStream_t st);
+// Greedy decode.  seq [B][stride] holds each sequence's tokens; step j uses the first len.
+// q [B][d] = embed_context of the last ctx of them (d <= 2048).
+void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
+                         hipStream_t st);
+// the repetition penalty over the same context, in place on logits [B][V]
+void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
+                        hipStream_t st);
+// seq[b][len] = out[b][j] = tok[b]  (out is [B][n_new])
+void launch_decode_append(const int32_t *tok, int32_t *seq, int stride, int len, int32_t *out, int n_new, int j, int B,
+                          hipStream_t st);
+// last[b] = seq[b][len - 1]
+void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st);
 
 // ---- carrier scan (scan.hip) -------------------------------------------------------------
 struct ScanBuffers {

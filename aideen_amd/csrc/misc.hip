@@ -166,12 +166,15 @@ void launch_transpose(const float *src, int rows, int cols, long batch, float *d
     hipLaunchKernelGGL(k_transpose, grid, dim3(32, 8), 0, st, src, rows, cols, dst);
 }
 
-// max |x| as the bit pattern of a non-negative float (which orders like the float), one atomic
-// per wave.  NaN inputs compare above every finite value and propagate into the scale.
+// max |x| over the finite elements, as the bit pattern of a non-negative float (which orders
+// like the float), one atomic per wave.  NaN and inf elements are skipped: they stay non-finite
+// in their own output rows, and must not turn the scale of every other row into 0 or NaN.
 __global__ void k_absmax(const float *x, long n, unsigned *out) {
     unsigned m = 0;
-    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
-        m = max(m, __float_as_uint(fabsf(x[i])));
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+        const float a = fabsf(x[i]);
+        if (a < INFINITY) m = max(m, __float_as_uint(a));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, off, 64));
     if ((threadIdx.x & 63) == 0 && m) atomicMax(out, m);

@@ -508,6 +508,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     SolveBuffers b = c->sb;
     if (o.h_star) b.h = o.h_star;
     if (o.iters) b.iters = o.iters;
+    b.conv = o.converged;
     b.mem_hist = nullptr;
     c->last_h = b.h;  // the adjoint reads this forward's h* and signal
     c->last_ntok = ntok;
@@ -532,6 +533,7 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
     SolveBuffers b = c->sb;
     if (o.h_star) b.h = o.h_star;
     if (o.iters) b.iters = o.iters;
+    b.conv = o.converged;
     b.mem_hist = nullptr;
     b.mem_T = T;
     c->last_h = b.h;
@@ -951,6 +953,7 @@ int adn_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
         if (o->iters) dout.iters = (int32_t *)staging_f(c, 4, (size_t)ntok * sizeof(int32_t));
         if (o->scan_y) dout.scan_y = staging_f(c, 5, hsz * sizeof(float));
         if (o->scan_state) dout.scan_state = staging_f(c, 6, stsz * sizeof(float));
+        if (o->converged) dout.converged = (int32_t *)staging_f(c, 7, (size_t)ntok * sizeof(int32_t));
         enqueue_run(c, dr, dout);
         ADN_HIP(hipGetLastError());
         auto d2h = [&](void *dst, const void *src, size_t bytes) {
@@ -963,6 +966,7 @@ int adn_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
         d2h(o->iters, dout.iters, (size_t)ntok * sizeof(int32_t));
         d2h(o->scan_y, dout.scan_y, hsz * sizeof(float));
         d2h(o->scan_state, dout.scan_state, stsz * sizeof(float));
+        d2h(o->converged, dout.converged, (size_t)ntok * sizeof(int32_t));
         ADN_HIP(hipStreamSynchronize(c->stream));
         return check_device_error(c);
     } catch (const HipError &e) {
@@ -970,41 +974,97 @@ int adn_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
     }
 }
 
-int adn_decode_greedy(adn_ctx *c, int32_t batch, const int32_t *start, int32_t n_new, int32_t max_iters,
-                      float eps, float damping, int32_t *out_tokens) {
-    if (!c || !start || !out_tokens) return fail(ADN_E_INVALID, "null argument");
+int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
+                      int32_t ctx_len, int32_t max_iters, float eps, float damping, float repetition_penalty,
+                      int32_t *out_tokens) {
+    if (!c || !prompt || !out_tokens) return fail(ADN_E_INVALID, "null argument");
     if (!c->has_weights) return fail(ADN_E_NO_WEIGHTS, "decode before adn_upload_weights");
-    if (batch < 1 || n_new < 0) return fail(ADN_E_INVALID, "batch must be >= 1 and n_new >= 0");
-    if (batch > c->cap_tok) return fail(ADN_E_CAPACITY, "batch exceeds the context capacity");
-    for (int b = 0; b < batch; ++b)
-        if (start[b] < 0 || start[b] >= c->D.V) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
-    if (c->cfg.flags & ADN_F_MEMORY)
-        return fail(ADN_E_INVALID, "adn_decode_greedy runs the canonical forward; not available with ADN_F_MEMORY");
-    if (n_new == 0) return ADN_OK;
+    if (batch < 1 || prompt_len < 1 || n_new < 0 || ctx_len < 1)
+        return fail(ADN_E_INVALID, "batch, prompt_len and ctx_len must be >= 1, n_new >= 0");
+    if (!(repetition_penalty > 0.0f) || !std::isfinite(repetition_penalty))
+        return fail(ADN_E_INVALID, "repetition_penalty must be finite and > 0");
+    const bool memory = (c->cfg.flags & ADN_F_MEMORY) != 0;
+    if (memory && (c->cfg.flags & ADN_F_TOKEN_CARRY))
+        return fail(ADN_E_INVALID, "the fixed-history decode solves every query from the init rule "
+                                   "(solve_query_with_fixed_history); ADN_F_TOKEN_CARRY is not available here");
+    if ((long)batch * (memory ? prompt_len : 1) > c->cap_tok)
+        return fail(ADN_E_CAPACITY, memory ? "batch*prompt_len exceeds the context capacity"
+                                           : "batch exceeds the context capacity");
+    for (long i = 0; i < (long)batch * prompt_len; ++i)
+        if (prompt[i] < 0 || prompt[i] >= c->D.V) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
     adn_run r{};
     r.batch = batch;
     r.seq = 1;
     r.max_iters = max_iters;
     r.eps = eps;
     r.damping = damping;
-    r.tokens = start;
+    r.tokens = prompt;  // placeholder for the checks; the device inputs are set per step
     int rc = check_run(c, &r);
     if (rc) return rc;
+    if (n_new == 0) return ADN_OK;
+    // LmHead::sample applies the penalty only when |penalty - 1| > 1e-4 (lm_head.rs:81)
+    const bool penalise = std::fabs(repetition_penalty - 1.0f) > 1e-4f;
+    const Dims &D = c->D;
+    const int stride = prompt_len + n_new;
+    hipStream_t st = c->stream;
     try {
-        int32_t *tok = (int32_t *)staging_f(c, 10, (size_t)batch * sizeof(int32_t));
-        int32_t *seq = (int32_t *)staging_f(c, 11, (size_t)batch * n_new * sizeof(int32_t));
-        ADN_HIP(hipMemcpyAsync(tok, start, batch * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
-        r.tokens = tok;
-        adn_outputs o{};
-        o.argmax = c->argmax_scratch;
+        int32_t *seq = (int32_t *)staging_f(c, 10, (size_t)batch * stride * sizeof(int32_t));
+        int32_t *outd = (int32_t *)staging_f(c, 11, (size_t)batch * n_new * sizeof(int32_t));
+        ADN_HIP(hipMemcpy2DAsync(seq, (size_t)stride * sizeof(int32_t), prompt, (size_t)prompt_len * sizeof(int32_t),
+                                 (size_t)prompt_len * sizeof(int32_t), batch, hipMemcpyHostToDevice, st));
+        float *lg = penalise ? staging_f(c, 24, (size_t)batch * D.V * sizeof(float)) : nullptr;
+        int32_t *am = c->argmax_scratch;
+        float *q = nullptr, *m_cur = nullptr, *m_nxt = nullptr;
+        int32_t *last = nullptr;
+        if (memory) {
+            // prime_fixed_history_state (trainer.rs:718-733): the memory after every prompt token
+            const size_t msz = (size_t)batch * D.H * D.d;
+            m_cur = staging_f(c, 25, msz * sizeof(float));
+            m_nxt = staging_f(c, 26, msz * sizeof(float));
+            last = (int32_t *)staging_f(c, 27, (size_t)batch * prompt_len * sizeof(int32_t));
+            ADN_HIP(hipMemcpyAsync(last, prompt, (size_t)batch * prompt_len * sizeof(int32_t), hipMemcpyHostToDevice,
+                                   st));
+            adn_run rp = r;
+            rp.seq = prompt_len;
+            rp.tokens = last;
+            adn_outputs op{};
+            op.scan_state = m_cur;
+            enqueue_forward_memory(c, rp, op);
+        } else {
+            q = staging_f(c, 28, (size_t)batch * D.d * sizeof(float));
+        }
         for (int j = 0; j < n_new; ++j) {
-            enqueue_forward(c, r, o);
-            launch_copy_tokens_from_argmax(c->argmax_scratch, tok, seq, batch, n_new, j, c->stream);
+            const int len = prompt_len + j;
+            adn_outputs o{};
+            if (penalise)
+                o.logits = lg;
+            else
+                o.argmax = am;
+            if (memory) {
+                // query = embed(last context token) with the history of m (trainer.rs:4395-4400)
+                launch_decode_last(seq, stride, len, last, batch, st);
+                r.tokens = last;
+                r.s_in = nullptr;
+                r.scan_state_in = m_cur;
+                o.scan_state = m_nxt;
+                enqueue_forward_memory(c, r, o);
+                std::swap(m_cur, m_nxt);
+            } else {
+                // query = embed_context(context, ctx_len) (trainer.rs:4388-4392)
+                launch_decode_query(c->embed, D.d, seq, stride, len, ctx_len, batch, q, st);
+                r.tokens = nullptr;
+                r.s_in = q;
+                enqueue_forward(c, r, o);
+            }
+            if (penalise) {
+                launch_rep_penalty(lg, D.V, seq, stride, len, ctx_len, repetition_penalty, batch, st);
+                launch_argmax(lg, batch, D.V, am, st);
+            }
+            launch_decode_append(am, seq, stride, len, outd, n_new, j, batch, st);
         }
         ADN_HIP(hipGetLastError());
-        ADN_HIP(hipMemcpyAsync(out_tokens, seq, (size_t)batch * n_new * sizeof(int32_t), hipMemcpyDeviceToHost,
-                               c->stream));
-        ADN_HIP(hipStreamSynchronize(c->stream));
+        ADN_HIP(hipMemcpyAsync(out_tokens, outd, (size_t)batch * n_new * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+        ADN_HIP(hipStreamSynchronize(st));
         return check_device_error(c);
     } catch (const HipError &e) {
         return hip_fail(e);

@@ -168,10 +168,19 @@ PRESETS = {
     "NS": dict(model=ModelConfig(d=512, H=8, V=50257, N=16), B=32, T=256, tokens="zipf"),
     "C3": dict(model=ModelConfig(d=512, H=8, V=50257, N=16, sigma=0.7, anderson_m=5),
                B=32, T=1024, tokens="zipf"),
-    "C4": dict(model=ModelConfig(d=512, H=8, V=50257, N=16), B=8, T=8192, tokens="uniform"),
+    # long-context scan stress: input-dependent decay logits N(0,1) through the model's own
+    # projection, decay bases spread from ~0.999 to ~0.01 across channels (make_weights)
+    "C4": dict(model=ModelConfig(d=512, H=8, V=50257, N=16), B=8, T=8192, tokens="uniform",
+               long_memory_gates=True),
     "C5": dict(model=ModelConfig(d=2048, H=16, V=50257, N=32, sigma=0.8, anderson_m=5),
                B=16, T=2048, tokens="zipf"),
 }
+
+
+def preset_weights(name: str, cfg: Optional[ModelConfig] = None, seed: int = 0) -> Dict[str, Optional[np.ndarray]]:
+    """The weights of a BASELINE preset (cfg overrides its model, e.g. with other GEMM flags)."""
+    p = PRESETS[name]
+    return make_weights(cfg or p["model"], seed=seed, long_memory_gates=p.get("long_memory_gates", False))
 
 
 def make_weights(cfg: ModelConfig, seed: int = 0, gates_seed: int = 2,

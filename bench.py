@@ -43,6 +43,43 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_info(threads: int) -> dict:
+    """nproc, the CPU model and the thread count used (one GPU's share of the host is 16 cores on
+    these boxes, whatever nproc reports, so the oracle runs at most 16 threads)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return dict(nproc=os.cpu_count(), affinity=affinity, cpu_model=model, threads=threads,
+                threads_basis="min(nproc, 16): one GPU's share of the box's cores")
+
+
+def config_metric(name: str, mc, B: int, T: int) -> str:
+    """The metric string of a configuration: the headline metric for NS, an own name otherwise."""
+    if name == "NS":
+        return METRIC
+    if name == "C4":
+        return (f"C4 long-context carrier stress: forward tokens/sec and carrier-scan HBM GB/s at "
+                f"d_r={mc.d},h_slots={mc.H},ctx={T},B={B}")
+    return f"{name} forward tokens/sec at d_r={mc.d},h_slots={mc.H},ctx={T},B={B} (not the headline metric)"
+
+
+def config_data(name: str, mc, tokens: str) -> str:
+    ids = "Zipf(1.1) token ids" if tokens == "zipf" else "uniform token ids"
+    gates = ("; decay bases 0.999..0.01 across channels, gate logits N(0,1) through the model's projection"
+             if name == "C4" else "")
+    return f"synthetic (seeded Xavier weights at spectral norm {mc.sigma}, {ids}{gates})"
+
+
 def cpu_baseline(mc, w, toks, seconds: float):
     """The C oracle (a port of the reference's CPU forward) timed on whole sequences of the same
     workload: one sequence calibrates, then as many sequences as fill about `seconds`."""
@@ -63,7 +100,7 @@ def cpu_baseline(mc, w, toks, seconds: float):
                 sample=(f"{nseq} of the {B} sequences ({n} tokens) of the same workload, same weights "
                         f"and token ids: solve + LM-head logits + arg-max + carrier scan, "
                         f"{threads} OpenMP threads over tokens, {t2:.1f} s"),
-                seconds=round(t2, 2))
+                seconds=round(t2, 2), host=host_info(threads))
 
 
 def cpu_baseline_memory(mc, w, toks, seconds: float):
@@ -89,7 +126,7 @@ def cpu_baseline_memory(mc, w, toks, seconds: float):
                 sample=(f"the first {tp} of {T} positions of {nseq} of the {B} sequences ({n} tokens) of the "
                         f"same workload, same weights and token ids: memory-coupled solve + carrier + "
                         f"LM-head logits + arg-max, {threads} OpenMP threads over sequences, {t2:.1f} s"),
-                seconds=round(t2, 2))
+                seconds=round(t2, 2), host=host_info(threads))
 
 
 def bench_embed(args, be, mc, w, toks, dev, torch) -> int:
@@ -261,7 +298,7 @@ def main() -> int:
         mc = dataclasses.replace(mc, eps=args.eps)
     B, T = p["B"], p["T"]
     log(f"config {args.config} ({args.mode}): d={mc.d} H={mc.H} V={mc.V} N={mc.N} B={B} T={T} eps={mc.eps}")
-    w = synth.make_weights(mc, seed=0)
+    w = synth.preset_weights(args.config, mc, seed=0)
     if memory:
         w = dict(w)
         w.update(synth.make_hist_weights(mc, seed=0))
@@ -362,10 +399,12 @@ def main() -> int:
         log(f"cpu baseline {cpu['value']} tokens/s on {cpu['cores']} threads")
 
     line = {
-        "metric": METRIC if not memory else "memory-coupled forward tokens/sec at d_r=512,h_slots=8,ctx=256,B=32", "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "metric": (config_metric(args.config, mc, B, T) if not memory else
+                   f"memory-coupled forward tokens/sec at d_r={mc.d},h_slots={mc.H},ctx={T},B={B}"),
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32" if args.gemm != "bf16" else "bf16-in/f32-acc",
-        "data": "synthetic (seeded Xavier weights at spectral norm 0.5, Zipf(1.1) token ids)",
+        "data": config_data(args.config, mc, p["tokens"]),
         "config": {"workload": (f"{args.config}: DEQ forward d_r={mc.d} h_slots={mc.H} vocab={mc.V} "
                                 f"d_state={mc.N} B={B} ctx={T}, Picard max {mc.max_iters} tol {mc.eps}, "
                                 f"anderson m={mc.anderson_m}; logits for all positions + arg-max + scan; "
@@ -385,6 +424,10 @@ def main() -> int:
         "stages": stages,
         "profiled_forward_ms": round(prof["total_ms"], 3),
     }
+    if args.config == "C4" and "scan" in hbm:  # the configuration's own figure: the carrier scan
+        sc = prof["stages"]["scan"]
+        line["scan"] = dict(gbs=hbm["scan"]["gbs"], frac=hbm["scan"]["frac"], ms=round(sc["ms"], 4),
+                            bytes=sc["bytes"], basis="compulsory bytes: read h* and the carrier record, write y")
     print(json.dumps(line), flush=True)
     return 0
 

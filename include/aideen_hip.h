@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define ADN_ABI_VERSION 2
+#define ADN_ABI_VERSION 3
 
 /* status codes */
 #define ADN_OK 0
@@ -155,6 +155,12 @@ typedef struct adn_outputs {
     int32_t *iters;     /* [B][T]       Picard updates applied                  */
     float *scan_y;      /* [B][T][H][d] carrier output Y_t                      */
     float *scan_state;  /* [B][H][d][N] carrier state after the last token      */
+    /* [B][T] 1 = the solve exited on the tolerance (or the homeostatic plateau), 0 = it stopped at
+     * max_iters unconverged.  A residual that is not finite (the state turned NaN or inf, e.g. from
+     * a non-finite input row) counts as infinite, so such a token always runs to max_iters and
+     * reports 0 (the reference's finite_or guards, deq_slot_attn_unified_clean.wgsl:99-108; its
+     * failure detection, trainer.rs:2931-2995). */
+    int32_t *converged;
 } adn_outputs;
 
 typedef struct adn_ctx adn_ctx;
@@ -187,12 +193,24 @@ int adn_forward(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
  * reported by the next adn_synchronize(). */
 int adn_forward_async(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
 
-/* Greedy decode, host memory, blocking (Trainer::generate trainer.rs:4219-4431 with
- * LmHead::sample at temperature <= 1e-4 = argmax, lm_head.rs:104-112).  Each step solves the
- * last token of every sequence and appends its argmax; all n_new steps run on the device
- * without host round trips.  out_tokens is [B][n_new]. */
-int adn_decode_greedy(adn_ctx *ctx, int32_t batch, const int32_t *start_tokens, int32_t n_new,
-                      int32_t max_iters, float eps, float damping, int32_t *out_tokens);
+/* Greedy decode, host memory, blocking: Trainer::generate (trainer.rs:4219-4431) with
+ * LmHead::sample at temperature <= 1e-4 (lm_head.rs:72-112).  prompt [B][prompt_len] token ids,
+ * out_tokens [B][n_new] the appended tokens.  At step j the context of sequence b is the last
+ * ctx_len of its prompt_len + j tokens (trainer.rs:4248-4249) and
+ *   - the canonical forward (trainer.rs:4388-4392, 4402-4406): the query is embed_context(context,
+ *     ctx_len) (tokenizer.rs:133-149), solved from init(query) with max_iters / eps / damping
+ *     (generate runs exactly 10 steps: max_iters = 10, eps = 0);
+ *   - with ADN_F_MEMORY, the fixed-history form (trainer.rs:4395-4400, 677-735): the memory is
+ *     primed over every prompt token (prime_fixed_history_state, :718-733), then each step solves
+ *     the embedding of the last context token with the history context of the memory and advances
+ *     it (eps = 0 runs the reference's fixed max_iters); ADN_F_TOKEN_CARRY is refused;
+ * then the logits of the LM head (lm_head.rs:50-54), the repetition penalty over the context when
+ * |repetition_penalty - 1| > 1e-4 (lm_head.rs:81-99), and the arg-max with the last-max tie rule.
+ * Every step runs on the device without host round trips.  Capacity: batch (canonical) or
+ * batch * prompt_len (memory) tokens. */
+int adn_decode_greedy(adn_ctx *ctx, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
+                      int32_t ctx_len, int32_t max_iters, float eps, float damping, float repetition_penalty,
+                      int32_t *out_tokens);
 
 /* --- weight preparation (spectral_norm.rs:25-80; spectral_renorm.wgsl:83-196) ----------- */
 /* sigma_max by n_iter power iterations from u0 = 1/sqrt(rows); host memory, blocking. */

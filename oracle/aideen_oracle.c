@@ -304,6 +304,11 @@ static void step_p(const prep *p, scratch *sc, const float *h, const float *sign
  * relative RMS change sqrt(mean (a-b)^2 + 1e-12) / max(rms, 1e-6) with rms the slot's RMSNorm
  * denominator of the step that produced a (the GPU reference's err_h,
  * deq_slot_attn_unified_clean.wgsl:1654-1695). */
+/* A non-finite value (a NaN or inf state) counts as an infinite residual, so the token never
+ * passes the exit test (the reference's finite_or guards, UWGSL:99-108); fmaxf alone would drop
+ * a NaN and report such a token converged. */
+static float nan_to_inf(float v) { return v != v ? INFINITY : v; }
+
 static float residual(const orc_cfg *c, const float *rms, const float *a, const float *b) {
     const int n = c->H * c->d;
     if (c->flags & ORC_F_RESID_RELRMS) {
@@ -315,7 +320,7 @@ static float residual(const orc_cfg *c, const float *rms, const float *a, const 
                 const float df = a[(size_t)s * d + i] - b[(size_t)s * d + i];
                 acc += df * df;
             }
-            mx = fmaxf(mx, sqrtf(acc / (float)d + 1e-12f) / fmaxf(rms[s], 1e-6f));
+            mx = fmaxf(mx, nan_to_inf(sqrtf(acc / (float)d + 1e-12f) / fmaxf(rms[s], 1e-6f)));
         }
         return mx;
     }
@@ -325,10 +330,10 @@ static float residual(const orc_cfg *c, const float *rms, const float *a, const 
             const float df = a[i] - b[i];
             acc += df * df;
         }
-        return sqrtf(acc);
+        return nan_to_inf(sqrtf(acc));
     }
     float mx = 0.0f;
-    for (int i = 0; i < n; ++i) mx = fmaxf(mx, fabsf(a[i] - b[i]));
+    for (int i = 0; i < n; ++i) mx = fmaxf(mx, nan_to_inf(fabsf(a[i] - b[i])));
     return mx;
 }
 
@@ -402,9 +407,11 @@ void orc_anderson_coeffs(int n, const float *g_in, float *beta) {
  * of updates applied.  Converged tokens are frozen.  Optional Anderson mixing after each step
  * (staged_adjoint_picard_clean.wgsl:1012-1134, gpu_deq.rs:4278-4293): the ring stores the
  * un-mixed Picard iterate; mixing starts at k >= 2 with n_res = min(k, m-1) >= 2. */
-/* warm != 0: h already holds the starting iterate (token carry), init_p is skipped */
+/* warm != 0: h already holds the starting iterate (token carry), init_p is skipped.
+ * *conv (when given) = 1 if the solve exited on the tolerance or the plateau, 0 if it stopped at
+ * max_iters unconverged. */
 static int solve_p(const prep *p, scratch *sc, const float *x, const float *hist, float *h,
-                   float *resid_trace, int warm) {
+                   float *resid_trace, int warm, int *conv) {
     const orc_cfg *c = &p->c;
     const int d = c->d, H = c->H;
     const size_t hd = (size_t)H * d;
@@ -412,6 +419,7 @@ static int solve_p(const prep *p, scratch *sc, const float *x, const float *hist
     signal_p(p, x, signal);
     if (!warm) init_p(p, x, signal, h);
     int iters = 0;
+    if (conv) *conv = 0;
     const int m = c->anderson_m;
     float r_prev = 1.0f; /* homeostatic exit: the previous update's residual (1 before the first) */
     for (int k = 0; k < c->max_iters; ++k) {
@@ -427,6 +435,7 @@ static int solve_p(const prep *p, scratch *sc, const float *x, const float *hist
             fabsf(r - r_prev) / fmaxf(r_prev, c->eps) <= 0.10f)
             stop = 1;
         r_prev = r;
+        if (stop && conv) *conv = 1;
         if (stop || m <= 0) {
             memcpy(h, sc->hn, sizeof(float) * hd);
             if (stop) break;
@@ -500,7 +509,7 @@ int orc_solve_token(const orc_cfg *c, const orc_weights *w, const float *x, floa
     scratch sc;
     prep_init(&p, c, w);
     scratch_init(&sc, c);
-    int it = solve_p(&p, &sc, x, NULL, h_star, resid_trace, 0);
+    int it = solve_p(&p, &sc, x, NULL, h_star, resid_trace, 0, NULL);
     scratch_free(&sc);
     prep_free(&p);
     return it;
@@ -710,8 +719,8 @@ void orc_model_free(orc_model *m) {
  * fixed-history query, tokenizer.rs:117-119): solve every token independently, pool, LM head,
  * greedy argmax; then the carrier over each sequence. */
 void orc_model_forward(orc_model *mdl, int B, int T, const int32_t *tokens, float *h_star,
-                       float *pooled, float *logits, int32_t *iters, int32_t *argmax,
-                       float *scan_y, float *scan_state, int nthreads) {
+                       float *pooled, float *logits, int32_t *iters, int32_t *converged,
+                       int32_t *argmax, float *scan_y, float *scan_state, int nthreads) {
     const orc_cfg *c = &mdl->p.c;
     const orc_weights *w = mdl->p.w;
     const int d = c->d, H = c->H, V = c->V;
@@ -740,8 +749,10 @@ void orc_model_forward(orc_model *mdl, int B, int T, const int32_t *tokens, floa
         for (long t = 0; t < ntok; ++t) {
             const int32_t tok = tokens[t];
             float *h = hs_all + hd * t;
-            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, NULL, h, NULL, 0);
+            int cv = 0;
+            int it = solve_p(p, &sc, w->embed + (size_t)tok * d, NULL, h, NULL, 0, &cv);
             if (iters) iters[t] = it;
+            if (converged) converged[t] = cv;
             if (pooled || logits || argmax) {
                 float *lt = logits ? logits + (size_t)V * t : lg;
                 lm_head_tok(c, w, lm_wt, h, pooled ? pooled + (size_t)d * t : NULL,
@@ -768,10 +779,10 @@ void orc_model_forward(orc_model *mdl, int B, int T, const int32_t *tokens, floa
 }
 
 void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
-                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
-                 float *scan_y, float *scan_state, int nthreads) {
+                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *converged,
+                 int32_t *argmax, float *scan_y, float *scan_state, int nthreads) {
     orc_model *m = orc_model_create(c, w);
-    orc_model_forward(m, B, T, tokens, h_star, pooled, logits, iters, argmax, scan_y, scan_state,
+    orc_model_forward(m, B, T, tokens, h_star, pooled, logits, iters, converged, argmax, scan_y, scan_state,
                       nthreads);
     orc_model_free(m);
 }
@@ -862,7 +873,8 @@ void orc_temporal_step(const orc_cfg *c, const orc_weights *w, const float *m_pr
  * every m_t; pooled/logits/argmax as in the canonical forward. */
 void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B,
                         int T, const int32_t *tokens, const float *m_in, float *h_star, float *pooled,
-                        float *logits, int32_t *iters, int32_t *argmax, float *m_seq, int nthreads) {
+                        float *logits, int32_t *iters, int32_t *converged, int32_t *argmax, float *m_seq,
+                        int nthreads) {
     const int d = c->d, H = c->H, V = c->V;
     const size_t hd = (size_t)H * d;
     prep p;
@@ -900,8 +912,10 @@ void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_w
                 /* token carry: h still holds h*_{t-1} of this sequence (UWGSL:898
                  * should_init_h = t == 0 || !ENABLE_TOKEN_CARRY) */
                 const int warm = (c->flags & ORC_F_TOKEN_CARRY) && t > 0;
-                const int it = solve_p(&p, &sc, x, hist, h, NULL, warm);
+                int cv = 0;
+                const int it = solve_p(&p, &sc, x, hist, h, NULL, warm, &cv);
                 if (iters) iters[row] = it;
+                if (converged) converged[row] = cv;
                 if (h_star) memcpy(h_star + hd * row, h, sizeof(float) * hd);
                 orc_temporal_step(c, w, have_m ? m : NULL, h, mn);
                 memcpy(m, mn, sizeof(float) * hd);
@@ -921,20 +935,127 @@ void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_w
     prep_free(&p);
 }
 
-/* Greedy decode (TRAINER:4219-4431 loop with LmHead::sample at temperature <= 1e-4 =
- * argmax, lm_head.rs:104-112): the next query is the embedding of the last token. */
-void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int32_t *start,
-                       int n_new, int32_t *out_tokens, int nthreads) {
-    int32_t *cur = (int32_t *)malloc(sizeof(int32_t) * B);
-    int32_t *nxt = (int32_t *)malloc(sizeof(int32_t) * B);
-    memcpy(cur, start, sizeof(int32_t) * B);
-    for (int j = 0; j < n_new; ++j) {
-        orc_forward(c, w, B, 1, cur, NULL, NULL, NULL, NULL, nxt, NULL, NULL, nthreads);
-        for (int b = 0; b < B; ++b) out_tokens[(size_t)b * n_new + j] = nxt[b];
-        memcpy(cur, nxt, sizeof(int32_t) * B);
+/* tokenizer.rs:133-149 embed_context over one window ctx[0..len) (len <= max_ctx, so the whole
+ * window is used): result += emb * pos_weight in window order, pos_weight = (pos + 1) as f32 /
+ * len as f32 (f32 division), then result / result.norm() when the norm exceeds 1e-6.  The norm's
+ * summation order (nalgebra) is restated as a sequential sum of squares: ulp-level, unpinned. */
+static void embed_window(int d, const float *embed, const int32_t *ctx, int len, float *r, float *out) {
+    for (int j = 0; j < d; ++j) r[j] = 0.0f;
+    for (int pos = 0; pos < len; ++pos) {
+        const float w = (float)(pos + 1) / (float)len;
+        const float *e = embed + (size_t)ctx[pos] * d;
+        for (int j = 0; j < d; ++j) {
+            const float t = e[j] * w;
+            r[j] = r[j] + t;
+        }
     }
-    free(cur);
-    free(nxt);
+    float ss = 0.0f;
+    for (int j = 0; j < d; ++j) ss += r[j] * r[j];
+    const float nrm = sqrtf(ss);
+    for (int j = 0; j < d; ++j) out[j] = nrm > 1e-6f ? r[j] / nrm : r[j];
+}
+
+/* LmHead::sample's repetition penalty (lm_head.rs:81-99): every distinct token of the context has
+ * its logit multiplied by the penalty when negative, divided by it otherwise; nothing happens when
+ * |penalty - 1| <= 1e-4 or the context is empty.  Greedy sampling (temperature <= 1e-4) then takes
+ * the arg-max of the penalised logits (lm_head.rs:101-112). */
+static void repetition_penalty(float *logits, int V, const int32_t *ctx, int len, float pen) {
+    if (!(fabsf(pen - 1.0f) > 1e-4f) || len == 0) return;
+    for (int p = 0; p < len; ++p) {
+        const int tok = ctx[p];
+        int seen = 0;
+        for (int q = 0; q < p && !seen; ++q) seen = ctx[q] == tok;
+        if (seen || tok < 0 || tok >= V) continue;
+        const float sc = logits[tok];
+        logits[tok] = sc < 0.0f ? sc * pen : sc / pen;
+    }
+}
+
+/* Greedy decode as Trainer::generate (TRAINER:4219-4431) with LmHead::sample at temperature
+ * <= 1e-4.  prompt [B][T0] (T0 >= 1), out_tokens [B][n_new].  At step j of sequence b the context
+ * is the last ctx_len of its T0 + j tokens (TRAINER:4248-4249), and
+ *   - canonical (TRAINER:4388-4392, 4402-4406): query = embed_context(context, ctx_len), h = the
+ *     solve from init(query) under c's iteration cap and exit rule (generate itself runs exactly 10
+ *     steps: max_iters = 10, eps = 0);
+ *   - ORC_F_MEMORY, the fixed-history reference mode (TRAINER:4395-4400 with 677-735): the memory is
+ *     first primed over every prompt token (prime_fixed_history_state, :718-733), then each step
+ *     solves query = embed(last context token) with hist = fixed_hist_ctx(m, signal) and advances
+ *     m = temporal_step(m, h*) (each solve from the init rule, as solve_query_with_fixed_history);
+ * then logits = LmHead::forward(h) (lm_head.rs:50-54), the repetition penalty over the context,
+ * and the arg-max with the last-max tie rule; the token is appended. */
+void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
+                       const int32_t *prompt, int n_new, int ctx_len, float rep_penalty,
+                       int32_t *out_tokens, int nthreads) {
+    const int d = c->d, H = c->H, V = c->V;
+    const size_t hd = (size_t)H * d;
+    const int memory = (c->flags & ORC_F_MEMORY) != 0;
+    prep p;
+    prep_init(&p, c, w);
+    float *lm_wt = (float *)malloc(sizeof(float) * (size_t)V * d);
+    transpose(w->lm_w, V, d, lm_wt);
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        scratch sc;
+        scratch_init(&sc, c);
+        int32_t *toks = (int32_t *)malloc(sizeof(int32_t) * (size_t)(T0 + n_new));
+        float *q = (float *)malloc(sizeof(float) * d);
+        float *r = (float *)malloc(sizeof(float) * d);
+        float *tmp = (float *)malloc(sizeof(float) * d);
+        float *h = (float *)malloc(sizeof(float) * hd);
+        float *sig = (float *)malloc(sizeof(float) * hd);
+        float *hist = (float *)malloc(sizeof(float) * hd);
+        float *m = (float *)malloc(sizeof(float) * hd);
+        float *mn = (float *)malloc(sizeof(float) * hd);
+        float *lg = (float *)malloc(sizeof(float) * V);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int b = 0; b < B; ++b) {
+            memcpy(toks, prompt + (size_t)b * T0, sizeof(int32_t) * T0);
+            int have_m = 0;
+            if (memory) {
+                for (int t = 0; t < T0; ++t) {
+                    const float *x = w->embed + (size_t)toks[t] * d;
+                    signal_p(&p, x, sig);
+                    orc_hist_ctx(c, hw, have_m ? m : NULL, sig, hist);
+                    solve_p(&p, &sc, x, hist, h, NULL, 0, NULL);
+                    orc_temporal_step(c, w, have_m ? m : NULL, h, mn);
+                    memcpy(m, mn, sizeof(float) * hd);
+                    have_m = 1;
+                }
+            }
+            for (int j = 0; j < n_new; ++j) {
+                const int len = T0 + j;
+                const int start = len > ctx_len ? len - ctx_len : 0;
+                const int32_t *ctx = toks + start;
+                const int L = len - start;
+                if (memory) {
+                    const float *x = w->embed + (size_t)ctx[L - 1] * d;
+                    signal_p(&p, x, sig);
+                    orc_hist_ctx(c, hw, have_m ? m : NULL, sig, hist);
+                    solve_p(&p, &sc, x, hist, h, NULL, 0, NULL);
+                    orc_temporal_step(c, w, have_m ? m : NULL, h, mn);
+                    memcpy(m, mn, sizeof(float) * hd);
+                    have_m = 1;
+                } else {
+                    embed_window(d, w->embed, ctx, L, r, q);
+                    solve_p(&p, &sc, q, NULL, h, NULL, 0, NULL);
+                }
+                lm_head_tok(c, w, lm_wt, h, NULL, lg, tmp);
+                repetition_penalty(lg, V, ctx, L, rep_penalty);
+                const int32_t tok = orc_argmax(lg, V);
+                toks[len] = tok;
+                out_tokens[(size_t)b * n_new + j] = tok;
+            }
+        }
+        free(toks); free(q); free(r); free(tmp); free(h); free(sig); free(hist); free(m); free(mn); free(lg);
+        scratch_free(&sc);
+    }
+    free(lm_wt);
+    prep_free(&p);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -1061,21 +1182,7 @@ void orc_embed_context(int d, const float *embed, int B, int T, const int32_t *t
     for (int b = 0; b < B; ++b) {
         for (int i = 0; i < T; ++i) {
             const int start = i + 1 > ctx ? i + 1 - ctx : 0;
-            const int len = i + 1 - start;
-            for (int j = 0; j < d; ++j) r[j] = 0.0f;
-            for (int pos = 0; pos < len; ++pos) {
-                const float w = (float)(pos + 1) / (float)len;
-                const float *e = embed + (size_t)tokens[(size_t)b * T + start + pos] * d;
-                for (int j = 0; j < d; ++j) {
-                    const float t = e[j] * w;
-                    r[j] = r[j] + t;
-                }
-            }
-            float ss = 0.0f;
-            for (int j = 0; j < d; ++j) ss += r[j] * r[j];
-            const float nrm = sqrtf(ss);
-            float *o = out + ((size_t)b * T + i) * d;
-            for (int j = 0; j < d; ++j) o[j] = nrm > 1e-6f ? r[j] / nrm : r[j];
+            embed_window(d, embed, tokens + (size_t)b * T + start, i + 1 - start, r, out + ((size_t)b * T + i) * d);
         }
     }
     free(r);

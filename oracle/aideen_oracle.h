@@ -97,22 +97,28 @@ void orc_temporal_step(const orc_cfg *c, const orc_weights *w, const float *m_pr
                        const float *h_star, float *m_next);
 void orc_forward_memory(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B,
                         int T, const int32_t *tokens, const float *m_in /* [B][H][d] or NULL */,
-                        float *h_star, float *pooled, float *logits, int32_t *iters,
+                        float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *converged,
                         int32_t *argmax, float *m_seq /* [B][T][H][d] */, int nthreads);
 
 /* --- whole forward and decode ----------------------------------------------- */
+/* converged [B][T] (or NULL): 1 = exit on the tolerance or plateau, 0 = stopped at max_iters
+ * (a non-finite residual counts as infinite, so a NaN state never converges). */
 void orc_forward(const orc_cfg *c, const orc_weights *w, int B, int T, const int32_t *tokens,
-                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *argmax,
-                 float *scan_y, float *scan_state, int nthreads);
+                 float *h_star, float *pooled, float *logits, int32_t *iters, int32_t *converged,
+                 int32_t *argmax, float *scan_y, float *scan_state, int nthreads);
 /* The same forward on a model prepared once (weights transposed for the CPU loops). */
 typedef struct orc_model orc_model;
 orc_model *orc_model_create(const orc_cfg *c, const orc_weights *w);
 void orc_model_forward(orc_model *m, int B, int T, const int32_t *tokens, float *h_star,
-                       float *pooled, float *logits, int32_t *iters, int32_t *argmax,
-                       float *scan_y, float *scan_state, int nthreads);
+                       float *pooled, float *logits, int32_t *iters, int32_t *converged,
+                       int32_t *argmax, float *scan_y, float *scan_state, int nthreads);
 void orc_model_free(orc_model *m);
-void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, int B, const int32_t *start,
-                       int n_new, int32_t *out_tokens, int nthreads);
+/* Trainer::generate's greedy loop (TRAINER:4219-4431): prompt [B][T0], out_tokens [B][n_new];
+ * canonical queries are embed_context over the last ctx_len tokens, ORC_F_MEMORY runs the
+ * fixed-history form (hw needed); rep_penalty as LmHead::sample (1 = none). */
+void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
+                       const int32_t *prompt, int n_new, int ctx_len, float rep_penalty,
+                       int32_t *out_tokens, int nthreads);
 
 /* --- other trait surfaces --------------------------------------------------- */
 /* Clean adjoint Picard (staged_adjoint_picard_clean.wgsl:143-337; driver gpu_deq.rs:4736-4975):

@@ -73,18 +73,18 @@ def lib():
         L.orc_scan_seq.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, F32P, F32P, F32P, F32P]
         L.orc_scan_recirculate.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, F32P, F32P, F32P]
         L.orc_forward.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, C.c_int, I32P,
-                                  F32P, F32P, F32P, I32P, I32P, F32P, F32P, C.c_int]
+                                  F32P, F32P, F32P, I32P, I32P, I32P, F32P, F32P, C.c_int]
         L.orc_model_create.restype = C.c_void_p
         L.orc_model_create.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights)]
         L.orc_model_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, I32P, F32P, F32P, F32P, I32P,
-                                        I32P, F32P, F32P, C.c_int]
+                                        I32P, I32P, F32P, F32P, C.c_int]
         L.orc_model_free.argtypes = [C.c_void_p]
-        L.orc_decode_greedy.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.c_int, I32P,
-                                        C.c_int, I32P, C.c_int]
+        L.orc_decode_greedy.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcHistWeights),
+                                        C.c_int, C.c_int, I32P, C.c_int, C.c_int, C.c_float, I32P, C.c_int]
         L.orc_hist_ctx.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcHistWeights), F32P, F32P, F32P]
         L.orc_temporal_step.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
         L.orc_forward_memory.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcHistWeights),
-                                         C.c_int, C.c_int, I32P, F32P, F32P, F32P, F32P, I32P, I32P,
+                                         C.c_int, C.c_int, I32P, F32P, F32P, F32P, F32P, I32P, I32P, I32P,
                                          F32P, C.c_int]
         L.orc_zoh_step.argtypes = [C.c_int, F32P, F32P, F32P, F32P, F32P, F32P]
         L.orc_embed_context.argtypes = [C.c_int, F32P, C.c_int, C.c_int, I32P, C.c_int, F32P]
@@ -209,12 +209,13 @@ class Oracle:
         out = dict(h_star=np.zeros((B, T, mc.H, mc.d), np.float32),
                    pooled=np.zeros((B, T, mc.d), np.float32),
                    logits=np.zeros((B, T, mc.V), np.float32),
-                   iters=np.zeros((B, T), np.int32), argmax=np.zeros((B, T), np.int32),
-                   m_seq=np.zeros((B, T, mc.H, mc.d), np.float32))
+                   iters=np.zeros((B, T), np.int32), converged=np.zeros((B, T), np.int32),
+                   argmax=np.zeros((B, T), np.int32), m_seq=np.zeros((B, T, mc.H, mc.d), np.float32))
         self.L.orc_forward_memory(C.byref(self.c), C.byref(self.w), C.byref(self.hw), B, T, ip(tokens),
                                   fp(None if m_in is None else np.ascontiguousarray(m_in, np.float32)),
                                   fp(out["h_star"]), fp(out["pooled"]), fp(out["logits"]),
-                                  ip(out["iters"]), ip(out["argmax"]), fp(out["m_seq"]), nthreads)
+                                  ip(out["iters"]), ip(out["converged"]), ip(out["argmax"]), fp(out["m_seq"]),
+                                  nthreads)
         return out
 
     # --- whole forward ------------------------------------------------------
@@ -226,6 +227,7 @@ class Oracle:
             h_star=np.zeros((B, T, mc.H, mc.d), np.float32),
             pooled=np.zeros((B, T, mc.d), np.float32),
             iters=np.zeros((B, T), np.int32),
+            converged=np.zeros((B, T), np.int32),
             argmax=np.zeros((B, T), np.int32),
         )
         if want_logits:
@@ -235,7 +237,7 @@ class Oracle:
             out["scan_state"] = np.zeros((B, mc.H, mc.d, mc.N), np.float32)
         self.L.orc_forward(C.byref(self.c), C.byref(self.w), B, T, ip(tokens),
                            fp(out["h_star"]), fp(out["pooled"]), fp(out.get("logits")),
-                           ip(out["iters"]), ip(out["argmax"]), fp(out.get("scan_y")),
+                           ip(out["iters"]), ip(out["converged"]), ip(out["argmax"]), fp(out.get("scan_y")),
                            fp(out.get("scan_state")), nthreads)
         return out
 
@@ -243,11 +245,14 @@ class Oracle:
         """A model handle with the CPU-side weight layout done once (for timing)."""
         return _Prepared(self)
 
-    def decode_greedy(self, start, n_new, nthreads=0):
-        start = np.ascontiguousarray(start, dtype=np.int32)
-        out = np.zeros((start.shape[0], n_new), np.int32)
-        self.L.orc_decode_greedy(C.byref(self.c), C.byref(self.w), start.shape[0], ip(start),
-                                 n_new, ip(out), nthreads)
+    def decode_greedy(self, prompt, n_new, ctx_len, rep_penalty=1.0, nthreads=0):
+        """Trainer::generate's greedy loop: prompt [B][T0] -> the n_new appended tokens [B][n_new]
+        (the model config's max_iters / eps / beta drive each solve; generate uses 10, 0)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        B, T0 = prompt.shape
+        out = np.zeros((B, n_new), np.int32)
+        self.L.orc_decode_greedy(C.byref(self.c), C.byref(self.w), C.byref(self.hw), B, T0, ip(prompt),
+                                 n_new, ctx_len, rep_penalty, ip(out), nthreads)
         return out
 
 
@@ -269,7 +274,7 @@ class _Prepared:
             out["scan_y"] = np.zeros((B, T, mc.H, mc.d), np.float32)
             out["scan_state"] = np.zeros((B, mc.H, mc.d, mc.N), np.float32)
         o.L.orc_model_forward(self.h, B, T, ip(tokens), fp(out["h_star"]), None, fp(out.get("logits")),
-                              ip(out["iters"]), ip(out["argmax"]), fp(out.get("scan_y")),
+                              ip(out["iters"]), None, ip(out["argmax"]), fp(out.get("scan_y")),
                               fp(out.get("scan_state")), nthreads)
         return out
 

@@ -14,7 +14,7 @@ def test_library_loads_and_exports_every_header_symbol():
     assert len(names) >= 15
     for n in names:
         assert hasattr(L, n), f"{n} declared in include/aideen_hip.h but not exported"
-    assert L.adn_abi_version() == 2
+    assert L.adn_abi_version() == 3
 
 
 def test_header_flag_values_match_oracle_and_synth():

@@ -144,8 +144,26 @@ def test_memory_errors():
     with pytest.raises(AdnError, match="w_hist"):
         be.upload_weights(w_missing)
     be.upload_weights(w)
-    with pytest.raises(AdnError, match="ADN_F_MEMORY"):
-        be.decode_greedy(np.array([1, 2], np.int32), 3)
+    mcc, wc = mem_model(64, 2, 100, flags=synth.F_TOKEN_CARRY)
+    bc = GpuDeqBackend(mcc, 2, 4)
+    bc.upload_weights(wc)
+    with pytest.raises(AdnError, match="TOKEN_CARRY"):
+        bc.decode_greedy(np.array([[1, 2], [3, 4]], np.int32), 3, 4)
+
+
+@pytest.mark.parametrize("pen", [1.0, 1.5])
+def test_memory_greedy_decode_matches_oracle(oracle_lib, pen):
+    """The fixed-history form of Trainer::generate (trainer.rs:4395-4400, 677-735): the memory is
+    primed over the prompt, then each step solves the last token with the memory's history
+    context (eps = 0: the reference's fixed max_iters) and advances the memory."""
+    log(f"memory decode pen={pen}")
+    mc, w = mem_model(128, 4, 400, max_iters=6, eps=0.0)
+    prompt = synth.make_tokens("uniform", 3, 7, mc.V, seed=14)
+    ref = oracle_lib.Oracle(mc, w).decode_greedy(prompt, 9, 5, pen)
+    be = GpuDeqBackend(mc, 3, 7)
+    be.upload_weights(w)
+    got = be.decode_greedy(prompt, 9, 5, max_iters=6, eps=0.0, repetition_penalty=pen)
+    assert np.array_equal(got, ref)
 
 
 def test_memory_profile_counts():

@@ -521,8 +521,134 @@ def test_forward_is_per_token_solve_plus_head(oracle_lib):
             assert out["argmax"][b, t] == oracle_lib.argmax(logits)
         y, st = o.scan(out["h_star"][b])
         assert np.array_equal(y, out["scan_y"][b]) and np.array_equal(st, out["scan_state"][b])
-    dec = o.decode_greedy(toks[:, 0], 3)
-    assert dec[0, 0] == out["argmax"][0, 0]
+    assert out["converged"].all()
+
+
+# ------------------------------------------------------------------------------------------
+# greedy decode: Trainer::generate (TRAINER:4219-4431), LmHead::sample (lm_head.rs:72-112)
+# ------------------------------------------------------------------------------------------
+def _penalise(logits, ctx, pen):
+    """lm_head.rs:81-99, written out independently: each distinct context token once."""
+    lg = logits.copy()
+    if abs(pen - 1.0) > 1e-4 and len(ctx):
+        for tok in sorted(set(int(t) for t in ctx)):
+            sc = lg[tok]
+            lg[tok] = np.float32(sc * np.float32(pen)) if sc < 0 else np.float32(sc / np.float32(pen))
+    return lg
+
+
+def _last_max(lg):
+    return int(np.flatnonzero(lg == lg.max())[-1])
+
+
+@pytest.mark.parametrize("pen", [1.0, 1.3])
+def test_decode_greedy_follows_generate(oracle_lib, pen):
+    """Every step rebuilt from the separately pinned pieces: the query is embed_context of the last
+    ctx_len tokens so far (prompt, then the generated ones), the solve runs generate's fixed 10
+    steps, then the LM head, the repetition penalty over that context and the last-max arg-max.
+    The window slides (ctx_len < prompt + new), and B = 3 by n_new = 7 pins the output layout."""
+    # a weak anchor and a strong input projection, so that the prompts decode differently
+    mc, w = small_model(d=32, H=4, V=70, N=1, max_iters=10, eps=0.0, win_sigma=3.0)
+    w = dict(w)
+    w["anchor"] = (w["anchor"] * np.float32(0.02)).astype(np.float32)
+    o = oracle(oracle_lib, mc, w)
+    B, T0, n_new, ctx = 3, 5, 7, 6
+    prompt = synth.make_tokens("uniform", B, T0, mc.V, seed=21)
+    dec = o.decode_greedy(prompt, n_new, ctx, pen)
+    assert dec.shape == (B, n_new) and len({tuple(r) for r in dec}) == B
+    for b in range(B):
+        toks = list(prompt[b])
+        for j in range(n_new):
+            window = np.array(toks[-ctx:], np.int32)
+            q = oracle_lib.embed_context(w["embed"], window[None], ctx)[0, -1]
+            h, it, _ = o.solve(q)
+            assert it == 10
+            _, logits = o.lm_head(h)
+            tok = _last_max(_penalise(logits, window, pen))
+            assert dec[b, j] == tok, (b, j)
+            toks.append(tok)
+    if pen == 1.0:  # the first step equals the canonical forward of the query of the prompt's end
+        w2 = dict(w)
+        w2["embed"] = oracle_lib.embed_context(w["embed"], prompt, ctx)[:, -1].copy()
+        first = o.__class__(mc, w2).forward(np.arange(B, dtype=np.int32)[:, None], want_scan=False)
+        assert np.array_equal(first["argmax"][:, 0], dec[:, 0])
+
+
+def test_decode_greedy_penalty_changes_the_choice(oracle_lib):
+    """A large penalty forbids repeating a context token: with pen = 1e4 every positive logit of a
+    context token is divided away, so no step picks a token of its window while a positive logit
+    outside it exists."""
+    mc, w = small_model(d=32, H=4, V=70, N=1, max_iters=10, eps=0.0)
+    o = oracle(oracle_lib, mc, w)
+    prompt = synth.make_tokens("uniform", 2, 4, mc.V, seed=22)
+    plain = o.decode_greedy(prompt, 6, 5, 1.0)
+    pen = o.decode_greedy(prompt, 6, 5, 1e4)
+    assert not np.array_equal(plain, pen)
+    for b in range(2):
+        toks = list(prompt[b]) + list(pen[b])
+        for j in range(6):
+            assert toks[4 + j] not in toks[max(0, 4 + j - 5):4 + j]
+
+
+def test_decode_greedy_fixed_history_follows_generate(oracle_lib):
+    """ORC_F_MEMORY: the memory primed over the whole prompt, then each step solves the last token
+    with that memory and advances it -- rebuilt from the pinned memory-coupled forward."""
+    mc, w = _mem_model(d=16, H=3, V=40, flags=F.F_MEMORY, max_iters=6, eps=0.0)
+    o = oracle(oracle_lib, mc, w)
+    B, T0, n_new, ctx = 2, 4, 5, 3
+    prompt = synth.make_tokens("uniform", B, T0, mc.V, seed=23)
+    for pen in (1.0, 1.5):
+        dec = o.decode_greedy(prompt, n_new, ctx, pen)
+        primed = o.forward_memory(prompt)
+        for b in range(B):
+            toks = list(prompt[b])
+            m = primed["m_seq"][b, -1]
+            for j in range(n_new):
+                step = o.forward_memory(np.array([[toks[-1]]], np.int32), m_in=m[None])
+                m = step["m_seq"][0, 0]
+                tok = _last_max(_penalise(step["logits"][0, 0], np.array(toks[-ctx:]), pen))
+                assert dec[b, j] == tok, (pen, b, j)
+                toks.append(tok)
+
+
+# ------------------------------------------------------------------------------------------
+# failure detection: non-finite states never pass the exit test (UWGSL:99-108 finite_or)
+# ------------------------------------------------------------------------------------------
+def test_nonfinite_state_runs_to_the_cap_unconverged(oracle_lib):
+    """A NaN (or inf) input row makes the state non-finite: every residual mode must report the
+    token unconverged at max_iters (fmaxf would drop the NaN and stop after one update), while
+    the finite tokens of the same batch are unaffected."""
+    for flags in (0, F.F_RESID_L2, F.F_RESID_RELRMS, F.F_RESID_RELRMS | F.F_HOMEOSTATIC_EXIT):
+        mc, w = small_model(d=32, H=3, V=20, N=1, flags=flags, max_iters=12)
+        w = dict(w)
+        emb = w["embed"].copy()
+        emb[3, 5] = np.nan
+        emb[4, :] = np.inf
+        w["embed"] = emb
+        o = oracle(oracle_lib, mc, w)
+        out = o.forward(np.array([[1, 3, 2, 4]], np.int32), want_scan=False)
+        assert out["iters"][0, 1] == 12 and out["iters"][0, 3] == 12, flags
+        assert list(out["converged"][0]) == [1, 0, 1, 0], flags
+        assert out["iters"][0, 0] < 12 and out["iters"][0, 2] < 12
+        assert np.isfinite(out["h_star"][0, [0, 2]]).all()
+        ref = oracle(oracle_lib, mc, small_model(d=32, H=3, V=20, N=1, flags=flags, max_iters=12)[1]).forward(
+            np.array([[1, 2]], np.int32), want_scan=False)
+        assert np.array_equal(ref["h_star"][0], out["h_star"][0, [0, 2]])
+
+
+def test_noncontractive_weights_report_nonconvergence(oracle_lib):
+    """sigma = 2 block matrices (non-contractive): the solve no longer settles within the cap,
+    and such tokens say so (converged = 0, iters = max_iters); the state stays bounded, as the
+    reference's step_is_stable_no_explosion asserts (FPMR:1519-1531: energy < 1e6)."""
+    mc, w = small_model(d=32, H=4, V=50, N=1, sigma=2.0, max_iters=15)
+    o = oracle(oracle_lib, mc, w)
+    toks = synth.make_tokens("uniform", 2, 20, mc.V, seed=31)
+    out = o.forward(toks, want_scan=False)
+    nc = out["converged"] == 0
+    assert nc.sum() >= 20
+    assert (out["iters"][nc] == 15).all()
+    assert (out["converged"][out["iters"] < 15] == 1).all()  # an early exit is a converged one
+    assert float((out["h_star"].astype(np.float64) ** 2).sum(axis=(2, 3)).max()) < 1e6
 
 
 # ------------------------------------------------------------------------------------------
