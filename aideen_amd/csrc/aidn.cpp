@@ -19,7 +19,10 @@
 // shared-weight model), the embedding is transposed to [V][d], and the carrier takes W_x's
 // diagonal (temporal_step, fixed_point_memory_reasoning.rs:1471-1475).
 #include <algorithm>
+#include <cerrno>
+#include <climits>
 #include <cstdio>
+#include <memory>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -114,7 +117,27 @@ int fail_invalid(const std::string &msg) {
 
 extern "C" {
 
+static int aidn_open(const char *path, adn_aidn **out);
+static int aidn_weights(adn_aidn *m, adn_weights *w, adn_config *cfg, adn_run *run);
+
+// No C++ exception (an allocation failure on a corrupt file's sizes) crosses the C ABI.
 int adn_aidn_open(const char *path, adn_aidn **out) {
+    try {
+        return aidn_open(path, out);
+    } catch (const std::exception &e) {
+        return fail_invalid(std::string("cannot load .aidn file: ") + e.what());
+    }
+}
+
+int adn_aidn_weights(adn_aidn *m, adn_weights *w, adn_config *cfg, adn_run *run) {
+    try {
+        return aidn_weights(m, w, cfg, run);
+    } catch (const std::exception &e) {
+        return fail_invalid(std::string("cannot map .aidn weights: ") + e.what());
+    }
+}
+
+static int aidn_open(const char *path, adn_aidn **out) {
     if (!path || !out) return fail_invalid("null argument");
     *out = nullptr;
     FILE *f = fopen(path, "rb");
@@ -123,7 +146,14 @@ int adn_aidn_open(const char *path, adn_aidn **out) {
     const long long size = ftell(f);
     fseek(f, 0, SEEK_SET);
     Reader r{f, size, {}};
-    adn_aidn *m = new adn_aidn();
+    struct Closer {  // the file is closed on every path, an exception's included
+        FILE *&f;
+        ~Closer() {
+            if (f) fclose(f);
+        }
+    } closer{f};
+    std::unique_ptr<adn_aidn> owner(new adn_aidn());
+    adn_aidn *m = owner.get();
     adn_aidn_config &c = m->cfg;
     r.usize(c.d_m) && r.usize(c.d_r) && r.usize(c.d_c) && r.usize(c.d_e) && r.usize(c.d_sim) &&
         r.usize(c.h_slots) && r.usize(c.vocab_size) && r.usize(c.ctx_len) && r.usize(c.max_deq_iters) &&
@@ -148,16 +178,9 @@ int adn_aidn_open(const char *path, adn_aidn **out) {
             m->meta[k] = v;
         }
     }
-    fclose(f);
-    if (!r.err.empty()) {
-        delete m;
-        return fail_invalid(r.err + " (" + path + ")");
-    }
-    if (r.left != 0) {
-        delete m;
-        return fail_invalid(std::string("trailing bytes after the model (") + path + ")");
-    }
-    *out = m;
+    if (!r.err.empty()) return fail_invalid(r.err + " (" + path + ")");
+    if (r.left != 0) return fail_invalid(std::string("trailing bytes after the model (") + path + ")");
+    *out = owner.release();
     return ADN_OK;
 }
 
@@ -198,14 +221,25 @@ int adn_aidn_metadata(const adn_aidn *m, const char *key, const char **value) {
     return ADN_OK;
 }
 
-int adn_aidn_weights(adn_aidn *m, adn_weights *w, adn_config *cfg, adn_run *run) {
+static int aidn_weights(adn_aidn *m, adn_weights *w, adn_config *cfg, adn_run *run) {
     if (!m || !w) return fail_invalid("null argument");
     const int64_t d = m->cfg.d_r, H = m->cfg.h_slots;
     int64_t V = m->cfg.vocab_size;
     auto mv = m->meta.find("vocab_size");  // the trainer sizes the tokenizer from the metadata
-    if (mv != m->meta.end()) V = std::atoll(mv->second.c_str());
+    if (mv != m->meta.end()) {
+        const char *txt = mv->second.c_str();
+        char *end = nullptr;
+        errno = 0;
+        const long long v = std::strtoll(txt, &end, 10);
+        if (errno || end == txt || *end != '\0') return fail_invalid("metadata vocab_size is not an integer");
+        V = v;
+    }
     constexpr int64_t R = 32;  // RETAIN_RANK (fixed_point_memory_reasoning.rs:291)
-    if (d < 1 || H < 1 || V < 1) return fail_invalid("model config has no d_r / h_slots / vocab_size");
+    // Bounds before any size product: with these, every tensor size below fits comfortably in
+    // 64 bits (V * d < 2^42) and the int32 fields of adn_config cannot truncate.
+    if (d < 1 || d > 2048) return fail_invalid("model d_r outside [1, 2048]");
+    if (H < 1 || H > 16) return fail_invalid("model h_slots outside [1, 16]");
+    if (V < 1 || V > INT32_MAX) return fail_invalid("model vocab_size outside [1, 2^31)");
     std::string err;
     auto get = [&](const char *name, int64_t n, bool required) -> const std::vector<float> * {
         auto it = m->weights.find(name);
@@ -298,7 +332,7 @@ int adn_aidn_weights(adn_aidn *m, adn_weights *w, adn_config *cfg, adn_run *run)
         cfg->d_state = 1;
         cfg->rank = (int32_t)R;
         cfg->max_batch = 1;
-        cfg->max_seq = m->cfg.ctx_len > 0 ? (int32_t)m->cfg.ctx_len : 1;
+        cfg->max_seq = (int32_t)std::max<int64_t>(1, std::min<int64_t>(m->cfg.ctx_len, 1 << 24));
         cfg->anderson_m = 0;
         cfg->flags = 0;
     }
@@ -306,7 +340,7 @@ int adn_aidn_weights(adn_aidn *m, adn_weights *w, adn_config *cfg, adn_run *run)
         std::memset(run, 0, sizeof(*run));
         run->batch = 1;
         run->seq = 1;
-        run->max_iters = m->cfg.max_deq_iters > 0 ? (int32_t)m->cfg.max_deq_iters : 1;
+        run->max_iters = (int32_t)std::max<int64_t>(1, std::min<int64_t>(m->cfg.max_deq_iters, 256));
         run->eps = m->cfg.deq_epsilon;
         run->damping = damp ? (*damp)[0] : 0.70f;  // FixedPointMemoryReasoning's default (:458)
     }

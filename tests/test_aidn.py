@@ -146,3 +146,24 @@ def test_metadata_vocab_size_wins(tmp_path):
     aidn.write_aidn(p, cfg, ex, meta)
     got, acfg, _ = aidn.AidnModel(p).weights()
     assert acfg["vocab"] == 120 and got["embed"].shape == (120, 64)
+
+
+@pytest.mark.parametrize("config,meta,match", [
+    (dict(d_r=64, h_slots=(1 << 58) + 1), {}, "h_slots"),      # H*d would wrap to 64 without bounds
+    (dict(d_r=4096, h_slots=1), {}, "d_r"),
+    (dict(d_r=64, h_slots=2, vocab_size=1 << 40), {}, "vocab_size"),
+    (dict(d_r=64, h_slots=2, vocab_size=10), {"vocab_size": "12x"}, "vocab_size"),
+    (dict(d_r=64, h_slots=2, vocab_size=10), {"vocab_size": "99999999999999999999"}, "vocab_size"),
+])
+def test_crafted_header_sizes_are_rejected(tmp_path, config, meta, match):
+    """Sizes from an untrusted header are bounded before any product of them is formed, so a tiny
+    file cannot pass the size checks through a wrapped product (an overflow of the per-slot
+    copies), and a malformed metadata vocabulary is refused."""
+    p = str(tmp_path / "crafted.aidn")
+    d = 64
+    w = {"reasoning.w_q": np.zeros(d * d, np.float32), "reasoning.slot_anchor": np.zeros(2 * d, np.float32)}
+    aidn.write_aidn(p, config, w, meta)
+    m = aidn.AidnModel(p)
+    with pytest.raises(AdnError, match=match):
+        m.weights()
+    m.close()
