@@ -122,19 +122,18 @@ struct ScanBuffers {
     float *y;          // [ntok][H][d] pre-readout output (or final if no W_out)
     float *chunk_s;    // [B][nch][H][d][N]
     float *chunk_p;    // [B][nch][H][d]
-    float *gate_a;     // [ntok][H][d] per-element decay abar
-    float *gate_x;     // [ntok][H][d] per-element input (1 - abar) x
+    float *mem_mn;     // [max_batch][H][d] memory mode: the state before W_out
+    float *mem_hist;   // [max_batch][H][d] memory mode: the history context
 };
 int scan_rec_len(const Dims &D);
 // rec[row*REC] = sqrt(mean(h_row^2) + 1e-6) for every (token, slot) row
 void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipStream_t st);
-// abar and (1-abar) x for every (token, slot, channel)
-void launch_scan_gate(const Dims &D, const float *h, const float *rec, int ntok, const float *a_log,
-                      const float *wx_diag, const float *b_delta, const float *w_vw, float *gate_a, float *gate_x,
-                      hipStream_t st);
-void launch_scan(const Dims &D, const float *gate_a, const float *gate_x, const float *rec, int B, int T,
-                 int has_bc, const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p,
-                 int nch, hipStream_t st);
+// The carrier over B sequences of T steps from h* [B][T][H][d] and the record: y [B][T][H][d],
+// state_out [B][H][d][N] (either may be null), state_in [B][H][d][N] or null; nch time chunks
+// (chunk_s / chunk_p hold B * nch chunks).
+void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
+                 const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
+                 float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st);
 int scan_chunks(int B, int T, int H, int d);
 
 // ---- misc (misc.hip) ----------------------------------------------------------------------

@@ -474,10 +474,8 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
         float *y = (o.scan_y && !c->w_out) ? o.scan_y : c->scb.y;
         {
             Span sp(prof, ADN_STAGE_SCAN, nch, st);
-            launch_scan_gate(D, b.h, c->scb.rec, ntok, c->a_log, c->wx_diag, c->b_delta, c->w_vw, c->scb.gate_a,
-                             c->scb.gate_x, st);
-            launch_scan(D, c->scb.gate_a, c->scb.gate_x, c->scb.rec, r.batch, r.seq, c->w_b != nullptr,
-                        r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch, st);
+            launch_scan(D, b.h, c->scb.rec, r.batch, r.seq, c->w_b != nullptr, c->a_log, c->wx_diag, c->b_delta,
+                        c->w_vw, r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch, st);
         }
         if (o.scan_y && c->w_out) {
             GemmParams g{};
@@ -540,8 +538,8 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
     c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
     float *mseq = o.scan_y ? o.scan_y : c->scb.y;  // [B][T][H][d]
-    float *hist = c->scb.gate_x;                     // [B][H][d]
-    float *mn = c->scb.gate_a;                       // [B][H][d] state before W_out
+    float *hist = c->scb.mem_hist;                   // [B][H][d]
+    float *mn = c->scb.mem_mn;                       // [B][H][d] state before W_out
     for (int t = 0; t < T; ++t) {
         {
             Span sp(prof, ADN_STAGE_CONVERGE, -1, st, B);
@@ -728,8 +726,10 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         c->am_idx = (int32_t *)dmalloc(c, (size_t)T * ntiles * sizeof(int32_t));
         c->scb.rec = (float *)dmalloc(c, (size_t)T * H * scan_rec_len(c->D) * sizeof(float));
         c->scb.y = (float *)dmalloc(c, hd);
-        c->scb.gate_a = (float *)dmalloc(c, hd);
-        c->scb.gate_x = (float *)dmalloc(c, hd);
+        if (cfg->flags & ADN_F_MEMORY) {
+            c->scb.mem_mn = (float *)dmalloc(c, (size_t)cfg->max_batch * H * d * sizeof(float));
+            c->scb.mem_hist = (float *)dmalloc(c, (size_t)cfg->max_batch * H * d * sizeof(float));
+        }
         c->scan_nch_cap = 16;
         const size_t chunk_states = (size_t)cfg->max_batch * c->scan_nch_cap * H * d;
         c->scb.chunk_s = (float *)dmalloc(c, chunk_states * cfg->d_state * sizeof(float));

@@ -9,16 +9,15 @@
 //   m_t[n] = abar m_{t-1}[n] + (1-abar) B_t[n] x,   y_t = sum_n C_t[n] m_t[n],
 //   Y_t = y_t + W_out y_t (readout GEMM, gemm.hip).
 //
-// Pipeline: k_row_rms (rms of every (token, slot) row) and one MFMA GEMM against the per-slot
+// Pipeline: the row RMS of every (token, slot) row (k_row_rms, or the pooling kernel from the same
+// loads) and one MFMA GEMM against the per-slot
 //   W_cat[s] = [W_kw[s]^T; W_B[s]; W_C[s]]  (r + 2N rows of length d)
 // fill the per-row record [rms, P_bn[0..r), P_B[0..N), P_C[0..N)] with un-normalised
-// projections P = W_cat h; the scan divides them by rms as it stages them.
-// k_scan_gate: the per-element decay and input (all transcendental and rank-r work), fully
-//   parallel over (token, slot, channel).
-// k_scan: one thread per (sequence, slot, channel) carries the N states in registers; per chunk
-//   of TC steps the B/C values are staged in LDS and the gate values prefetched into registers.
-//   Long sequences are split into time chunks: pass A (zero start) produces each chunk's end
-//   state and decay product, pass B carries the chunk starts, pass C re-runs every chunk.
+// projections P = W_cat h.  k_scan_fused then forms each element's decay and input from h* and
+// the record and carries the recurrence in the same pass: nothing per element is written but y.
+// Sequences too few to fill the GPU are split into time chunks: pass A (zero start) produces
+// each chunk's end state and decay product, k_scan_carry the chunk starts, and pass C re-runs
+// every chunk from its start.
 #include "kernels.h"
 
 namespace adn {
@@ -26,6 +25,9 @@ namespace adn {
 namespace {
 
 constexpr int WPB = 4;
+#ifndef SCAN_MIN_WGS
+#define SCAN_MIN_WGS 512
+#endif
 
 // E = d/64 values per lane, all loaded before the sum (in the same order as a strided loop)
 template <int E>
@@ -47,207 +49,214 @@ __global__ __launch_bounds__(256) void k_row_rms(const float *h, long rows, floa
 
 constexpr int SCAN_NT = 256;
 constexpr int TC = 16;
-constexpr int GATE_ROWS = 16;
 
-// Gate: for every (token, slot, channel) the decay abar and the carrier input (1-abar) x,
-// fully parallel (the rank-r bottleneck comes from the record; W_vw's column for the channel
-// is held in registers across GATE_ROWS tokens of one slot).  The block's GATE_ROWS records
-// (rms and the r projections) are staged in LDS, and a thread loads all of its h values before
-// its first store: a load issued after stores would be waited for behind them (the
-// vector-memory counter retires in issue order).
-template <int RK, bool SEL>
-__global__ __launch_bounds__(SCAN_NT) void k_scan_gate(Dims D, const float *__restrict__ h,
-                                                       const float *__restrict__ rec, int ntok,
-                                                       const float *__restrict__ a_log,
-                                                       const float *__restrict__ wx_diag,
-                                                       const float *__restrict__ b_delta,
-                                                       const float *__restrict__ w_vw,
-                                                       float *__restrict__ gate_a, float *__restrict__ gate_x) {
-    constexpr int RKA = RK > 0 ? RK : 1;
-    constexpr int RS = 4 + RKA;  // [0] rms, [4 + q] projection q (16-byte aligned for broadcast reads)
-    __shared__ __attribute__((aligned(16))) float srec[GATE_ROWS][RS];
+// Fused gate and recurrence over time, one thread per (sequence, slot, channel) with the N states
+// in registers.  Per step the thread forms the gate from h* and the row's record itself
+// (selective: u = h / rms, x = u + 0.5 tanh(w_x) u, pre = b + W_vw^T (W_kw^T u),
+// abar = 0.1 + 0.9 sigmoid(-a_log)^softplus(pre); otherwise abar = sigmoid(-a_log)), so no
+// per-element gate tensor is written or read back:
+//   m[n] = abar m[n] + B[n] ((1 - abar) x),   y = sum_n C[n] m[n].
+// softplus and the power use the hardware base-2 exponential and logarithm:
+//   sigmoid(-a_log)^softplus(pre) = 2^(log2(1 + 2^(pre log2 e)) ln(sigmoid(-a_log))).
+// MODE 0: whole sequence from state_in, emit y and state_out.
+// MODE 1: chunk pass A, zero start, emit the chunk's end state and decay product.
+// MODE 2: chunk pass C, start from chunk_s (carried), emit y; the last chunk writes state_out.
+// Per TC steps the record values a step needs (1/rms, and divided by rms the rank-r projections
+// and B/C) are staged in LDS; h and the next TC steps' record values are fetched into a second
+// register set before the current steps are processed (a load issued after stores would wait
+// behind them: the vector-memory counter retires in issue order).  RK: rank bucket (0 = not
+// selective); EXACT: NS == N.
+template <int NS, int RK, int MODE, bool EXACT>
+__global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__restrict__ h,
+                                                        const float *__restrict__ rec, int T, int nch, int has_bc,
+                                                        const float *__restrict__ a_log,
+                                                        const float *__restrict__ wx_diag,
+                                                        const float *__restrict__ b_delta,
+                                                        const float *__restrict__ w_vw,
+                                                        const float *__restrict__ state_in, float *__restrict__ y,
+                                                        float *__restrict__ state_out, float *__restrict__ chunk_s,
+                                                        float *__restrict__ chunk_p) {
+    constexpr bool SEL = RK > 0;
+    constexpr int RKA = SEL ? RK : 0;
+    constexpr int BC0 = 4 + RKA;         // staged step: [0] 1/rms, [4 + q] projection q / rms,
+    constexpr int SW = BC0 + 2 * NS;     // [BC0 + n] B[n] / rms, [BC0 + NS + n] C[n] / rms
+    constexpr int QMAX = 1 + RKA + 2 * NS;
+    constexpr int RPT = (TC * QMAX + SCAN_NT - 1) / SCAN_NT;  // staged values per thread
+    __shared__ __attribute__((aligned(16))) float sr[TC][SW];
+    // the rank-r term of every step of every channel, [channel][step] (row stride TC + 4: the
+    // b128 writes and reads of eight consecutive rows hit distinct banks)
+    __shared__ __attribute__((aligned(16))) float sp[SEL ? SCAN_NT : 1][TC + 4];
     const int d = D.d, H = D.H, r = D.r;
-    const int dim = blockIdx.x * SCAN_NT + threadIdx.x;
-    const int s = blockIdx.y;
-    const int t0 = blockIdx.z * GATE_ROWS;
-    const int REC = 1 + D.r + 2 * D.N;
-    const int nrow = min(ntok - t0, GATE_ROWS);
-    for (int idx = threadIdx.x; idx < GATE_ROWS * RS; idx += SCAN_NT) {
-        const int j = idx / RS, q = idx - j * RS;
-        float v = 0.0f;
-        if (j < nrow) {
-            const float *rc = rec + ((long)(t0 + j) * H + s) * REC;
-            if (q == 0)
-                v = rc[0];
-            else if (SEL && q >= 4 && q - 4 < r)
-                v = rc[1 + (q - 4)];
-        }
-        srec[j][q] = v;
-    }
-    __syncthreads();
-    if (dim >= d) return;
-    // h* is not read again after the gate: non-temporal loads keep it from displacing cached data
-    float hv[GATE_ROWS];
-#pragma unroll
-    for (int j = 0; j < GATE_ROWS; ++j) hv[j] = j < nrow ? __builtin_nontemporal_load(h + ((long)(t0 + j) * H + s) * d + dim) : 0.0f;
-    const float al = a_log[(long)s * d + dim];
-    const float abase = 1.0f / (1.0f + expf(al));
-    const float ln_ab = logf(fmaxf(abase, 1.0e-6f));
-    const float wx = 0.5f * tanhf(wx_diag[(long)s * d + dim]);
-    const float bd = b_delta ? b_delta[(long)s * d + dim] : 0.0f;
-    float wv[RKA];
-#pragma unroll
-    for (int q = 0; q < RKA; ++q) wv[q] = (SEL && q < r) ? w_vw[((long)s * r + q) * d + dim] : 0.0f;
-#pragma unroll
-    for (int j = 0; j < GATE_ROWS; ++j) {
-        if (j >= nrow) continue;
-        const long row = (long)(t0 + j) * H + s;
-        const float rms = srec[j][0];
-        const float u = hv[j] / rms;
-        const float x = u + wx * u;
-        float abar;
-        if (SEL) {
-            // W_vw^T (W_kw^T u) with u = h/rms: the record holds W_kw^T h, so divide once (the
-            // weights and the staged projections past r are zero)
-            float dot = 0.0f;
-#pragma unroll
-            for (int q = 0; q < RKA; ++q) dot += wv[q] * srec[j][4 + q];
-            const float pre = bd + dot / rms;
-            const float delta = logf(1.0f + expf(pre));
-            const float acore = expf(delta * ln_ab);
-            abar = 0.10f + (1.0f - 0.10f) * acore;
-        } else {
-            abar = abase;
-        }
-        gate_a[row * d + dim] = abar;
-        gate_x[row * d + dim] = (1.0f - abar) * x;
-    }
-}
-
-// Recurrence over time for one (sequence, slot, channel) per thread, N states in registers:
-//   m[n] = abar m[n] + B[n] ((1-abar) x),  y = sum_n C[n] m[n].
-// MODE 0: full scan from state_in, emit y and state_out (single chunk).
-// MODE 1: chunk pass A, zero start, emit chunk end state and decay product.
-// MODE 2: chunk pass C, start from chunk_s (carried), emit y; last chunk writes state_out.
-// Per TC steps the B/C values (projection / rms) are staged in LDS and the gate values are
-// loaded into registers up front.  EXACT: NS == N (branch-free inner loops).
-template <int NS, int MODE, bool EXACT>
-__global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restrict__ gate_a,
-                                                  const float *__restrict__ gate_x,
-                                                  const float *__restrict__ rec, int T, int nch, int has_bc,
-                                                  const float *__restrict__ state_in, float *__restrict__ y,
-                                                  float *__restrict__ state_out, float *__restrict__ chunk_s,
-                                                  float *__restrict__ chunk_p) {
-    __shared__ float sbc[TC][2 * NS];
-    const int d = D.d, H = D.H;
     const int N = EXACT ? NS : D.N;
     const int tid = threadIdx.x;
     const int dim = blockIdx.x * SCAN_NT + tid;
     const int s = blockIdx.y;
     const int bc = blockIdx.z;
     const int b = bc / nch, c = bc - (bc / nch) * nch;
-    const bool active = dim < d;
-    const int REC = 1 + D.r + 2 * D.N;
-    const int boff = 1 + D.r;
+    // d is a multiple of 64: a wave's channels are all inside d or all outside (wave-uniform)
+    const bool active = __builtin_amdgcn_readfirstlane(dim < d ? 1 : 0) != 0;
+    const int REC = 1 + r + 2 * D.N;
     const int Tc = (T + nch - 1) / nch;
     const int t0 = c * Tc, t1 = min(T, t0 + Tc);
     const int dd = active ? dim : 0;
+    const int nq = 1 + RKA + 2 * N;  // staged values per step (bucket-padded rank; B = C = 1 without has_bc)
+
+    // per-channel constants
+    const float al = a_log[(long)s * d + dd];
+    const float abase = 1.0f / (1.0f + expf(al));
+    const float ln_ab = logf(fmaxf(abase, 1.0e-6f));
+    const float wxh = 0.5f * tanhf(wx_diag[(long)s * d + dd]);
+    const float bd = (SEL && b_delta) ? b_delta[(long)s * d + dd] : 0.0f;
+    // W_vw as the B operand of v_mfma_f32_16x16x4f32: per 16-channel tile t of this wave and rank
+    // block kb, lane l holds W_vw[s][4 kb + l / 16][channel of tile t, l % 16]
+    const int lane = tid & 63, wave = tid >> 6;
+    constexpr int KB = SEL ? RKA / 4 : 1;
+    float wb[4][KB];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int ch = blockIdx.x * SCAN_NT + wave * 64 + t * 16 + (lane & 15);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const int q = 4 * kb + (lane >> 4);
+            wb[t][kb] = (SEL && q < r && ch < d) ? w_vw[((long)s * r + q) * d + ch] : 0.0f;
+        }
+    }
+
     float m[NS];
     const long st_off = (((long)b * H + s) * d + dd) * D.N;
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
         m[n] = 0.0f;
-        if (n < N && active) {
+        if ((EXACT || n < N) && active) {
             if (MODE == 0 && state_in) m[n] = state_in[st_off + n];
             if (MODE == 2) m[n] = chunk_s[((((long)b * nch + c) * H + s) * d + dd) * D.N + n];
         }
     }
     float prod = 1.0f;
-    // Per chunk of TC steps the B/C values (projection / rms) are staged in LDS and the gate
-    // values held in registers.  Where y is stored (passes 0 and C) two register sets alternate
-    // (the chunk loop is unrolled by two)
-    // so that the next chunk's loads are issued before this chunk's y stores: a load issued
-    // after stores is waited for behind them (the vector-memory counter retires in issue order).
-    // The loads are unconditional, at addresses clamped into the chunk (steps past its end are
-    // not used), so that the compiler can count them exactly.
-    constexpr int BCP = (TC * 2 * NS + SCAN_NT - 1) / SCAN_NT;  // staged B/C values per thread
+
     struct Chunk {
-        float a[TC], x[TC], bv[BCP], rv[BCP];
+        float hv[TC], rv[RPT], rr[RPT];
     };
     const long tstride = (long)H * d;                          // one time step of (b, s, dim)
     const long gbase = (long)b * T * tstride + (long)s * d + dd;  // (b, t = 0, s, dd)
     const int last = t1 - 1;
-    // pass C is the gate values' last use: loaded non-temporally there
+    // staged value q of a step -> its record field (0: rms, 1 + q': projection q' < r, padded
+    // projections -1 (zero), then B and C)
+    auto field = [&](int q) {
+        if (q == 0) return 0;
+        if (q <= RKA) return q - 1 < r ? q : -1;
+        return 1 + r + (q - 1 - RKA);
+    };
+    // h is read again by pass C after pass A (through the caches where it fits): non-temporal
+    // only where this is its last read
     auto fetch = [&](Chunk &k, int tb) {
+        if (tb + TC <= t1) {  // a whole block of steps: no clamping
+            const float *hp = h + gbase + (long)tb * tstride;
 #pragma unroll
-        for (int j = 0; j < TC; ++j) {
-            const long off = gbase + (long)min(tb + j, last) * tstride;
-            k.a[j] = MODE == 2 ? __builtin_nontemporal_load(gate_a + off) : gate_a[off];
-            k.x[j] = MODE == 2 ? __builtin_nontemporal_load(gate_x + off) : gate_x[off];
-        }
-        if (has_bc) {
+            for (int j = 0; j < TC; ++j)
+                k.hv[j] = MODE == 1 ? hp[(long)j * tstride] : __builtin_nontemporal_load(hp + (long)j * tstride);
+        } else {
 #pragma unroll
-            for (int q2 = 0; q2 < BCP; ++q2) {
-                const int idx = min(tid + q2 * SCAN_NT, TC * 2 * N - 1);
-                const int j = idx / (2 * N), q = idx - j * 2 * N;
-                const float *rc = rec + (((long)b * T + min(tb + j, last)) * H + s) * REC;
-                k.bv[q2] = rc[boff + q];
-                k.rv[q2] = rc[0];
+            for (int j = 0; j < TC; ++j) {
+                const long off = gbase + (long)min(tb + j, last) * tstride;
+                k.hv[j] = MODE == 1 ? h[off] : __builtin_nontemporal_load(h + off);
             }
+        }
+#pragma unroll
+        for (int q2 = 0; q2 < RPT; ++q2) {
+            const int idx = min(tid + q2 * SCAN_NT, TC * nq - 1);
+            const int j = idx / nq, q = idx - j * nq;
+            const float *rc = rec + (((long)b * T + min(tb + j, last)) * H + s) * REC;
+            const int f = field(q);
+            k.rv[q2] = f >= 0 ? rc[f] : 0.0f;
+            k.rr[q2] = rc[0];
         }
     };
     auto process = [&](const Chunk &k, int tb) {
         const int nt = min(TC, t1 - tb);
-        if (has_bc) {
 #pragma unroll
-            for (int q2 = 0; q2 < BCP; ++q2) {
-                const int idx = tid + q2 * SCAN_NT;
-                if (idx < nt * 2 * N) {
-                    const int j = idx / (2 * N), q = idx - j * 2 * N;
-                    sbc[j][q] = k.bv[q2] / k.rv[q2];
-                }
+        for (int q2 = 0; q2 < RPT; ++q2) {
+            const int idx = tid + q2 * SCAN_NT;
+            if (idx < nt * nq) {
+                const int j = idx / nq, q = idx - j * nq;
+                const float inv = 1.0f / k.rr[q2];
+                const int qb = q - 1 - RKA;  // B[0..N) then C[0..N) in the record; C staged at BC0 + NS
+                const int slot = q == 0 ? 0 : (q <= RKA ? 4 + (q - 1) : BC0 + (qb < N ? qb : NS + qb - N));
+                sr[j][slot] = q == 0 ? inv : (q > RKA && !has_bc) ? 1.0f : k.rv[q2] * inv;
             }
         }
         __syncthreads();
+        // the rank-r dot of every step, W_vw^T (W_kw^T u), on the matrix cores: per rank block of
+        // four, one MFMA per 16-channel tile (A: the staged projections of the 16 steps), then
+        // through LDS so that each thread holds its own channel's 16 values
+        float pj[TC];
+        if constexpr (SEL) {
+            floatx4 acc[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const float a = sr[lane & 15][4 + 4 * kb + (lane >> 4)];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, wb[t][kb], acc[t], 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                *reinterpret_cast<floatx4 *>(&sp[wave * 64 + t * 16 + (lane & 15)][4 * (lane >> 4)]) = acc[t];
+            // the rows a thread reads were written by lanes of its own wave
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int q = 0; q < TC / 4; ++q) {
+                const floatx4 v = *reinterpret_cast<const floatx4 *>(&sp[tid][4 * q]);
+                pj[4 * q] = v[0];
+                pj[4 * q + 1] = v[1];
+                pj[4 * q + 2] = v[2];
+                pj[4 * q + 3] = v[3];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < TC; ++j) {
             if (j < nt) {
-                float acc = 0.0f;
+                const float inv = sr[j][0];
+                const float u = k.hv[j] * inv;
+                const float x = u + wxh * u;
+                float abar = abase;
+                if constexpr (SEL) {
+                    const float pre = bd + pj[j];
+                    const float l2 = __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(pre * 1.44269504088896341f));
+                    abar = 0.10f + (1.0f - 0.10f) * __builtin_amdgcn_exp2f(l2 * ln_ab);
+                }
+                const float xin = (1.0f - abar) * x;
+                float a2[2] = {0.0f, 0.0f};
 #pragma unroll
                 for (int n = 0; n < NS; ++n) {
                     if (EXACT || n < N) {
-                        const float Bn = has_bc ? sbc[j][n] : 1.0f;
-                        const float Cn = has_bc ? sbc[j][N + n] : 1.0f;
-                        m[n] = k.a[j] * m[n] + Bn * k.x[j];
-                        acc += Cn * m[n];
+                        const float Bn = sr[j][BC0 + n];
+                        const float Cn = sr[j][BC0 + NS + n];
+                        m[n] = abar * m[n] + Bn * xin;
+                        a2[n & 1] += Cn * m[n];
                     }
                 }
                 if (MODE == 1)
-                    prod *= k.a[j];
+                    prod *= abar;
                 else if (active)
-                    y[gbase + (long)(tb + j) * tstride] = acc;
+                    y[gbase + (long)(tb + j) * tstride] = a2[0] + a2[1];
             }
         }
         __syncthreads();
     };
-    // (the fetches are unconditional too: past the end they re-read the last step, unused).
-    // Pass A stores nothing in the loop, so there one register set serves.
-    Chunk ca;
-    if constexpr (MODE == 1) {
-        for (int tb = t0; tb < t1; tb += TC) {
-            fetch(ca, tb);
-            process(ca, tb);
-        }
-    } else {
-        Chunk cb;
-        if (t0 < t1) fetch(ca, t0);
-        for (int tb = t0; tb < t1; tb += 2 * TC) {
-            fetch(cb, tb + TC);
-            process(ca, tb);
-            if (tb + TC >= t1) break;
-            fetch(ca, tb + 2 * TC);
-            process(cb, tb + TC);
-        }
+    // two register sets alternate so that the next TC steps' loads are issued before this TC's
+    // y stores; loads are unconditional, at addresses clamped into the chunk (unused past it)
+    Chunk ca, cb;
+    if (t0 < t1) fetch(ca, t0);
+    for (int tb = t0; tb < t1; tb += 2 * TC) {
+        fetch(cb, tb + TC);
+        process(ca, tb);
+        if (tb + TC >= t1) break;
+        fetch(ca, tb + 2 * TC);
+        process(cb, tb + TC);
     }
     if (!active) return;
     if (MODE == 1) {
@@ -255,11 +264,11 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan(Dims D, const float *__restric
         chunk_p[co] = prod;
 #pragma unroll
         for (int n = 0; n < NS; ++n)
-            if (n < N) chunk_s[co * D.N + n] = m[n];
+            if (EXACT || n < N) chunk_s[co * D.N + n] = m[n];
     } else if (state_out && (MODE == 0 || c == nch - 1)) {
 #pragma unroll
         for (int n = 0; n < NS; ++n)
-            if (n < N) state_out[st_off + n] = m[n];
+            if (EXACT || n < N) state_out[st_off + n] = m[n];
     }
 }
 
@@ -286,33 +295,57 @@ __global__ void k_scan_carry(Dims D, int B, int nch, const float *state_in, floa
     }
 }
 
-template <int NS, bool EXACT>
-void scan_modes(const Dims &D, const float *ga, const float *gx, const float *rec, int B, int T, int has_bc,
-                const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p, int nch,
-                hipStream_t st) {
-    const dim3 grid((unsigned)((D.d + SCAN_NT - 1) / SCAN_NT), (unsigned)D.H, (unsigned)(B * nch));
-    if (nch <= 1) {
-        hipLaunchKernelGGL((k_scan<NS, 0, EXACT>), grid, dim3(SCAN_NT), 0, st, D, ga, gx, rec, T, 1, has_bc,
-                           state_in, y, state_out, chunk_s, chunk_p);
+struct ScanArgs {
+    const float *h, *rec;
+    int B, T, has_bc;
+    const float *a_log, *wx_diag, *b_delta, *w_vw, *state_in;
+    float *y, *state_out, *chunk_s, *chunk_p;
+    int nch;
+};
+
+template <int NS, int RK, bool EXACT>
+void scan_modes(const Dims &D, const ScanArgs &a, hipStream_t st) {
+    const dim3 grid((unsigned)((D.d + SCAN_NT - 1) / SCAN_NT), (unsigned)D.H, (unsigned)(a.B * a.nch));
+#define ADN_SCAN_K(MODE)                                                                                          \
+    hipLaunchKernelGGL((k_scan_fused<NS, RK, MODE, EXACT>), grid, dim3(SCAN_NT), 0, st, D, a.h, a.rec, a.T, a.nch, \
+                       a.has_bc, a.a_log, a.wx_diag, a.b_delta, a.w_vw, a.state_in, a.y, a.state_out, a.chunk_s,   \
+                       a.chunk_p)
+    if (a.nch <= 1) {
+        ADN_SCAN_K(0);
         return;
     }
-    hipLaunchKernelGGL((k_scan<NS, 1, EXACT>), grid, dim3(SCAN_NT), 0, st, D, ga, gx, rec, T, nch, has_bc,
-                       state_in, y, state_out, chunk_s, chunk_p);
-    const long total = (long)B * D.H * D.d * D.N;
-    hipLaunchKernelGGL(k_scan_carry, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, D, B, nch,
-                       state_in, chunk_s, chunk_p);
-    hipLaunchKernelGGL((k_scan<NS, 2, EXACT>), grid, dim3(SCAN_NT), 0, st, D, ga, gx, rec, T, nch, has_bc,
-                       state_in, y, state_out, chunk_s, chunk_p);
+    ADN_SCAN_K(1);
+    const long total = (long)a.B * D.H * D.d * D.N;
+    hipLaunchKernelGGL(k_scan_carry, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, D, a.B, a.nch,
+                       a.state_in, a.chunk_s, a.chunk_p);
+    ADN_SCAN_K(2);
+#undef ADN_SCAN_K
+}
+
+template <int RK>
+void scan_n(const Dims &D, const ScanArgs &a, hipStream_t st) {
+    if (D.N == 16)
+        scan_modes<16, RK, true>(D, a, st);
+    else if (D.N == 1)
+        scan_modes<1, RK, true>(D, a, st);
+    else if (D.N == 32)
+        scan_modes<32, RK, true>(D, a, st);
+    else if (D.N <= 8)
+        scan_modes<8, RK, false>(D, a, st);
+    else
+        scan_modes<32, RK, false>(D, a, st);
 }
 
 }  // namespace
 
 int scan_rec_len(const Dims &D) { return 1 + D.r + 2 * D.N; }
 
+// Time chunks only where the sequences alone leave the GPU short of about two workgroups per
+// CU: a chunked scan runs the recurrence twice (pass A, then pass C from the carried start).
 int scan_chunks(int B, int T, int H, int d) {
     const long wgs = (long)B * H * ((d + SCAN_NT - 1) / SCAN_NT);
     int nch = 1;
-    while (wgs * nch < 2048 && T / (nch * 2) >= 4 * TC) nch *= 2;
+    while (wgs * nch < SCAN_MIN_WGS && T / (nch * 2) >= 4 * TC) nch *= 2;
     return nch;
 }
 
@@ -329,37 +362,16 @@ void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipSt
     }
 }
 
-void launch_scan_gate(const Dims &D, const float *h, const float *rec, int ntok, const float *a_log,
-                      const float *wx_diag, const float *b_delta, const float *w_vw, float *gate_a, float *gate_x,
-                      hipStream_t st) {
-    const dim3 grid((unsigned)((D.d + SCAN_NT - 1) / SCAN_NT), (unsigned)D.H,
-                    (unsigned)((ntok + GATE_ROWS - 1) / GATE_ROWS));
-    const bool sel = (D.flags & ADN_F_SCAN_SELECTIVE) != 0;
-#define ADN_GATE_ARGS D, h, rec, ntok, a_log, wx_diag, b_delta, w_vw, gate_a, gate_x
-    if (!sel)
-        hipLaunchKernelGGL((k_scan_gate<0, false>), grid, dim3(SCAN_NT), 0, st, ADN_GATE_ARGS);
+void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
+                 const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
+                 float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st) {
+    const ScanArgs a{h, rec, B, T, has_bc, a_log, wx_diag, b_delta, w_vw, state_in, y, state_out, chunk_s, chunk_p, nch};
+    if (!(D.flags & ADN_F_SCAN_SELECTIVE))
+        scan_n<0>(D, a, st);
     else if (D.r <= 32)
-        hipLaunchKernelGGL((k_scan_gate<32, true>), grid, dim3(SCAN_NT), 0, st, ADN_GATE_ARGS);
+        scan_n<32>(D, a, st);
     else
-        hipLaunchKernelGGL((k_scan_gate<64, true>), grid, dim3(SCAN_NT), 0, st, ADN_GATE_ARGS);
-#undef ADN_GATE_ARGS
-}
-
-void launch_scan(const Dims &D, const float *gate_a, const float *gate_x, const float *rec, int B, int T,
-                 int has_bc, const float *state_in, float *y, float *state_out, float *chunk_s, float *chunk_p,
-                 int nch, hipStream_t st) {
-#define ADN_SCAN_ARGS D, gate_a, gate_x, rec, B, T, has_bc, state_in, y, state_out, chunk_s, chunk_p, nch, st
-    if (D.N == 16)
-        scan_modes<16, true>(ADN_SCAN_ARGS);
-    else if (D.N == 1)
-        scan_modes<1, true>(ADN_SCAN_ARGS);
-    else if (D.N == 32)
-        scan_modes<32, true>(ADN_SCAN_ARGS);
-    else if (D.N <= 8)
-        scan_modes<8, false>(ADN_SCAN_ARGS);
-    else
-        scan_modes<32, false>(ADN_SCAN_ARGS);
-#undef ADN_SCAN_ARGS
+        scan_n<64>(D, a, st);
 }
 
 }  // namespace adn
