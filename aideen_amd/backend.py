@@ -128,7 +128,7 @@ class GpuDeqBackend:
     def forward(self, tokens: Optional[np.ndarray] = None, s_in: Optional[np.ndarray] = None, *,
                 max_iters: Optional[int] = None, eps: Optional[float] = None,
                 damping: Optional[float] = None, want=("h_star", "pooled", "logits", "argmax", "iters",
-                                                        "scan_y", "scan_state"),
+                                                        "scan_y", "scan_state", "converged"),
                 scan_state_in: Optional[np.ndarray] = None) -> Dict[str, np.ndarray]:
         """Host-memory forward (blocking).  Returns the requested outputs."""
         m = self.model

@@ -50,6 +50,18 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Raise *word, the bit pattern of a non-negative float bound on an array's magnitude, to the
+// wave's largest finite |v| (a > 0 float orders like its bits).  NaN and inf are left out: they
+// stay in their own rows and must not turn the split GEMMs' scale of every row into 0 or NaN.
+// One atomic per wave, issued only when the wave's value exceeds the word as read (a stale read
+// costs at most an extra atomic).  Every lane of the wave calls it.
+__device__ __forceinline__ void track_absmax(unsigned *word, float v) {
+    float a = fabsf(v);
+    a = a < INFINITY ? a : 0.0f;
+    a = wave_max(a);
+    if ((threadIdx.x & 63) == 0 && a > __uint_as_float(*word)) atomicMax(word, __float_as_uint(a));
+}
+
 // Sequential-in-slot order of the reference is kept where it matters (pooling); wave
 // reductions are tree-ordered (fp32 reassociation within the parity tolerance).
 

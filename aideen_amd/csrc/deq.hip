@@ -30,13 +30,18 @@ __global__ void k_init(Dims D, SolveBuffers b, const float *x_src, const int32_t
     const int t = row / D.H, s = row - t * D.H;
     const int d = D.d;
     float *h = b.h + (long)row * d;
+    float mx = 0.0f;  // largest finite |h0| of this lane
+    auto put = [&](int i, float v) {
+        h[i] = v;
+        mx = fmaxf(mx, fabsf(v) < INFINITY ? fabsf(v) : 0.0f);
+    };
     if (D.flags & ADN_F_INIT_SIGNAL_RMS) {
         const float *sg = b.signal + (long)row * d;
         float ss = 0.0f;
         for (int i = lane; i < d; i += 64) ss += sg[i] * sg[i];
         ss = wave_sum(ss);
         const float rms = sqrtf(ss / (float)d + 1e-6f);
-        for (int i = lane; i < d; i += 64) h[i] = sg[i] / rms;
+        for (int i = lane; i < d; i += 64) put(i, sg[i] / rms);
     } else {
         long xr = t;
         if (tokens) {
@@ -48,8 +53,9 @@ __global__ void k_init(Dims D, SolveBuffers b, const float *x_src, const int32_t
         }
         const float *x = x_src + xr * d;
         const float *an = anchor + (long)s * d;
-        for (int i = lane; i < d; i += 64) h[i] = x[i] + an[i];
+        for (int i = lane; i < d; i += 64) put(i, x[i] + an[i]);
     }
+    if (b.amax_h) track_absmax(b.amax_h, mx);  // the bound on |h| the split GEMMs scale their A by
     if (s == 0 && lane == 0) {
         b.act[0][t] = t;
         b.iters[t] = 0;
@@ -570,6 +576,7 @@ __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int
             for (int q2 = 0; q2 < NRES; ++q2) beta_s[q2] = bt[q2];
         }
         __syncthreads();
+        float hmax = 0.0f;
         for (long e0 = tid; e0 < hd; e0 += AB * AND_NT) {
             float acc[AB];
 #pragma unroll
@@ -584,9 +591,15 @@ __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int
 #pragma unroll
             for (int q = 0; q < AB; ++q) {
                 const long e = e0 + (long)q * AND_NT;
-                if (e < hd) h[e] = acc[q];
+                if (e < hd) {
+                    h[e] = acc[q];
+                    hmax = fmaxf(hmax, fabsf(acc[q]) < INFINITY ? fabsf(acc[q]) : 0.0f);
+                }
             }
         }
+        // a mixed iterate can leave the update's bound (the coefficients are normalised by their
+        // sum), so the mix raises the bound on |h| itself
+        if (b.amax_h) track_absmax(b.amax_h, hmax);
     }
 }
 

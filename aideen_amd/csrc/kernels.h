@@ -77,6 +77,9 @@ struct SolveBuffers {
     // sequence (token / mem_T), added to the update's sum; null = none
     const float *mem_hist;
     int mem_T;
+    // bound on |h| (float bits) for the split GEMMs' A scale: seeded with the update's RMSNorm
+    // bound, raised by the init and the Anderson mix; null = not tracked
+    unsigned *amax_h;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -131,9 +134,10 @@ void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipSt
 // The carrier over B sequences of T steps from h* [B][T][H][d] and the record: y [B][T][H][d],
 // state_out [B][H][d][N] (either may be null), state_in [B][H][d][N] or null; nch time chunks
 // (chunk_s / chunk_p hold B * nch chunks).
+// amax_y (or null): raised to the largest finite |y| (the readout GEMM's A scale).
 void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
                  const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
-                 float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st);
+                 float *state_out, float *chunk_s, float *chunk_p, int nch, unsigned *amax_y, hipStream_t st);
 int scan_chunks(int B, int T, int H, int d);
 
 // ---- misc (misc.hip) ----------------------------------------------------------------------
@@ -147,6 +151,13 @@ void launch_gemv_colmajor(const float *w, const float *x, int in_dim, int out_di
 void launch_transpose(const float *src, int rows, int cols, long batch, float *dst,
                       hipStream_t st);
 void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
+// Magnitude bounds (float bits) of the split GEMMs' A operands during one forward: [0] |h| (the
+// iterate: seeded with the update's RMSNorm bound, raised by the init and the Anderson mix),
+// [1] |y| (the carrier output, raised by the scan), [2] |m| (memory mode's carrier state, raised
+// by the temporal step and by a caller-supplied start state).  Reset by a kernel (not a memset:
+// the forward may be captured in a graph).
+constexpr int ADN_BOUNDS = 4;
+void launch_reset_bounds(unsigned *words, float h_bound, hipStream_t st);
 // ---- memory-coupled solve (memory.hip) -----------------------------------------------------
 // act[0] = tokens (b, t) = b*T + t for b < B, cnt[0] = B, cnt[1] = 0.
 // embed_context of the window ending at every position; tot0/tot1 hold
@@ -175,8 +186,10 @@ void launch_mem_begin(const SolveBuffers &b, int B, int T, int t, hipStream_t st
 void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm, const float *signal, int B,
                      int T, int t, const float *slot_scale, const float *gate_logit, hipStream_t st);
 // out[b][s] = abar m_prev + (1 - abar) x for the tokens at position t (m_prev null = zeros).
+// amax (or null): raised to the largest finite |out|.
 void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const float *m_prev, long m_sm,
-                     const float *a_log, const float *wx_diag, float *out, long out_sm, hipStream_t st);
+                     const float *a_log, const float *wx_diag, float *out, long out_sm, unsigned *amax,
+                     hipStream_t st);
 // *out = bit pattern of max |x[i]| over n floats (atomic max; *out must be zeroed first)
 void launch_absmax(const float *x, long n, unsigned *out, hipStream_t st);
 

@@ -78,7 +78,8 @@ __global__ __launch_bounds__(64 * MW) void k_hist_ctx(Dims D, float *hist, const
 template <int E>
 __global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, int B, int T, int t,
                                                       const float *m_prev, long m_sm, const float *a_log,
-                                                      const float *wx_diag, float *out, long out_sm) {
+                                                      const float *wx_diag, float *out, long out_sm,
+                                                      unsigned *amax) {
     constexpr int d = 64 * E;
     const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int H = D.H;
@@ -100,14 +101,18 @@ __global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, in
     for (int e = 0; e < E; ++e) ss += vh[e] * vh[e];
     const float rms = sqrtf(wave_sum(ss) / (float)d + 1e-6f);
     float *o = out + (long)bb * out_sm + (long)s * d;
+    float mx = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const float u = vh[e] / rms;
         const float wx = 0.5f * tanhf(vw[e]);
         const float x = u + wx * u;
         const float ab = 1.0f / (1.0f + expf(va[e]));
-        o[lane + 64 * e] = ab * vp[e] + (1.0f - ab) * x;
+        const float v = ab * vp[e] + (1.0f - ab) * x;
+        o[lane + 64 * e] = v;
+        mx = fmaxf(mx, fabsf(v) < INFINITY ? fabsf(v) : 0.0f);
     }
+    if (amax) track_absmax(amax, mx);  // the bound the next GEMMs scale this state by
 }
 
 }  // namespace
@@ -135,11 +140,12 @@ void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm,
 }
 
 void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const float *m_prev, long m_sm,
-                     const float *a_log, const float *wx_diag, float *out, long out_sm, hipStream_t st) {
+                     const float *a_log, const float *wx_diag, float *out, long out_sm, unsigned *amax,
+                     hipStream_t st) {
     const int rows = B * D.H;
     const dim3 grid((unsigned)((rows + MW - 1) / MW)), blk(64 * MW);
 #define ADN_TP(E) hipLaunchKernelGGL(k_temporal<E>, grid, blk, 0, st, D, h, B, T, t, m_prev, m_sm, a_log, wx_diag, \
-                                     out, out_sm)
+                                     out, out_sm, amax)
     switch (D.d) {
         case 64: ADN_TP(1); break;
         case 128: ADN_TP(2); break;

@@ -4,6 +4,8 @@
 //  * BlockBackend::fpm_batch_step ZOH step (gpu_backend.rs:18-56)
 //  * ComputeBackend::ffn_forward column-major GEMV (aideen-engine ffn_forward.wgsl:22-37)
 //  * layout helpers (tiled transpose, fill)
+#include <cstring>
+
 #include "kernels.h"
 
 namespace adn {
@@ -137,7 +139,19 @@ __global__ void k_fill_i32(int32_t *p, int32_t v, long n) {
         p[i] = v;
 }
 
+// The operand bounds of one forward: words[0] = w0 (float bits), the other ADN_BOUNDS - 1 zero.
+__global__ void k_reset_bounds(unsigned *words, unsigned w0) {
+    const int i = threadIdx.x;
+    if (i < ADN_BOUNDS) words[i] = i == 0 ? w0 : 0u;
+}
+
 }  // namespace
+
+void launch_reset_bounds(unsigned *words, float h_bound, hipStream_t st) {
+    unsigned bits;
+    memcpy(&bits, &h_bound, sizeof bits);
+    hipLaunchKernelGGL(k_reset_bounds, dim3(1), dim3(64), 0, st, words, bits);
+}
 
 void launch_spectral_norm(const float *w, int rows, int cols, int n_iter, float *sigma, float *work,
                           hipStream_t st) {

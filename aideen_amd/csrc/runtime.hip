@@ -80,6 +80,13 @@ struct adn_ctx {
     float *am_val = nullptr;      // [cap_tok][ceil(V/128)] LM-head tile arg-max partials
     int32_t *am_idx = nullptr;
     unsigned *absmax = nullptr;   // max |s_in| (float bits) for the signal GEMM's A scale
+    // fp16-split range guard: the A operands' magnitude bounds (ADN_BOUNDS words, reset per forward)
+    // and the weight-derived constants they are combined with (set at upload)
+    unsigned *bounds = nullptr;
+    float h_bound = 0.0f;      // max|norm_scale| (sqrt(d) + 1e3 max|anchor| when the RMS leaves the anchor out)
+    float l1_wv = 0.0f;        // largest row L1 norm of W_v: |mix| <= l1_wv |h|
+    float l1_wout = 0.0f;      // largest row L1 norm of W_out: |m_t| <= (1 + l1_wout) |m_inner|
+    float lm_a_scale = 1.0f;   // LM head A scale: |pnorm| <= max|lm_g| sqrt(d)
     unsigned *d_err = nullptr;
 
     // host-API staging (lazy, capacity-sized)
@@ -253,6 +260,29 @@ void set_split(const adn_ctx *c, GemmParams &g, const adn_ctx::Split &sp, float 
     g.out_scale = 1.0f / (sp.scale * a_scale);
 }
 
+// The fp16 halves hold values below 65504: an A operand whose bound (bound word w, times 1/gain)
+// reaches 2^14 is scaled down by a power of two inside the GEMM (results are unchanged in the
+// ordinary range, where the scale stays 1).  bf16 halves have fp32's exponent range.
+void set_range(const adn_ctx *c, GemmParams &g, int w, float gain = 1.0f) {
+    if (c->prec != PREC_F16X3) return;
+    g.a_absmax = c->bounds + w;
+    g.a_headroom = gain > 0.0f ? 16384.0f / gain : INFINITY;
+}
+
+// Largest L1 norm of an output row of H [d][d] matrices (host, either upload layout).
+float max_row_l1(const float *w, int H, int d, bool in_out) {
+    float best = 0.0f;
+    std::vector<double> acc((size_t)d);
+    for (int s = 0; s < H; ++s) {
+        const float *m = w + (size_t)s * d * d;
+        std::fill(acc.begin(), acc.end(), 0.0);
+        for (int i = 0; i < d; ++i)
+            for (int j = 0; j < d; ++j) acc[in_out ? j : i] += std::fabs(m[(size_t)i * d + j]);
+        for (int i = 0; i < d; ++i) best = std::max(best, (float)acc[i]);
+    }
+    return best;
+}
+
 // ---------------------------------------------------------------------------------------
 // the forward pipeline (device pointers; enqueue only)
 // ---------------------------------------------------------------------------------------
@@ -261,6 +291,7 @@ void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, in
     const Dims &D = c->D;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
+    launch_reset_bounds(c->bounds, c->h_bound, st);
     // x gathered from the embedding when tokens are given
     {
         GemmParams g{};
@@ -333,6 +364,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             g.err = b.err;
             g.epi = c->qk_bias ? EPI_BIAS : EPI_NONE;
             set_split(c, g, c->sp_qkv);
+            set_range(c, g, 0);
             Span sp(prof, ADN_STAGE_QKV_GEMM, k, st);
             launch_gemm(g, st);
         }
@@ -359,6 +391,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             g.err = b.err;
             g.epi = EPI_NONE;
             set_split(c, g, c->sp_o);
+            set_range(c, g, 0, c->l1_wv);  // mix is a convex combination of V = W_v h rows
             Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
             launch_gemm(g, st);
         }
@@ -399,6 +432,7 @@ void enqueue_scan_prep(adn_ctx *c, int ntok, const SolveBuffers &b, Prof *prof, 
     g.err = b.err;
     g.epi = EPI_NONE;
     set_split(c, g, c->sp_cat);
+    set_range(c, g, 0);
     launch_gemm(g, st);
 }
 
@@ -441,7 +475,7 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
         g.S = 1;
         g.err = b.err;
         g.epi = c->lm_b ? EPI_BIAS : EPI_NONE;
-        set_split(c, g, c->sp_lm);
+        set_split(c, g, c->sp_lm, c->lm_a_scale);
         const int ntiles = (D.V + GEMM_BN - 1) / GEMM_BN;
         if (o.argmax) {
             g.am_val = c->am_val;
@@ -475,7 +509,8 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
         {
             Span sp(prof, ADN_STAGE_SCAN, nch, st);
             launch_scan(D, b.h, c->scb.rec, r.batch, r.seq, c->w_b != nullptr, c->a_log, c->wx_diag, c->b_delta,
-                        c->w_vw, r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch, st);
+                        c->w_vw, r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch,
+                        c->bounds + 1, st);
         }
         if (o.scan_y && c->w_out) {
             GemmParams g{};
@@ -495,6 +530,7 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
             g.err = b.err;
             g.epi = EPI_ADD_A;
             set_split(c, g, c->sp_out);
+            set_range(c, g, 1);
             Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st);
             launch_gemm(g, st);
         }
@@ -508,6 +544,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     if (o.iters) b.iters = o.iters;
     b.conv = o.converged;
     b.mem_hist = nullptr;
+    b.amax_h = c->bounds;
     c->last_h = b.h;  // the adjoint reads this forward's h* and signal
     c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
@@ -533,10 +570,13 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
     if (o.iters) b.iters = o.iters;
     b.conv = o.converged;
     b.mem_hist = nullptr;
+    b.amax_h = c->bounds;
     b.mem_T = T;
     c->last_h = b.h;
     c->last_ntok = ntok;
     enqueue_signal_init(c, r, b, ntok, prof);
+    if (r.scan_state_in && c->prec == PREC_F16X3)  // a caller-supplied memory bounds m as well
+        launch_absmax(r.scan_state_in, hd * B, c->bounds + 2, st);
     float *mseq = o.scan_y ? o.scan_y : c->scb.y;  // [B][T][H][d]
     float *hist = c->scb.mem_hist;                   // [B][H][d]
     float *mn = c->scb.mem_mn;                       // [B][H][d] state before W_out
@@ -570,6 +610,7 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
             g.err = b.err;
             g.epi = EPI_NONE;
             set_split(c, g, c->sp_hist);
+            set_range(c, g, 2, 1.0f + (c->w_out ? c->l1_wout : 0.0f));  // m_{t-1} = (I + W_out) m_inner
             {
                 Span sp(prof, ADN_STAGE_HIST_GEMM, -1, st, B);
                 launch_gemm(g, st);
@@ -583,7 +624,7 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
         if (c->w_out) {
             {
                 Span sp(prof, ADN_STAGE_TEMPORAL, -1, st, B);
-                launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mn, hd, st);
+                launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mn, hd, c->bounds + 2, st);
             }
             GemmParams g{};  // m_t = m_inner + W_out m_inner
             g.role = ROLE_READOUT;
@@ -602,11 +643,12 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
             g.err = b.err;
             g.epi = EPI_ADD_A;
             set_split(c, g, c->sp_out);
+            set_range(c, g, 2);
             Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st, B);
             launch_gemm(g, st);
         } else {
             Span sp(prof, ADN_STAGE_TEMPORAL, -1, st, B);
-            launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mt, (long)T * hd, st);
+            launch_temporal(D, b.h, B, T, t, mprev, msm, c->a_log, c->wx_diag, mt, (long)T * hd, c->bounds + 2, st);
         }
     }
     if (o.scan_state)
@@ -717,6 +759,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
         c->absmax = (unsigned *)dmalloc(c, sizeof(unsigned));
+        c->bounds = (unsigned *)dmalloc(c, ADN_BOUNDS * sizeof(unsigned));
         b.err = c->d_err;
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
         c->pnorm = (float *)dmalloc(c, (size_t)T * d * sizeof(float));
@@ -876,6 +919,16 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
                                 {w->w_c, (size_t)H * N * d}}));
         make_split(c, c->sp_lm, c->lm_w, 1, V, d, host_maxabs({{w->lm_w, (size_t)V * d}}));
         if (c->w_hist) make_split(c, c->sp_hist, c->w_hist, 1, d, d, host_maxabs({{w->w_hist, mat}}));
+        {  // the fp16-split range guard's weight-derived bounds (see set_range)
+            const float sq = std::sqrt((float)d);
+            const float gmax = host_maxabs({{w->norm_scale, (size_t)d}});
+            const float anmax = host_maxabs({{w->anchor, (size_t)H * d}});
+            c->h_bound = gmax * (sq + ((cf.flags & ADN_F_RMS_EXCL_ANCHOR) ? 1e3f * anmax : 0.0f));
+            c->l1_wv = max_row_l1(w->w_v, H, d, in_out);
+            c->l1_wout = w->w_out ? max_row_l1(w->w_out, H, d, in_out) : 0.0f;
+            const float lg = w->lm_g ? host_maxabs({{w->lm_g, (size_t)d}}) : 1.0f;
+            c->lm_a_scale = std::min(1.0f, split_scale(c->prec, lg * sq));
+        }
         // The signal GEMM's A operand (gathered embedding rows, or s_in rows of the same
         // scale) is scaled up too, with 6 bits of headroom: inputs up to 64x the table's
         // maximum magnitude stay inside the fp16 range.

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
                                                         const float *__restrict__ w_vw,
                                                         const float *__restrict__ state_in, float *__restrict__ y,
                                                         float *__restrict__ state_out, float *__restrict__ chunk_s,
-                                                        float *__restrict__ chunk_p) {
+                                                        float *__restrict__ chunk_p, unsigned *amax_y) {
     constexpr bool SEL = RK > 0;
     constexpr int RKA = SEL ? RK : 0;
     constexpr int BC0 = 4 + RKA;         // staged step: [0] 1/rms, [4 + q] projection q / rms,
@@ -133,6 +133,7 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
         }
     }
     float prod = 1.0f;
+    float ymax = 0.0f;  // largest finite |y| this thread stores
 
     struct Chunk {
         float hv[TC], rv[RPT], rr[RPT];
@@ -239,10 +240,13 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
                         a2[n & 1] += Cn * m[n];
                     }
                 }
-                if (MODE == 1)
+                if (MODE == 1) {
                     prod *= abar;
-                else if (active)
-                    y[gbase + (long)(tb + j) * tstride] = a2[0] + a2[1];
+                } else if (active) {
+                    const float yv = a2[0] + a2[1];
+                    y[gbase + (long)(tb + j) * tstride] = yv;
+                    ymax = fmaxf(ymax, fabsf(yv) < INFINITY ? fabsf(yv) : 0.0f);
+                }
             }
         }
         __syncthreads();
@@ -258,6 +262,7 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
         fetch(ca, tb + 2 * TC);
         process(cb, tb + TC);
     }
+    if (MODE != 1 && amax_y) track_absmax(amax_y, ymax);  // the readout GEMM's A bound
     if (!active) return;
     if (MODE == 1) {
         const long co = (((long)b * nch + c) * H + s) * d + dd;
@@ -301,6 +306,7 @@ struct ScanArgs {
     const float *a_log, *wx_diag, *b_delta, *w_vw, *state_in;
     float *y, *state_out, *chunk_s, *chunk_p;
     int nch;
+    unsigned *amax_y;
 };
 
 template <int NS, int RK, bool EXACT>
@@ -309,7 +315,7 @@ void scan_modes(const Dims &D, const ScanArgs &a, hipStream_t st) {
 #define ADN_SCAN_K(MODE)                                                                                          \
     hipLaunchKernelGGL((k_scan_fused<NS, RK, MODE, EXACT>), grid, dim3(SCAN_NT), 0, st, D, a.h, a.rec, a.T, a.nch, \
                        a.has_bc, a.a_log, a.wx_diag, a.b_delta, a.w_vw, a.state_in, a.y, a.state_out, a.chunk_s,   \
-                       a.chunk_p)
+                       a.chunk_p, a.amax_y)
     if (a.nch <= 1) {
         ADN_SCAN_K(0);
         return;
@@ -364,8 +370,9 @@ void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipSt
 
 void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
                  const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
-                 float *state_out, float *chunk_s, float *chunk_p, int nch, hipStream_t st) {
-    const ScanArgs a{h, rec, B, T, has_bc, a_log, wx_diag, b_delta, w_vw, state_in, y, state_out, chunk_s, chunk_p, nch};
+                 float *state_out, float *chunk_s, float *chunk_p, int nch, unsigned *amax_y, hipStream_t st) {
+    const ScanArgs a{h,     rec, B,       T,       has_bc,  a_log, wx_diag, b_delta, w_vw, state_in,
+                     y,     state_out, chunk_s, chunk_p, nch, amax_y};
     if (!(D.flags & ADN_F_SCAN_SELECTIVE))
         scan_n<0>(D, a, st);
     else if (D.r <= 32)
