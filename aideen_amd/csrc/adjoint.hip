@@ -20,11 +20,11 @@ namespace {
 
 constexpr int AW = 4;  // waves per block
 
-template <int E>
-__global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, const float *signal, const float *h_star,
+template <int E, bool PART>
+__global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, int dd, const float *signal, const float *h_star,
                                                        const float *dl, int rows, float *pre, float *terms,
                                                        float *v0) {
-    constexpr int d = 64 * E;
+    const int d = PART ? dd : 64 * E, er = PART ? dd / 64 : E;  // chunks e >= er are outside the row
     const int row = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const int t = row / H;
@@ -35,16 +35,19 @@ __global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, const float *signal
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        pv[e] = signal[o + i] + 1.0f * h_star[o + i];
-        rv[e] = dl[(long)t * d + i];
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        pv[e] = on ? signal[o + i] + 1.0f * h_star[o + i] : 0.0f;
+        rv[e] = on ? dl[(long)t * d + i] : 0.0f;
     }
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        pre[o + i] = pv[e];
+        if (!PART || e < er) {
+            pre[o + i] = pv[e];
+            v0[o + i] = rv[e] * rhs_scale;
+        }
         ss += pv[e] * pv[e];
-        v0[o + i] = rv[e] * rhs_scale;
     }
     ss = wave_sum(ss);
     if (lane == 0) {
@@ -55,11 +58,11 @@ __global__ __launch_bounds__(64 * AW) void k_adj_prep(int H, const float *signal
 }
 
 // the first step fused with the preparation: v_0 = rhs is formed in registers (never stored)
-template <int E>
-__global__ __launch_bounds__(64 * AW) void k_adj_first(int H, const float *signal, const float *h_star,
+template <int E, bool PART>
+__global__ __launch_bounds__(64 * AW) void k_adj_first(int H, int dd, const float *signal, const float *h_star,
                                                         const float *g, const float *dl, int rows, float beta,
                                                         float *pre, float *terms, float *vn) {
-    constexpr int d = 64 * E;
+    const int d = PART ? dd : 64 * E, er = PART ? dd / 64 : E;  // chunks e >= er are outside the row
     const int row = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const int t = row / H;
@@ -70,14 +73,15 @@ __global__ __launch_bounds__(64 * AW) void k_adj_first(int H, const float *signa
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        pv[e] = signal[o + i] + 1.0f * h_star[o + i];
-        rv[e] = dl[(long)t * d + i] * rhs_scale;
-        gv[e] = g[i];
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        pv[e] = on ? signal[o + i] + 1.0f * h_star[o + i] : 0.0f;
+        rv[e] = on ? dl[(long)t * d + i] * rhs_scale : 0.0f;
+        gv[e] = on ? g[i] : 0.0f;
     }
     float ss = 0.0f, cf = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        pre[o + lane + 64 * e] = pv[e];
+        if (!PART || e < er) pre[o + lane + 64 * e] = pv[e];
         ss += pv[e] * pv[e];
         cf += beta * rv[e] * gv[e] * pv[e];
     }
@@ -94,15 +98,15 @@ __global__ __launch_bounds__(64 * AW) void k_adj_first(int H, const float *signa
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const float ng = (gv[e] * inv_rms) * (beta * rv[e]) - pv[e] * cs;
-        vn[o + lane + 64 * e] = rv[e] + (1.0f * ng + (1.0f - beta) * rv[e]);
+        if (!PART || e < er) vn[o + lane + 64 * e] = rv[e] + (1.0f * ng + (1.0f - beta) * rv[e]);
     }
 }
 
-template <int E>
-__global__ __launch_bounds__(64 * AW) void k_adj_step(int H, const float *pre, const float *terms,
+template <int E, bool PART>
+__global__ __launch_bounds__(64 * AW) void k_adj_step(int H, int dd, const float *pre, const float *terms,
                                                        const float *g, const float *dl, int rows, float beta,
                                                        const float *v, float *vn) {
-    constexpr int d = 64 * E;
+    const int d = PART ? dd : 64 * E, er = PART ? dd / 64 : E;  // chunks e >= er are outside the row
     const int row = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const int t = row / H;
@@ -115,10 +119,11 @@ __global__ __launch_bounds__(64 * AW) void k_adj_step(int H, const float *pre, c
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        pv[e] = pre[o + i];
-        vv[e] = v[o + i];
-        gv[e] = g[i];
-        rv[e] = dl[(long)t * d + i];
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        pv[e] = on ? pre[o + i] : 0.0f;
+        vv[e] = on ? v[o + i] : 0.0f;
+        gv[e] = on ? g[i] : 0.0f;
+        rv[e] = on ? dl[(long)t * d + i] : 0.0f;
         cf += beta * vv[e] * gv[e] * pv[e];
     }
     const float inv_rms = terms[2 * row];
@@ -127,15 +132,15 @@ __global__ __launch_bounds__(64 * AW) void k_adj_step(int H, const float *pre, c
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
         const float ng = (gv[e] * inv_rms) * (beta * vv[e]) - pv[e] * cs;
-        vn[o + i] = rv[e] * rhs_scale + (1.0f * ng + (1.0f - beta) * vv[e]);
+        if (!PART || e < er) vn[o + i] = rv[e] * rhs_scale + (1.0f * ng + (1.0f - beta) * vv[e]);
     }
 }
 
-template <int E>
-__global__ __launch_bounds__(64 * AW) void k_adj_source(int H, const float *pre, const float *terms,
+template <int E, bool PART>
+__global__ __launch_bounds__(64 * AW) void k_adj_source(int H, int dd, const float *pre, const float *terms,
                                                          const float *g, int ntok, float beta, const float *v,
                                                          float *src) {
-    constexpr int d = 64 * E;
+    const int d = PART ? dd : 64 * E, er = PART ? dd / 64 : E;  // chunks e >= er are outside the row
     const int t = blockIdx.x * AW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= ntok) return;
     float acc[E];
@@ -149,17 +154,20 @@ __global__ __launch_bounds__(64 * AW) void k_adj_source(int H, const float *pre,
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int i = lane + 64 * e;
-            pv[e] = pre[o + i];
-            up[e] = beta * v[o + i];
-            cf += up[e] * g[i] * pv[e];
+            const bool on = !PART || e < er;  // zeros outside the row add nothing below
+            pv[e] = on ? pre[o + i] : 0.0f;
+            up[e] = on ? beta * v[o + i] : 0.0f;
+            cf += up[e] * (on ? g[i] : 0.0f) * pv[e];
         }
         const float inv_rms = terms[2 * row];
         const float cs = wave_sum(cf) * terms[2 * row + 1];
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[e] = acc[e] + ((g[lane + 64 * e] * inv_rms) * up[e] - pv[e] * cs);
+        for (int e = 0; e < E; ++e)
+            if (!PART || e < er) acc[e] = acc[e] + ((g[lane + 64 * e] * inv_rms) * up[e] - pv[e] * cs);
     }
 #pragma unroll
-    for (int e = 0; e < E; ++e) src[(long)t * d + lane + 64 * e] = acc[e];
+    for (int e = 0; e < E; ++e)
+        if (!PART || e < er) src[(long)t * d + lane + 64 * e] = acc[e];
 }
 
 __global__ void k_iota(int32_t *a, int n, int32_t *cnt) {
@@ -168,7 +176,7 @@ __global__ void k_iota(int32_t *a, int n, int32_t *cnt) {
     if (i == 0) cnt[0] = n;
 }
 
-template <int E>
+template <int E, bool PART>
 const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
     const int rows = a.ntok * D.H;
     const dim3 rg((unsigned)((rows + AW - 1) / AW)), blk(64 * AW);
@@ -177,10 +185,10 @@ const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
     float *v;
     if (a.iters == 0) {
         v = a.v_out ? a.v_out : a.v0;
-        hipLaunchKernelGGL(k_adj_prep<E>, rg, blk, 0, st, D.H, a.signal, a.h_star, a.dl, rows, a.pre, a.terms, v);
+        hipLaunchKernelGGL((k_adj_prep<E, PART>), rg, blk, 0, st, D.H, D.d, a.signal, a.h_star, a.dl, rows, a.pre, a.terms, v);
     } else {
         v = dst(0);
-        hipLaunchKernelGGL(k_adj_first<E>, rg, blk, 0, st, D.H, a.signal, a.h_star, a.g, a.dl, rows, a.beta, a.pre,
+        hipLaunchKernelGGL((k_adj_first<E, PART>), rg, blk, 0, st, D.H, D.d, a.signal, a.h_star, a.g, a.dl, rows, a.beta, a.pre,
                            a.terms, v);
     }
     SolveBuffers b = a.sb;
@@ -192,7 +200,7 @@ const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
     for (int k = 0; k < a.iters; ++k) {
         float *vn = dst(k);
         if (k > 0)
-            hipLaunchKernelGGL(k_adj_step<E>, rg, blk, 0, st, D.H, a.pre, a.terms, a.g, a.dl, rows, a.beta, v, vn);
+            hipLaunchKernelGGL((k_adj_step<E, PART>), rg, blk, 0, st, D.H, D.d, a.pre, a.terms, a.g, a.dl, rows, a.beta, v, vn);
         if (a.anderson_m > 0) {  // store the new iterate, mix from the third step (per token)
             b.h = vn;
             launch_anderson(D, b, 0, a.ntok, a.ntok, k, a.anderson_m, st);
@@ -200,7 +208,7 @@ const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
         v = vn;
     }
     if (a.src)
-        hipLaunchKernelGGL(k_adj_source<E>, dim3((unsigned)((a.ntok + AW - 1) / AW)), blk, 0, st, D.H, a.pre,
+        hipLaunchKernelGGL((k_adj_source<E, PART>), dim3((unsigned)((a.ntok + AW - 1) / AW)), blk, 0, st, D.H, D.d, a.pre,
                            a.terms, a.g, a.ntok, a.beta, v, a.src);
     return v;
 }
@@ -208,15 +216,9 @@ const float *adj_run(const Dims &D, const AdjointArgs &a, hipStream_t st) {
 }  // namespace
 
 const float *launch_adjoint(const Dims &D, const AdjointArgs &a, hipStream_t st) {
-    switch (D.d) {
-        case 64: return adj_run<1>(D, a, st);
-        case 128: return adj_run<2>(D, a, st);
-        case 256: return adj_run<4>(D, a, st);
-        case 512: return adj_run<8>(D, a, st);
-        case 1024: return adj_run<16>(D, a, st);
-        case 2048: return adj_run<32>(D, a, st);
-        default: return nullptr;  // rejected at context creation
-    }
+    const float *v = nullptr;
+    dispatch_width(D.d, [&](auto Ec, auto Pc) { v = adj_run<decltype(Ec)::value, decltype(Pc)::value>(D, a, st); });
+    return v;
 }
 
 }  // namespace adn

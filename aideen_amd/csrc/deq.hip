@@ -220,6 +220,80 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
     }
 }
 
+// The same attention for any slot count H <= 16 (read at run time): one wave per (token, query
+// slot), the scores summed and the softmax formed as in k_attn's few-score path (the same
+// per-lane partial sums, one wave_sum per score, max and sum in key order).
+template <int VEC>
+__global__ __launch_bounds__(256) void k_attn_rt(Dims D, SolveBuffers b, int cur, int k) {
+    constexpr int HM = 16;
+    const int H = D.H;
+    const int gw = blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = b.cnt[cur];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        b.cnt[cur ^ 1] = 0;
+        b.cnt_hist[k] += n;
+    }
+    const int i = gw / H, a = gw - (gw / H) * H;
+    if (i >= n) return;
+    const int d = D.d;
+    const long rowstride = 3L * d;
+    const float *base = b.qkv + (long)i * H * rowstride;
+    float part[HM];
+#pragma unroll
+    for (int c = 0; c < HM; ++c) part[c] = 0.0f;
+    for (int off = lane * VEC; off < d; off += 64 * VEC) {
+        float q[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) q[v] = base[(long)a * rowstride + off + v];
+#pragma unroll
+        for (int c = 0; c < HM; ++c) {
+            if (c < H) {
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) part[c] += q[v] * base[(long)c * rowstride + d + off + v];
+            }
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)d);
+    float e[HM];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < HM; ++c) {
+        if (c < H) {
+            float sc = wave_sum(part[c]) * scale;
+            if (D.flags & ADN_F_SCORE_CLAMP4) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
+            e[c] = sc;
+            mx = fmaxf(mx, sc);
+        }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < HM; ++c) {
+        if (c < H) {
+            e[c] = expf(e[c] - mx);
+            sum += e[c];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < HM; ++c)
+        if (c < H) e[c] = e[c] / sum;
+    float *mixrow = b.mix + ((long)i * H + a) * d;
+    for (int off = lane * VEC; off < d; off += 64 * VEC) {
+        float acc[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < HM; ++c) {
+            if (c < H) {
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + base[(long)c * rowstride + 2 * d + off + v] * e[c];
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) mixrow[off + v] = acc[v];
+    }
+}
+
 // Token residual modes: max-abs over [H][d] (default), L2 over [H][d] (ADN_F_RESID_L2), or the
 // largest per-slot relative RMS change (ADN_F_RESID_RELRMS).  Per slot, `acc` is the max |dh|
 // (mode 0) or the sum of dh^2 (modes 1, 2) after the wave reduction; `rms` the slot's RMSNorm
@@ -263,7 +337,7 @@ __device__ __forceinline__ int token_exit(float r, float eps, int k, int max_ite
 // issued after stores is waited for behind them (the vector-memory counter retires in issue
 // order), and a fully unrolled walk lets the compiler count the loads exactly.  HT = 0: the
 // slot count is read at run time (one slot at a time).  HIST: the memory-coupled history term.
-template <int E, int HT, bool HIST>
+template <int E, int HT, bool HIST, bool PART>
 __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur, int k, int max_iters,
                                                 float eps, const float *anchor, const float *norm_scale,
                                                 float beta) {
@@ -274,7 +348,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
     if (blockIdx.x * WAVES_PER_BLOCK >= n) return;
     const int i = blockIdx.x * WAVES_PER_BLOCK + wave;
     const int H = HT > 0 ? HT : D.H;
-    constexpr int d = 64 * E;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
     const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
     const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
     bool keep = false;
@@ -283,7 +357,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
         t = b.act[cur][i];
         float g[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) g[e] = norm_scale[lane + 64 * e];
+        for (int e = 0; e < E; ++e) g[e] = (!PART || e < er) ? norm_scale[lane + 64 * e] : 0.0f;
         const float omb = 1.0f - beta;
         float rtok = 0.0f;
         const float *hc_tok = HIST ? b.mem_hist + (long)(t / b.mem_T) * H * d : nullptr;
@@ -302,11 +376,12 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 const int idx = lane + 64 * e;
-                q.o[e] = __builtin_nontemporal_load(o + idx);
-                q.sg[e] = __builtin_nontemporal_load(sg + idx);
-                q.an[e] = an[idx];
-                q.h[e] = h[idx];
-                if constexpr (HIST) q.hc[e] = hc_tok[(long)s * d + idx];
+                const bool on = !PART || e < er;  // zeros outside the row add nothing below
+                q.o[e] = on ? __builtin_nontemporal_load(o + idx) : 0.0f;
+                q.sg[e] = on ? __builtin_nontemporal_load(sg + idx) : 0.0f;
+                q.an[e] = on ? an[idx] : 0.0f;
+                q.h[e] = on ? h[idx] : 0.0f;
+                if constexpr (HIST) q.hc[e] = on ? hc_tok[(long)s * d + idx] : 0.0f;
             }
         };
         auto step = [&](int s, const SlotIn &q) {
@@ -327,7 +402,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
             for (int e = 0; e < E; ++e) {
                 const float f = g[e] * cval[e] / rms;
                 const float hn = f * beta + q.h[e] * omb;
-                h[lane + 64 * e] = hn;
+                if (!PART || e < er) h[lane + 64 * e] = hn;
                 const float df = hn - q.h[e];
                 r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
             }
@@ -442,7 +517,7 @@ __device__ void anderson_coeffs(int n, const float *g, float *beta) {
 // and one wave per slot, so that the slots' row updates run side by side instead of one after
 // another in a single wave.  Same arithmetic as k_update (the token residual is combined over
 // the slots in slot order).
-template <int E>
+template <int E, bool PART>
 __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int cur, int k, int max_iters,
                                                      float eps, const float *anchor, const float *norm_scale,
                                                      float beta) {
@@ -451,7 +526,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     if (i >= b.cnt[cur]) return;
     const int s = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int H = D.H;
-    constexpr int d = 64 * E;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
     const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
     const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
     const int t = b.act[cur][i];
@@ -467,11 +542,12 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int idx = lane + 64 * e;
-        const float as_ = (o[idx] + sg[idx]) + (hc ? hc[idx] : 0.0f);
-        const float c = as_ + an[idx];
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        const float as_ = on ? (o[idx] + sg[idx]) + (hc ? hc[idx] : 0.0f) : 0.0f;
+        const float c = as_ + (on ? an[idx] : 0.0f);
         cval[e] = c;
-        hold[e] = h[idx];
-        gs[e] = norm_scale[idx];
+        hold[e] = on ? h[idx] : 0.0f;
+        gs[e] = on ? norm_scale[idx] : 0.0f;
         ss += excl ? as_ * as_ : c * c;
     }
     ss = wave_sum(ss);
@@ -482,7 +558,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     for (int e = 0; e < E; ++e) {
         const float f = gs[e] * cval[e] / rms;
         const float hn = f * beta + hold[e] * omb;
-        h[lane + 64 * e] = hn;
+        if (!PART || e < er) h[lane + 64 * e] = hn;
         const float df = hn - hold[e];
         r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
     }
@@ -626,6 +702,16 @@ void launch_init(const Dims &D, const SolveBuffers &b, const float *x_src, const
 }
 
 void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok, hipStream_t st) {
+    if (D.H & (D.H - 1)) {  // slot counts other than powers of two
+        const dim3 grid((unsigned)(((long)ntok * D.H + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK));
+        if (D.d % 256 == 0)
+            hipLaunchKernelGGL(k_attn_rt<4>, grid, dim3(256), 0, st, D, b, cur, k);
+        else if (D.d % 128 == 0)
+            hipLaunchKernelGGL(k_attn_rt<2>, grid, dim3(256), 0, st, D, b, cur, k);
+        else
+            hipLaunchKernelGGL(k_attn_rt<1>, grid, dim3(256), 0, st, D, b, cur, k);
+        return;
+    }
     if (ntok <= SMALL_ROWS) {  // one wave per (token, query slot): the same scores, more waves
         switch (D.H) {
             case 1: attn_dispatch_vec<1, 1>(D, b, cur, k, ntok, st); break;
@@ -643,62 +729,50 @@ void launch_attn(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok,
         case 4: attn_dispatch_vec<4, 4>(D, b, cur, k, ntok, st); break;
         case 8: attn_dispatch_vec<8, 8>(D, b, cur, k, ntok, st); break;
         case 16: attn_dispatch_vec<16, 4>(D, b, cur, k, ntok, st); break;
-        default: break;  // rejected at context creation
+        default: break;  // other slot counts take k_attn_rt
     }
 }
 
 // k_update for d = 64 E: the slot count as a template argument (1, 2, 4, 8, 16) up to d = 1024
-// without the history term, read at run time otherwise.
-template <int E>
+// for power-of-two rows without the history term, read at run time otherwise.
+template <int E, bool PART>
 void launch_update_e(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps,
                      const float *anchor, const float *norm_scale, float beta, dim3 grid, dim3 blk,
                      hipStream_t st) {
 #define ADN_UPD_ARGS D, b, cur, k, max_iters, eps, anchor, norm_scale, beta
     if (b.mem_hist) {
-        hipLaunchKernelGGL((k_update<E, 0, true>), grid, blk, 0, st, ADN_UPD_ARGS);
+        hipLaunchKernelGGL((k_update<E, 0, true, PART>), grid, blk, 0, st, ADN_UPD_ARGS);
         return;
     }
-    if constexpr (E <= 16) {
+    if constexpr (E <= 16 && !PART) {
         switch (D.H) {
-            case 1: hipLaunchKernelGGL((k_update<E, 1, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
-            case 2: hipLaunchKernelGGL((k_update<E, 2, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
-            case 4: hipLaunchKernelGGL((k_update<E, 4, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
-            case 8: hipLaunchKernelGGL((k_update<E, 8, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
-            case 16: hipLaunchKernelGGL((k_update<E, 16, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 1: hipLaunchKernelGGL((k_update<E, 1, false, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 2: hipLaunchKernelGGL((k_update<E, 2, false, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 4: hipLaunchKernelGGL((k_update<E, 4, false, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 8: hipLaunchKernelGGL((k_update<E, 8, false, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
+            case 16: hipLaunchKernelGGL((k_update<E, 16, false, false>), grid, blk, 0, st, ADN_UPD_ARGS); return;
             default: break;
         }
     }
-    hipLaunchKernelGGL((k_update<E, 0, false>), grid, blk, 0, st, ADN_UPD_ARGS);
+    hipLaunchKernelGGL((k_update<E, 0, false, PART>), grid, blk, 0, st, ADN_UPD_ARGS);
 #undef ADN_UPD_ARGS
 }
 
 void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max_iters, float eps, int ntok,
                    const float *anchor, const float *norm_scale, float beta, hipStream_t st) {
-#define ADN_UPD_ARGS D, b, cur, k, max_iters, eps, anchor, norm_scale, beta
     if (ntok <= SMALL_ROWS) {
         const dim3 tgrid((unsigned)ntok), tblk(64 * D.H);
-        switch (D.d) {
-            case 64: hipLaunchKernelGGL(k_update_tok<1>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
-            case 128: hipLaunchKernelGGL(k_update_tok<2>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
-            case 256: hipLaunchKernelGGL(k_update_tok<4>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
-            case 512: hipLaunchKernelGGL(k_update_tok<8>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
-            case 1024: hipLaunchKernelGGL(k_update_tok<16>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
-            case 2048: hipLaunchKernelGGL(k_update_tok<32>, tgrid, tblk, 0, st, ADN_UPD_ARGS); break;
-            default: break;  // rejected at context creation
-        }
+        dispatch_width(D.d, [&](auto Ec, auto Pc) {
+            hipLaunchKernelGGL((k_update_tok<decltype(Ec)::value, decltype(Pc)::value>), tgrid, tblk, 0, st, D, b,
+                               cur, k, max_iters, eps, anchor, norm_scale, beta);
+        });
         return;
     }
     const dim3 grid((unsigned)((ntok + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK)), blk(64 * WAVES_PER_BLOCK);
-    switch (D.d) {
-        case 64: launch_update_e<1>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
-        case 128: launch_update_e<2>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
-        case 256: launch_update_e<4>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
-        case 512: launch_update_e<8>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
-        case 1024: launch_update_e<16>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
-        case 2048: launch_update_e<32>(D, b, cur, k, max_iters, eps, anchor, norm_scale, beta, grid, blk, st); break;
-        default: break;  // rejected at context creation
-    }
-#undef ADN_UPD_ARGS
+    dispatch_width(D.d, [&](auto Ec, auto Pc) {
+        launch_update_e<decltype(Ec)::value, decltype(Pc)::value>(D, b, cur, k, max_iters, eps, anchor, norm_scale,
+                                                                  beta, grid, blk, st);
+    });
 }
 
 void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int rows, int k, int m,

@@ -12,13 +12,13 @@ constexpr int WPB = 4;
 
 // pooled = fold(0, acc + h_s)/H (slot order kept); pnorm = (pooled/rms) * g, eps 1e-5.  One wave
 // per token; each lane keeps its E = d/64 pooled values in registers between the two passes.
-template <int E>
+template <int E, bool PART>
 __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int ntok, const float *g,
                                                    float *pooled, float *pnorm, float *rec, int REC) {
     const int t = blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (t >= ntok) return;
-    constexpr int d = 64 * E;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
     const int H = D.H;
     const float *ht = h + (long)t * H * d;
     // slot by slot: the pooled sums add the slots in order; with `rec` each slot row's RMS
@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int n
     for (int s = 0; s < H; ++s) {
         float x[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) x[e] = ht[(long)s * d + lane + 64 * e];
+        for (int e = 0; e < E; ++e) x[e] = (!PART || e < er) ? ht[(long)s * d + lane + 64 * e] : 0.0f;
 #pragma unroll
         for (int e = 0; e < E; ++e) pv[e] = pv[e] + x[e];
         if (rec) {
@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int n
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
         pv[e] = pv[e] / (float)H;
-        if (pooled) pooled[(long)t * d + i] = pv[e];
+        if (pooled && (!PART || e < er)) pooled[(long)t * d + i] = pv[e];
         ss += pv[e] * pv[e];
     }
     if (!pnorm) return;
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int n
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        pnorm[(long)t * d + i] = (pv[e] / rms) * (g ? g[i] : 1.0f);
+        if (!PART || e < er) pnorm[(long)t * d + i] = (pv[e] / rms) * (g ? g[i] : 1.0f);
     }
 }
 
@@ -245,15 +245,10 @@ __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
                       float *pnorm, float *rec, int REC, hipStream_t st) {
     const dim3 grid((unsigned)((ntok + WPB - 1) / WPB)), blk(64 * WPB);
-    switch (D.d) {
-        case 64: hipLaunchKernelGGL(k_pool_norm<1>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
-        case 128: hipLaunchKernelGGL(k_pool_norm<2>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
-        case 256: hipLaunchKernelGGL(k_pool_norm<4>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
-        case 512: hipLaunchKernelGGL(k_pool_norm<8>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
-        case 1024: hipLaunchKernelGGL(k_pool_norm<16>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
-        case 2048: hipLaunchKernelGGL(k_pool_norm<32>, grid, blk, 0, st, D, h, ntok, g, pooled, pnorm, rec, REC); break;
-        default: break;  // rejected at context creation
-    }
+    dispatch_width(D.d, [&](auto Ec, auto Pc) {
+        hipLaunchKernelGGL((k_pool_norm<decltype(Ec)::value, decltype(Pc)::value>), grid, blk, 0, st, D, h, ntok, g,
+                           pooled, pnorm, rec, REC);
+    });
 }
 
 void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st) {

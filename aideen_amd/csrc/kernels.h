@@ -1,9 +1,39 @@
 // Kernel launch interfaces shared by the runtime (runtime.cpp) and the kernel sources.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace adn {
+
+// Kernels templated on E = d / 64 values per lane (a lane's share of a d-wide row): d a power of
+// two runs the exact instantiation (E = d / 64, PART = false); any other multiple of 64 runs the
+// next power of two up with PART = true, where a lane's chunks e >= d / 64 are neither loaded nor
+// stored (the rows keep their true width d).  f(std::integral_constant<int, E>, std::bool_constant<PART>).
+template <typename F>
+void dispatch_width(int d, F &&f) {
+    using std::bool_constant;
+    using std::integral_constant;
+    switch (d) {
+        case 64: f(integral_constant<int, 1>{}, bool_constant<false>{}); return;
+        case 128: f(integral_constant<int, 2>{}, bool_constant<false>{}); return;
+        case 256: f(integral_constant<int, 4>{}, bool_constant<false>{}); return;
+        case 512: f(integral_constant<int, 8>{}, bool_constant<false>{}); return;
+        case 1024: f(integral_constant<int, 16>{}, bool_constant<false>{}); return;
+        case 2048: f(integral_constant<int, 32>{}, bool_constant<false>{}); return;
+        default: break;
+    }
+    const int er = d / 64;
+    if (er <= 4)
+        f(integral_constant<int, 4>{}, bool_constant<true>{});
+    else if (er <= 8)
+        f(integral_constant<int, 8>{}, bool_constant<true>{});
+    else if (er <= 16)
+        f(integral_constant<int, 16>{}, bool_constant<true>{});
+    else
+        f(integral_constant<int, 32>{}, bool_constant<true>{});
+}
 
 enum GemmEpilogue { EPI_NONE = 0, EPI_BIAS = 1, EPI_ADD_A = 2 };
 // GemmParams.am_val/am_idx != null: also write each row's (max, last arg-max) over every

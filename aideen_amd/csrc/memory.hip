@@ -29,11 +29,11 @@ __global__ void k_mem_begin(SolveBuffers b, int B, int T, int t) {
 // hist holds u = W_hist m_prev on entry ([B][H][d]); m_prev rows are m_prev + b*m_sm + s*d.
 // E = d/64 values per lane, held in registers: every load of the row is issued before the
 // first store (a load issued after stores is waited for behind them), and u is not re-read.
-template <int E>
+template <int E, bool PART>
 __global__ __launch_bounds__(64 * MW) void k_hist_ctx(Dims D, float *hist, const float *m_prev, long m_sm,
                                                       const float *signal, int B, int T, int t,
                                                       const float *slot_scale, const float *gate_logit) {
-    constexpr int d = 64 * E;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
     const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int H = D.H;
     if (row >= B * H) return;
@@ -46,10 +46,11 @@ __global__ __launch_bounds__(64 * MW) void k_hist_ctx(Dims D, float *hist, const
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        vs[e] = sg[i];
-        vp[e] = pm[i];
-        vu[e] = u[i];
-        vc[e] = sc[i];
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        vs[e] = on ? sg[i] : 0.0f;
+        vp[e] = on ? pm[i] : 0.0f;
+        vu[e] = on ? u[i] : 0.0f;
+        vc[e] = on ? sc[i] : 0.0f;
     }
     float ssg = 0.0f, spm = 0.0f;
 #pragma unroll
@@ -70,17 +71,18 @@ __global__ __launch_bounds__(64 * MW) void k_hist_ctx(Dims D, float *hist, const
     const float sigma = 1.0f / (1.0f + expf(-gate_logit[s]));
     const float g = (0.070f + (0.20f - 0.070f) * sigma) * scale;
 #pragma unroll
-    for (int e = 0; e < E; ++e) u[lane + 64 * e] = vu[e] * g;
+    for (int e = 0; e < E; ++e)
+        if (!PART || e < er) u[lane + 64 * e] = vu[e] * g;
 }
 
 // m_inner for the tokens at position t; m_prev == nullptr is the zero state.  E = d/64 values
 // per lane in registers, all loads before the stores.
-template <int E>
+template <int E, bool PART>
 __global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, int B, int T, int t,
                                                       const float *m_prev, long m_sm, const float *a_log,
                                                       const float *wx_diag, float *out, long out_sm,
                                                       unsigned *amax) {
-    constexpr int d = 64 * E;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
     const int row = blockIdx.x * MW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int H = D.H;
     if (row >= B * H) return;
@@ -91,10 +93,11 @@ __global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, in
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
-        vh[e] = hs[i];
-        vw[e] = wx_diag[(long)s * d + i];
-        va[e] = a_log[(long)s * d + i];
-        vp[e] = pm ? pm[i] : 0.0f;
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        vh[e] = on ? hs[i] : 0.0f;
+        vw[e] = on ? wx_diag[(long)s * d + i] : 0.0f;
+        va[e] = on ? a_log[(long)s * d + i] : 0.0f;
+        vp[e] = (on && pm) ? pm[i] : 0.0f;
     }
     float ss = 0.0f;
 #pragma unroll
@@ -109,8 +112,10 @@ __global__ __launch_bounds__(64 * MW) void k_temporal(Dims D, const float *h, in
         const float x = u + wx * u;
         const float ab = 1.0f / (1.0f + expf(va[e]));
         const float v = ab * vp[e] + (1.0f - ab) * x;
-        o[lane + 64 * e] = v;
-        mx = fmaxf(mx, fabsf(v) < INFINITY ? fabsf(v) : 0.0f);
+        if (!PART || e < er) {
+            o[lane + 64 * e] = v;
+            mx = fmaxf(mx, fabsf(v) < INFINITY ? fabsf(v) : 0.0f);
+        }
     }
     if (amax) track_absmax(amax, mx);  // the bound the next GEMMs scale this state by
 }
@@ -125,18 +130,10 @@ void launch_hist_ctx(const Dims &D, float *hist, const float *m_prev, long m_sm,
                      int T, int t, const float *slot_scale, const float *gate_logit, hipStream_t st) {
     const int rows = B * D.H;
     const dim3 grid((unsigned)((rows + MW - 1) / MW)), blk(64 * MW);
-#define ADN_HC(E) hipLaunchKernelGGL(k_hist_ctx<E>, grid, blk, 0, st, D, hist, m_prev, m_sm, signal, B, T, t, \
-                                     slot_scale, gate_logit)
-    switch (D.d) {
-        case 64: ADN_HC(1); break;
-        case 128: ADN_HC(2); break;
-        case 256: ADN_HC(4); break;
-        case 512: ADN_HC(8); break;
-        case 1024: ADN_HC(16); break;
-        case 2048: ADN_HC(32); break;
-        default: break;  // rejected at context creation
-    }
-#undef ADN_HC
+dispatch_width(D.d, [&](auto Ec, auto Pc) {
+        hipLaunchKernelGGL((k_hist_ctx<decltype(Ec)::value, decltype(Pc)::value>), grid, blk, 0, st, D, hist, m_prev,
+                           m_sm, signal, B, T, t, slot_scale, gate_logit);
+    });
 }
 
 void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const float *m_prev, long m_sm,
@@ -144,18 +141,10 @@ void launch_temporal(const Dims &D, const float *h, int B, int T, int t, const f
                      hipStream_t st) {
     const int rows = B * D.H;
     const dim3 grid((unsigned)((rows + MW - 1) / MW)), blk(64 * MW);
-#define ADN_TP(E) hipLaunchKernelGGL(k_temporal<E>, grid, blk, 0, st, D, h, B, T, t, m_prev, m_sm, a_log, wx_diag, \
-                                     out, out_sm, amax)
-    switch (D.d) {
-        case 64: ADN_TP(1); break;
-        case 128: ADN_TP(2); break;
-        case 256: ADN_TP(4); break;
-        case 512: ADN_TP(8); break;
-        case 1024: ADN_TP(16); break;
-        case 2048: ADN_TP(32); break;
-        default: break;  // rejected at context creation
-    }
-#undef ADN_TP
+dispatch_width(D.d, [&](auto Ec, auto Pc) {
+        hipLaunchKernelGGL((k_temporal<decltype(Ec)::value, decltype(Pc)::value>), grid, blk, 0, st, D, h, B, T, t,
+                           m_prev, m_sm, a_log, wx_diag, out, out_sm, amax);
+    });
 }
 
 }  // namespace adn

@@ -126,12 +126,9 @@ int hip_fail(const HipError &e) {
     return fail(ADN_E_HIP, std::string("HIP error ") + hipGetErrorString(e.code) + " in " + e.where);
 }
 
-bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
-
 std::string validate_config(const adn_config &c) {
-    if (c.d_r < 64 || c.d_r > 2048 || !is_pow2(c.d_r)) return "d_r must be a power of two in [64, 2048]";
-    if (!(c.h_slots == 1 || c.h_slots == 2 || c.h_slots == 4 || c.h_slots == 8 || c.h_slots == 16))
-        return "h_slots must be 1, 2, 4, 8 or 16";
+    if (c.d_r < 64 || c.d_r > 2048 || c.d_r % 64) return "d_r must be a multiple of 64 in [64, 2048]";
+    if (c.h_slots < 1 || c.h_slots > 16) return "h_slots must be in [1, 16]";
     if (c.vocab < 1) return "vocab must be >= 1";
     if (c.d_state < 1 || c.d_state > 32) return "d_state must be in [1, 32]";
     if (c.rank < 1 || c.rank > 64) return "rank must be in [1, 64]";

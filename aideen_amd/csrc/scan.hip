@@ -30,16 +30,16 @@ constexpr int WPB = 4;
 #endif
 
 // E = d/64 values per lane, all loaded before the sum (in the same order as a strided loop)
-template <int E>
-__global__ __launch_bounds__(256) void k_row_rms(const float *h, long rows, float *rec, int REC) {
-    constexpr int d = 64 * E;
+template <int E, bool PART>
+__global__ __launch_bounds__(256) void k_row_rms(const float *h, long rows, int dd, float *rec, int REC) {
+    const int d = PART ? dd : 64 * E, er = PART ? dd / 64 : E;  // chunks e >= er are outside the row
     const long row = (long)blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float *hr = h + row * d;
     float x[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) x[e] = hr[lane + 64 * e];
+    for (int e = 0; e < E; ++e) x[e] = (!PART || e < er) ? hr[lane + 64 * e] : 0.0f;
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) ss += x[e] * x[e];
@@ -357,15 +357,10 @@ int scan_chunks(int B, int T, int H, int d) {
 
 void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipStream_t st) {
     const dim3 grid((unsigned)((rows + WPB - 1) / WPB)), blk(64 * WPB);
-    switch (d) {
-        case 64: hipLaunchKernelGGL(k_row_rms<1>, grid, blk, 0, st, h, rows, rec, REC); break;
-        case 128: hipLaunchKernelGGL(k_row_rms<2>, grid, blk, 0, st, h, rows, rec, REC); break;
-        case 256: hipLaunchKernelGGL(k_row_rms<4>, grid, blk, 0, st, h, rows, rec, REC); break;
-        case 512: hipLaunchKernelGGL(k_row_rms<8>, grid, blk, 0, st, h, rows, rec, REC); break;
-        case 1024: hipLaunchKernelGGL(k_row_rms<16>, grid, blk, 0, st, h, rows, rec, REC); break;
-        case 2048: hipLaunchKernelGGL(k_row_rms<32>, grid, blk, 0, st, h, rows, rec, REC); break;
-        default: break;  // rejected at context creation
-    }
+    dispatch_width(d, [&](auto Ec, auto Pc) {
+        hipLaunchKernelGGL((k_row_rms<decltype(Ec)::value, decltype(Pc)::value>), grid, blk, 0, st, h, rows, d, rec,
+                           REC);
+    });
 }
 
 void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,

@@ -95,8 +95,8 @@ extern "C" {
  * batch/seq capacities AIDEEN_BATCH_SIZE / AIDEEN_SEQ_CAP, gpu_deq.rs:577-596;
  * Anderson depth AIDEEN_ANDERSON_M, gpu_deq.rs:2093). */
 typedef struct adn_config {
-    int32_t d_r;        /* slot width d (multiple of 64)                         */
-    int32_t h_slots;    /* H: 1, 2, 4, 8 or 16                                   */
+    int32_t d_r;        /* slot width d: a multiple of 64 in [64, 2048]          */
+    int32_t h_slots;    /* H: 1 .. 16                                            */
     int32_t vocab;      /* V                                                     */
     int32_t d_state;    /* N: carrier states per channel (1..32)                 */
     int32_t rank;       /* write/selective rank r (multiple of 4, <= 64; ref 32) */

@@ -39,7 +39,7 @@ def test_struct_layouts_match_header():
 
 
 @pytest.mark.parametrize("bad", [
-    dict(d_r=100), dict(d_r=4096), dict(h_slots=3), dict(d_state=0), dict(d_state=64),
+    dict(d_r=100), dict(d_r=4096), dict(d_r=0), dict(h_slots=0), dict(h_slots=17), dict(d_state=0), dict(d_state=64),
     dict(rank=0), dict(max_batch=0), dict(anderson_m=6), dict(flags=1 << 13), dict(flags=(1 << 4) | (1 << 11)),
     dict(flags=1 << 10, d_state=1),
     dict(flags=1 << 9, d_state=4),

@@ -52,6 +52,8 @@ CASES = [
     dict(d=64, H=1, iters=0), dict(d=64, H=4, iters=1), dict(d=128, H=4, iters=2),
     dict(d=128, H=8, iters=10), dict(d=512, H=8, iters=2), dict(d=256, H=2, iters=40),
     dict(d=128, H=4, iters=6, anderson_m=3), dict(d=128, H=8, iters=3, anderson_m=4),
+    # widths other than powers of two (the reference's benchmark width 192) and odd slot counts
+    dict(d=192, H=6, iters=2), dict(d=320, H=3, iters=0), dict(d=1536, H=5, iters=3),
 ]
 # With three or more residuals (anderson_m >= 4 past the third step) the mixing solves a 3x3 (4x4)
 # Gram system of differences of the adjoint's nearly collinear iterates: condition numbers 4e5-2e6

@@ -151,6 +151,14 @@ def test_memory_errors():
         bc.decode_greedy(np.array([[1, 2], [3, 4]], np.int32), 3, 4)
 
 
+def test_memory_reference_shape(oracle_lib):
+    """A width and slot count other than powers of two (d = 192, H = 6) in memory mode."""
+    log("memory d=192 H=6")
+    mc, w = mem_model(192, 6, 300)
+    toks = synth.make_tokens("uniform", 2, 11, mc.V, seed=15)
+    check(gpu_memory(mc, w, toks), oracle_lib.Oracle(mc, w).forward_memory(toks), "d192 H6")
+
+
 @pytest.mark.parametrize("pen", [1.0, 1.5])
 def test_memory_greedy_decode_matches_oracle(oracle_lib, pen):
     """The fixed-history form of Trainer::generate (trainer.rs:4395-4400, 677-735): the memory is

@@ -165,6 +165,39 @@ def test_many_token_update_matches_oracle(oracle_lib, var):
     assert_forward_parity(got, ref, str(var))
 
 
+# ArchitectureConfig allows any d_r and h_slots (aideen-core/src/state.rs:7-58); the reference's own
+# benchmark runs d_r = 192 with the default 8 slots (aideen-bench/src/main.rs:36).  Widths other
+# than powers of two run the kernels' bucketed instantiations, slot counts other than powers of
+# two the run-time-H attention.  Few tokens (<= 512) and many tokens take different update
+# kernels; every width bucket (d/64 of 3, 5, 24) appears.
+REF_SHAPES = [
+    dict(d=192, H=8, V=65, N=1, flags=0, B=3, T=37),                                        # arch_bench shape
+    dict(d=192, H=6, V=300, N=4, flags=synth.F_SCAN_SELECTIVE, anderson_m=3, B=3, T=37),
+    dict(d=320, H=3, V=500, N=16, flags=synth.F_SCAN_SELECTIVE | synth.F_SCORE_CLAMP4, B=5, T=131),
+    dict(d=1536, H=5, V=300, N=2, flags=synth.F_SCAN_SELECTIVE | synth.F_RESID_RELRMS, B=5, T=131),
+    dict(d=192, H=12, V=300, N=4, flags=synth.F_SCAN_SELECTIVE | synth.F_RMS_EXCL_ANCHOR | synth.F_INIT_SIGNAL_RMS,
+         B=5, T=131),
+]
+
+
+@pytest.mark.parametrize("var", REF_SHAPES, ids=lambda v: "-".join(f"{k}{v[k]}" for k in v))
+def test_reference_shapes_match_oracle(oracle_lib, var):
+    var = dict(var)
+    B, T = var.pop("B"), var.pop("T")
+    log(f"reference shape {var} B={B} T={T}")
+    mc, w = _small(**var)
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=5)
+    ref = oracle_lib.Oracle(mc, w).forward(toks, nthreads=16)
+    be = make(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks)
+    assert_forward_parity(got, ref, str(var))
+    # the carrier alone (its own row-RMS pass instead of the pooling kernel's)
+    only = be.forward(toks, want=("scan_y", "scan_state", "iters"))
+    np.testing.assert_allclose(only["scan_y"], ref["scan_y"], rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(only["scan_state"], ref["scan_state"], rtol=RTOL, atol=ATOL)
+
+
 def test_homeostatic_exit_shortens_the_solve(oracle_lib):
     """With damping 0.1 the relative residual shrinks slowly; the plateau rule stops the tokens
     well before the tolerance would (GPU and oracle agree on every count), and without the flag
