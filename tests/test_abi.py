@@ -64,3 +64,14 @@ def test_null_arguments_are_errors():
     assert L.adn_synchronize(None) == _lib.ADN_E_INVALID
     assert L.adn_forward(None, None, None) == _lib.ADN_E_INVALID
     L.adn_destroy(None)
+
+
+def test_integration_ffi_block_binds_every_header_symbol():
+    """INTEGRATION.md's `extern "C"` block (the Rust -sys crate a maintainer adds) declares every
+    function the header does, and nothing else."""
+    import os
+    text = open(os.path.join(os.path.dirname(_lib.HEADER), "..", "INTEGRATION.md")).read()
+    block = text[text.index('extern "C" {'):]
+    block = block[:block.index("\n}\n")]
+    names = sorted(set(re.findall(r"pub fn (adn_\w+)\s*\(", block)))
+    assert names == _lib.header_functions()
