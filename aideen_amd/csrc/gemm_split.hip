@@ -189,12 +189,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     }
     floatx16 acc[WTM][WTN];
 
-    // Fragments in registers: A of a slice is read raw (fp32) one step ahead and split just
-    // before its slice is multiplied; B is streamed one 32-column tile at a time through two
-    // buffers, tile j + 1 (or the next slice's tile 0) being read while tile j's MFMAs run, so
-    // that the LDS reads are spread over the MFMA phase instead of preceding it.
+    // Fragments in registers.  B is streamed one 32-column tile at a time through two buffers,
+    // tile j + 1 (or the next slice's tile 0) being read while tile j's MFMAs run.  A of the next
+    // slice is read raw (fp32) at the top of a slice and split into its halves in pieces placed
+    // between the current slice's MFMAs, so that the split's VALU work issues while the matrix
+    // core is busy; the split halves are double-buffered (ah/al[P] in use, [P ^ 1] being
+    // filled) and the k loop is unrolled by two so that the buffers swap without moves.
     floatx4 anx[WTM][2];
-    V8 ah[WTM], al[WTM];
+    V8 ah[2][WTM], al[2][WTM];
     V8 bq[2][PARTS];
     auto read_a = [&](int st) {
 #pragma unroll
@@ -204,30 +206,35 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
             anx[i][1] = *reinterpret_cast<const floatx4 *>(&As[st][row][pa1]);
         }
     };
-    auto split_a = [&]() {
+    // The empty asm pins the halves where they are formed: without it the compiler sinks a
+    // piece into the next slice's block, after its barrier, out of reach of the MFMAs it is
+    // meant to overlap.
+    auto split_i = [&](int i, V8 &h, V8 &l) {
 #pragma unroll
-        for (int i = 0; i < WTM; ++i)
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float x = anx[i][q >> 2][q & 3] * asc;
-                const T hv = (T)x;
-                ah[i][q] = hv;
-                if constexpr (TERMS == 3) al[i][q] = (T)(x - (float)hv);
-            }
+        for (int q = 0; q < 8; ++q) {
+            const float x = anx[i][q >> 2][q & 3] * asc;
+            const T hv = (T)x;
+            h[q] = hv;
+            if constexpr (TERMS == 3) l[q] = (T)(x - (float)hv);
+        }
+        if constexpr (TERMS == 3)
+            asm volatile("" : "+v"(h), "+v"(l));
+        else
+            asm volatile("" : "+v"(h));
     };
     auto read_b = [&](int st, int j, V8 (&bb)[PARTS]) {
         const int row = (wn * WTN + j) * 32 + r;
 #pragma unroll
         for (int q = 0; q < PARTS; ++q) bb[q] = *reinterpret_cast<const V8 *>(&Bs[st][q][row][pb]);
     };
-    auto mfma_tile = [&](int j, const V8 (&bb)[PARTS]) {
+    auto mfma_tile = [&](int j, const V8 (&bb)[PARTS], const V8 (&h)[WTM], const V8 (&l)[WTM]) {
 #pragma unroll
         for (int i = 0; i < WTM; ++i) {
             if constexpr (TERMS == 3) {
-                acc[i][j] = mfma16(al[i], bb[0], acc[i][j]);
-                acc[i][j] = mfma16(ah[i], bb[1], acc[i][j]);
+                acc[i][j] = mfma16(l[i], bb[0], acc[i][j]);
+                acc[i][j] = mfma16(h[i], bb[1], acc[i][j]);
             }
-            acc[i][j] = mfma16(ah[i], bb[0], acc[i][j]);
+            acc[i][j] = mfma16(h[i], bb[0], acc[i][j]);
         }
     };
 
@@ -236,6 +243,52 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
 #pragma unroll
         for (int st = 0; st < STAGES - 1; ++st)
             if (st < nk) issue(st, st);
+    };
+    // One 16-K slice: P selects the split A buffer in use.
+    auto step = [&](int kt, auto par) {
+        constexpr int P = decltype(par)::value;
+        const int cs = kt % STAGES, ns = (kt + 1) % STAGES;
+        if (kt + 1 < nk) {
+            // slice kt+1 visible: this wave's loads of it are done once at most STAGES-3 later
+            // slices are in flight; the barrier covers the other waves' loads and their reads of
+            // the slot about to be refilled (slice kt-1's, last read in the previous step)
+            if (kt + STAGES - 2 < nk)
+                wait_vmcnt<(STAGES - 3) * LOADS>();
+            else
+                wait_vmcnt<0>();
+            lds_barrier();
+            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+        }
+        // The reads below are unconditional so that the wait counts stay exact: after the last
+        // slice they read a slot no load writes any more, and the values are not used.
+        // sched_barrier keeps each tile's reads ahead of the previous tile's MFMAs; within a
+        // tile the split pieces are interleaved with the MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+            if (j == 0) read_a(ns);
+            read_b(j + 1 < WTN ? cs : ns, (j + 1) % WTN, bq[(j + 1) & 1]);
+            mfma_tile(j, bq[j & 1], ah[P], al[P]);
+            if (j >= 1 && j - 1 < WTM) split_i(j - 1, ah[P ^ 1][j - 1], al[P ^ 1][j - 1]);
+            // Order within the tile: its first MFMA (whose operands were read a tile earlier:
+            // the wait before it then covers only those), the reads for the next tile, then the
+            // remaining MFMAs each followed by up to 6 split instructions.
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, PARTS + 2 * WTM, 0);
+#pragma unroll
+            for (int u = 1; u < WTM * (TERMS == 3 ? 3 : 1); ++u) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (WTN & 1) {  // the next slice's tile 0 went to buffer 1
+#pragma unroll
+            for (int q = 0; q < PARTS; ++q) bq[0][q] = bq[1][q];
+        }
+#pragma unroll
+        for (int i = WTN - 1; i < WTM; ++i)
+            if (i >= 0) split_i(i, ah[P ^ 1][i], al[P ^ 1][i]);
     };
     set_tile(t);
     prologue();
@@ -258,38 +311,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     lds_barrier();
     read_a(0);
     read_b(0, 0, bq[0]);
-    split_a();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cs = kt % STAGES, ns = (kt + 1) % STAGES;
-        if (kt + 1 < nk) {
-            // slice kt+1 visible: this wave's loads of it are done once at most STAGES-3 later
-            // slices are in flight; the barrier covers the other waves' loads and their reads of
-            // the slot about to be refilled (slice kt-1's, last read in the previous step)
-            if (kt + STAGES - 2 < nk)
-                wait_vmcnt<(STAGES - 3) * LOADS>();
-            else
-                wait_vmcnt<0>();
-            lds_barrier();
-            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        }
-        // The reads below are unconditional so that the wait counts stay exact: after the last
-        // slice they read a slot no load writes any more, and the values are not used.
-        // sched_barrier keeps each tile's reads ahead of the previous tile's MFMAs.
-        __builtin_amdgcn_sched_barrier(0);
-        read_a(ns);
 #pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-            read_b(j + 1 < WTN ? cs : ns, (j + 1) % WTN, bq[(j + 1) & 1]);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_tile(j, bq[j & 1]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (WTN & 1) {  // the next slice's tile 0 went to buffer 1
-#pragma unroll
-            for (int q = 0; q < PARTS; ++q) bq[0][q] = bq[1][q];
-        }
-        split_a();
+    for (int i = 0; i < WTM; ++i) split_i(i, ah[0][i], al[0][i]);
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        step(kt, std::integral_constant<int, 0>());
+        step(kt + 1, std::integral_constant<int, 1>());
     }
+    if (kt < nk) step(kt, std::integral_constant<int, 0>());
     lds_barrier();  // every wave is done with the ring
     // The next tile's first slices are loaded into ring slots 0..STAGES-2 while this tile's
     // results are stored; the epilogue's LDS scratch (arg-max partials) is slot STAGES-1.
