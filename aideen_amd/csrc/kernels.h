@@ -167,8 +167,10 @@ void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipSt
 // amax_y (or null): raised to the largest finite |y| (the readout GEMM's A scale).
 void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
                  const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
-                 float *state_out, float *chunk_s, float *chunk_p, int nch, unsigned *amax_y, hipStream_t st);
-int scan_chunks(int B, int T, int H, int d);
+                 float *state_out, float *chunk_s, float *chunk_p, int nch, unsigned *amax_y, bool ssd,
+                 hipStream_t st);
+int scan_chunks(int B, int T, int H, int d, bool ssd);
+bool scan_use_ssd(const Dims &D, int B, int T, float min_fixed_decay);
 
 // ---- misc (misc.hip) ----------------------------------------------------------------------
 void launch_spectral_norm(const float *w, int rows, int cols, int n_iter, float *sigma,

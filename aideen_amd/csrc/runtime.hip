@@ -87,6 +87,7 @@ struct adn_ctx {
     float l1_wv = 0.0f;        // largest row L1 norm of W_v: |mix| <= l1_wv |h|
     float l1_wout = 0.0f;      // largest row L1 norm of W_out: |m_t| <= (1 + l1_wout) |m_inner|
     float lm_a_scale = 1.0f;   // LM head A scale: |pnorm| <= max|lm_g| sqrt(d)
+    float scan_min_decay = 0.0f;  // min over channels of the fixed carrier decay sigmoid(-a_log)
     unsigned *d_err = nullptr;
 
     // host-API staging (lazy, capacity-sized)
@@ -501,13 +502,14 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
         if (!prep_done) enqueue_scan_prep(c, ntok, b, prof, false);
         // chunk buffers hold max_batch * scan_nch_cap sequence-chunks
         const int nch_fit = std::max(1, (c->cfg.max_batch * c->scan_nch_cap) / r.batch);
-        const int nch = std::min(std::min(scan_chunks(r.batch, r.seq, H, d), c->scan_nch_cap), nch_fit);
+        const bool ssd = scan_use_ssd(D, r.batch, r.seq, c->scan_min_decay);
+        const int nch = std::min(std::min(scan_chunks(r.batch, r.seq, H, d, ssd), c->scan_nch_cap), nch_fit);
         float *y = (o.scan_y && !c->w_out) ? o.scan_y : c->scb.y;
         {
             Span sp(prof, ADN_STAGE_SCAN, nch, st);
             launch_scan(D, b.h, c->scb.rec, r.batch, r.seq, c->w_b != nullptr, c->a_log, c->wx_diag, c->b_delta,
                         c->w_vw, r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch,
-                        c->bounds + 1, st);
+                        c->bounds + 1, ssd, st);
         }
         if (o.scan_y && c->w_out) {
             GemmParams g{};
@@ -866,6 +868,11 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
         upload(c, &c->lm_b, w->lm_b, V, "lm_b", false);
         upload(c, &c->lm_g, w->lm_g, d, "lm_g", false);
         upload(c, &c->a_log, w->a_log, (size_t)H * d, "a_log", true);
+        {
+            float mn = 1.0f;
+            for (size_t i = 0; i < (size_t)H * d; ++i) mn = std::min(mn, 1.0f / (1.0f + std::exp(w->a_log[i])));
+            c->scan_min_decay = mn;  // NaN a_log compares false: a NaN decay leaves mn as it was
+        }
         upload(c, &c->wx_diag, w->wx_diag, (size_t)H * d, "wx_diag", true);
         if (w->w_out) {
             if (!c->w_out) c->w_out = (float *)dmalloc(c, H * mat * sizeof(float));

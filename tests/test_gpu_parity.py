@@ -280,6 +280,41 @@ def test_scan_state_continuation():
     np.testing.assert_allclose(second["scan_state"], full["scan_state"], rtol=1e-5, atol=1e-5)
 
 
+# The carrier scan runs in chunked matrix form (inputs scaled by 16-step decay products) where the
+# per-step recurrence would be split into time chunks (few sequences: B = 2, T = 300 here, which the
+# matrix form runs as two time chunks of 150 steps, not a multiple of its 16-step tile) and the
+# decay is selective (at least 0.1) or every fixed decay is at least 0.02; otherwise as the per-step
+# recurrence (B = 3, T = 53 here, and fixed decays down to 0.005).  5 and 9 states (padded to a
+# 16-state tile), 16 and 32 states.
+SCAN_PATHS = [
+    dict(lo=0.03, N=16, flags=0, B=3, T=53),
+    dict(lo=0.005, N=16, flags=0, B=3, T=53),
+    dict(lo=0.03, N=5, flags=0, B=2, T=300),
+    dict(lo=0.005, N=5, flags=0, B=2, T=300),
+    dict(lo=None, N=32, flags=synth.F_SCAN_SELECTIVE, B=2, T=300),
+    dict(lo=None, N=9, flags=synth.F_SCAN_SELECTIVE, B=3, T=53),
+]
+
+
+@pytest.mark.parametrize("var", SCAN_PATHS, ids=lambda v: "-".join(f"{k}{v[k]}" for k in v))
+def test_scan_paths_match_oracle(oracle_lib, var):
+    log(f"scan path {var}")
+    mc, w = _small(d=128, H=4, V=300, N=var["N"], flags=var["flags"])
+    if var["lo"] is not None:  # fixed decays spread from lo to 0.999 over the channels
+        a = var["lo"] + np.linspace(0.0, 1.0, mc.H * mc.d).reshape(mc.H, mc.d) * (0.999 - var["lo"])
+        w["a_log"] = np.log((1.0 - a) / a).astype(np.float32)
+    B, T = var["B"], var["T"]
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=9)
+    be = make(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks, want=("h_star", "scan_y", "scan_state"))
+    o = oracle_lib.Oracle(mc, w)
+    for b in range(B):
+        y, st = o.scan(got["h_star"][b])
+        np.testing.assert_allclose(got["scan_y"][b], y, rtol=RTOL, atol=ATOL, err_msg=f"{var} scan_y[{b}]")
+        np.testing.assert_allclose(got["scan_state"][b], st, rtol=RTOL, atol=ATOL, err_msg=f"{var} state[{b}]")
+
+
 @pytest.mark.parametrize("pen", [1.0, 1.3])
 def test_greedy_decode_matches_oracle(oracle_lib, pen):
     """Trainer::generate's greedy loop: embed_context of the last ctx_len tokens (the window slides
