@@ -312,30 +312,33 @@ __device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[
         else
             epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, true>(p, acc, c);
     } else if constexpr (ROLE == ROLE_LMHEAD) {
-        // the arg-max branch and the bias branch are uniform over the grid
+        // the arg-max branch and the bias branch are uniform over the grid; the logits (nothing in
+        // the forward reads them back) are stored non-temporally, which keeps the A rows and weights
+        // of the tiles still being multiplied in L2
+        constexpr bool LM_ST = true;
         if (p.am_val) {
             if (p.epi == EPI_BIAS) {
                 if (interior)
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, false>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, false, LM_ST>(p, acc, c);
                 else
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, true>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, true, LM_ST>(p, acc, c);
             } else {
                 if (interior)
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, false>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, false, LM_ST>(p, acc, c);
                 else
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, true>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, true, LM_ST>(p, acc, c);
             }
         } else {
             if (p.epi == EPI_BIAS) {
                 if (interior)
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false, LM_ST>(p, acc, c);
                 else
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, true>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, true, LM_ST>(p, acc, c);
             } else {
                 if (interior)
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false, LM_ST>(p, acc, c);
                 else
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true, LM_ST>(p, acc, c);
             }
         }
     } else {
