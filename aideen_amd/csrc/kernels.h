@@ -168,7 +168,7 @@ void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipSt
 void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
                  const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
                  float *state_out, float *chunk_s, float *chunk_p, int nch, unsigned *amax_y, bool ssd,
-                 hipStream_t st);
+                 float min_fixed_decay, hipStream_t st);
 int scan_chunks(int B, int T, int H, int d, bool ssd);
 bool scan_use_ssd(const Dims &D, int B, int T, float min_fixed_decay);
 

@@ -509,7 +509,7 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
             Span sp(prof, ADN_STAGE_SCAN, nch, st);
             launch_scan(D, b.h, c->scb.rec, r.batch, r.seq, c->w_b != nullptr, c->a_log, c->wx_diag, c->b_delta,
                         c->w_vw, r.scan_state_in, y, o.scan_state, c->scb.chunk_s, c->scb.chunk_p, nch,
-                        c->bounds + 1, ssd, st);
+                        c->bounds + 1, ssd, c->scan_min_decay, st);
         }
         if (o.scan_y && c->w_out) {
             GemmParams g{};

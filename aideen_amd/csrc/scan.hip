@@ -61,12 +61,16 @@ constexpr int TC = 16;
 // MODE 0: whole sequence from state_in, emit y and state_out.
 // MODE 1: chunk pass A, zero start, emit the chunk's end state and decay product.
 // MODE 2: chunk pass C, start from chunk_s (carried), emit y; the last chunk writes state_out.
-// Per TC steps the record values a step needs (1/rms, and divided by rms the rank-r projections
-// and B/C) are staged in LDS; h and the next TC steps' record values are fetched into a second
-// register set before the current steps are processed (a load issued after stores would wait
-// behind them: the vector-memory counter retires in issue order).  RK: rank bucket (0 = not
-// selective); EXACT: NS == N.
-template <int NS, int RK, int MODE, bool EXACT>
+// Per TC steps the record values a step needs (1/rms, the rank-r projections, B and C) are staged
+// raw in LDS and the 1/rms scales applied where they are used; h and the next TC steps' record
+// values are fetched into a second register set before the current steps are processed (a load
+// issued after stores would wait behind them: the vector-memory counter retires in issue order).
+// NORM: within a block of TC steps the states are carried divided by the block's running decay
+// product P (m = P mh): mh[n] += B[n] (xin / P), y = P sum_n C[n] mh[n], one FMA per state and
+// step instead of two; m = P mh at the block's end.  It needs every TC-step decay product to stay
+// a normal fp32 number (the selective decay is at least 0.1; a fixed one is checked at upload).
+// RK: rank bucket (0 = not selective); EXACT: NS == N.
+template <int NS, int RK, int MODE, bool EXACT, bool NORM>
 __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__restrict__ h,
                                                         const float *__restrict__ rec, int T, int nch, int has_bc,
                                                         const float *__restrict__ a_log,
@@ -78,11 +82,12 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
                                                         float *__restrict__ chunk_p, unsigned *amax_y) {
     constexpr bool SEL = RK > 0;
     constexpr int RKA = SEL ? RK : 0;
-    constexpr int BC0 = 4 + RKA;         // staged step: [0] 1/rms, [4 + q] projection q / rms,
-    constexpr int SW = BC0 + 2 * NS;     // [BC0 + n] B[n] / rms, [BC0 + NS + n] C[n] / rms
+    constexpr int BC0 = 4 + RKA;         // staged step: [0] 1/rms, [4 + q] projection q,
+    constexpr int SW = BC0 + 2 * NS;     // [BC0 + n] B[n], [BC0 + NS + n] C[n] (un-normalised)
     constexpr int QMAX = 1 + RKA + 2 * NS;
     constexpr int RPT = (TC * QMAX + SCAN_NT - 1) / SCAN_NT;  // staged values per thread
     __shared__ __attribute__((aligned(16))) float sr[TC][SW];
+    float *srf = &sr[0][0];
     // the rank-r term of every step of every channel, [channel][step] (row stride TC + 4: the
     // b128 writes and reads of eight consecutive rows hit distinct banks)
     __shared__ __attribute__((aligned(16))) float sp[SEL ? SCAN_NT : 1][TC + 4];
@@ -100,6 +105,35 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
     const int t0 = c * Tc, t1 = min(T, t0 + Tc);
     const int dd = active ? dim : 0;
     const int nq = 1 + RKA + 2 * N;  // staged values per step (bucket-padded rank; B = C = 1 without has_bc)
+    // this thread's staged values (fixed over the blocks): LDS offset, step, record field; the
+    // value staged is 1 / x for the rms, else x * s_mul + s_add (threads without a value write the
+    // unused column 1 of step 0)
+    int s_off[RPT], s_j[RPT], s_f[RPT];
+    bool s_inv[RPT];
+    float s_mul[RPT], s_add[RPT];
+#pragma unroll
+    for (int q2 = 0; q2 < RPT; ++q2) {
+        const int idx = tid + q2 * SCAN_NT;
+        s_off[q2] = 1;
+        s_j[q2] = 0;
+        s_f[q2] = 0;
+        s_inv[q2] = false;
+        s_mul[q2] = 0.0f;
+        s_add[q2] = 0.0f;
+        if (idx < TC * nq) {
+            const int j = idx / nq, q = idx - j * nq;
+            const int qb = q - 1 - RKA;  // B[0..N) then C[0..N) in the record; C staged at BC0 + NS
+            const int slot = q == 0 ? 0 : (q <= RKA ? 4 + (q - 1) : BC0 + (qb < N ? qb : NS + qb - N));
+            const int f = q == 0 ? 0 : (q <= RKA ? (q - 1 < r ? q : -1) : 1 + r + qb);
+            const int kind = q == 0 ? 0 : (q <= RKA ? (f >= 0 ? 1 : 3) : (has_bc ? 1 : 2));
+            s_off[q2] = j * SW + slot;
+            s_j[q2] = j;
+            s_f[q2] = f < 0 ? 0 : f;
+            s_inv[q2] = kind == 0;
+            s_mul[q2] = kind == 1 ? 1.0f : 0.0f;
+            s_add[q2] = kind == 2 ? 1.0f : 0.0f;
+        }
+    }
 
     // per-channel constants
     const float al = a_log[(long)s * d + dd];
@@ -136,18 +170,13 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
     float ymax = 0.0f;  // largest finite |y| this thread stores
 
     struct Chunk {
-        float hv[TC], rv[RPT], rr[RPT];
+        float hv[TC], rv[RPT];
     };
     const long tstride = (long)H * d;                          // one time step of (b, s, dim)
     const long gbase = (long)b * T * tstride + (long)s * d + dd;  // (b, t = 0, s, dd)
+    const long rstride = (long)H * REC;                        // one time step of the records
     const int last = t1 - 1;
-    // staged value q of a step -> its record field (0: rms, 1 + q': projection q' < r, padded
-    // projections -1 (zero), then B and C)
-    auto field = [&](int q) {
-        if (q == 0) return 0;
-        if (q <= RKA) return q - 1 < r ? q : -1;
-        return 1 + r + (q - 1 - RKA);
-    };
+    const float *recb = rec + ((long)b * T * H + s) * REC;
     // h is read again by pass C after pass A (through the caches where it fits): non-temporal
     // only where this is its last read
     auto fetch = [&](Chunk &k, int tb) {
@@ -164,27 +193,14 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
             }
         }
 #pragma unroll
-        for (int q2 = 0; q2 < RPT; ++q2) {
-            const int idx = min(tid + q2 * SCAN_NT, TC * nq - 1);
-            const int j = idx / nq, q = idx - j * nq;
-            const float *rc = rec + (((long)b * T + min(tb + j, last)) * H + s) * REC;
-            const int f = field(q);
-            k.rv[q2] = f >= 0 ? rc[f] : 0.0f;
-            k.rr[q2] = rc[0];
-        }
+        for (int q2 = 0; q2 < RPT; ++q2) k.rv[q2] = recb[(long)min(tb + s_j[q2], last) * rstride + s_f[q2]];
     };
     auto process = [&](const Chunk &k, int tb) {
         const int nt = min(TC, t1 - tb);
 #pragma unroll
         for (int q2 = 0; q2 < RPT; ++q2) {
-            const int idx = tid + q2 * SCAN_NT;
-            if (idx < nt * nq) {
-                const int j = idx / nq, q = idx - j * nq;
-                const float inv = 1.0f / k.rr[q2];
-                const int qb = q - 1 - RKA;  // B[0..N) then C[0..N) in the record; C staged at BC0 + NS
-                const int slot = q == 0 ? 0 : (q <= RKA ? 4 + (q - 1) : BC0 + (qb < N ? qb : NS + qb - N));
-                sr[j][slot] = q == 0 ? inv : (q > RKA && !has_bc) ? 1.0f : k.rv[q2] * inv;
-            }
+            const float x = k.rv[q2];
+            srf[s_off[q2]] = s_inv[q2] ? __builtin_amdgcn_rcpf(x) : x * s_mul[q2] + s_add[q2];
         }
         __syncthreads();
         // the rank-r dot of every step, W_vw^T (W_kw^T u), on the matrix cores: per rank block of
@@ -217,37 +233,53 @@ __global__ __launch_bounds__(SCAN_NT) void k_scan_fused(Dims D, const float *__r
                 pj[4 * q + 3] = v[3];
             }
         }
+        float P = 1.0f;  // NORM: the block's running decay product (m = P mh)
 #pragma unroll
         for (int j = 0; j < TC; ++j) {
             if (j < nt) {
                 const float inv = sr[j][0];
+                const float cs = has_bc ? inv : 1.0f;  // B and C are projections of u = h / rms
                 const float u = k.hv[j] * inv;
                 const float x = u + wxh * u;
                 float abar = abase;
                 if constexpr (SEL) {
-                    const float pre = bd + pj[j];
+                    const float pre = bd + pj[j] * inv;
                     const float l2 = __builtin_amdgcn_logf(1.0f + __builtin_amdgcn_exp2f(pre * 1.44269504088896341f));
                     abar = 0.10f + (1.0f - 0.10f) * __builtin_amdgcn_exp2f(l2 * ln_ab);
                 }
-                const float xin = (1.0f - abar) * x;
+                const float xin = (1.0f - abar) * x * cs;
                 float a2[2] = {0.0f, 0.0f};
+                if constexpr (NORM) {
+                    P *= abar;
+                    const float z = xin * __builtin_amdgcn_rcpf(P);
 #pragma unroll
-                for (int n = 0; n < NS; ++n) {
-                    if (EXACT || n < N) {
-                        const float Bn = sr[j][BC0 + n];
-                        const float Cn = sr[j][BC0 + NS + n];
-                        m[n] = abar * m[n] + Bn * xin;
-                        a2[n & 1] += Cn * m[n];
+                    for (int n = 0; n < NS; ++n) {
+                        if (EXACT || n < N) {
+                            m[n] += sr[j][BC0 + n] * z;
+                            a2[n & 1] += sr[j][BC0 + NS + n] * m[n];
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int n = 0; n < NS; ++n) {
+                        if (EXACT || n < N) {
+                            m[n] = abar * m[n] + sr[j][BC0 + n] * xin;
+                            a2[n & 1] += sr[j][BC0 + NS + n] * m[n];
+                        }
                     }
                 }
                 if (MODE == 1) {
                     prod *= abar;
                 } else if (active) {
-                    const float yv = a2[0] + a2[1];
+                    const float yv = (NORM ? P : 1.0f) * cs * (a2[0] + a2[1]);
                     y[gbase + (long)(tb + j) * tstride] = yv;
                     ymax = fmaxf(ymax, fabsf(yv) < INFINITY ? fabsf(yv) : 0.0f);
                 }
             }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int n = 0; n < NS; ++n) m[n] *= P;
         }
         __syncthreads();
     };
@@ -634,11 +666,12 @@ struct ScanArgs {
     unsigned *amax_y;
 };
 
-template <int NS, int RK, bool EXACT>
+template <int NS, int RK, bool EXACT, bool NORM>
 void scan_modes(const Dims &D, const ScanArgs &a, hipStream_t st) {
     const dim3 grid((unsigned)((D.d + SCAN_NT - 1) / SCAN_NT), (unsigned)D.H, (unsigned)(a.B * a.nch));
 #define ADN_SCAN_K(MODE)                                                                                          \
-    hipLaunchKernelGGL((k_scan_fused<NS, RK, MODE, EXACT>), grid, dim3(SCAN_NT), 0, st, D, a.h, a.rec, a.T, a.nch, \
+    hipLaunchKernelGGL((k_scan_fused<NS, RK, MODE, EXACT, NORM>), grid, dim3(SCAN_NT), 0, st, D, a.h, a.rec, a.T,  \
+                       a.nch,                                                                                     \
                        a.has_bc, a.a_log, a.wx_diag, a.b_delta, a.w_vw, a.state_in, a.y, a.state_out, a.chunk_s,   \
                        a.chunk_p, a.amax_y)
     if (a.nch <= 1) {
@@ -680,18 +713,18 @@ void scan_ssd_n(const Dims &D, const ScanArgs &a, hipStream_t st) {
         scan_modes_ssd<32, RK>(D, a, st);
 }
 
-template <int RK>
+template <int RK, bool NORM>
 void scan_n(const Dims &D, const ScanArgs &a, hipStream_t st) {
     if (D.N == 16)
-        scan_modes<16, RK, true>(D, a, st);
+        scan_modes<16, RK, true, NORM>(D, a, st);
     else if (D.N == 1)
-        scan_modes<1, RK, true>(D, a, st);
+        scan_modes<1, RK, true, NORM>(D, a, st);
     else if (D.N == 32)
-        scan_modes<32, RK, true>(D, a, st);
+        scan_modes<32, RK, true, NORM>(D, a, st);
     else if (D.N <= 8)
-        scan_modes<8, RK, false>(D, a, st);
+        scan_modes<8, RK, false, NORM>(D, a, st);
     else
-        scan_modes<32, RK, false>(D, a, st);
+        scan_modes<32, RK, false, NORM>(D, a, st);
 }
 
 }  // namespace
@@ -740,7 +773,7 @@ void launch_row_rms(const float *h, long rows, int d, float *rec, int REC, hipSt
 void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, int has_bc, const float *a_log,
                  const float *wx_diag, const float *b_delta, const float *w_vw, const float *state_in, float *y,
                  float *state_out, float *chunk_s, float *chunk_p, int nch, unsigned *amax_y, bool ssd,
-                 hipStream_t st) {
+                 float min_fixed_decay, hipStream_t st) {
     const ScanArgs a{h,     rec, B,       T,       has_bc,  a_log, wx_diag, b_delta, w_vw, state_in,
                      y,     state_out, chunk_s, chunk_p, nch, amax_y};
     if (ssd) {
@@ -752,12 +785,18 @@ void launch_scan(const Dims &D, const float *h, const float *rec, int B, int T, 
             scan_ssd_n<64>(D, a, st);
         return;
     }
-    if (!(D.flags & ADN_F_SCAN_SELECTIVE))
-        scan_n<0>(D, a, st);
-    else if (D.r <= 32)
-        scan_n<32>(D, a, st);
-    else
-        scan_n<64>(D, a, st);
+    // the per-step form carries the states divided by the block's decay product where every
+    // 16-step product stays normal (the same condition as the matrix form's)
+    if (!(D.flags & ADN_F_SCAN_SELECTIVE)) {
+        if (min_fixed_decay >= 0.02f)
+            scan_n<0, true>(D, a, st);
+        else
+            scan_n<0, false>(D, a, st);
+    } else if (D.r <= 32) {
+        scan_n<32, true>(D, a, st);
+    } else {
+        scan_n<64, true>(D, a, st);
+    }
 }
 
 }  // namespace adn
