@@ -293,13 +293,16 @@ SCAN_PATHS = [
     dict(lo=0.005, N=5, flags=0, B=2, T=300),
     dict(lo=None, N=32, flags=synth.F_SCAN_SELECTIVE, B=2, T=300),
     dict(lo=None, N=9, flags=synth.F_SCAN_SELECTIVE, B=3, T=53),
+    # widths that leave part of the matrix form's 128-channel block without channels
+    dict(lo=None, N=16, flags=synth.F_SCAN_SELECTIVE, B=2, T=300, d=192, H=3),
+    dict(lo=0.03, N=4, flags=0, B=2, T=200, d=64, H=2),
 ]
 
 
 @pytest.mark.parametrize("var", SCAN_PATHS, ids=lambda v: "-".join(f"{k}{v[k]}" for k in v))
 def test_scan_paths_match_oracle(oracle_lib, var):
     log(f"scan path {var}")
-    mc, w = _small(d=128, H=4, V=300, N=var["N"], flags=var["flags"])
+    mc, w = _small(d=var.get("d", 128), H=var.get("H", 4), V=300, N=var["N"], flags=var["flags"])
     if var["lo"] is not None:  # fixed decays spread from lo to 0.999 over the channels
         a = var["lo"] + np.linspace(0.0, 1.0, mc.H * mc.d).reshape(mc.H, mc.d) * (0.999 - var["lo"])
         w["a_log"] = np.log((1.0 - a) / a).astype(np.float32)
