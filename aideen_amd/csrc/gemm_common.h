@@ -271,7 +271,9 @@ __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WT
         static_assert(CPW == 64 || CPW == 128, "arg-max partials need 64 or 128 columns per wave");
         constexpr int TPW = 128 / CPW;
         constexpr int QT = WGN / TPW;  // 128-column tiles per block
-        lds_barrier();  // the partials are exchanged through LDS; the logits stores need not wait
+        // the partials are exchanged through LDS; the logits stores need not wait.  A one-wave
+        // block reads back its own writes (a wave's LDS operations complete in order).
+        if constexpr (WGM * WGN > 1) lds_barrier();
         const int tid = threadIdx.x;
         for (int idx = tid; idx < BMt * QT; idx += 64 * WGM * WGN) {
             const int ml = idx % BMt, q = idx / BMt;

@@ -348,6 +348,9 @@ template <int ROLE, typename T, int TERMS, int KW, int WTN>
 __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     typedef typename Vec8<T>::type V8;
     __shared__ float red[KW > 1 ? KW - 1 : 1][WTN * 16][64];  // [wave-1][element][lane]
+    // LM head: the 32 rows' (max, arg-max) partials of the block's 128 columns
+    __shared__ float am_v[ROLE == ROLE_LMHEAD ? 32 : 1];
+    __shared__ int am_i[ROLE == ROLE_LMHEAD ? 32 : 1];
     constexpr int BNt = 32 * WTN;
     const int nN = (p.N + BNt - 1) / BNt;
     int s, mt, nt;
@@ -447,7 +450,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[0][j][e] += red[w][j * 16 + e][lane];
     }
-    epilogue_t<ROLE, 1, WTN, 1, 1>(p, acc, M, s, 0, n0, osc, nullptr, nullptr);
+    epilogue_t<ROLE, 1, WTN, 1, 1>(p, acc, M, s, 0, n0, osc, am_v, am_i);
 }
 
 // Weight split at upload: hi = T(w * scale), lo = T(w * scale - hi), from [S][N][K] fp32 into
@@ -502,7 +505,17 @@ void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
 // tile, whose short k loops would otherwise wait on the previous tile's stores.
 template <int ROLE, typename T, int TERMS>
 void launch_cfg(const GemmParams &p, hipStream_t st) {
-    if constexpr (ROLE != ROLE_LMHEAD) {
+    if constexpr (ROLE == ROLE_LMHEAD) {
+        if (p.M <= 32 && p.K % 64 == 0) {
+            // skinny LM head (a decode step): 128-column blocks, the arg-max partials' width,
+            // K split as below
+            const int steps = p.K / 64;
+            int kw = steps >= 16 ? 8 : steps >= 8 ? 4 : steps >= 4 ? 2 : 1;
+            while (steps % kw) kw >>= 1;
+            launch_skinny<ROLE, T, TERMS, 4>(p, kw, st);
+            return;
+        }
+    } else {
         if (p.M <= 32 && p.K % 64 == 0) {
             // skinny: K split over the waves of a workgroup, about two 64-K steps per wave;
             // wide outputs take two column tiles per wave (each A fragment feeds both)
@@ -518,8 +531,8 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
         if (p.M <= 32) {
             // skinny (at most 32 rows, e.g. one position of every sequence): 32x32 blocks of one
             // wave, an 8-deep ring, so that the weight stream is spread over as many CUs as
-            // possible (the LM head keeps 128-column tiles: its arg-max partials are per 128
-            // columns)
+            // possible (an LM head with K not a multiple of 64 keeps the 128x128 tiles below: its
+            // arg-max partials are per 128 columns)
             const int total = ((p.N + 31) / 32) * p.S;
             if (total > 0)
                 hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 1, 1, 1, 1, 8>), dim3(total), dim3(64), 0, st, p);

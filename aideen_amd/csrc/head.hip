@@ -156,53 +156,71 @@ __global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val
 // sequence's tokens so far (the prompt, then the appended arg-maxes); step j works on the first
 // len = T0 + j of them, its context being the last ctx of those (trainer.rs:4248-4249).
 // ---------------------------------------------------------------------------------------
-constexpr int DQ_W = 8;  // waves per decode-query block
-
 // The context query embed_context(context, ctx) (tokenizer.rs:133-149) of every sequence, one
-// block per sequence: v = sum_{p < L} (p + 1) E[tok_p] over the window in fp64 (wave w takes the
-// positions p = w mod DQ_W, combined in wave order), q = v / |v| -- r = v / L itself when
-// |r| <= 1e-6, as embed_context keeps a near-zero sum unnormalised.  The same quantity as
-// k_ctx_window's at the last position, formed directly for one window per sequence.
-__global__ __launch_bounds__(64 * DQ_W) void k_decode_query(const float *E, int d, const int32_t *seq, int stride,
-                                                            int len, int ctx, float *q) {
-    __shared__ double part[DQ_W][64];
-    __shared__ double vbuf[2048];
-    __shared__ double red[DQ_W];
-    const int b = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// block per sequence: v = sum_{p < L} (p + 1) E[tok_p] over the window in fp64, q = v / |v| --
+// r = v / L itself when |r| <= 1e-6, as embed_context keeps a near-zero sum unnormalised.  The
+// same quantity as k_ctx_window's at the last position, formed directly for one window per
+// sequence.  Wave w sums the positions p = w mod W over whole rows (lane l holds columns
+// l + 64 e, so each load is 256 contiguous bytes), four rows in flight; the W partial rows are
+// then added in wave order (deterministic).  W waves x the padded row in fp64 stay within 64 KB
+// of LDS: W = 16 up to d = 512, 8 at 1024, 4 at 2048.
+constexpr int dq_waves(int E) { return E <= 8 ? 16 : (E <= 16 ? 8 : 4); }
+
+template <int E, bool PART>
+__global__ __launch_bounds__(64 * dq_waves(E)) void k_decode_query(const float *Emb, int d, const int32_t *seq,
+                                                                   int stride, int len, int ctx, float *q) {
+    constexpr int W = dq_waves(E);
+    __shared__ double part[W][64 * E];
+    __shared__ double red[W];
+    const int b = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int er = PART ? d / 64 : E;
     const int start = len > ctx ? len - ctx : 0, L = len - start;
     const int32_t *tk = seq + (long)b * stride + start;
-    for (int j0 = 0; j0 < d; j0 += 64) {
-        const int j = j0 + lane;
-        double acc = 0.0;
-        int p = wave;
-        for (; p + 3 * DQ_W < L; p += 4 * DQ_W) {  // four rows in flight
-            float x[4];
+    double acc[E];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) x[u] = E[(long)tk[p + u * DQ_W] * d + j];
+    for (int e = 0; e < E; ++e) acc[e] = 0.0;
+    int p = wave;
+    for (; p + 3 * W < L; p += 4 * W) {
+        float x[4][E];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc += (double)(p + u * DQ_W + 1) * (double)x[u];
+        for (int u = 0; u < 4; ++u) {
+            const float *row = Emb + (long)tk[p + u * W] * d + lane;
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[u][e] = e < er ? row[64 * e] : 0.0f;
         }
-        for (; p < L; p += DQ_W) acc += (double)(p + 1) * (double)E[(long)tk[p] * d + j];
-        part[wave][lane] = acc;
-        __syncthreads();
-        if (wave == 0) {
-            double v = 0.0;
-            for (int w = 0; w < DQ_W; ++w) v += part[w][lane];
-            vbuf[j] = v;
-        }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[e] += (double)(p + u * W + 1) * (double)x[u][e];
     }
+    for (; p < L; p += W) {
+        const float *row = Emb + (long)tk[p] * d + lane;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if (e < er) acc[e] += (double)(p + 1) * (double)row[64 * e];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) part[wave][lane + 64 * e] = acc[e];
+    __syncthreads();
+    // column sums in wave order, then |v|^2
     double ss = 0.0;
-    for (int j = threadIdx.x; j < d; j += 64 * DQ_W) ss += vbuf[j] * vbuf[j];
+    for (int j = threadIdx.x; j < d; j += 64 * W) {
+        double v = 0.0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) v += part[w][j];
+        part[0][j] = v;  // column j is read and written by this thread only
+        ss += v * v;
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     double n2 = 0.0;
-    for (int w = 0; w < DQ_W; ++w) n2 += red[w];
+#pragma unroll
+    for (int w = 0; w < W; ++w) n2 += red[w];
     const double nv = sqrt(n2);
     const double inv = 1.0 / (nv > 1e-6 * (double)L ? nv : (double)L);
-    for (int j = threadIdx.x; j < d; j += 64 * DQ_W) q[(long)b * d + j] = (float)(vbuf[j] * inv);
+    for (int j = threadIdx.x; j < d; j += 64 * W) q[(long)b * d + j] = (float)(part[0][j] * inv);
 }
 
 // LmHead::sample's repetition penalty (lm_head.rs:81-99) on each sequence's logits row: every
@@ -263,7 +281,11 @@ void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, 
 
 void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
                          hipStream_t st) {
-    hipLaunchKernelGGL(k_decode_query, dim3((unsigned)B), dim3(64 * DQ_W), 0, st, E, d, seq, stride, len, ctx, q);
+    dispatch_width(d, [&](auto Ec, auto Pc) {
+        constexpr int EC = decltype(Ec)::value;
+        hipLaunchKernelGGL((k_decode_query<EC, decltype(Pc)::value>), dim3((unsigned)B), dim3(64 * dq_waves(EC)), 0, st,
+                           E, d, seq, stride, len, ctx, q);
+    });
 }
 
 void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,

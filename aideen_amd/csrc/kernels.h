@@ -189,7 +189,7 @@ void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st);
 // by the temporal step and by a caller-supplied start state).  Reset by a kernel (not a memset:
 // the forward may be captured in a graph).
 constexpr int ADN_BOUNDS = 4;
-void launch_reset_bounds(unsigned *words, float h_bound, hipStream_t st);
+void launch_reset_bounds(unsigned *words, float h_bound, unsigned *zero, hipStream_t st);  // zero: also cleared, or null
 // ---- memory-coupled solve (memory.hip) -----------------------------------------------------
 // act[0] = tokens (b, t) = b*T + t for b < B, cnt[0] = B, cnt[1] = 0.
 // embed_context of the window ending at every position; tot0/tot1 hold

@@ -139,18 +139,20 @@ __global__ void k_fill_i32(int32_t *p, int32_t v, long n) {
         p[i] = v;
 }
 
-// The operand bounds of one forward: words[0] = w0 (float bits), the other ADN_BOUNDS - 1 zero.
-__global__ void k_reset_bounds(unsigned *words, unsigned w0) {
+// The operand bounds of one forward: words[0] = w0 (float bits), the other ADN_BOUNDS - 1 zero;
+// also *zero = 0 when given (the signal GEMM's A-magnitude word).
+__global__ void k_reset_bounds(unsigned *words, unsigned w0, unsigned *zero) {
     const int i = threadIdx.x;
     if (i < ADN_BOUNDS) words[i] = i == 0 ? w0 : 0u;
+    if (i == ADN_BOUNDS && zero) *zero = 0u;
 }
 
 }  // namespace
 
-void launch_reset_bounds(unsigned *words, float h_bound, hipStream_t st) {
+void launch_reset_bounds(unsigned *words, float h_bound, unsigned *zero, hipStream_t st) {
     unsigned bits;
     memcpy(&bits, &h_bound, sizeof bits);
-    hipLaunchKernelGGL(k_reset_bounds, dim3(1), dim3(64), 0, st, words, bits);
+    hipLaunchKernelGGL(k_reset_bounds, dim3(1), dim3(64), 0, st, words, bits, zero);
 }
 
 void launch_spectral_norm(const float *w, int rows, int cols, int n_iter, float *sigma, float *work,

@@ -289,7 +289,10 @@ void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, in
     const Dims &D = c->D;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
-    launch_reset_bounds(c->bounds, c->h_bound, st);
+    // caller-supplied rows on the fp16 split: the signal GEMM's A scale also honours their actual
+    // magnitude (max |s_in|, accumulated into c->absmax, which the reset clears)
+    const bool dyn_scale = r.s_in && c->prec == PREC_F16X3;
+    launch_reset_bounds(c->bounds, c->h_bound, dyn_scale ? c->absmax : nullptr, st);
     // x gathered from the embedding when tokens are given
     {
         GemmParams g{};
@@ -312,11 +315,9 @@ void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, in
         g.epi = EPI_NONE;
         set_split(c, g, c->sp_in, c->embed_scale);
         Span sp(prof, ADN_STAGE_SIGNAL_GEMM, -1, st);
-        if (r.s_in && c->prec == PREC_F16X3) {
-            // caller-supplied rows: the A scale also honours their actual magnitude, so rows of
-            // any size stay inside the fp16 range (rows no larger than the embedding table's
-            // entries keep the embedding's scale, and match the token path bit for bit)
-            launch_fill_i32(reinterpret_cast<int32_t *>(c->absmax), 0, 1, st);
+        if (dyn_scale) {
+            // rows of any size stay inside the fp16 range (rows no larger than the embedding
+            // table's entries keep the embedding's scale, and match the token path bit for bit)
             launch_absmax(r.s_in, (long)ntok * d, c->absmax, st);
             g.a_absmax = c->absmax;
             g.a_headroom = 1024.0f;

@@ -253,6 +253,97 @@ def bench_adjoint(args, be, mc, w, toks, dev, torch) -> int:
     return 0
 
 
+def bench_decode(args, be, mc, w, toks, dev, torch) -> int:
+    """Greedy decode (``Trainer::generate`` with greedy sampling, trainer.rs:4219-4431): n_new
+    tokens after the B x T prompt, each one position solved with generate's 10 fixed Picard
+    steps from embed_context(context, ctx_len), its logits and arg-max.  One position per
+    sequence makes every GEMM a weight stream (B rows against the per-slot d x d matrices and
+    W_lm), so a step is bound by the weight bytes it reads; the roofline names the stage with
+    the most device time in one profiled step and its algorithmic bytes (weights as their hi and
+    lo halves, 4 bytes per weight, plus activations)."""
+    import dataclasses
+    import numpy as np
+    from aideen_amd import synth
+    B, T = toks.shape
+    n_new, ctx_len = args.n_new, T
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
+    be.set_stream(stream.cuda_stream)
+    for _ in range(args.warmup):
+        be.decode_greedy(toks, n_new, ctx_len)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        out = be.decode_greedy(toks, n_new, ctx_len)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ev0.elapsed_time(ev1) / args.steps
+    tok_s = B * n_new / (ms / 1e3)
+    log(f"decode {n_new} tokens x B={B}: {ms:.3f} ms per call on the stream ({wall * 1e3 / args.steps:.3f} ms wall)"
+        f" -> {ms * 1e3 / n_new:.1f} us per token, {tok_s:,.0f} tokens/s")
+
+    # one decode step as a device forward: the query row (the prompt's embed_context at its last
+    # position), 10 Picard steps without early exit, the arg-max of the position's logits
+    q = be.embed_context(toks, ctx_len)[:, -1:, :]
+    q_d = torch.from_numpy(np.ascontiguousarray(q)).to(dev)
+    am = torch.empty((B, 1), dtype=torch.int32, device=dev)
+    be.forward_async(s_in=q_d, outputs=dict(argmax=am), max_iters=10, eps=0.0)
+    prof = be.profile_forward(s_in=q_d, outputs=dict(argmax=am), max_iters=10, eps=0.0)
+    st = prof["stages"]
+    dom = max(st, key=lambda n: st[n]["ms"])
+    gbs = st[dom]["bytes"] / st[dom]["ms"] / 1e6
+    step_bytes = sum(s["bytes"] for s in st.values())
+    stages = {n: dict(ms=round(s["ms"], 4), launches=s["launches"],
+                      gbs=round(s["bytes"] / s["ms"] / 1e6, 1) if s["ms"] > 0 else None) for n, s in st.items()}
+    log(f"profiled step: {prof['total_ms'] * 1e3:.1f} us; dominant {dom} {st[dom]['ms'] * 1e3:.1f} us "
+        f"({st[dom]['launches']} launches, {gbs:.0f} GB/s)")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import pyoracle
+        pyoracle.build()
+        o = pyoracle.Oracle(dataclasses.replace(mc, max_iters=10, eps=0.0), w)
+        t0 = time.perf_counter()
+        ref1 = o.decode_greedy(toks, 1, ctx_len, nthreads=1)
+        t1 = time.perf_counter() - t0
+        nn = int(max(1, min(n_new, args.cpu_seconds / max(t1, 1e-6))))
+        t0 = time.perf_counter()
+        ref = o.decode_greedy(toks, nn, ctx_len, nthreads=1)
+        t2 = time.perf_counter() - t0
+        if not (np.array_equal(ref[:, :1], ref1) and np.array_equal(ref, out[:, :nn])):
+            raise SystemExit("decode: the GPU tokens differ from the C oracle's")
+        cpu = dict(value=round(B * nn / t2, 2), unit="tokens/s", cores=1, kind="port",
+                   sample=(f"the first {nn} of the {n_new} decoded tokens of the same prompt and weights "
+                           f"(one sequence: the oracle's decode runs sequences in parallel, so one thread), "
+                           f"{t2:.1f} s; tokens identical to the GPU's"),
+                   seconds=round(t2, 2), host=host_info(1))
+    line = {
+        "metric": f"greedy decode tokens/sec at d_r={mc.d},h_slots={mc.H},vocab={mc.V},B={B},prompt={T}",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": config_data(args.config, mc, synth.PRESETS[args.config]["tokens"]),
+        "config": {"workload": (f"{args.config}-decode: {n_new} greedy tokens after a {B}x{T} prompt, ctx_len "
+                                f"{ctx_len}, 10 Picard steps per token (no early exit), d_r={mc.d} "
+                                f"h_slots={mc.H} vocab={mc.V}; one step = one call of {n_new} tokens"),
+                   "mode": "decode", "global_batch": B, "seq_len": T, "n_new": n_new,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": dict(kernel=dom, bound="hbm", achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                         frac=round(gbs / PEAK_HBM_GBS, 4), traffic=None,
+                         basis="algorithmic bytes of one profiled decode step: weights read once per launch "
+                               "(hi + lo halves) + activation rows; weights may be served from the MALL",
+                         launches=st[dom]["launches"], avg_launch_ms=round(st[dom]["ms"] / st[dom]["launches"], 5),
+                         bytes_per_launch=st[dom]["bytes"] / st[dom]["launches"]),
+        "cpu_baseline": cpu,
+        "step_profile": {"total_ms": round(prof["total_ms"], 4), "bytes": step_bytes,
+                         "gbs": round(step_bytes / prof["total_ms"] / 1e6, 1), "stages": stages},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -263,12 +354,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates HBM byte counters)")
-    ap.add_argument("--mode", choices=["forward", "memory", "embed", "adjoint"], default="forward",
+    ap.add_argument("--mode", choices=["forward", "memory", "embed", "adjoint", "decode"], default="forward",
                     help="forward: the canonical (token-parallel) forward, the headline metric; memory: "
                          "the memory-coupled forward (positions in order, history context and carrier "
                          "state between them) on the same shape with a one-dimensional carrier state; "
                          "embed: embed_context queries for every position (window = ctx); adjoint: the "
-                         "clean adjoint Picard backward of the NS forward")
+                         "clean adjoint Picard backward of the NS forward; decode: greedy decode of "
+                         "--n-new tokens after the configuration's B x T prompt (C2 is its shape)")
+    ap.add_argument("--n-new", type=int, default=64, help="decode: tokens generated per call")
     ap.add_argument("--adj-iters", type=int, default=2,
                     help="adjoint steps (ArchitectureConfig::adj_iters defaults to 2)")
     ap.add_argument("--eps", type=float, default=None, help="override the Picard tolerance")
@@ -311,6 +404,8 @@ def main() -> int:
         return bench_embed(args, be, mc, w, toks, dev, torch)
     if args.mode == "adjoint":
         return bench_adjoint(args, be, mc, w, toks, dev, torch)
+    if args.mode == "decode":
+        return bench_decode(args, be, mc, w, toks, dev, torch)
     # a dedicated (default-priority) stream: the library's kernels and the timing events share it
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)

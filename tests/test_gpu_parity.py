@@ -337,6 +337,69 @@ def test_greedy_decode_matches_oracle(oracle_lib, pen):
         assert not np.array_equal(got, oracle_lib.Oracle(mc, w).decode_greedy(prompt, 14, 6, 1.0))
 
 
+@pytest.mark.parametrize("pen", [1.0, 1.3])
+def test_greedy_decode_repeated_calls(oracle_lib, pen):
+    """A serving loop's use: five decode calls alternating two prompts of one shape on one context
+    (its staging buffers reused), a forward and a synchronisation after each, all against the
+    oracle; then new weights uploaded into the same context."""
+    log(f"decode repeated pen={pen}")
+    mc, w = _small(d=128, H=4, V=600, N=1, max_iters=10, eps=0.0, win_sigma=3.0)
+    w["anchor"] = (w["anchor"] * np.float32(0.02)).astype(np.float32)
+    prompts = [synth.make_tokens("uniform", 3, 9, mc.V, seed=s) for s in (12, 13)]
+    o = oracle_lib.Oracle(mc, w)
+    refs = [o.decode_greedy(p, 14, 6, pen) for p in prompts]
+    assert not np.array_equal(refs[0], refs[1])
+    be = make(mc, 3, 9)
+    be.upload_weights(w)
+    toks = synth.make_tokens("uniform", 3, 9, mc.V, seed=5)
+    f0 = be.forward(toks, want=("h_star", "argmax"))
+    for call in range(5):
+        i = call % 2
+        got = be.decode_greedy(prompts[i], 14, 6, repetition_penalty=pen)
+        assert np.array_equal(got, refs[i]), f"call {call}"
+        f = be.forward(toks, want=("h_star", "argmax"))
+        be.synchronize()
+        np.testing.assert_allclose(f["h_star"], f0["h_star"], rtol=0, atol=1e-6)
+        assert np.array_equal(f["argmax"], f0["argmax"])
+    w2 = synth.make_weights(mc, seed=4)
+    w2["anchor"] = (w2["anchor"] * np.float32(0.02)).astype(np.float32)
+    ref2 = oracle_lib.Oracle(mc, w2).decode_greedy(prompts[0], 14, 6, pen)
+    assert not np.array_equal(ref2, refs[0])
+    be.upload_weights(w2)
+    for call in range(3):
+        assert np.array_equal(be.decode_greedy(prompts[0], 14, 6, repetition_penalty=pen), ref2), f"new weights {call}"
+
+
+@pytest.mark.parametrize("d,H", [(64, 2), (192, 3), (1024, 2), (2048, 1)])
+def test_greedy_decode_widths(oracle_lib, d, H):
+    """The decode's context query at every width bucket of its kernel (16 waves up to d = 512,
+    8 at 1024, 4 at 2048; d = 192 a partial bucket) and a window longer than ctx_len."""
+    log(f"decode d={d} H={H}")
+    mc, w = _small(d=d, H=H, V=300, N=1, max_iters=10, eps=0.0, win_sigma=3.0)
+    w["anchor"] = (w["anchor"] * np.float32(0.02)).astype(np.float32)
+    prompt = synth.make_tokens("uniform", 2, 70, mc.V, seed=21)
+    ref = oracle_lib.Oracle(mc, w).decode_greedy(prompt, 5, 64, 1.0)
+    be = make(mc, 2, 1)
+    be.upload_weights(w)
+    assert np.array_equal(be.decode_greedy(prompt, 5, 64), ref)
+
+
+@pytest.mark.parametrize("B,T", [(1, 1), (2, 5), (4, 8), (3, 11)])
+def test_lm_head_few_rows_matches_oracle(oracle_lib, B, T):
+    """The LM head at 32 rows or fewer (a decode step's shape) runs the skinny kernel: logits and
+    the last-max arg-max of every row against the oracle, with a vocabulary that ends in a partial
+    128-column block and a nonzero bias; 33 rows (the tiled kernel) for comparison."""
+    log(f"lm head rows B={B} T={T}")
+    mc, w = _small(d=128, H=4, V=1000, N=1)
+    w["lm_b"] = np.random.default_rng(6).uniform(-0.5, 0.5, mc.V).astype(np.float32)
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=7)
+    be = make(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks, want=("h_star", "logits", "argmax", "iters"))
+    ref = oracle_lib.Oracle(mc, w).forward(toks)
+    assert_forward_parity(got, ref, f"lm head B={B} T={T}")
+
+
 def test_c2_forward_and_greedy_decode(oracle_lib):
     """C2: the v0.1 production shape for one sequence (d=512, H=8, V=50257, N=16, B=1, T=256):
     every output of every position against the oracle, then a 64-token greedy decode from the
