@@ -384,20 +384,42 @@ def test_greedy_decode_widths(oracle_lib, d, H):
     assert np.array_equal(be.decode_greedy(prompt, 5, 64), ref)
 
 
+@pytest.mark.parametrize("prec", list(PRECISIONS), ids=list(PRECISIONS))
 @pytest.mark.parametrize("B,T", [(1, 1), (2, 5), (4, 8), (3, 11)])
-def test_lm_head_few_rows_matches_oracle(oracle_lib, B, T):
+def test_lm_head_few_rows_matches_oracle(oracle_lib, B, T, prec):
     """The LM head at 32 rows or fewer (a decode step's shape) runs the skinny kernel: logits and
     the last-max arg-max of every row against the oracle, with a vocabulary that ends in a partial
-    128-column block and a nonzero bias; 33 rows (the tiled kernel) for comparison."""
-    log(f"lm head rows B={B} T={T}")
-    mc, w = _small(d=128, H=4, V=1000, N=1)
+    128-column block and a nonzero bias, in every fp32-accurate GEMM arithmetic; 33 rows (the
+    tiled kernel) for comparison."""
+    log(f"lm head rows B={B} T={T} {prec}")
+    mc, w = _small(d=128, H=4, V=1000, N=1, flags=PRECISIONS[prec])
     w["lm_b"] = np.random.default_rng(6).uniform(-0.5, 0.5, mc.V).astype(np.float32)
     toks = synth.make_tokens("uniform", B, T, mc.V, seed=7)
     be = make(mc, B, T)
     be.upload_weights(w)
     got = be.forward(toks, want=("h_star", "logits", "argmax", "iters"))
     ref = oracle_lib.Oracle(mc, w).forward(toks)
-    assert_forward_parity(got, ref, f"lm head B={B} T={T}")
+    assert_forward_parity(got, ref, f"lm head B={B} T={T} {prec}")
+
+
+def test_lm_head_few_rows_bf16_input():
+    """The bf16-input variant's skinny LM head (one product per multiply): logits within the bf16
+    bar of the fp32-accurate path's, the arg-max equal wherever the top two logits are apart."""
+    mc, w = _small(d=128, H=4, V=1000, N=1, eps=5e-3)
+    w["lm_b"] = np.random.default_rng(6).uniform(-0.5, 0.5, mc.V).astype(np.float32)
+    toks = synth.make_tokens("uniform", 2, 5, mc.V, seed=7)
+    ref = make(mc, 2, 5)
+    ref.upload_weights(w)
+    r = ref.forward(toks, want=("logits", "argmax"))
+    mcb = dataclasses.replace(mc, flags=mc.flags | synth.F_GEMM_BF16)
+    be = make(mcb, 2, 5)
+    be.upload_weights(w)
+    got = be.forward(toks, want=("logits", "argmax"))
+    np.testing.assert_allclose(got["logits"], r["logits"], rtol=0, atol=3e-2)
+    top2 = np.sort(r["logits"], axis=-1)[..., -2:]
+    clear = (top2[..., 1] - top2[..., 0]) > 6e-2
+    assert np.array_equal(got["argmax"][clear], r["argmax"][clear])
+    assert np.array_equal(got["argmax"], last_max(got["logits"]))
 
 
 def test_c2_forward_and_greedy_decode(oracle_lib):
