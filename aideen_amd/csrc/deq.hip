@@ -84,6 +84,68 @@ __device__ __forceinline__ float qkv_load(const float *p) {
         return *p;
 }
 
+// W_o's A operand written pre-split (b.mix_pre): the scale the split GEMM derives for it (its
+// a_scale 1, lowered to 2^floor(log2(headroom / bound)) when the h bound calls for it), and VEC
+// consecutive elements of a row from e0 (VEC divides 8) as fp16 halves of x = v * asc,
+// hi = f16(x) and lo = f16(x - hi), in the GEMM's pre-split layout: each 8 consecutive
+// elements as their 8 hi halves followed by their 8 lo halves (4 bytes per element, as in fp32).
+__device__ __forceinline__ float presplit_scale(const SolveBuffers &b) {
+    float asc = 1.0f;
+    if (b.mix_bound) {
+        const float mx = __uint_as_float(*b.mix_bound);
+        if (mx > 0.0f) {
+            const float dyn = exp2f(floorf(log2f(b.mix_headroom / mx)));
+            if (dyn < asc) asc = dyn;
+        }
+    }
+    return asc;
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_presplit(float *row, int e0, const float (&v)[VEC], float asc) {
+    static_assert(8 % VEC == 0, "a run stays inside one group of 8");
+    _Float16 hi[VEC], lo[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) {
+        const float x = v[q] * asc;
+        hi[q] = (_Float16)x;
+        lo[q] = (_Float16)(x - (float)hi[q]);
+    }
+    _Float16 *hp = reinterpret_cast<_Float16 *>(row) + (e0 >> 3) * 16 + (e0 & 7);
+    if constexpr (VEC == 4) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<h4 *>(hp) = h4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<h4 *>(hp + 8) = h4{lo[0], lo[1], lo[2], lo[3]};
+    } else if constexpr (VEC == 2) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<h2 *>(hp) = h2{hi[0], hi[1]};
+        *reinterpret_cast<h2 *>(hp + 8) = h2{lo[0], lo[1]};
+    } else {
+        hp[0] = hi[0];
+        hp[8] = lo[0];
+    }
+}
+
+// store_presplit for VEC = 4 when the lanes of a pair (2k, 2k + 1) hold the two halves of one
+// group of 8 (elements e0 = 8m and 8m + 4): the pair swaps halves so that the even lane stores the
+// group's 16 hi bytes and the odd lane its 16 lo bytes, one 16-byte store per lane
+__device__ __forceinline__ void store_presplit_pair(float *row, int e0, const float (&v)[4], float asc, int lane) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 hi, lo;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float x = v[q] * asc;
+        hi[q] = (_Float16)x;
+        lo[q] = (_Float16)(x - (float)hi[q]);
+    }
+    const bool odd = (lane & 1) != 0;
+    const uint2 mine = __builtin_bit_cast(uint2, odd ? hi : lo);
+    const uint2 got = make_uint2((unsigned)__shfl_xor((int)mine.x, 1, 64), (unsigned)__shfl_xor((int)mine.y, 1, 64));
+    const uint2 keep = __builtin_bit_cast(uint2, odd ? lo : hi);
+    const uint4 out = odd ? make_uint4(got.x, got.y, keep.x, keep.y) : make_uint4(keep.x, keep.y, got.x, got.y);
+    *reinterpret_cast<uint4 *>(reinterpret_cast<_Float16 *>(row) + (e0 >> 3) * 16 + (odd ? 8 : 0)) = out;
+}
+
 template <int H, int QA, int VEC>
 __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, int k) {
     constexpr int NG = H / QA;
@@ -197,6 +259,7 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
     }
 
     float *mixbase = b.mix + (long)i * H * d;
+    const float asc = b.mix_pre ? presplit_scale(b) : 1.0f;
     for (int off = lane * VEC; off < d; off += 64 * VEC) {
         float acc[QA][VEC];
 #pragma unroll
@@ -213,10 +276,20 @@ __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, i
 #pragma unroll
                 for (int v = 0; v < VEC; ++v) acc[a][v] = acc[a][v] + vv[v] * w[a * H + c];
         }
+        if (b.mix_pre) {
 #pragma unroll
-        for (int a = 0; a < QA; ++a)
+            for (int a = 0; a < QA; ++a) {
+                if constexpr (VEC == 4)  // lane pairs hold whole groups of 8 (off = 4 lane + 256 j)
+                    store_presplit_pair(mixbase + (long)(g * QA + a) * d, off, acc[a], asc, lane);
+                else
+                    store_presplit<VEC>(mixbase + (long)(g * QA + a) * d, off, acc[a], asc);
+            }
+        } else {
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) mixbase[(long)(g * QA + a) * d + off + v] = acc[a][v];
+            for (int a = 0; a < QA; ++a)
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) mixbase[(long)(g * QA + a) * d + off + v] = acc[a][v];
+        }
     }
 }
 
@@ -278,6 +351,7 @@ __global__ __launch_bounds__(256) void k_attn_rt(Dims D, SolveBuffers b, int cur
     for (int c = 0; c < HM; ++c)
         if (c < H) e[c] = e[c] / sum;
     float *mixrow = b.mix + ((long)i * H + a) * d;
+    const float asc = b.mix_pre ? presplit_scale(b) : 1.0f;
     for (int off = lane * VEC; off < d; off += 64 * VEC) {
         float acc[VEC];
 #pragma unroll
@@ -289,8 +363,12 @@ __global__ __launch_bounds__(256) void k_attn_rt(Dims D, SolveBuffers b, int cur
                 for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + base[(long)c * rowstride + 2 * d + off + v] * e[c];
             }
         }
+        if (b.mix_pre) {
+            store_presplit<VEC>(mixrow, off, acc, asc);
+        } else {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) mixrow[off + v] = acc[v];
+            for (int v = 0; v < VEC; ++v) mixrow[off + v] = acc[v];
+        }
     }
 }
 

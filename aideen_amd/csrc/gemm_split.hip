@@ -84,7 +84,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 
-template <int ROLE, typename T, int TERMS, int WTM, int WTN, int WGM, int WGN, int STAGES>
+template <int ROLE, typename T, int TERMS, int WTM, int WTN, int WGM, int WGN, int STAGES, bool PRE = false>
 __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_gemm_split(GemmParams p) {
     typedef typename Vec8<T>::type V8;
     constexpr int NW = WGM * WGN;
@@ -125,6 +125,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     // k_split): each DMA block is one such block, lane L taking the chunk its LDS position
     // holds; row groups past N read group 0.
     int s = 0, m0 = 0, n0 = 0;
+    static_assert(!PRE || (std::is_same<T, _Float16>::value && TERMS == 3), "pre-split A: fp16 halves");
+    // A pre-split by its producer (PRE): fp16 halves hi = f16(x), lo = f16(x - hi) of x = A * asc,
+    // asc being the scale derived below, 4 bytes per value as in fp32, each 8 consecutive K values
+    // as their 8 hi halves followed by their 8 lo halves (one 16-byte chunk each).  A slice's 64
+    // bytes then hold the hi and lo chunks of its K values [0, 8) where the fp32 path has its
+    // chunks 0 and 1 and those of [8, 16) at 2 and 3: the loads and fragment reads are the fp32
+    // path's, and the fragments are the halves as loaded, with no split work in the k loop.
+    const float *Abase = PRE ? p.a_pre : p.A;
     const float *asrc[A_PW];
     const T *bsrc[B_PW][PARTS];
     auto set_tile = [&](int tt) {
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
                     ar = 0;
                 }
             }
-            asrc[j] = p.A + ar * p.a_sm + (long)s * p.a_ss + c * 4;
+            asrc[j] = Abase + ar * p.a_sm + (long)s * p.a_ss + c * 4;
         }
 #pragma unroll
         for (int j = 0; j < B_PW; ++j) {
@@ -173,8 +181,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
 
     const int wm = wave / WGN, wn = wave % WGN;
     const int r = lane & 31, hh = lane >> 5;
-    // fragment chunk positions: rows r + 32t share swz(r) (the swizzles read row bits 1..3)
-    const int pa0 = ((2 * hh) ^ swz_a(r)) * 4, pa1 = ((2 * hh + 1) ^ swz_a(r)) * 4;
     const int pb = (hh ^ swz_b(r)) * 8;
     float asc = p.a_scale, osc = p.out_scale;
     if (p.a_absmax) {  // data-dependent A scale (power of two, never above the static one)
@@ -187,6 +193,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
             }
         }
     }
+    // fragment chunk positions: rows r + 32t share swz(r) (the swizzles read row bits 1..3); a
+    // lane's 8 K values are chunks 2 hh and 2 hh + 1 (fp32 values, or their hi and lo halves)
+    const int pa0 = ((2 * hh) ^ swz_a(r)) * 4, pa1 = ((2 * hh + 1) ^ swz_a(r)) * 4;
     floatx16 acc[WTM][WTN];
 
     // Fragments in registers.  B is streamed one 32-column tile at a time through two buffers,
@@ -210,12 +219,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
     // piece into the next slice's block, after its barrier, out of reach of the MFMAs it is
     // meant to overlap.
     auto split_i = [&](int i, V8 &h, V8 &l) {
+        if constexpr (PRE) {
+            h = __builtin_bit_cast(V8, anx[i][0]);
+            l = __builtin_bit_cast(V8, anx[i][1]);
+        } else {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float x = anx[i][q >> 2][q & 3] * asc;
-            const T hv = (T)x;
-            h[q] = hv;
-            if constexpr (TERMS == 3) l[q] = (T)(x - (float)hv);
+            for (int q = 0; q < 8; ++q) {
+                const float x = anx[i][q >> 2][q & 3] * asc;
+                const T hv = (T)x;
+                h[q] = hv;
+                if constexpr (TERMS == 3) l[q] = (T)(x - (float)hv);
+            }
         }
         if constexpr (TERMS == 3)
             asm volatile("" : "+v"(h), "+v"(l));
@@ -539,13 +553,21 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
             return;
         }
     }
-    const bool big = p.N >= 512 && p.M >= 1024;
+    const bool big = p.N >= 512 && p.M >= 1024;  // the configuration gemm_presplit_ok names
     const int bm = big ? 256 : 128, bn = big ? 256 : 128;
     const int total = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.S;
     if (total <= 0) return;
-    if (big)
+    if (big) {
+        if constexpr (std::is_same<T, _Float16>::value && TERMS == 3) {
+            if (p.a_pre) {
+                hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4, true>), dim3(ring_grid(total, 1)),
+                                   dim3(512), 0, st, p);
+                return;
+            }
+        }
         hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4>), dim3(ring_grid(total, 1)), dim3(512), 0, st,
                            p);
+    }
     else
         hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 2, 2, 2, 4>), dim3(total), dim3(256), 0, st, p);
 }
@@ -571,6 +593,8 @@ void launch_gemm_split(const GemmParams &p, hipStream_t st) {
         default: launch_role<_Float16, 3>(p, st); break;
     }
 }
+
+bool gemm_presplit_ok(int prec, int M, int N) { return prec == PREC_F16X3 && M >= 1024 && N >= 512; }
 
 long split_weight_elems(int S, int N, int K) { return (long)S * ((N + 31) / 32 * 32) * K; }
 

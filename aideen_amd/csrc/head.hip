@@ -14,7 +14,7 @@ constexpr int WPB = 4;
 // per token; each lane keeps its E = d/64 pooled values in registers between the two passes.
 template <int E, bool PART>
 __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int ntok, const float *g,
-                                                   float *pooled, float *pnorm, float *rec, int REC) {
+                                                   float *pooled, float *pnorm, float *rec, int REC, float pre) {
     const int t = blockIdx.x * WPB + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (t >= ntok) return;
@@ -55,6 +55,22 @@ __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int n
     if (!pnorm) return;
     ss = wave_sum(ss);
     const float rms = sqrtf(ss / (float)d + 1e-5f);
+    if (pre > 0.0f) {
+        // the LM head's A operand pre-split: fp16 halves of x = pnorm * pre, hi = f16(x) and
+        // lo = f16(x - hi), each 8 consecutive elements as 8 hi halves then 8 lo halves
+        _Float16 *row = reinterpret_cast<_Float16 *>(pnorm + (long)t * d);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = lane + 64 * e;
+            if (!PART || e < er) {
+                const float x = ((pv[e] / rms) * (g ? g[i] : 1.0f)) * pre;
+                const _Float16 hv = (_Float16)x;
+                row[(i >> 3) * 16 + (i & 7)] = hv;
+                row[(i >> 3) * 16 + 8 + (i & 7)] = (_Float16)(x - (float)hv);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int i = lane + 64 * e;
@@ -261,11 +277,11 @@ __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *
 }  // namespace
 
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
-                      float *pnorm, float *rec, int REC, hipStream_t st) {
+                      float *pnorm, float *rec, int REC, float pre_scale, hipStream_t st) {
     const dim3 grid((unsigned)((ntok + WPB - 1) / WPB)), blk(64 * WPB);
     dispatch_width(D.d, [&](auto Ec, auto Pc) {
         hipLaunchKernelGGL((k_pool_norm<decltype(Ec)::value, decltype(Pc)::value>), grid, blk, 0, st, D, h, ntok, g,
-                           pooled, pnorm, rec, REC);
+                           pooled, pnorm, rec, REC, pre_scale);
     });
 }
 

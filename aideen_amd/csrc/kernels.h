@@ -76,10 +76,16 @@ struct GemmParams {
     // adjusts out_scale to match, so caller-supplied rows of any magnitude stay in range.
     const unsigned *a_absmax;
     float a_headroom;
+    // A given instead as fp16 hi/lo halves split by its producer with the kernel's own A scale
+    // (k_gemm_split's pre-split layout); only for the shapes gemm_presplit_ok names, null = none
+    const float *a_pre;
 };
 constexpr int GEMM_BN = 128;
 void launch_gemm(const GemmParams &p, hipStream_t st);
 void launch_gemm_split(const GemmParams &p, hipStream_t st);
+// Whether a split GEMM of this shape reads a pre-split A operand (GemmParams::a_pre): fp16
+// halves and the 256x256 persistent tiles (M >= 1024, N >= 512).
+bool gemm_presplit_ok(int prec, int M, int N);
 // hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16, from [S][N][K]
 // fp32 weights into the split GEMM's blocked layout (split_weight_elems halves each, N padded to
 // a multiple of 32); lo may be null.  The GEMMs' b_ss is then 0 (one matrix for every slot) or
@@ -110,6 +116,12 @@ struct SolveBuffers {
     // bound on |h| (float bits) for the split GEMMs' A scale: seeded with the update's RMSNorm
     // bound, raised by the init and the Anderson mix; null = not tracked
     unsigned *amax_h;
+    // W_o's A written pre-split by the attention instead of mix in fp32 (the same memory; see
+    // GemmParams::a_pre), scaled as the split GEMM scales it: its bound word and headroom for mix
+    // (a_absmax, a_headroom); mix_pre null = fp32
+    float *mix_pre;
+    const unsigned *mix_bound;
+    float mix_headroom;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -129,8 +141,10 @@ void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, in
 // ---- LM head (head.hip) -----------------------------------------------------------------
 // pooled = mean_s h*, pnorm = (pooled/rms(pooled, 1e-5)) * g
 // rec: when non-null, also each (token, slot) row's RMS into rec[row * REC] (the carrier record).
+// pre_scale > 0: pnorm is written as the split GEMM's pre-split A operand (GemmParams::a_pre) of
+// pnorm * pre_scale instead of fp32.
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
-                      float *pnorm, float *rec, int REC, hipStream_t st);
+                      float *pnorm, float *rec, int REC, float pre_scale, hipStream_t st);
 // argmax over each row of logits with the last-max tie rule.
 void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st);
 // final reduction of the per-tile arg-max partials written by the LM-head GEMM

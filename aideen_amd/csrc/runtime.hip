@@ -337,6 +337,15 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
     const int m = c->cfg.anderson_m;
+    // W_o on the 256x256 fp16-split tiles reads its A (mix) pre-split: the attention writes the
+    // halves, in mix's memory, with the scale the GEMM derives from the h bound (set_range below)
+    const bool wo_pre = gemm_presplit_ok(c->prec, rows, d);
+    SolveBuffers ba = b;
+    if (wo_pre) {
+        ba.mix_pre = b.mix;
+        ba.mix_bound = c->bounds;
+        ba.mix_headroom = c->l1_wv > 0.0f ? 16384.0f / c->l1_wv : INFINITY;
+    }
     for (int k = 0; k < r.max_iters; ++k) {
         const int cur = k & 1;
         {  // Q|K|V for every slot of every active token
@@ -369,7 +378,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         }
         {
             Span sp(prof, ADN_STAGE_ATTN, k, st);
-            launch_attn(D, b, cur, k, rows, st);
+            launch_attn(D, ba, cur, k, rows, st);
         }
         {  // o = W_o mix
             GemmParams g{};
@@ -391,6 +400,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             g.epi = EPI_NONE;
             set_split(c, g, c->sp_o);
             set_range(c, g, 0, c->l1_wv);  // mix is a convex combination of V = W_v h rows
+            if (wo_pre) g.a_pre = b.mix;
             Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
             launch_gemm(g, st);
         }
@@ -446,10 +456,13 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
     hipStream_t st = c->stream;
     const bool want_logits = o.logits || o.argmax;
     const bool pool = o.pooled || want_logits;
+    // the LM head on the 256x256 fp16-split tiles reads its A pre-split, written so by the pool
+    // kernel with the head's A scale
+    const bool lm_pre = want_logits && gemm_presplit_ok(c->prec, ntok, D.V);
     if (pool) {
         Span sp(prof, ADN_STAGE_POOL, -1, st);
         launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr,
-                         scan_rms ? c->scb.rec : nullptr, scan_rec_len(D), st);
+                         scan_rms ? c->scb.rec : nullptr, scan_rec_len(D), lm_pre ? c->lm_a_scale : 0.0f, st);
     }
     if (pool && scan_rms) enqueue_scan_prep(c, ntok, b, prof, true);
     if (want_logits) {
@@ -475,6 +488,7 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
         g.err = b.err;
         g.epi = c->lm_b ? EPI_BIAS : EPI_NONE;
         set_split(c, g, c->sp_lm, c->lm_a_scale);
+        if (lm_pre) g.a_pre = c->pnorm;
         const int ntiles = (D.V + GEMM_BN - 1) / GEMM_BN;
         if (o.argmax) {
             g.am_val = c->am_val;

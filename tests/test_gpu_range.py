@@ -68,6 +68,29 @@ def test_operands_beyond_fp16_range(oracle_lib, flags, anderson_m):
     assert np.array_equal(got["argmax"], ref["argmax"])
 
 
+def test_operands_beyond_fp16_range_wide_tiles(oracle_lib):
+    """The same scaled model with 1024 tokens at d = 512, V = 600: W_o and the LM head run on the
+    256x256 tiles, whose A operands (the slot mix, the normalised pooled row) their producers write
+    already split into fp16 halves, at the scale the GEMM derives from the h bound (mix) or the
+    head's static bound (pooled row)."""
+    log("range guard on the 256x256 tiles: d=512 H=2 V=600, 1024 tokens")
+    mc, w = scaled_model(synth.F_SCAN_SELECTIVE, 0, d=512, H=2, V=600)
+    B, T = 4, 256
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=6)
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks)
+    ref = oracle_lib.Oracle(mc, w).forward(toks, nthreads=16)
+    assert np.abs(got["h_star"]).max() > 65504
+    for k, v in got.items():
+        if v.dtype.kind == "f":
+            assert np.isfinite(v).all(), k
+    assert np.abs(got["iters"].astype(int) - ref["iters"]).max() <= 1
+    for k, f in (("h_star", G), ("pooled", G), ("logits", G), ("scan_y", 4e4), ("scan_state", 200.0)):
+        np.testing.assert_allclose(got[k] / f, ref[k] / f, rtol=RTOL, atol=ATOL, err_msg=k)
+    assert np.array_equal(got["argmax"], ref["argmax"])
+
+
 def test_memory_state_beyond_fp16_range(oracle_lib):
     """Memory mode with a carried state of magnitude ~10^6: the W_hist product of m_{t-1} and the
     W_out readout of the carrier state run on operands beyond the fp16 range."""
