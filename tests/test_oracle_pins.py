@@ -949,3 +949,27 @@ def test_adjoint_anderson_bookkeeping(oracle_lib):
             beta = np.zeros(2, np.float32)
             oracle_lib.lib().orc_anderson_coeffs(2, oracle_lib.fp(np.ascontiguousarray(g.ravel())), oracle_lib.fp(beta))
             np.testing.assert_allclose(got[t], beta[0] * X[2][t] + beta[1] * X[1][t], rtol=1e-5, atol=1e-6)
+
+
+def test_anderson_exit_moves_by_two_under_one_ulp_at_c3(oracle_lib):
+    """The C3 configuration (sigma 0.7, Anderson m = 5, eps 1e-4) sits on an Anderson residual
+    that is not monotone: for sequence 0, position 0 the oracle's residual is 1.02e-4 after
+    update 11, 2.04e-4 after 12 and 4.6e-5 after 13, so it exits at 13, and the same solve with 8
+    of the 512 input values moved by one ulp exits at 11.  Two fp32 implementations that round
+    differently (here: three fp16 products per fp32 product against plain fp32) therefore cannot
+    hold the +-1 bar on such tokens; the GPU tests accept a larger difference only where the
+    oracle's residual at the earlier exit lies within 10% of eps, as it does here."""
+    p = synth.PRESETS["C3"]
+    mc = p["model"]
+    w = synth.preset_weights("C3")
+    toks = synth.make_tokens(p["tokens"], p["B"], p["T"], mc.V, seed=1)
+    o = oracle(oracle_lib, mc, w)
+    x = np.ascontiguousarray(w["embed"][toks[0, 0]], np.float32)
+    _, it, trace = o.solve(x)
+    assert it == 13
+    assert mc.eps <= trace[10] <= 1.1 * mc.eps and trace[11] > trace[10] and trace[12] < mc.eps
+    xp = x.copy()
+    idx = np.random.default_rng(1).choice(x.size, 8, replace=False)
+    xp[idx] = np.nextafter(xp[idx], np.float32(np.inf))
+    _, itp, tracep = o.solve(xp)
+    assert itp == 11 and tracep[10] < mc.eps
