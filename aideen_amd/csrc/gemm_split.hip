@@ -558,7 +558,8 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
     const int total = ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn) * p.S;
     if (total <= 0) return;
     if (big) {
-        if constexpr (std::is_same<T, _Float16>::value && TERMS == 3) {
+        // the roles whose A a producer writes pre-split (the slot mix, the LM head's normalised row)
+        if constexpr (std::is_same<T, _Float16>::value && TERMS == 3 && (ROLE == ROLE_WO || ROLE == ROLE_LMHEAD)) {
             if (p.a_pre) {
                 hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4, true>), dim3(ring_grid(total, 1)),
                                    dim3(512), 0, st, p);

@@ -77,7 +77,8 @@ struct GemmParams {
     const unsigned *a_absmax;
     float a_headroom;
     // A given instead as fp16 hi/lo halves split by its producer with the kernel's own A scale
-    // (k_gemm_split's pre-split layout); only for the shapes gemm_presplit_ok names, null = none
+    // (k_gemm_split's pre-split layout); W_o and the LM head, for the shapes gemm_presplit_ok
+    // names; null = none
     const float *a_pre;
 };
 constexpr int GEMM_BN = 128;
