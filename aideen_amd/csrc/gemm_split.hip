@@ -32,9 +32,10 @@
 // fetches the chunk that belongs at its LDS position.
 //
 // Each wave owns WTM x WTN MFMA tiles of 32x32 (v_mfma_f32_32x32x16), the workgroup a WGM x WGN
-// grid of waves.  Wide GEMMs use 256x256 blocks of 8 waves (64x128 each, 2 waves per SIMD), run
-// persistent: a resident workgroup per CU walks its share of the tiles, loading the next tile's
-// first slices while the current tile's results are stored.
+// grid of waves.  Wide GEMMs use 256x256 blocks of 8 waves (64x128 each, 2 waves per SIMD; the
+// Q|K|V product 32x256 each, so that every A row block is split by one wave), run persistent: a
+// resident workgroup per CU walks its share of the tiles, loading the next tile's first slices
+// while the current tile's results are stored.
 #include "gemm_common.h"
 
 namespace adn {
@@ -283,7 +284,25 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
             if (j == 0) read_a(ns);
             read_b(j + 1 < WTN ? cs : ns, (j + 1) % WTN, bq[(j + 1) & 1]);
             mfma_tile(j, bq[j & 1], ah[P], al[P]);
-            if (j >= 1 && j - 1 < WTM) split_i(j - 1, ah[P ^ 1][j - 1], al[P ^ 1][j - 1]);
+            if constexpr (WTM == 1 && WTN >= 8 && !PRE) {
+                // a single A tile: its split in pieces of one value per tile j = 2..7 (two at
+                // j = 1), so that each tile's MFMAs have a few split instructions beside them
+                if (j >= 1 && j <= 7) {
+#pragma unroll
+                    for (int q = (j == 1 ? 0 : j); q <= j; ++q) {
+                        const float x = anx[0][q >> 2][q & 3] * asc;
+                        const T hv = (T)x;
+                        ah[P ^ 1][0][q] = hv;
+                        if constexpr (TERMS == 3) al[P ^ 1][0][q] = (T)(x - (float)hv);
+                    }
+                    if constexpr (TERMS == 3)
+                        asm volatile("" : "+v"(ah[P ^ 1][0]), "+v"(al[P ^ 1][0]));
+                    else
+                        asm volatile("" : "+v"(ah[P ^ 1][0]));
+                }
+            } else {
+                if (j >= 1 && j - 1 < WTM) split_i(j - 1, ah[P ^ 1][j - 1], al[P ^ 1][j - 1]);
+            }
             // Order within the tile: its first MFMA (whose operands were read a tile earlier:
             // the wait before it then covers only those), the reads for the next tile, then the
             // remaining MFMAs each followed by up to 6 split instructions.
@@ -565,6 +584,12 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
                                    dim3(512), 0, st, p);
                 return;
             }
+        }
+        if constexpr (ROLE == ROLE_QKV) {
+            // waves of 32 x 256 (8 down the block): each A row block is split by one wave only
+            hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 1, 8, 8, 1, 4>), dim3(ring_grid(total, 1)), dim3(512), 0, st,
+                               p);
+            return;
         }
         hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4>), dim3(ring_grid(total, 1)), dim3(512), 0, st,
                            p);
