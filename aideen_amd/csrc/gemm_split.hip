@@ -594,7 +594,12 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
         hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 4, 4, 2, 4>), dim3(ring_grid(total, 1)), dim3(512), 0, st,
                            p);
     }
-    else
+    else if (p.N <= 64 && p.M >= 1024) {
+        // narrow outputs (the carrier's projections, r + 2N = 64 columns): 128 x 64 blocks of two
+        // 64 x 64 waves, no zero-padded half tile
+        const int t64 = ((p.M + 127) / 128) * ((p.N + 63) / 64) * p.S;
+        hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 2, 2, 1, 4>), dim3(t64), dim3(128), 0, st, p);
+    } else
         hipLaunchKernelGGL((k_gemm_split<ROLE, T, TERMS, 2, 2, 2, 2, 4>), dim3(total), dim3(256), 0, st, p);
 }
 
