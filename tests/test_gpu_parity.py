@@ -772,6 +772,36 @@ def test_nonfinite_inputs_report_nonconvergence(oracle_lib, flags):
     assert_forward_parity(good, {k: ref[k][~bad][None] for k in good}, f"finite tokens, flags {flags}")
 
 
+def test_nonfinite_inputs_on_wide_tiles(oracle_lib):
+    """The same non-finite rows among 1024 tokens at d = 512, V = 600: the projections, W_o and
+    the LM head on the 256x256 tiles (W_o's and the head's A written pre-split by the attention
+    and the pool kernel).  The two tokens run to the cap unconverged with non-finite states; the
+    other 1022 match the oracle."""
+    log("non-finite inputs on the 256x256 tiles")
+    mc, w = _small(d=512, H=4, V=600, N=4, flags=synth.F_SCAN_SELECTIVE, max_iters=12)
+    B, T = 4, 256
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=14)
+    s_in = np.ascontiguousarray(w["embed"][toks])
+    s_in[1, 100, 300] = np.nan
+    s_in[3, 7, :] = -np.inf
+    be = make(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(s_in=s_in, want=("h_star", "pooled", "logits", "argmax", "iters", "converged"))
+    be.close()
+    w2 = dict(w)
+    w2["embed"] = s_in.reshape(B * T, mc.d)
+    ref = oracle_lib.Oracle(mc, w2).forward(np.arange(B * T, dtype=np.int32).reshape(B, T), want_scan=False,
+                                            nthreads=16)
+    bad = np.zeros((B, T), bool)
+    bad[1, 100] = bad[3, 7] = True
+    assert (got["iters"][bad] == 12).all() and (got["converged"][bad] == 0).all()
+    assert (ref["iters"][bad] == 12).all() and (ref["converged"][bad] == 0).all()
+    assert not np.isfinite(got["h_star"][bad]).any()
+    assert np.isfinite(got["h_star"][~bad]).all() and got["converged"][~bad].all()
+    good = {k: got[k][~bad][None] for k in got}
+    assert_forward_parity(good, {k: ref[k][~bad][None] for k in good}, "finite tokens, 256x256 tiles")
+
+
 def test_noncontractive_weights_report_nonconvergence(oracle_lib):
     """Block matrices at spectral norm 2 (non-contractive): no token settles within the cap; every
     one reports converged = 0 at max_iters, as in the oracle, and the state stays bounded (the
