@@ -188,14 +188,19 @@ PRESPLIT_SHAPES = [
     dict(d=640, H=4, V=600, N=2, flags=synth.F_SCAN_SELECTIVE | synth.F_SCORE_CLAMP4, qk_bias=True),
     dict(d=576, H=2, V=700, N=1, flags=0),
     dict(d=512, H=4, V=600, N=4, flags=synth.F_SCAN_SELECTIVE, sigma=0.7, anderson_m=3),
+    # ragged token count (3 x 400, the last tiles of every GEMM partial), a 3-slot run-time attention
+    dict(d=768, H=3, V=900, N=8, flags=synth.F_SCAN_SELECTIVE | synth.F_RESID_RELRMS, B=3, T=400),
+    # a vocabulary just above one 512-column block, Anderson m = 5, the L2 exit
+    dict(d=1024, H=2, V=520, N=16, flags=synth.F_SCAN_SELECTIVE | synth.F_RESID_L2, sigma=0.7, anderson_m=5),
 ]
 
 
 @pytest.mark.parametrize("var", PRESPLIT_SHAPES, ids=lambda v: f"d{v['d']}H{v['H']}")
 def test_presplit_operands_match_oracle(oracle_lib, var):
-    log(f"pre-split operands {var}, B=4 T=256")
+    var = dict(var)
+    B, T = var.pop("B", 4), var.pop("T", 256)
+    log(f"pre-split operands {var}, B={B} T={T}")
     mc, w = _small(**var)
-    B, T = 4, 256
     toks = synth.make_tokens("uniform", B, T, mc.V, seed=6)
     ref = oracle_lib.Oracle(mc, w).forward(toks, nthreads=16)
     be = make(mc, B, T)
