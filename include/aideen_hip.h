@@ -190,7 +190,9 @@ int adn_reset_state(adn_ctx *ctx);
 int adn_forward(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
 /* Device memory, enqueue only: run_forward_deq_no_readback / run_forward_from_seq_buf
  * (gpu_deq.rs:3855-4078).  Errors detected on the device (a token id outside [0, V)) are
- * reported by the next adn_synchronize(). */
+ * reported by the next adn_synchronize().  It enqueues kernels and device-to-device copies
+ * only, so once a first call with the same shapes and outputs has run, a call can be captured
+ * into a HIP graph on the context stream and replayed. */
 int adn_forward_async(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
 
 /* Greedy decode, host memory, blocking: Trainer::generate (trainer.rs:4219-4431) with
