@@ -87,3 +87,63 @@ def test_memory_forward_graph_replays_match_eager():
     B, T = 3, 10
     toks = synth.make_tokens("uniform", B, T, mc.V, seed=9)
     capture_and_replay(mc, w, B, T, toks)
+
+
+def test_serving_step_graph_with_noalloc_embed():
+    """A serving step that allocates nothing, captured whole: the queries of every position from
+    the token windows (adn_embed_context_noalloc, whose totals live in the library's fixed device
+    buffer) and the forward on those queries (logits, arg-max, h*).  The graph reads the token ids
+    from device memory at each replay: replays on two different token sets, written into the
+    captured input buffer between replays, must each equal the eager step on those tokens."""
+    import torch
+    log("graph capture, embed_context_noalloc + forward on the queries")
+    mc = synth.ModelConfig(d=512, H=2, V=700, N=4, r=32, max_iters=20)
+    w = synth.make_weights(mc, seed=12)
+    B, T, ctx = 4, 300, 64
+    dev = torch.device("cuda:0")
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    stream = torch.cuda.Stream(dev)
+    be.set_stream(stream.cuda_stream)
+    token_sets = [torch.from_numpy(synth.make_tokens("zipf", B, T, mc.V, seed=s)).to(dev) for s in (13, 14)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        tok = torch.empty((B, T), dtype=torch.int32, device=dev)
+        q = torch.empty((B, T, mc.d), device=dev)
+        outs = dict(h_star=torch.empty((B, T, mc.H, mc.d), device=dev),
+                    iters=torch.empty((B, T), dtype=torch.int32, device=dev),
+                    logits=torch.empty((B, T, mc.V), device=dev),
+                    argmax=torch.empty((B, T), dtype=torch.int32, device=dev))
+
+    def step():
+        be.embed_context_noalloc(tok, ctx, q)
+        be.forward_async(s_in=q, outputs=outs)
+
+    refs = []
+    for ts in token_sets:
+        with torch.cuda.stream(stream):
+            tok.copy_(ts)
+            step()
+        torch.cuda.synchronize()
+        be.synchronize()
+        refs.append({k: v.clone() for k, v in outs.items()})
+    assert not torch.equal(refs[0]["argmax"], refs[1]["argmax"])
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    for rep, i in enumerate((1, 0, 1)):
+        with torch.cuda.stream(stream):
+            tok.copy_(token_sets[i])
+            q.fill_(7)
+            for v in outs.values():
+                v.fill_(7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for k in outs:
+            assert torch.equal(outs[k], refs[i][k]), f"replay {rep} (token set {i}): {k} differs from the eager step"
+    be.synchronize()
+    be.close()
+    log("  replays on two token sets identical to the eager steps")
