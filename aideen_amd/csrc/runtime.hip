@@ -784,8 +784,10 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         c->scb.rec = (float *)dmalloc(c, (size_t)T * H * scan_rec_len(c->D) * sizeof(float));
         c->scb.y = (float *)dmalloc(c, hd);
         if (cfg->flags & ADN_F_MEMORY) {
-            c->scb.mem_mn = (float *)dmalloc(c, (size_t)cfg->max_batch * H * d * sizeof(float));
-            c->scb.mem_hist = (float *)dmalloc(c, (size_t)cfg->max_batch * H * d * sizeof(float));
+            // [batch][H][d] per position; a memory forward may run any batch with batch * seq <=
+            // cap_tok (e.g. max_batch = 1, max_seq = 8 admits batch 2 x seq 4), so size for cap_tok rows
+            c->scb.mem_mn = (float *)dmalloc(c, hd);
+            c->scb.mem_hist = (float *)dmalloc(c, hd);
         }
         c->scan_nch_cap = 16;
         const size_t chunk_states = (size_t)cfg->max_batch * c->scan_nch_cap * H * d;

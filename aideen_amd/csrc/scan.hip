@@ -557,10 +557,22 @@ __global__ __launch_bounds__(SSD_NT) void k_scan_ssd(Dims D, const float *__rest
             P[v] = ex * p[v];
             z[v] = xt[v] * __builtin_amdgcn_rcpf(P[v]) * bs[v];
         }
+        // A non-finite input (NaN / inf h*, record or decay at step tau) makes z non-finite from tau
+        // on.  The causal mask is a select on G, so in the product below a masked entry would still
+        // add 0 * z[tau] = NaN to the earlier steps t < tau, which the sequential recurrence keeps
+        // finite: the masked product takes such z as 0, and the steps from the channel's first
+        // non-finite one on are written as NaN after it (the state update below keeps the raw z,
+        // so the state turns non-finite as the recurrence's does).
+        bool bad[4], anybad = false;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            bad[v] = !(fabsf(z[v]) < INFINITY);
+            anybad |= bad[v];
+        }
         // Y = G_masked Z + C M0 (the old state) before the row scale of C: register v = step 4g + v
         floatx4 Y = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) Y = mfma4(4 * g + kb <= cl ? gt[kb] : 0.0f, z[kb], Y);
+        for (int kb = 0; kb < 4; ++kb) Y = mfma4(4 * g + kb <= cl ? gt[kb] : 0.0f, bad[kb] ? 0.0f : z[kb], Y);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -580,10 +592,24 @@ __global__ __launch_bounds__(SSD_NT) void k_scan_ssd(Dims D, const float *__rest
             float *yp = y + ylane + (long)tb * tstride;
             float yv[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                yv[v] = P[v] * bs[v] * Y[v];
-                ymax = fmaxf(ymax, (4 * g + v < nt_ && fabsf(yv[v]) < INFINITY) ? fabsf(yv[v]) : 0.0f);
+            for (int v = 0; v < 4; ++v) yv[v] = P[v] * bs[v] * Y[v];
+            if (__builtin_amdgcn_ballot_w64(anybad)) {  // wave-uniform: rare
+                // the channel's first non-finite step over its four lane groups (16 = none)
+                int fb = 16;
+#pragma unroll
+                for (int v = 3; v >= 0; --v) fb = bad[v] ? 4 * g + v : fb;
+                const int f0 = __builtin_amdgcn_ds_bpermute(cl << 2, fb);
+                const int f1 = __builtin_amdgcn_ds_bpermute((16 + cl) << 2, fb);
+                const int f2 = __builtin_amdgcn_ds_bpermute((32 + cl) << 2, fb);
+                const int f3 = __builtin_amdgcn_ds_bpermute((48 + cl) << 2, fb);
+                const int first = min(min(f0, f1), min(f2, f3));
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (4 * g + v >= first) yv[v] = __builtin_nanf("");
             }
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                ymax = fmaxf(ymax, (4 * g + v < nt_ && fabsf(yv[v]) < INFINITY) ? fabsf(yv[v]) : 0.0f);
             if (nt_ == SSD_L) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) yp[v * tstride] = yv[v];

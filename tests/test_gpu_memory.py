@@ -212,3 +212,21 @@ def test_token_carry_repeated_token_converges_at_once():
     got = gpu_memory(mc, w, toks)
     assert got["iters"][0, 0] > 3
     assert np.all(got["iters"][:, 1:] == 1)
+
+
+def test_memory_batch_beyond_max_batch(oracle_lib):
+    """A context created with max_batch = 1, max_seq = 8 (an .aidn-derived shape) admits any
+    batch * seq <= 8: a memory forward at batch 2 x seq 4, and a fixed-history decode of batch 2
+    whose priming runs 2 x 4 prompt tokens, both against the oracle.  Every per-position buffer of
+    the memory driver ([batch][H][d]) must hold that batch."""
+    log("memory batch beyond max_batch")
+    mc, w = mem_model(128, 4, 400, max_iters=6, eps=0.0)
+    toks = synth.make_tokens("uniform", 2, 4, mc.V, seed=16)
+    be = GpuDeqBackend(mc, 1, 8)
+    be.upload_weights(w)
+    o = oracle_lib.Oracle(mc, w)
+    check(be.forward(toks), o.forward_memory(toks), "batch 2 x seq 4 on max_batch 1")
+    got = be.decode_greedy(toks, 3, 4, max_iters=6, eps=0.0)
+    assert np.array_equal(got, o.decode_greedy(toks, 3, 4, 1.0))
+    with pytest.raises(AdnError, match="capacity"):
+        be.forward(synth.make_tokens("uniform", 3, 3, mc.V, seed=17))
