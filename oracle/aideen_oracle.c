@@ -613,15 +613,25 @@ static void carrier_inputs(const orc_cfg *c, const orc_weights *w, int s, const 
 void orc_scan_seq(const orc_cfg *c, const orc_weights *w, int T, const float *h_star,
                   const float *state_in, float *y, float *state_out) {
     const int d = c->d, H = c->H, N = c->N, r = c->r > 0 ? c->r : 1;
-    float *m = (float *)malloc(sizeof(float) * (size_t)d * N);
-    float *x = (float *)malloc(sizeof(float) * d);
-    float *ab = (float *)malloc(sizeof(float) * d);
-    float *yt = (float *)malloc(sizeof(float) * d);
-    float *wy = (float *)malloc(sizeof(float) * d);
-    float *Bv = (float *)malloc(sizeof(float) * N);
-    float *Cv = (float *)malloc(sizeof(float) * N);
-    float *bn = (float *)malloc(sizeof(float) * r);
+    /* The slots are independent carriers: they run in parallel (OpenMP; inside a caller's
+     * parallel region the nested region runs on one thread), each with its own buffers.  W_out
+     * is applied through its transpose (gemv_t, bit-identical to gemv_rm: the same per-output
+     * order). */
+#pragma omp parallel for schedule(dynamic, 1)
     for (int s = 0; s < H; ++s) {
+        float *m = (float *)malloc(sizeof(float) * (size_t)d * N);
+        float *x = (float *)malloc(sizeof(float) * d);
+        float *ab = (float *)malloc(sizeof(float) * d);
+        float *yt = (float *)malloc(sizeof(float) * d);
+        float *wy = (float *)malloc(sizeof(float) * d);
+        float *Bv = (float *)malloc(sizeof(float) * N);
+        float *Cv = (float *)malloc(sizeof(float) * N);
+        float *bn = (float *)malloc(sizeof(float) * r);
+        float *wt = NULL;
+        if (w->w_out) {
+            wt = (float *)malloc(sizeof(float) * (size_t)d * d);
+            transpose(w->w_out + (size_t)s * d * d, d, d, wt);
+        }
         if (state_in)
             memcpy(m, state_in + (size_t)s * d * N, sizeof(float) * d * N);
         else
@@ -640,16 +650,16 @@ void orc_scan_seq(const orc_cfg *c, const orc_weights *w, int T, const float *h_
                 yt[i] = acc;
             }
             float *out = y + ((size_t)t * H + s) * d;
-            if (w->w_out) {
-                gemv_rm(w->w_out + (size_t)s * d * d, d, d, yt, wy);
+            if (wt) {
+                gemv_t(wt, d, d, yt, wy);
                 for (int i = 0; i < d; ++i) out[i] = yt[i] + wy[i];
             } else {
                 memcpy(out, yt, sizeof(float) * d);
             }
         }
         if (state_out) memcpy(state_out + (size_t)s * d * N, m, sizeof(float) * d * N);
+        free(m); free(x); free(ab); free(yt); free(wy); free(Bv); free(Cv); free(bn); free(wt);
     }
-    free(m); free(x); free(ab); free(yt); free(wy); free(Bv); free(Cv); free(bn);
 }
 
 /* FPMR:1455-1486 temporal_step iterated over a sequence: the carried state is the output
