@@ -235,6 +235,44 @@ def make_weights(cfg: ModelConfig, seed: int = 0, gates_seed: int = 2,
     return w
 
 
+def make_token_sensitive_weights(cfg: ModelConfig, seed: int = 0,
+                                 long_memory_gates: bool = False) -> Dict[str, Optional[np.ndarray]]:
+    """A weight set whose outputs depend strongly on the token, for parity tests that must be able
+    to fail on a per-token error (a row written to the wrong token, a shifted index).
+
+    With the reference's own initialisation the solve is anchor-dominated: the anchors are U(-1, 1)
+    (FPMR:225-232) while an embedding row of the golden-ratio closed form has entries below
+    0.25/sqrt(d), and the closed forms of E and W_lm (f32 index cast) repeat rows.  Here, on top of
+    ``make_weights``: anchors x0.02, W_in at spectral norm 3, seeded random E = U(+-0.2) (every
+    row distinct), W_lm at Xavier range sqrt(3/d), a random bias U(+-0.05) and an LM-head gain
+    U(0.75, 1.25).  The signal W_in x then dominates the anchor, so the solve
+    is token-driven and still contracts (NS shape: 10-12 Picard iterations, the logits' token-
+    dependent part of order 1, as many distinct arg-max values as distinct tokens)."""
+    w = make_weights(dataclasses.replace(cfg, win_sigma=3.0), seed=seed, long_memory_gates=long_memory_gates)
+    d, V = cfg.d, cfg.V
+    xr = float(np.sqrt(np.float32(3.0) / np.float32(d)))
+    w["anchor"] = (w["anchor"] * np.float32(0.02)).astype(np.float32)
+    w["embed"] = uniform(seed, "ts_embed", (V, d), -0.2, 0.2)
+    w["lm_w"] = uniform(seed, "ts_lm_w", (V, d), -xr, xr)
+    w["lm_b"] = uniform(seed, "ts_lm_b", (V,), -0.05, 0.05)
+    w["lm_g"] = uniform(seed, "ts_lm_g", (d,), 0.75, 1.25)
+    return w
+
+
+WEIGHT_SETS = ("preset", "token_sensitive")
+
+
+def weights_of_kind(kind: str, cfg: ModelConfig, seed: int = 0,
+                    long_memory_gates: bool = False) -> Dict[str, Optional[np.ndarray]]:
+    """``make_weights`` ("preset": the reference's initialisation) or
+    ``make_token_sensitive_weights`` ("token_sensitive")."""
+    if kind == "preset":
+        return make_weights(cfg, seed=seed, long_memory_gates=long_memory_gates)
+    if kind == "token_sensitive":
+        return make_token_sensitive_weights(cfg, seed=seed, long_memory_gates=long_memory_gates)
+    raise ValueError(f"unknown weight set {kind!r}")
+
+
 def make_hist_weights(cfg: ModelConfig, seed: int = 0, strong: bool = False) -> Dict[str, np.ndarray]:
     """Weights of the memory-coupled solve, following the reference's initial values
     (FPMR:279 w_hist_shared = 0.15 I + U(+-0.01); FPMR:312-318 hist_slot_scale = centred slot *

@@ -14,7 +14,7 @@ def load_case(name):
     import dataclasses
     meta = json.load(open(os.path.join(HERE, name + ".json")))
     mc = synth.ModelConfig(**meta["config"])
-    w = synth.make_weights(mc, seed=meta["weights_seed"])
+    w = synth.weights_of_kind(meta.get("weights", "preset"), mc, seed=meta["weights_seed"])
     assert synth.weights_digest(w) == meta["weights_sha256"], "synthetic generator drifted"
     data = dict(np.load(os.path.join(HERE, name + ".npz")))
     toks = synth.make_tokens("uniform", meta["B"], meta["T"], mc.V, seed=meta["tokens_seed"])
@@ -22,7 +22,7 @@ def load_case(name):
     return mc, w, data
 
 
-@pytest.mark.parametrize("name", ["c1_forward", "c1_anderson_m5"])
+@pytest.mark.parametrize("name", ["c1_forward", "c1_anderson_m5", "c1_token_sensitive"])
 def test_oracle_reproduces_golden(oracle_lib, name):
     mc, w, data = load_case(name)
     out = oracle_lib.Oracle(mc, w).forward(data["tokens"])
@@ -40,3 +40,18 @@ def test_golden_fixed_points_are_fixed_points(oracle_lib):
         x = w["embed"][data["tokens"][0, t]]
         hn, _ = o.step(data["h_star"][0, t], o.signal(x))
         assert np.abs(hn - data["h_star"][0, t]).max() < mc.eps
+
+
+def test_token_sensitive_golden_can_fail(oracle_lib):
+    """The token-sensitive fixture discriminates tokens (the check can fail on a per-token error, as
+    the reference's pipeline test asserts of its own comparison, picard_pipeline_test.rs:1021-1030):
+    its arg-max takes many values, the logits' token-dependent part is far above the forward's
+    atol 1e-3, and the logits of neighbouring positions (a one-row shift) differ by far more."""
+    mc, w, data = load_case("c1_token_sensitive")
+    lg = data["logits"][0]
+    assert len(set(data["argmax"].ravel().tolist())) >= 16
+    assert np.abs(lg - lg.mean(axis=0)).max() >= 1e-2
+    assert (np.abs(lg[1:] - lg[:-1]).max(axis=-1) > 1e-2).mean() > 0.9
+    assert np.abs(data["h_star"][0, 1:] - data["h_star"][0, :-1]).max() > 1e-2
+    it = data["iters"].ravel()
+    assert it.min() < it.max() < mc.max_iters  # iteration counts vary and every token converges
