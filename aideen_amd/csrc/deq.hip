@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
             }
         };
         auto step = [&](int s, const SlotIn &q) {
-            float *h = b.h + ((long)t * H + s) * d;
+            float *h = (b.h_out ? b.h_out : b.h) + ((long)t * H + s) * d;
             float cval[E];
             float ss = 0.0f;
 #pragma unroll
@@ -612,7 +612,8 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     const float *sg = b.signal + ((long)t * H + s) * d;
     const float *an = anchor + (long)s * d;
     const float *hc = b.mem_hist ? b.mem_hist + ((long)(t / b.mem_T) * H + s) * d : nullptr;
-    float *h = b.h + ((long)t * H + s) * d;
+    const float *h = b.h + ((long)t * H + s) * d;
+    float *hw = (b.h_out ? b.h_out : b.h) + ((long)t * H + s) * d;
     // every load (the norm scale too) before the first store of h: a load issued after stores
     // is waited for behind them (the vector-memory counter retires in issue order)
     float cval[E], hold[E], gs[E];
@@ -636,7 +637,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     for (int e = 0; e < E; ++e) {
         const float f = gs[e] * cval[e] / rms;
         const float hn = f * beta + hold[e] * omb;
-        if (!PART || e < er) h[lane + 64 * e] = hn;
+        if (!PART || e < er) hw[lane + 64 * e] = hn;
         const float df = hn - hold[e];
         r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
     }
@@ -757,6 +758,129 @@ __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int
     }
 }
 
+// One-pass form of k_anderson (NRES in 2..4) for token states of at most AND_NT * EPT floats: each
+// thread holds its elements of the current iterate and of the NRES previous ones in registers, so
+// the ring is read once per iteration (NRES + 1 vectors read, the ring slot and h written) instead
+// of twice (2 NRES + 2 read); after an update that wrote the slot itself (SLOT), NRES + 1 read and
+// h alone written.  Element e = tid + q AND_NT of thread tid, q ascending: the same assignment and
+// summation order as k_anderson's Gram and mix, so the results are bit-identical.
+// (EXACT: the state is exactly AND_NT * EPT floats, so no element needs a bounds test.)
+// SLOT: the update wrote its iterate into ring slot k % m (SolveBuffers::h_out) and list `lst` is
+// the update's own list: a token that exited at iteration k (iters = k + 1) or any token while
+// NRES = 0 gets h = its iterate; a continuing one the mix, without writing the slot again.
+// Otherwise list `lst` holds the continuing tokens, whose iterate is in h.
+template <int NRES, int EPT, bool EXACT, bool SLOT>
+__global__ __launch_bounds__(AND_NT) void k_anderson_reg(Dims D, SolveBuffers b, int lst, int ntok, int k,
+                                                         int m) {
+    __shared__ float red[AND_NT / 64][10];
+    __shared__ float beta_s[4];
+    const int i = blockIdx.x;
+    if (i >= b.cnt[lst]) return;
+    const int t = b.act[lst][i];
+    const int hd = D.H * D.d;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *h = b.h + (long)t * hd;
+    auto X = [&](int j) { return b.hist + ((long)(j % m) * ntok + t) * hd; };
+    float *slot = X(k);
+    if constexpr (SLOT) {
+        if (NRES == 0 || b.iters[t] == k + 1) {  // h = the update's iterate
+            float v[EPT];
+#pragma unroll
+            for (int q = 0; q < EPT; ++q) {
+                const int e = tid + q * AND_NT;
+                v[q] = (EXACT || e < hd) ? slot[e] : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < EPT; ++q) {
+                const int e = tid + q * AND_NT;
+                if (EXACT || e < hd) h[e] = v[q];
+            }
+            return;
+        }
+    }
+    if constexpr (NRES >= 2) {
+        // every load before the first store (the vector-memory counter retires in issue order)
+        float x[NRES + 1][EPT];  // x[0] = X(k) (in h, or in the slot), x[ri] = X(k - ri)
+#pragma unroll
+        for (int ri = 0; ri <= NRES; ++ri) {
+            const float *src = ri == 0 ? (SLOT ? slot : h) : X(k + m - ri);
+#pragma unroll
+            for (int q = 0; q < EPT; ++q) {
+                const int e = tid + q * AND_NT;
+                x[ri][q] = (EXACT || e < hd) ? src[e] : 0.0f;
+            }
+        }
+        if constexpr (!SLOT) {
+#pragma unroll
+            for (int q = 0; q < EPT; ++q) {
+                const int e = tid + q * AND_NT;
+                if (EXACT || e < hd) slot[e] = x[0][q];
+            }
+        }
+        constexpr int NPK = NRES * (NRES + 1) / 2;
+        float gp[NPK];
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) gp[q] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < EPT; ++q) {
+            float dl[NRES];
+#pragma unroll
+            for (int ri = 0; ri < NRES; ++ri) dl[ri] = x[ri][q] - x[ri + 1][q];
+            int p = 0;
+#pragma unroll
+            for (int ri = 0; ri < NRES; ++ri)
+#pragma unroll
+                for (int rj = ri; rj < NRES; ++rj) gp[p++] += dl[ri] * dl[rj];
+        }
+        // the NPK wave sums interleaved (wave_sum's pairings, each round issued for all of them at once)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            float o[NPK];
+#pragma unroll
+            for (int q = 0; q < NPK; ++q) o[q] = __shfl_xor(gp[q], off, 64);
+#pragma unroll
+            for (int q = 0; q < NPK; ++q) gp[q] += o[q];
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int q = 0; q < NPK; ++q) red[wave][q] = gp[q];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float g[16];
+            int q = 0;
+            for (int ri = 0; ri < NRES; ++ri)
+                for (int rj = ri; rj < NRES; ++rj) {
+                    float v = 0.0f;
+                    for (int w = 0; w < AND_NT / 64; ++w) v += red[w][q];
+                    g[ri * NRES + rj] = v;
+                    g[rj * NRES + ri] = v;
+                    ++q;
+                }
+            float bt[4];
+            anderson_coeffs(NRES, g, bt);
+            for (int q2 = 0; q2 < NRES; ++q2) beta_s[q2] = bt[q2];
+        }
+        __syncthreads();
+        float bl[NRES];
+#pragma unroll
+        for (int ri = 0; ri < NRES; ++ri) bl[ri] = beta_s[ri];
+        float hmax = 0.0f;
+#pragma unroll
+        for (int q = 0; q < EPT; ++q) {
+            const int e = tid + q * AND_NT;
+            float acc = 0.0f;
+#pragma unroll
+            for (int ri = 0; ri < NRES; ++ri) acc += bl[ri] * x[ri][q];
+            if (EXACT || e < hd) {
+                h[e] = acc;
+                hmax = fmaxf(hmax, fabsf(acc) < INFINITY ? fabsf(acc) : 0.0f);
+            }
+        }
+        if (b.amax_h) track_absmax(b.amax_h, hmax);
+    }
+}
+
 template <int H, int QA>
 void attn_dispatch_vec(const Dims &D, const SolveBuffers &b, int cur, int k, int ntok, hipStream_t st) {
     constexpr int NG = H / QA;
@@ -858,12 +982,71 @@ void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, in
     const int n_res = k < m - 1 ? k : m - 1;
     const int nres = (k >= 2 && n_res >= 2) ? n_res : 0;
     const dim3 grid((unsigned)rows), blk(AND_NT);
+    const long hd = (long)D.H * D.d;
+    // the one-pass form where a thread's elements fit in registers (16 per vector: at most 157 VGPRs,
+    // 3 waves per SIMD; 32 would take 256, one wave per SIMD)
+    if (nres >= 2 && hd <= 16L * AND_NT) {
+        auto go = [&](auto ept) {
+            constexpr int EPT = decltype(ept)::value;
+            auto go2 = [&](auto exact) {
+                constexpr bool EX = decltype(exact)::value;
+                switch (nres) {
+                    case 2: hipLaunchKernelGGL((k_anderson_reg<2, EPT, EX, false>), grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
+                    case 3: hipLaunchKernelGGL((k_anderson_reg<3, EPT, EX, false>), grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
+                    default: hipLaunchKernelGGL((k_anderson_reg<4, EPT, EX, false>), grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
+                }
+            };
+            if (hd == (long)EPT * AND_NT)
+                go2(std::true_type{});
+            else
+                go2(std::false_type{});
+        };
+        if (hd <= 4L * AND_NT)
+            go(std::integral_constant<int, 4>{});
+        else if (hd <= 8L * AND_NT)
+            go(std::integral_constant<int, 8>{});
+        else
+            go(std::integral_constant<int, 16>{});
+        return;
+    }
     switch (nres) {
         case 0: hipLaunchKernelGGL(k_anderson<0>, grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
         case 2: hipLaunchKernelGGL(k_anderson<2>, grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
         case 3: hipLaunchKernelGGL(k_anderson<3>, grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
         default: hipLaunchKernelGGL(k_anderson<4>, grid, blk, 0, st, D, b, nxt, ntok, k, m); break;
     }
+}
+
+bool anderson_from_slot_ok(const Dims &D) { return (long)D.H * D.d <= 16L * AND_NT; }
+
+void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, int ntok, int rows, int k, int m,
+                               hipStream_t st) {
+    const int n_res = k < m - 1 ? k : m - 1;
+    const int nres = (k >= 2 && n_res >= 2) ? n_res : 0;
+    const dim3 grid((unsigned)rows), blk(AND_NT);
+    const long hd = (long)D.H * D.d;
+    auto go = [&](auto ept) {
+        constexpr int EPT = decltype(ept)::value;
+        auto go2 = [&](auto exact) {
+            constexpr bool EX = decltype(exact)::value;
+            switch (nres) {
+                case 0: hipLaunchKernelGGL((k_anderson_reg<0, EPT, EX, true>), grid, blk, 0, st, D, b, cur, ntok, k, m); break;
+                case 2: hipLaunchKernelGGL((k_anderson_reg<2, EPT, EX, true>), grid, blk, 0, st, D, b, cur, ntok, k, m); break;
+                case 3: hipLaunchKernelGGL((k_anderson_reg<3, EPT, EX, true>), grid, blk, 0, st, D, b, cur, ntok, k, m); break;
+                default: hipLaunchKernelGGL((k_anderson_reg<4, EPT, EX, true>), grid, blk, 0, st, D, b, cur, ntok, k, m); break;
+            }
+        };
+        if (hd == (long)EPT * AND_NT)
+            go2(std::true_type{});
+        else
+            go2(std::false_type{});
+    };
+    if (hd <= 4L * AND_NT)
+        go(std::integral_constant<int, 4>{});
+    else if (hd <= 8L * AND_NT)
+        go(std::integral_constant<int, 8>{});
+    else
+        go(std::integral_constant<int, 16>{});
 }
 
 }  // namespace adn

@@ -123,6 +123,9 @@ struct SolveBuffers {
     float *mix_pre;
     const unsigned *mix_bound;
     float mix_headroom;
+    // non-null: the update writes its iterate here (rows indexed like h: the Anderson ring slot
+    // of the iteration) instead of into h, and the Anderson pass that follows sets h
+    float *h_out;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -138,6 +141,14 @@ void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max
 // ntok is the token stride of the ring).
 void launch_anderson(const Dims &D, const SolveBuffers &b, int nxt, int ntok, int rows, int k, int m,
                      hipStream_t st);
+// Whether launch_anderson_from_slot serves this state width (a thread's share in registers).
+bool anderson_from_slot_ok(const Dims &D);
+// Anderson after an update that wrote its iterate into ring slot k % m (SolveBuffers::h_out), over
+// every token of list cur (the ones the update saw): a token that exited at iteration k gets
+// h = its iterate, a continuing one h = the mix (or its iterate while fewer than two residuals
+// exist).  The ring slot is not written again.
+void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, int ntok, int rows, int k, int m,
+                               hipStream_t st);
 
 // ---- LM head (head.hip) -----------------------------------------------------------------
 // pooled = mean_s h*, pnorm = (pooled/rms(pooled, 1e-5)) * g

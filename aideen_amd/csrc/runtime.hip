@@ -404,13 +404,24 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
             launch_gemm(g, st);
         }
+        // With Anderson mixing after this update, the update writes its iterate straight into the
+        // iteration's ring slot and the mixing pass, over every token the update saw, sets h (the
+        // mix, or the iterate of a token that exited): the iterate is written once instead of to h
+        // and then again to the slot.
+        const bool mix = m > 0 && k + 1 < r.max_iters;
+        const bool from_slot = mix && anderson_from_slot_ok(D);
         {
             Span sp(prof, ADN_STAGE_UPDATE, k, st);
-            launch_update(D, b, cur, k, r.max_iters, r.eps, rows, c->anchor, c->norm_scale, r.damping, st);
+            SolveBuffers bu = b;
+            if (from_slot) bu.h_out = b.hist + (long)(k % m) * ntok * H * d;
+            launch_update(D, bu, cur, k, r.max_iters, r.eps, rows, c->anchor, c->norm_scale, r.damping, st);
         }
-        if (m > 0 && k + 1 < r.max_iters) {
+        if (mix) {
             Span sp(prof, ADN_STAGE_ANDERSON, k, st);
-            launch_anderson(D, b, cur ^ 1, ntok, rows, k, m, st);
+            if (from_slot)
+                launch_anderson_from_slot(D, b, cur, ntok, rows, k, m, st);
+            else
+                launch_anderson(D, b, cur ^ 1, ntok, rows, k, m, st);
         }
     }
 }
