@@ -464,6 +464,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
         };
         auto step = [&](int s, const SlotIn &q) {
             float *h = (b.h_out ? b.h_out : b.h) + ((long)t * H + s) * d;
+            float *h2 = b.h_both ? b.h + ((long)t * H + s) * d : nullptr;
             float cval[E];
             float ss = 0.0f;
 #pragma unroll
@@ -480,7 +481,10 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
             for (int e = 0; e < E; ++e) {
                 const float f = g[e] * cval[e] / rms;
                 const float hn = f * beta + q.h[e] * omb;
-                if (!PART || e < er) h[lane + 64 * e] = hn;
+                if (!PART || e < er) {
+                    h[lane + 64 * e] = hn;
+                    if (h2) h2[lane + 64 * e] = hn;
+                }
                 const float df = hn - q.h[e];
                 r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
             }
@@ -612,7 +616,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     const float *sg = b.signal + ((long)t * H + s) * d;
     const float *an = anchor + (long)s * d;
     const float *hc = b.mem_hist ? b.mem_hist + ((long)(t / b.mem_T) * H + s) * d : nullptr;
-    const float *h = b.h + ((long)t * H + s) * d;
+    float *h = b.h + ((long)t * H + s) * d;
     float *hw = (b.h_out ? b.h_out : b.h) + ((long)t * H + s) * d;
     // every load (the norm scale too) before the first store of h: a load issued after stores
     // is waited for behind them (the vector-memory counter retires in issue order)
@@ -637,7 +641,10 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
     for (int e = 0; e < E; ++e) {
         const float f = gs[e] * cval[e] / rms;
         const float hn = f * beta + hold[e] * omb;
-        if (!PART || e < er) hw[lane + 64 * e] = hn;
+        if (!PART || e < er) {
+            hw[lane + 64 * e] = hn;
+            if (b.h_both) h[lane + 64 * e] = hn;
+        }
         const float df = hn - hold[e];
         r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
     }

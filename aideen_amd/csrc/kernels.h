@@ -126,6 +126,8 @@ struct SolveBuffers {
     // non-null: the update writes its iterate here (rows indexed like h: the Anderson ring slot
     // of the iteration) instead of into h, and the Anderson pass that follows sets h
     float *h_out;
+    // with h_out: write the iterate into h as well (iterations before the first mix)
+    int h_both;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -224,8 +226,9 @@ long embed_context_chunks(int T);
 // doubles each of tot0 / tot1 that launch_embed_context writes for B sequences of T positions
 // at width d (B * its chunk count * d; never more than B * embed_context_chunks(T) * d)
 long embed_context_total_doubles(int d, int B, int T);
+// busy (or null): the overlap guard of a shared tot0/tot1 array (two words, zero when idle)
 void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
-                          double *tot1, float *out, unsigned *err, hipStream_t st);
+                          double *tot1, float *out, unsigned *err, unsigned *busy, hipStream_t st);
 // Clean adjoint Picard for ntok tokens (rows = ntok * H of d floats); scratch pre, v0, v1 hold
 // rows * d floats, terms 2 * rows.  Returns the buffer holding the final iterate (v_out when given).
 struct AdjointArgs {

@@ -28,8 +28,12 @@ void set_error(const std::string &msg) { g_last_error = msg; }
 // process ends.  Host code never passes the symbol itself to a kernel (on the host it names a
 // stand-in, not device memory): the device address is looked up once per device, with that
 // device current, when the first context on it is created, and only that address is used.
+// After the data, 256 bytes hold the overlap guard (two words, zero when idle: the calls in
+// flight and the finished blocks of the current call's last kernel); static device memory starts
+// zeroed.
 constexpr long NOALLOC_MAX_DOUBLES = 1L << 22;
-static __device__ __align__(256) double scratch[NOALLOC_MAX_DOUBLES];
+constexpr long NOALLOC_GUARD_DOUBLES = 32;
+static __device__ __align__(256) double scratch[NOALLOC_MAX_DOUBLES + NOALLOC_GUARD_DOUBLES];
 static std::mutex g_scratch_mu;
 static double *g_scratch_ptr[256];  // by device ordinal; null until looked up
 
@@ -408,15 +412,20 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         // iteration's ring slot and the mixing pass, over every token the update saw, sets h (the
         // mix, or the iterate of a token that exited): the iterate is written once instead of to h
         // and then again to the slot.
+        // Before the first mix (k < 2) the update writes the iterate into both, and no mixing pass
+        // runs.
         const bool mix = m > 0 && k + 1 < r.max_iters;
         const bool from_slot = mix && anderson_from_slot_ok(D);
         {
             Span sp(prof, ADN_STAGE_UPDATE, k, st);
             SolveBuffers bu = b;
-            if (from_slot) bu.h_out = b.hist + (long)(k % m) * ntok * H * d;
+            if (from_slot) {
+                bu.h_out = b.hist + (long)(k % m) * ntok * H * d;
+                bu.h_both = k < 2;
+            }
             launch_update(D, bu, cur, k, r.max_iters, r.eps, rows, c->anchor, c->norm_scale, r.damping, st);
         }
-        if (mix) {
+        if (mix && !(from_slot && k < 2)) {
             Span sp(prof, ADN_STAGE_ANDERSON, k, st);
             if (from_slot)
                 launch_anderson_from_slot(D, b, cur, ntok, rows, k, m, st);
@@ -714,6 +723,10 @@ int check_device_error(adn_ctx *c) {
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
         ADN_HIP(hipStreamSynchronize(c->stream));
         if (err & ADN_DEVERR_TOKEN) return fail(ADN_E_INVALID, "token id outside [0, vocab)");
+        if (err & ADN_DEVERR_OVERLAP)
+            return fail(ADN_E_INVALID, "adn_embed_context_noalloc calls overlapped on one GPU (other streams or "
+                                       "threads): the shared device array they use was raced, their outputs are "
+                                       "not valid");
         return fail(ADN_E_INVALID, "device-side error");
     }
     return ADN_OK;
@@ -1281,7 +1294,7 @@ void enqueue_embed_context(adn_ctx *c, int32_t batch, int32_t seq, const int32_t
         c->ctx_tot_n = need;
     }
     launch_embed_context(c->embed, c->D.d, c->D.V, tokens, batch, seq, max_ctx, c->ctx_tot, c->ctx_tot + need, out,
-                         c->d_err, c->stream);
+                         c->d_err, nullptr, c->stream);
 }
 
 }  // namespace
@@ -1315,8 +1328,22 @@ int adn_embed_context_noalloc(adn_ctx *c, int32_t batch, int32_t seq, const int3
         // every total the window kernel reads is written by the chunk kernel of this call first,
         // so the buffer needs no clearing
         launch_embed_context(c->embed, c->D.d, c->D.V, tokens, batch, seq, max_ctx, p, p + half, out, c->d_err,
-                             c->stream);
+                             reinterpret_cast<unsigned *>(p + NOALLOC_MAX_DOUBLES), c->stream);
         ADN_HIP(hipGetLastError());
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_noalloc_guard_set(adn_ctx *c, uint32_t calls_in_flight) {
+    if (!c) return fail(ADN_E_INVALID, "null context");
+    double *p = g_scratch_ptr[c->device];
+    if (!p) return fail(ADN_E_HIP, "adn_noalloc_guard_set: no device buffer for this device");
+    try {
+        const uint32_t words[2] = {calls_in_flight, 0u};
+        ADN_HIP(hipMemcpyAsync(p + NOALLOC_MAX_DOUBLES, words, sizeof(words), hipMemcpyHostToDevice, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
     } catch (const HipError &e) {
         return hip_fail(e);
     }
