@@ -130,6 +130,7 @@ def lib():
         "adn_embed_context": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_embed_context_async": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
         "adn_embed_context_noalloc": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, F32P]),
+        "adn_noalloc_guard_set": (C.c_int, [ctx_p, C.c_uint32]),
         "adn_profile_forward": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs),
                                           C.POINTER(AdnProfile)]),
     }

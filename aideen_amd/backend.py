@@ -216,6 +216,11 @@ class GpuDeqBackend:
         B, T = tokens.shape
         check(lib().adn_embed_context_noalloc(self._ctx, B, T, _dev_i(tokens), int(max_ctx), _dev_f(out)))
 
+    def noalloc_guard_set(self, calls_in_flight: int) -> None:
+        """Diagnostics: set this GPU's count of embed_context_noalloc calls in flight (tests force
+        an overlap with it)."""
+        check(lib().adn_noalloc_guard_set(self._ctx, int(calls_in_flight)))
+
     # backward ----------------------------------------------------------------------------------
     def adjoint(self, dl: np.ndarray, iters: int, damping: Optional[float] = None,
                 h_star: Optional[np.ndarray] = None):

@@ -15,6 +15,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // Device error flags (set by kernels, read back by adn_synchronize).
 #define ADN_DEVERR_TOKEN 1u
+#define ADN_DEVERR_OVERLAP 2u  // adn_embed_context_noalloc calls overlapped on one GPU
 
 namespace adn {
 

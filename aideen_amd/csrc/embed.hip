@@ -62,9 +62,14 @@ __device__ __forceinline__ void load_rows(float (&x)[CHK][DPT], const float *E, 
 }
 
 template <int DPT>
+// busy (or null): the overlap guard of a shared chunk-total array, [0] the calls in flight, [1] the
+// window kernel's finished blocks.  The chunk kernel raises [0] (a call that finds it raised
+// overlaps another: ADN_DEVERR_OVERLAP), the last block of the window kernel lowers it.
 __global__ __launch_bounds__(ENT) void k_ctx_chunks(const float *E, int d, int V, const int32_t *tokens, int T,
-                                                     int nch, double *tot0, double *tot1, unsigned *err) {
+                                                     int nch, double *tot0, double *tot1, unsigned *err,
+                                                     unsigned *busy) {
     constexpr int CHK = chunk_len<DPT>();
+    if (busy && blockIdx.x == 0 && threadIdx.x == 0 && atomicAdd(busy, 1u) != 0u) atomicOr(err, ADN_DEVERR_OVERLAP);
     const int b = blockIdx.x / nch, c = blockIdx.x - b * nch;
     const int p0 = c * CHK;
     float x[CHK][DPT];
@@ -110,7 +115,7 @@ __global__ __launch_bounds__(ENT) void k_ctx_scan(int d, int nch, int B, double 
 template <int DPT>
 __global__ __launch_bounds__(ENT) void k_ctx_window(const float *E, int d, int V, const int32_t *tokens, int T,
                                                      int nch, int ctx, const double *tot0, const double *tot1,
-                                                     float *out, unsigned *err) {
+                                                     float *out, unsigned *err, unsigned *busy) {
     constexpr int CHK = chunk_len<DPT>();
     __shared__ double red[CHK][ENT / 64];
     const int b = blockIdx.x / nch, c = blockIdx.x - b * nch;
@@ -198,17 +203,28 @@ __global__ __launch_bounds__(ENT) void k_ctx_window(const float *E, int d, int V
             if (j < d) o[j] = (float)(v[p][q] * inv);
         }
     }
+    if (busy) {  // the call's last block (every block has read its totals) lowers the guard
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();
+            if (atomicAdd(busy + 1, 1u) == gridDim.x - 1) {
+                atomicExch(busy + 1, 0u);
+                atomicSub(busy, 1u);
+            }
+        }
+    }
 }
 
 template <int DPT>
 void launch_ctx(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
-                double *tot1, float *out, unsigned *err, hipStream_t st) {
+                double *tot1, float *out, unsigned *err, unsigned *busy, hipStream_t st) {
     constexpr int CHK = chunk_len<DPT>();
     const int nch = (T + CHK - 1) / CHK;
     const dim3 grid((unsigned)(B * nch)), blk(ENT);
-    hipLaunchKernelGGL(k_ctx_chunks<DPT>, grid, blk, 0, st, E, d, V, tokens, T, nch, tot0, tot1, err);
+    hipLaunchKernelGGL(k_ctx_chunks<DPT>, grid, blk, 0, st, E, d, V, tokens, T, nch, tot0, tot1, err, busy);
     hipLaunchKernelGGL(k_ctx_scan, dim3((unsigned)(((long)B * d + ENT - 1) / ENT)), blk, 0, st, d, nch, B, tot0, tot1);
-    hipLaunchKernelGGL(k_ctx_window<DPT>, grid, blk, 0, st, E, d, V, tokens, T, nch, ctx, tot0, tot1, out, err);
+    hipLaunchKernelGGL(k_ctx_window<DPT>, grid, blk, 0, st, E, d, V, tokens, T, nch, ctx, tot0, tot1, out, err,
+                       busy);
 }
 
 }  // namespace
@@ -228,16 +244,16 @@ long embed_context_total_doubles(int d, int B, int T) {
 }
 
 void launch_embed_context(const float *E, int d, int V, const int32_t *tokens, int B, int T, int ctx, double *tot0,
-                          double *tot1, float *out, unsigned *err, hipStream_t st) {
+                          double *tot1, float *out, unsigned *err, unsigned *busy, hipStream_t st) {
     const int dpt = ctx_dpt(d);
     if (dpt <= 1)
-        launch_ctx<1>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, st);
+        launch_ctx<1>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, busy, st);
     else if (dpt <= 2)
-        launch_ctx<2>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, st);
+        launch_ctx<2>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, busy, st);
     else if (dpt <= 4)
-        launch_ctx<4>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, st);
+        launch_ctx<4>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, busy, st);
     else
-        launch_ctx<8>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, st);
+        launch_ctx<8>(E, d, V, tokens, B, T, ctx, tot0, tot1, out, err, busy, st);
 }
 
 }  // namespace adn

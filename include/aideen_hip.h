@@ -271,11 +271,19 @@ int adn_embed_context_async(adn_ctx *ctx, int32_t batch, int32_t seq, const int3
  * process ends) instead of context memory grown on demand; a request needing more than that
  * (2 * batch * ceil(seq / chunk) * d_r doubles, chunk = 32, 16, 8 or 4 positions for d_r up to
  * 256, 512, 1024, 2048) fails with ADN_E_CAPACITY.  Every call on one GPU, from any context, shares
- * that array: calls that overlap on one GPU (other streams, other threads) race.  The context's
- * uploaded embedding table is read; device memory, enqueue only. */
+ * that array: calls that overlap on one GPU (other streams, other threads) race.  Such an overlap
+ * is detected on the device (a counter of calls in flight beside the array, raised by a call's
+ * first kernel and lowered by its last one) and reported by the next blocking call on the context
+ * that found the array in use (ADN_E_INVALID, "... overlapped ..."); the raced outputs are not
+ * valid.  Callers that use several streams or contexts on one GPU order these calls themselves.
+ * The context's uploaded embedding table is read; device memory, enqueue only. */
 #define ADN_EMBED_NOALLOC_MAX_DOUBLES 4194304
 int adn_embed_context_noalloc(adn_ctx *ctx, int32_t batch, int32_t seq, const int32_t *tokens,
                               int32_t max_ctx, float *out);
+/* No counterpart in the reference.  Diagnostics of the overlap detection above: sets the count
+ * of adn_embed_context_noalloc calls in flight on the context's GPU (0 when idle), so that tests
+ * can force an overlap from the host.  Blocking. */
+int adn_noalloc_guard_set(adn_ctx *ctx, uint32_t calls_in_flight);
 
 /* --- byte-level BPE (Tokenizer::encode / decode, tokenizer.rs:94-116, which run the HF
  *     `tokenizers` crate on aideen-backbone/tokenizer.json) --------------------------------------

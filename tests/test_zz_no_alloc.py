@@ -56,3 +56,31 @@ def test_noalloc_rejects_requests_beyond_its_buffer():
     be.synchronize()
     assert np.isfinite(out[:, :4096].cpu().numpy()).all()
     be.close()
+
+
+def test_noalloc_overlap_is_reported():
+    """Overlapping calls on one GPU race on the shared array; the library detects them.  The
+    overlap is forced from the host: with the guard's count of calls in flight set to 1 (as if
+    another call were running), a call reports the overlap on the context's next blocking call;
+    with the count back at 0, calls in stream order report nothing, and leave the count at 0."""
+    log("noalloc overlap guard")
+    mc = synth.ModelConfig(d=128, H=2, V=300, N=1, flags=0)
+    be = GpuDeqBackend(mc, 2, 40)
+    be.upload_weights(synth.make_weights(mc, seed=2))
+    dev = torch.device("cuda:0")
+    toks_h = synth.make_tokens("uniform", 2, 40, mc.V, seed=3)
+    toks = torch.from_numpy(toks_h).to(dev)
+    out = torch.empty((2, 40, 128), dtype=torch.float32, device=dev)
+    be.noalloc_guard_set(1)
+    be.embed_context_noalloc(toks, 8, out)
+    with pytest.raises(AdnError, match="overlapped"):
+        be.forward(toks_h, want=("iters",))
+    be.noalloc_guard_set(0)
+    for _ in range(3):
+        be.embed_context_noalloc(toks, 8, out)
+    be.forward(toks_h, want=("iters",))  # no error: the calls ran in stream order
+    ref = torch.empty_like(out)
+    be.embed_context_async(toks, 8, ref)
+    be.synchronize()
+    assert np.array_equal(out.cpu().numpy(), ref.cpu().numpy())
+    be.close()
