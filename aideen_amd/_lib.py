@@ -106,6 +106,8 @@ def lib():
                                         C.c_float, C.c_float, C.c_float, I32P]),
         "adn_spectral_norm": (C.c_int, [ctx_p, F32P, C.c_int32, C.c_int32, C.c_int32, F32P]),
         "adn_normalize_if_needed": (C.c_int, [ctx_p, F32P, C.c_int32, C.c_int32, C.c_float, C.c_int32]),
+        "adn_renormalize_spectral": (C.c_int, [ctx_p, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float,
+                                               C.c_int32, F32P]),
         "adn_block_step": (C.c_int, [ctx_p, C.c_int32, F32P, F32P, F32P, F32P, F32P, F32P]),
         "adn_load_tensor": (C.c_int, [ctx_p, F32P, C.c_int64, I32P]),
         "adn_ffn_forward": (C.c_int, [ctx_p, C.c_int32, C.c_int32, C.c_int32, F32P]),

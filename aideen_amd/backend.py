@@ -17,6 +17,7 @@ Failures raise ``AdnError`` carrying the library's message (the Rust side return
 from __future__ import annotations
 
 import ctypes as C
+import os
 from typing import Dict, Optional
 
 import numpy as np
@@ -281,6 +282,39 @@ class GpuDeqBackend:
         w = np.ascontiguousarray(w, np.float32).copy()
         check(lib().adn_normalize_if_needed(self._ctx, _fp(w), w.shape[0], w.shape[1], threshold, n_iter))
         return w
+
+    @staticmethod
+    def _env_f32(name: str) -> Optional[float]:
+        v = os.environ.get(name)
+        try:
+            return float(v) if v is not None else None
+        except ValueError:
+            return None
+
+    def renormalize_spectral(self, n_iters: int = 12) -> np.ndarray:
+        """GpuDeqBackend::renormalize_spectral (gpu_deq.rs:5567-5591): the uploaded block matrices
+        renormalised on the device with the reference's thresholds and their environment overrides
+        (AIDEEN_DEQ_ATTN_THRESHOLD 0.10 for W_q/W_k, AIDEEN_DEQ_WIN_THRESHOLD 0.30 for W_in,
+        AIDEEN_DEQ_WV_THRESHOLD and AIDEEN_DEQ_WO_THRESHOLD 0.50, the carrier's W_x/W_out 0.70).
+        Returns the sigma estimates before rescaling, [7][h_slots] (W_q, W_k, W_v, W_o, W_in, W_x,
+        W_out)."""
+        def thr(name, default, floor):  # env_f32(name).unwrap_or(default).max(floor)
+            v = self._env_f32(name)
+            return max(default if v is None else v, floor)
+        attn = thr("AIDEEN_DEQ_ATTN_THRESHOLD", 0.10, 0.01)
+        win = thr("AIDEEN_DEQ_WIN_THRESHOLD", 0.30, 0.05)
+        wv = thr("AIDEEN_DEQ_WV_THRESHOLD", 0.50, 0.01)
+        wo = thr("AIDEEN_DEQ_WO_THRESHOLD", 0.50, 0.01)
+        return self.renormalize_spectral_with(attn, win, 0.70, wv, wo, n_iters)
+
+    def renormalize_spectral_with(self, attn_threshold: float, win_threshold: float, fpm_threshold: float,
+                                  wv_threshold: float, wo_threshold: float, n_iters: int = 12) -> np.ndarray:
+        """RustDeqBridge::renormalize_spectral (deq_bridge.rs:1742-1791) with explicit thresholds."""
+        sig = np.zeros((7, self.model.H), np.float32)
+        check(lib().adn_renormalize_spectral(self._ctx, float(attn_threshold), float(win_threshold),
+                                             float(fpm_threshold), float(wv_threshold), float(wo_threshold),
+                                             int(n_iters), _fp(sig)))
+        return sig
 
 
 class HipBlockBackend:

@@ -204,6 +204,17 @@ bool scan_use_ssd(const Dims &D, int B, int T, float min_fixed_decay);
 void launch_spectral_norm(const float *w, int rows, int cols, int n_iter, float *sigma,
                           float *work, hipStream_t st);
 void launch_scale_if(float *w, long n, const float *sigma, float threshold, hipStream_t st);
+// The GPU's spectral renormalisation of uploaded block matrices (spectral_renorm.wgsl:83-196): per
+// job, the shader's power iteration on the matrix as the shader's buffer holds it, then
+// m *= threshold / sigma when sigma > threshold; sigma goes to sigmas[out].  d <= 2048.
+enum RenormKind { RENORM_T = 0, RENORM_N = 1, RENORM_DIAG = 2 };
+struct RenormJob {
+    float *m;         // [d][d] row-major, or [d] (RENORM_DIAG)
+    int kind;         // RenormKind: the shader's buffer is m^T, m, or diag(m)
+    float threshold;
+    int out;          // index into sigmas
+};
+void launch_spectral_renorm(const RenormJob *jobs, int njobs, int d, int n_iters, float *sigmas, hipStream_t st);
 void launch_zoh(int d, const float *x, const float *dt, const float *a, const float *b,
                 const float *c, float *y, hipStream_t st);
 void launch_gemv_colmajor(const float *w, const float *x, int in_dim, int out_dim, float *y,

@@ -147,6 +147,81 @@ __global__ void k_reset_bounds(unsigned *words, unsigned w0, unsigned *zero) {
     if (i == ADN_BOUNDS && zero) *zero = 0u;
 }
 
+// The GPU spectral renormalisation (spectral_renorm.wgsl:83-196): one workgroup of 256 per matrix.
+// The shader indexes its buffer as wg[i*d + j]; with the matrix M as stored here (row-major
+// [d][d]) that buffer is M^T (RENORM_T, the per-slot Q/K/V/O and W_out, whose reference buffers
+// are [in][out]), M itself (RENORM_N: W_in, uploaded row-major) or a diagonal (RENORM_DIAG: W_x,
+// of which the carrier keeps the diagonal).  u = 1/sqrt(d); per iteration v = wg^T u / sqrt(|.|^2 +
+// 1e-12), u = wg v, sigma = sqrt(|u|^2 + 1e-12), u /= sigma; then, when sigma exceeds the
+// matrix's threshold, M *= threshold / sigma.  Thread t owns rows t, t + 256, ...: every dot
+// product is summed over j in order and every squared norm by the shader's tree, without
+// contracted multiply-adds, as the oracle restates it.
+constexpr int RN_NT = 256;
+constexpr int RN_MAXD = 2048;
+
+__device__ float rn_tree(float v, float *part) {
+    __syncthreads();
+    part[threadIdx.x] = v;
+    __syncthreads();
+    for (int stride = RN_NT / 2; stride > 0; stride >>= 1) {
+        if ((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
+        __syncthreads();
+    }
+    return part[0];
+}
+
+__global__ __launch_bounds__(RN_NT) void k_spectral_renorm(const RenormJob *jobs, int d, int n_iters,
+                                                           float *sigmas) {
+#pragma clang fp contract(off)
+    __shared__ float u[RN_MAXD], v[RN_MAXD], part[RN_NT];
+    const RenormJob J = jobs[blockIdx.x];
+    const float *M = J.m;
+    const int tid = threadIdx.x;
+    // wg[a][b] of the shader's buffer
+    auto wg = [&](int a, int b) {
+        return J.kind == RENORM_T ? M[(long)b * d + a] : J.kind == RENORM_N ? M[(long)a * d + b] : (a == b ? M[a] : 0.0f);
+    };
+    for (int i = tid; i < d; i += RN_NT) u[i] = 1.0f / sqrtf((float)d);
+    __syncthreads();
+    float sigma = 1.0f;
+    for (int it = 0; it < n_iters; ++it) {
+        float acc = 0.0f;
+        for (int row = tid; row < d; row += RN_NT) {
+            float vt = 0.0f;
+            if (J.kind == RENORM_DIAG) {
+                vt = M[row] * u[row];  // the other terms of the shader's sum are zero
+            } else {
+                for (int j = 0; j < d; ++j) vt += wg(j, row) * u[j];
+            }
+            v[row] = vt;
+            acc += vt * vt;
+        }
+        const float vn = sqrtf(rn_tree(acc, part) + 1e-12f);
+        for (int row = tid; row < d; row += RN_NT) v[row] = v[row] / vn;
+        __syncthreads();
+        acc = 0.0f;
+        for (int row = tid; row < d; row += RN_NT) {
+            float ut = 0.0f;
+            if (J.kind == RENORM_DIAG) {
+                ut = M[row] * v[row];
+            } else {
+                for (int j = 0; j < d; ++j) ut += wg(row, j) * v[j];
+            }
+            u[row] = ut;
+            acc += ut * ut;
+        }
+        sigma = sqrtf(rn_tree(acc, part) + 1e-12f);
+        for (int row = tid; row < d; row += RN_NT) u[row] = u[row] / sigma;
+        __syncthreads();
+    }
+    if (tid == 0) sigmas[J.out] = sigma;
+    if (sigma > J.threshold) {
+        const float scale = J.threshold / sigma;
+        const long n = J.kind == RENORM_DIAG ? d : (long)d * d;
+        for (long e = tid; e < n; e += RN_NT) J.m[e] = M[e] * scale;
+    }
+}
+
 }  // namespace
 
 void launch_reset_bounds(unsigned *words, float h_bound, unsigned *zero, hipStream_t st) {
@@ -205,6 +280,11 @@ void launch_fill_i32(int32_t *p, int32_t v, long n, hipStream_t st) {
     const long blocks = (n + 255) / 256;
     hipLaunchKernelGGL(k_fill_i32, dim3((unsigned)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096)),
                        dim3(256), 0, st, p, v, n);
+}
+
+void launch_spectral_renorm(const RenormJob *jobs, int njobs, int d, int n_iters, float *sigmas, hipStream_t st) {
+    if (njobs > 0)
+        hipLaunchKernelGGL(k_spectral_renorm, dim3((unsigned)njobs), dim3(RN_NT), 0, st, jobs, d, n_iters, sigmas);
 }
 
 }  // namespace adn

@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cstring>
 #include <cmath>
 #include <initializer_list>
 #include <utility>
@@ -1207,6 +1208,79 @@ int adn_normalize_if_needed(adn_ctx *c, float *w, int32_t rows, int32_t cols, fl
         ADN_HIP(hipGetLastError());
         ADN_HIP(hipMemcpyAsync(w, dw, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
         ADN_HIP(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+    return ADN_OK;
+}
+
+int adn_renormalize_spectral(adn_ctx *c, float attn_threshold, float win_threshold, float fpm_threshold,
+                             float wv_threshold, float wo_threshold, int32_t n_iters, float *sigmas) {
+    if (!c) return fail(ADN_E_INVALID, "null context");
+    if (!c->has_weights) return fail(ADN_E_NO_WEIGHTS, "renormalize_spectral before adn_upload_weights");
+    if (n_iters < 1 || n_iters > 1000) return fail(ADN_E_INVALID, "n_iters must be in [1, 1000]");
+    for (float t : {attn_threshold, win_threshold, fpm_threshold, wv_threshold, wo_threshold})
+        if (!(t > 0.0f) || !std::isfinite(t)) return fail(ADN_E_INVALID, "thresholds must be finite and > 0");
+    const int d = c->D.d, H = c->D.H;
+    const size_t mat = (size_t)d * d;
+    try {
+        // jobs in the shader's matrix order per slot role: W_q, W_k (attention threshold), W_v, W_o,
+        // W_in, W_x, W_out (the carrier's threshold); sigmas[role * H + s]
+        std::vector<RenormJob> jobs;
+        const bool win_t = (c->cfg.flags & ADN_F_WIN_TRANSPOSED) != 0;
+        for (int s = 0; s < H; ++s) {
+            float *qkv = c->w_qkv + (size_t)s * 3 * mat;
+            jobs.push_back({qkv, RENORM_T, attn_threshold, 0 * H + s});
+            jobs.push_back({qkv + mat, RENORM_T, attn_threshold, 1 * H + s});
+            jobs.push_back({qkv + 2 * mat, RENORM_T, wv_threshold, 2 * H + s});
+            jobs.push_back({c->w_o + (size_t)s * mat, RENORM_T, wo_threshold, 3 * H + s});
+            // the reference's W_in buffer is the CPU matrix; the GEMM copy here holds it (or its
+            // transpose under ADN_F_WIN_TRANSPOSED, whose product is W_in^T x)
+            jobs.push_back({c->w_in + (size_t)s * mat, win_t ? RENORM_T : RENORM_N, win_threshold, 4 * H + s});
+            jobs.push_back({c->wx_diag + (size_t)s * d, RENORM_DIAG, fpm_threshold, 5 * H + s});
+            if (c->w_out) jobs.push_back({c->w_out + (size_t)s * mat, RENORM_T, fpm_threshold, 6 * H + s});
+        }
+        const int nj = (int)jobs.size();
+        auto *djobs = (RenormJob *)staging_f(c, 29, jobs.size() * sizeof(RenormJob));
+        float *dsig = staging_f(c, 30, (7 * (size_t)H + 8) * sizeof(float));
+        unsigned *words = reinterpret_cast<unsigned *>(dsig + 7 * H);  // 4 absmax words
+        ADN_HIP(hipMemsetAsync(dsig, 0, (7 * (size_t)H + 8) * sizeof(float), c->stream));
+        ADN_HIP(hipMemcpyAsync(djobs, jobs.data(), jobs.size() * sizeof(RenormJob), hipMemcpyHostToDevice,
+                               c->stream));
+        launch_spectral_renorm(djobs, nj, d, n_iters, dsig, c->stream);
+        // the split copies from the rescaled matrices, with scales from their new magnitudes
+        launch_absmax(c->w_qkv, (long)(3 * H * mat), words + 0, c->stream);
+        launch_absmax(c->w_o, (long)(H * mat), words + 1, c->stream);
+        launch_absmax(c->w_in, (long)(H * mat), words + 2, c->stream);
+        if (c->w_out) launch_absmax(c->w_out, (long)(H * mat), words + 3, c->stream);
+        std::vector<float> hs(7 * (size_t)H + 8);
+        ADN_HIP(hipMemcpyAsync(hs.data(), dsig, hs.size() * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        float mx[4];
+        std::memcpy(mx, hs.data() + 7 * H, sizeof(mx));
+        make_split(c, c->sp_qkv, c->w_qkv, H, 3 * d, d, mx[0]);
+        make_split(c, c->sp_o, c->w_o, H, d, d, mx[1]);
+        make_split(c, c->sp_in, c->w_in, H, d, d, mx[2]);
+        if (c->w_out) make_split(c, c->sp_out, c->w_out, H, d, d, mx[3]);
+        // row-L1 bounds of W_v and W_out (the range guard's): a slot scaled by f has f times its
+        // rows' L1 norms, so the largest factor keeps the bound valid
+        auto factor = [&](int role, float thr) {
+            float f = 0.0f;
+            for (int s = 0; s < H; ++s) {
+                const float sg = hs[(size_t)role * H + s];
+                f = std::max(f, sg > thr ? thr / sg : 1.0f);
+            }
+            return f;
+        };
+        c->l1_wv *= factor(2, wv_threshold);
+        if (c->w_out) c->l1_wout *= factor(6, fpm_threshold);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipStreamSynchronize(c->stream));
+        if (sigmas) {
+            std::memcpy(sigmas, hs.data(), 7 * (size_t)H * sizeof(float));
+            if (!c->w_out)
+                for (int s = 0; s < H; ++s) sigmas[6 * H + s] = 0.0f;
+        }
     } catch (const HipError &e) {
         return hip_fail(e);
     }

@@ -221,6 +221,19 @@ int adn_spectral_norm(adn_ctx *ctx, const float *w, int32_t rows, int32_t cols, 
 /* In place: W *= threshold/sigma when sigma > threshold (normalize_if_needed). */
 int adn_normalize_if_needed(adn_ctx *ctx, float *w, int32_t rows, int32_t cols, float threshold,
                             int32_t n_iter);
+/* GpuDeqBackend::renormalize_spectral (gpu_deq.rs:5567-5591) -> RustDeqBridge::renormalize_spectral
+ * (aideen-block/src/deq_bridge.rs:1742-1791), spectral_renorm.wgsl:83-196: the uploaded block
+ * matrices renormalised in place on the device.  Per slot: W_q and W_k against attn_threshold,
+ * W_v against wv_threshold, W_o against wo_threshold, W_in against win_threshold, W_x (its
+ * diagonal, which is what the carrier keeps) and W_out against fpm_threshold; each matrix's sigma
+ * is the shader's n_iters-step power iteration on the matrix as the reference's buffer holds it
+ * (W^T for the per-slot [in][out] matrices, W_in as uploaded), and a matrix with sigma > threshold
+ * becomes W * (threshold / sigma).  The GEMMs' split copies are rebuilt.  The reference's defaults
+ * are 0.10, 0.30, 0.70, 0.50, 0.50 and 12 iterations.  sigmas (or null) receives the 7 * h_slots
+ * estimates before rescaling, [role][slot] with roles W_q, W_k, W_v, W_o, W_in, W_x, W_out (0 for
+ * W_out when there is none).  Blocking. */
+int adn_renormalize_spectral(adn_ctx *ctx, float attn_threshold, float win_threshold, float fpm_threshold,
+                             float wv_threshold, float wo_threshold, int32_t n_iters, float *sigmas);
 
 /* --- BlockBackend (aideen-core/src/block_backend.rs:22-31) ------------------------------ */
 /* fpm_batch_step: ZOH single step, h_prev = 0 (gpu_backend.rs:18-56, :98-248).  All [d]. */

@@ -564,6 +564,71 @@ int orc_argmax(const float *logits, int V) {
     return best;
 }
 
+/* spectral_renorm.wgsl:26-47: the workgroup reduction (256 partial sums folded at strides
+ * 128, 64, ..., 1). */
+static float wg_tree_sum(float *part) {
+    for (int stride = 128; stride > 0; stride >>= 1)
+        for (int t = 0; t < stride; ++t) part[t] += part[t + stride];
+    return part[0];
+}
+
+/* spectral_renorm.wgsl:83-160: thread tid of 256 owns rows tid, tid + 256, ...; its partial sum of
+ * squares runs over those rows in order. */
+float orc_spectral_norm_gpu(const float *wg, int d, int n_iters) {
+    float *u = (float *)malloc(sizeof(float) * d);
+    float *v = (float *)malloc(sizeof(float) * d);
+    float part[256];
+    const int items = (d + 255) / 256;
+    for (int i = 0; i < d; ++i) u[i] = 1.0f / sqrtf((float)d);
+    float sigma = 1.0f;
+    for (int it = 0; it < n_iters; ++it) {
+        for (int row = 0; row < d; ++row) {
+            float vt = 0.0f;
+            for (int j = 0; j < d; ++j) vt += wg[(size_t)j * d + row] * u[j];
+            v[row] = vt;
+        }
+        for (int t = 0; t < 256; ++t) {
+            float acc = 0.0f;
+            for (int i = 0; i < items; ++i) {
+                const int row = t + i * 256;
+                if (row < d) acc += v[row] * v[row];
+            }
+            part[t] = acc;
+        }
+        const float vn = sqrtf(wg_tree_sum(part) + 1e-12f);
+        for (int row = 0; row < d; ++row) v[row] = v[row] / vn;
+        for (int t = 0; t < 256; ++t) part[t] = 0.0f;
+        for (int row = 0; row < d; ++row) {
+            float ut = 0.0f;
+            for (int j = 0; j < d; ++j) ut += wg[(size_t)row * d + j] * v[j];
+            u[row] = ut;
+        }
+        for (int t = 0; t < 256; ++t) {
+            float acc = 0.0f;
+            for (int i = 0; i < items; ++i) {
+                const int row = t + i * 256;
+                if (row < d) acc += u[row] * u[row];
+            }
+            part[t] = acc;
+        }
+        sigma = sqrtf(wg_tree_sum(part) + 1e-12f);
+        for (int row = 0; row < d; ++row) u[row] = u[row] / sigma;
+    }
+    free(u);
+    free(v);
+    return sigma;
+}
+
+/* spectral_renorm.wgsl:162-195: rescale when sigma exceeds the matrix's threshold. */
+float orc_renorm_gpu(float *w, long n, const float *wg, int d, float threshold, int n_iters) {
+    const float sigma = orc_spectral_norm_gpu(wg, d, n_iters);
+    if (sigma > threshold) {
+        const float scale = threshold / sigma;
+        for (long i = 0; i < n; ++i) w[i] = w[i] * scale;
+    }
+    return sigma;
+}
+
 /* ------------------------------------------------------------------------- */
 /* temporal carrier (selective scan)                                          */
 /* ------------------------------------------------------------------------- */

@@ -62,6 +62,17 @@ typedef struct orc_weights {
 float orc_spectral_norm(const float *w, int rows, int cols, int n_iter);
 void  orc_normalize(float *w, int rows, int cols, float target, int n_iter);
 void  orc_normalize_if_needed(float *w, int rows, int cols, float threshold, int n_iter);
+
+/* --- spectral_renorm.wgsl:83-196 (GpuDeqBackend::renormalize_spectral, gpu_deq.rs:5567-5591;
+ *     RustDeqBridge::renormalize_spectral, deq_bridge.rs:1742-1791) ------------------------------
+ * sigma of one d x d matrix as the shader estimates it, from the matrix as the shader's buffer
+ * holds it, wg[i*d + j]: u = 1/sqrt(d); per iteration v = wg^T u / sqrt(|.|^2 + 1e-12),
+ * u' = wg v, sigma = sqrt(|u'|^2 + 1e-12), u = u' / sigma; each dot product summed over j in
+ * order, each squared norm as the shader's 256-thread tree. */
+float orc_spectral_norm_gpu(const float *wg, int d, int n_iters);
+/* The renormalisation of one matrix w (n floats): sigma from orc_spectral_norm_gpu of its buffer
+ * form wg; when sigma > threshold every element becomes w * (threshold / sigma).  Returns sigma. */
+float orc_renorm_gpu(float *w, long n, const float *wg, int d, float threshold, int n_iters);
 void  orc_damped_update(const float *h, const float *f, float beta, int n, float *out);
 
 /* --- FPMR per-token pieces ------------------------------------------------ */

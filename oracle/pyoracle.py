@@ -60,6 +60,10 @@ def lib():
         L.orc_spectral_norm.argtypes = [F32P, C.c_int, C.c_int, C.c_int]
         L.orc_normalize.argtypes = [F32P, C.c_int, C.c_int, C.c_float, C.c_int]
         L.orc_normalize_if_needed.argtypes = [F32P, C.c_int, C.c_int, C.c_float, C.c_int]
+        L.orc_spectral_norm_gpu.restype = C.c_float
+        L.orc_spectral_norm_gpu.argtypes = [F32P, C.c_int, C.c_int]
+        L.orc_renorm_gpu.restype = C.c_float
+        L.orc_renorm_gpu.argtypes = [F32P, C.c_long, F32P, C.c_int, C.c_float, C.c_int]
         L.orc_damped_update.argtypes = [F32P, F32P, C.c_float, C.c_int, F32P]
         L.orc_signal.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P]
         L.orc_init.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
@@ -300,6 +304,45 @@ def normalize_if_needed(w: np.ndarray, threshold: float, n_iter: int = 20) -> np
     w = np.ascontiguousarray(w, np.float32).copy()
     lib().orc_normalize_if_needed(fp(w), w.shape[0], w.shape[1], threshold, n_iter)
     return w
+
+
+def spectral_norm_gpu(wg: np.ndarray, n_iters: int = 12) -> float:
+    """spectral_renorm.wgsl's sigma estimate of the d x d buffer wg (indexed wg[i, j])."""
+    wg = np.ascontiguousarray(wg, np.float32)
+    return lib().orc_spectral_norm_gpu(fp(wg), wg.shape[0], n_iters)
+
+
+# (weight, threshold index, buffer form) of renormalize_spectral's roles: the reference's buffers
+# are [in][out] per slot for W_q/W_k/W_v/W_o (w_*_gpu_flat, fixed_point_memory_reasoning.rs:516-561)
+# and for the carrier's W_out (nalgebra's column-major storage), the CPU matrix for W_in (uploaded
+# row-major, read transposed by the forward kernel: D2), and the diagonal for W_x (what the carrier
+# keeps of it).  Thresholds: (attn, win, fpm, wv, wo).
+RENORM_ROLES = (("w_q", 0, "T"), ("w_k", 0, "T"), ("w_v", 3, "T"), ("w_o", 4, "T"), ("w_in", 1, "N"),
+                ("wx_diag", 2, "diag"), ("w_out", 2, "T"))
+
+
+def renormalize_spectral(weights: Dict[str, Optional[np.ndarray]], thresholds=(0.10, 0.30, 0.70, 0.50, 0.50),
+                         n_iters: int = 12):
+    """GpuDeqBackend::renormalize_spectral (gpu_deq.rs:5567-5591; deq_bridge.rs:1742-1791;
+    spectral_renorm.wgsl:83-196) on a weight dict in include/aideen_hip.h's [s][out][in] layout:
+    (renormalised copy, sigmas [7][H] in RENORM_ROLES order, 0 for an absent W_out)."""
+    w = {k: (None if v is None else np.array(v, np.float32, copy=True)) for k, v in weights.items()}
+    H = w["w_q"].shape[0]
+    sig = np.zeros((7, H), np.float32)
+    for role, (name, ti, form) in enumerate(RENORM_ROLES):
+        if w.get(name) is None:
+            continue
+        for s in range(H):
+            m = np.ascontiguousarray(w[name][s])
+            if form == "T":
+                wg = np.ascontiguousarray(m.T)
+            elif form == "N":
+                wg = m
+            else:
+                wg = np.diag(m).astype(np.float32)
+            sig[role, s] = lib().orc_renorm_gpu(fp(m), m.size, fp(wg), wg.shape[0], float(thresholds[ti]), n_iters)
+            w[name][s] = m
+    return w, sig
 
 
 def damped_update(h, f, beta):

@@ -498,6 +498,53 @@ def test_spectral_norm_matches_oracle(oracle_lib):
     assert abs(be.spectral_norm(np.eye(64, dtype=np.float32)) - 1.0) < 1e-3
 
 
+RENORM_CASES = [
+    dict(d=128, H=4, flags=synth.F_SCAN_SELECTIVE, big_out=True),
+    dict(d=192, H=3, flags=synth.F_WIN_TRANSPOSED, big_out=False),
+    dict(d=512, H=2, flags=synth.F_SCAN_SELECTIVE, big_out=None),  # no W_out
+]
+
+
+@pytest.mark.parametrize("var", RENORM_CASES, ids=lambda v: f"d{v['d']}H{v['H']}f{v['flags']}")
+def test_renormalize_spectral_matches_oracle(oracle_lib, var, monkeypatch):
+    """GpuDeqBackend::renormalize_spectral (gpu_deq.rs:5567-5591, spectral_renorm.wgsl:83-196) on the
+    device: every block matrix at spectral norm 0.6 (above the attention, W_in and W_v/W_o
+    thresholds), W_out above the carrier's 0.70 or far below it or absent, a W_x diagonal entry of
+    0.9.  The sigma estimates match the oracle's restatement of the shader, and the forward on the
+    renormalised device weights matches the oracle's forward on the oracle-renormalised weights.
+    A second call finds nothing above its threshold; an environment override of the attention
+    threshold is honoured."""
+    log(f"renormalize_spectral {var}")
+    mc = synth.ModelConfig(d=var["d"], H=var["H"], V=400, N=4, flags=var["flags"], sigma=0.6)
+    w = synth.make_weights(mc, seed=8)
+    w["wx_diag"] = w["wx_diag"].copy()
+    w["wx_diag"][:, 3] = 0.9
+    if var["big_out"] is None:
+        w["w_out"] = None
+    elif var["big_out"]:
+        w["w_out"] = (w["w_out"] * np.float32(100.0)).astype(np.float32)
+    be = make(mc, 3, 20)
+    be.upload_weights(w)
+    monkeypatch.delenv("AIDEEN_DEQ_ATTN_THRESHOLD", raising=False)
+    sig = be.renormalize_spectral()
+    w2, sref = oracle_lib.renormalize_spectral(w)
+    np.testing.assert_allclose(sig, sref, rtol=1e-6, atol=0)
+    assert (sref[0:5] > np.array([0.10, 0.10, 0.50, 0.50, 0.30])[:, None]).all()
+    toks = synth.make_tokens("uniform", 3, 20, mc.V, seed=4)
+    got = be.forward(toks)
+    ref = oracle_lib.Oracle(mc, w2).forward(toks)
+    assert_forward_parity(got, ref, f"renormalised {var}")
+    again = be.renormalize_spectral()
+    thr = np.array([0.10, 0.10, 0.50, 0.50, 0.30, 0.70, 0.70])[:, None]
+    assert (again <= thr * (1 + 1e-5)).all()
+    monkeypatch.setenv("AIDEEN_DEQ_ATTN_THRESHOLD", "0.05")
+    be.renormalize_spectral()
+    w3, _ = oracle_lib.renormalize_spectral(w2, thresholds=(0.05, 0.30, 0.70, 0.50, 0.50))
+    got3 = be.forward(toks)
+    assert_forward_parity(got3, oracle_lib.Oracle(mc, w3).forward(toks), f"attention threshold 0.05 {var}")
+    be.close()
+
+
 def test_block_step_and_compute_backend(oracle_lib):
     be = make(synth.ModelConfig(d=64, H=1, V=10), 1, 1)
     rng = np.random.default_rng(1)

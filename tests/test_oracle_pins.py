@@ -973,3 +973,82 @@ def test_anderson_exit_moves_by_two_under_one_ulp_at_c3(oracle_lib):
     xp[idx] = np.nextafter(xp[idx], np.float32(np.inf))
     _, itp, tracep = o.solve(xp)
     assert itp == 11 and tracep[10] < mc.eps
+
+
+# ------------------------------------------------------------------------------------------
+# spectral_renorm.wgsl:83-196 (GpuDeqBackend::renormalize_spectral)
+# ------------------------------------------------------------------------------------------
+def _shader_sigma_f64(wg, n_iters):
+    """The shader's power iteration in float64 (a textbook restatement, for the oracle's steps)."""
+    wg = wg.astype(np.float64)
+    d = wg.shape[0]
+    u = np.full(d, 1.0 / np.sqrt(d))
+    sigma = 1.0
+    for _ in range(n_iters):
+        v = wg.T @ u
+        v = v / np.sqrt(v @ v + 1e-12)
+        u = wg @ v
+        sigma = np.sqrt(u @ u + 1e-12)
+        u = u / sigma
+    return sigma
+
+
+@pytest.mark.parametrize("d,n_iters", [(64, 1), (64, 3), (192, 12), (300, 2)])
+def test_gpu_spectral_norm_steps(oracle_lib, d, n_iters):
+    """The restated shader iteration equals its float64 restatement step for step (few iterations
+    on a non-normal matrix, where the estimate still depends on the starting side: the transposed
+    buffer gives a different value, so the orientation is pinned too)."""
+    rng = np.random.default_rng(d + n_iters)
+    wg = (rng.standard_normal((d, d)) / np.sqrt(d)).astype(np.float32)
+    wg[:, 0] *= 6.0  # strongly non-normal
+    s = oracle_lib.spectral_norm_gpu(wg, n_iters)
+    ref = _shader_sigma_f64(wg, n_iters)
+    assert abs(s - ref) <= 2e-6 * ref
+    if n_iters == 1:
+        assert abs(_shader_sigma_f64(np.ascontiguousarray(wg.T), n_iters) - ref) > 1e-3 * ref
+
+
+def test_gpu_spectral_norm_closed_forms(oracle_lib):
+    """c I -> sqrt(c^2 + 1e-12) after one step; a rank-one a b^T -> |a| |b| after one step; a
+    matrix with a known SVD and a gap of 3 converges to its largest singular value."""
+    d = 128
+    assert abs(oracle_lib.spectral_norm_gpu(0.7 * np.eye(d, dtype=np.float32), 1) - 0.7) < 1e-6
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal(d).astype(np.float32)
+    b = rng.standard_normal(d).astype(np.float32)
+    r1 = np.outer(a, b).astype(np.float32)
+    want = float(np.linalg.norm(a.astype(np.float64)) * np.linalg.norm(b.astype(np.float64)))
+    assert abs(oracle_lib.spectral_norm_gpu(r1, 1) - want) < 2e-5 * want
+    U, _ = np.linalg.qr(rng.standard_normal((d, d)))
+    V, _ = np.linalg.qr(rng.standard_normal((d, d)))
+    s = np.linspace(0.1, 1.0, d)
+    s[0] = 3.0
+    W = (U @ np.diag(s) @ V.T).astype(np.float32)
+    assert abs(oracle_lib.spectral_norm_gpu(W, 12) - 3.0) < 1e-4
+
+
+def test_renormalize_spectral_roles(oracle_lib):
+    """The model-level renormalisation: each role against its threshold (W_q/W_k 0.10, W_in 0.30,
+    W_v/W_o 0.50, W_x/W_out 0.70), rescaled exactly by threshold / sigma when above it and left
+    bit-identical otherwise; W_q's sigma is its buffer's (W^T), W_in's the uploaded matrix's; W_x
+    is its diagonal (sigma = max |diag| for a converged iteration)."""
+    from aideen_amd import synth
+    mc = synth.ModelConfig(d=64, H=2, V=50, N=1, flags=0, sigma=0.6)
+    w = synth.make_weights(mc, seed=5)
+    w["wx_diag"] = np.tile(np.linspace(-0.3, 0.2, 64, dtype=np.float32), (2, 1))
+    w["wx_diag"][:, 7] = -0.9  # a clear gap: the 12 steps converge to max |diag|
+    w["w_out"] = (w["w_out"] * np.float32(0.01)).astype(np.float32)  # far below 0.70
+    out, sig = oracle_lib.renormalize_spectral(w, n_iters=12)
+    thr = {"w_q": 0.10, "w_k": 0.10, "w_v": 0.50, "w_o": 0.50, "w_in": 0.30, "wx_diag": 0.70, "w_out": 0.70}
+    for role, (name, _, form) in enumerate(oracle_lib.RENORM_ROLES):
+        for s in range(2):
+            m = w[name][s]
+            wg = m.T if form == "T" else (m if form == "N" else np.diag(m))
+            assert sig[role, s] == oracle_lib.spectral_norm_gpu(np.ascontiguousarray(wg, np.float32), 12)
+            t = thr[name]
+            if sig[role, s] > t:
+                assert np.array_equal(out[name][s], (m * np.float32(np.float32(t) / sig[role, s])).astype(np.float32))
+            else:
+                assert np.array_equal(out[name][s], m)
+    assert (sig[0] > 0.10).all() and (sig[5] > 0.70).all() and (sig[6] < 0.70).all()
+    assert abs(sig[5, 0] - 0.9) < 1e-5  # the diagonal's largest magnitude
