@@ -346,8 +346,10 @@ __device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[
     } else {
         // Q|K|V and W_o outputs are read by the very next kernel (attention, update): stored
         // non-temporally they stream past L2, which keeps the operands of the tiles still being
-        // multiplied in L2 and leaves the outputs to the consumer in the memory-side cache.
-        constexpr bool ST = ROLE == ROLE_QKV || ROLE == ROLE_WO;
+        // multiplied in L2 and leaves the outputs to the consumer in the memory-side cache.  The
+        // one-wave blocks of the few-row products store normally: their outputs are a few
+        // kilobytes that the next kernel reads straight from L2.
+        constexpr bool ST = (ROLE == ROLE_QKV || ROLE == ROLE_WO) && WGM * WGN > 1;
         if (p.epi == EPI_BIAS) {
             if (interior)
                 epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, false, false, ST>(p, acc, c);

@@ -377,23 +377,133 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
 // [8j, 8j + 8) of that run.  A and B use the same K order, so each MFMA still contracts
 // matching K indices.  The KW partial blocks are summed in LDS in wave order (deterministic)
 // and wave 0 runs the role's epilogue.
-template <int ROLE, typename T, int TERMS, int KW, int WTN>
+//
+// ATTN (W_o at a few rows, GemmParams::attn_qkv): A, the attention mix of slot s, is formed here
+// from the compact Q|K|V rows (fixed_point_memory_reasoning.rs:1397-1421: scores q_s.k_c / sqrt(d),
+// optionally clamped to [-4, 4], softmax with max and sum in key order, mix = sum over c in order
+// of w_c v_c), so that the attention needs no kernel of its own; its work is repeated by the
+// slot's column blocks, which at a few rows costs less than a launch.  The block forms each row's
+// mix in LDS: every thread loads its elements of every key slot at once (clamped addresses, so the
+// loads do not wait behind per-slot branches), the score shares are summed over the waves in order,
+// and the K loop then reads A from LDS.
+template <int ROLE, typename T, int TERMS, int KW, int WTN, bool ATTN = false>
 __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     typedef typename Vec8<T>::type V8;
     __shared__ float red[KW > 1 ? KW - 1 : 1][WTN * 16][64];  // [wave-1][element][lane]
     // LM head: the 32 rows' (max, arg-max) partials of the block's 128 columns
     __shared__ float am_v[ROLE == ROLE_LMHEAD ? 32 : 1];
     __shared__ int am_i[ROLE == ROLE_LMHEAD ? 32 : 1];
+    constexpr int HM = 16;         // slots at most
+    constexpr int DM = 2048;       // row width at most
+    constexpr int NT = 64 * KW;
+    __shared__ float sc_w[ATTN ? KW : 1][HM];                        // per wave: score shares
+    __shared__ float attn_w[ATTN ? HM : 1];                          // the softmax weights
+    __shared__ __attribute__((aligned(16))) float mix_l[ATTN ? ATTN_FUSE_ROWS : 1][ATTN ? DM : 1];
     constexpr int BNt = 32 * WTN;
     const int nN = (p.N + BNt - 1) / BNt;
     int s, mt, nt;
     map_block(blockIdx.x, nN * p.S, 1, nN, s, mt, nt);
+    if constexpr (ATTN) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) {  // the attention kernel's bookkeeping
+            const int n = *p.m_count;
+            *p.attn_cnt_next = 0;  // the update of this iteration appends survivors there
+            *p.attn_cnt_hist += n;
+        }
+    }
     const int M = p.m_count ? min(*p.m_count, p.M) : p.M;
     if (M <= 0) return;
     const int n0 = nt * BNt;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int q = lane & 31, g = lane >> 5;
+    const int kw = p.K / KW;  // a multiple of 64 (checked by the launcher)
+    if constexpr (ATTN) {
+        const int H = p.S, dd = p.K;
+        const long rs3 = 3L * dd;
+        const float scale = 1.0f / sqrtf((float)dd);
+        for (int r = 0; r < M; ++r) {  // M <= ATTN_FUSE_ROWS
+            const float *row = p.attn_qkv + (long)r * H * rs3;
+            float part[HM];
+#pragma unroll
+            for (int c = 0; c < HM; ++c) part[c] = 0.0f;
+            // up to d = 2 NT (512 at 4 waves) the V elements are loaded with Q and K, one round
+            // trip for the three; wider rows load V in the mix loop below
+            float vpre[HM][2];
+            const bool one = dd <= 2 * NT;
+            for (int e0 = 0; e0 < dd; e0 += 2 * NT) {
+                float qv[2], kv[HM][2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int e = min(e0 + tid + j * NT, dd - 1);
+                    qv[j] = e0 + tid + j * NT < dd ? row[(long)s * rs3 + e] : 0.0f;
+#pragma unroll
+                    for (int c = 0; c < HM; ++c) kv[c][j] = row[(long)(c < H ? c : 0) * rs3 + dd + e];
+                    if (one) {
+#pragma unroll
+                        for (int c = 0; c < HM; ++c) vpre[c][j] = row[(long)(c < H ? c : 0) * rs3 + 2 * dd + e];
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < HM; ++c)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) part[c] += qv[j] * kv[c][j];
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {  // wave sums, the rounds issued for every slot at once
+                float o[HM];
+#pragma unroll
+                for (int c = 0; c < HM; ++c) o[c] = __shfl_xor(part[c], off, 64);
+#pragma unroll
+                for (int c = 0; c < HM; ++c) part[c] += o[c];
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int c = 0; c < HM; ++c) sc_w[wave][c] = part[c];
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float e[HM];
+                float mx = -INFINITY;
+                for (int c = 0; c < H; ++c) {
+                    float t = 0.0f;
+                    for (int w = 0; w < KW; ++w) t += sc_w[w][c];
+                    float sc = t * scale;
+                    if (p.attn_clamp) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
+                    e[c] = sc;
+                    mx = fmaxf(mx, sc);
+                }
+                float sum = 0.0f;
+                for (int c = 0; c < H; ++c) {
+                    e[c] = expf(e[c] - mx);
+                    sum += e[c];
+                }
+                for (int c = 0; c < H; ++c) attn_w[c] = e[c] / sum;
+            }
+            __syncthreads();
+            float wv[HM];
+#pragma unroll
+            for (int c = 0; c < HM; ++c) wv[c] = c < H ? attn_w[c] : 0.0f;
+            for (int e0 = 0; e0 < dd; e0 += 2 * NT) {
+                float vv[HM][2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int e = min(e0 + tid + j * NT, dd - 1);
+#pragma unroll
+                    for (int c = 0; c < HM; ++c)
+                        vv[c][j] = one ? vpre[c][j] : row[(long)(c < H ? c : 0) * rs3 + 2 * dd + e];
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < HM; ++c)
+                        if (c < H) acc = acc + vv[c][j] * wv[c];
+                    if (e0 + tid + j * NT < dd) mix_l[r][e0 + tid + j * NT] = acc;
+                }
+            }
+            __syncthreads();  // sc_w and attn_w are reused by the next row; mix_l complete
+        }
+    }
 
     // rows past M read row 0, columns past N row 0 of B (their outputs are not stored)
     long ar = 0;
@@ -433,7 +543,6 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[0][j][e] = 0.0f;
 
-    const int kw = p.K / KW;  // a multiple of 64 (checked by the launcher)
     for (int k = wave * kw; k < (wave + 1) * kw; k += 64) {
         const int ko = k + 32 * g;
         floatx4 a[8];
@@ -446,8 +555,13 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
                 bh[j][st] = *reinterpret_cast<const V8 *>(bhp[j] + e);
                 if constexpr (TERMS == 3) bl[j][st] = *reinterpret_cast<const V8 *>(blp[j] + e);
             }
+        if constexpr (ATTN) {  // the mix rows formed above (rows past M read row 0)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const floatx4 *>(ap + ko + 4 * i);
+            for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const floatx4 *>(&mix_l[q < M ? q : 0][ko + 4 * i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const floatx4 *>(ap + ko + 4 * i);
+        }
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             V8 ah, al;
@@ -518,15 +632,15 @@ int ring_grid(int total, int per_cu) {
     return (int)std::min<long>(total, g);
 }
 
-template <int ROLE, typename T, int TERMS, int WTN>
+template <int ROLE, typename T, int TERMS, int WTN, bool ATTN = false>
 void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
     const int total = ((p.N + 32 * WTN - 1) / (32 * WTN)) * p.S;
     if (total <= 0) return;
     switch (kw) {  // kw divides K / 64
-        case 8: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 8, WTN>), dim3(total), dim3(512), 0, st, p); break;
-        case 4: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 4, WTN>), dim3(total), dim3(256), 0, st, p); break;
-        case 2: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 2, WTN>), dim3(total), dim3(128), 0, st, p); break;
-        default: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 1, WTN>), dim3(total), dim3(64), 0, st, p); break;
+        case 8: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 8, WTN, ATTN>), dim3(total), dim3(512), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 4, WTN, ATTN>), dim3(total), dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 2, WTN, ATTN>), dim3(total), dim3(128), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 1, WTN, ATTN>), dim3(total), dim3(64), 0, st, p); break;
     }
 }
 
@@ -555,6 +669,15 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
             const int steps = p.K / 64;
             int kw = steps >= 16 ? 8 : steps >= 8 ? 4 : steps >= 4 ? 2 : 1;
             while (steps % kw) kw >>= 1;  // each wave's K range is whole 64-K steps
+            if constexpr (ROLE == ROLE_WO) {
+                if (p.attn_qkv) {  // the attention formed in the kernel (a few rows)
+                    if (p.N >= 1024)
+                        launch_skinny<ROLE, T, TERMS, 2, true>(p, kw, st);
+                    else
+                        launch_skinny<ROLE, T, TERMS, 1, true>(p, kw, st);
+                    return;
+                }
+            }
             if (p.N >= 1024)
                 launch_skinny<ROLE, T, TERMS, 2>(p, kw, st);
             else
@@ -626,6 +749,10 @@ void launch_gemm_split(const GemmParams &p, hipStream_t st) {
 }
 
 bool gemm_presplit_ok(int prec, int M, int N) { return prec == PREC_F16X3 && M >= 1024 && N >= 512; }
+
+bool gemm_attn_fusable(int prec, int M, int K, int S) {
+    return prec != PREC_FP32 && M <= ATTN_FUSE_ROWS && K % 64 == 0 && K <= 2048 && S <= 16;
+}
 
 long split_weight_elems(int S, int N, int K) { return (long)S * ((N + 31) / 32 * 32) * K; }
 

@@ -80,13 +80,25 @@ struct GemmParams {
     // (k_gemm_split's pre-split layout); W_o and the LM head, for the shapes gemm_presplit_ok
     // names; null = none
     const float *a_pre;
+    // W_o on at most ATTN_FUSE_ROWS rows (the skinny kernel, split arithmetic): with attn_qkv set
+    // the A operand (the attention mix of slot s) is formed in the kernel from the compact
+    // [row][S][3K] Q|K|V rows instead of read, so no attention kernel runs; the kernel also does
+    // that kernel's bookkeeping (attn_cnt_next = 0, attn_cnt_hist += the active count)
+    const float *attn_qkv;
+    int attn_clamp;            // ADN_F_SCORE_CLAMP4
+    int32_t *attn_cnt_next;
+    int32_t *attn_cnt_hist;
 };
+constexpr int ATTN_FUSE_ROWS = 4;
 constexpr int GEMM_BN = 128;
 void launch_gemm(const GemmParams &p, hipStream_t st);
 void launch_gemm_split(const GemmParams &p, hipStream_t st);
 // Whether a split GEMM of this shape reads a pre-split A operand (GemmParams::a_pre): fp16
 // halves and the 256x256 persistent tiles (M >= 1024, N >= 512).
 bool gemm_presplit_ok(int prec, int M, int N);
+// Whether W_o on at most M rows runs with the attention formed in its kernel (GemmParams::attn_qkv):
+// the skinny split-arithmetic kernel, M <= ATTN_FUSE_ROWS, K a multiple of 64, at most 16 slots.
+bool gemm_attn_fusable(int prec, int M, int K, int S);
 // hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16, from [S][N][K]
 // fp32 weights into the split GEMM's blocked layout (split_weight_elems halves each, N padded to
 // a multiple of 32); lo may be null.  The GEMMs' b_ss is then 0 (one matrix for every slot) or

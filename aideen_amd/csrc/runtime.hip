@@ -381,7 +381,10 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             Span sp(prof, ADN_STAGE_QKV_GEMM, k, st);
             launch_gemm(g, st);
         }
-        {
+        // At a few rows the attention is formed inside the W_o product (one launch less per
+        // iteration; the attention stage then reads zero)
+        const bool attn_in_wo = gemm_attn_fusable(c->prec, rows, d, H);
+        if (!attn_in_wo) {
             Span sp(prof, ADN_STAGE_ATTN, k, st);
             launch_attn(D, ba, cur, k, rows, st);
         }
@@ -406,6 +409,12 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             set_split(c, g, c->sp_o);
             set_range(c, g, 0, c->l1_wv);  // mix is a convex combination of V = W_v h rows
             if (wo_pre) g.a_pre = b.mix;
+            if (attn_in_wo) {
+                g.attn_qkv = b.qkv;
+                g.attn_clamp = (D.flags & ADN_F_SCORE_CLAMP4) != 0;
+                g.attn_cnt_next = b.cnt + (cur ^ 1);
+                g.attn_cnt_hist = b.cnt_hist + k;
+            }
             Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
             launch_gemm(g, st);
         }

@@ -344,6 +344,41 @@ def bench_decode(args, be, mc, w, toks, dev, torch) -> int:
     return 0
 
 
+SIMDS, CLOCK_GHZ = 1024, 2.4  # MI355X: 256 CUs x 4 SIMDs; the peak-rate clock
+
+
+def scan_compute_bound(mc, B, T, ms):
+    """The carrier scan's compute floor beside its HBM fraction.  Which form runs follows the
+    library's rule (the matrix form where the per-step form would need time chunks: fewer than 512
+    workgroups of 256 channels, and a decay that keeps 16-step products normal).  Per-step form
+    (k_scan_fused): one thread per (sequence, slot, channel), 290 SIMD cycles per wave and step
+    counted in the compiled 16-state instance (31 state and output FMAs and 25 other VALU
+    instructions at 4 cycles, 4.3 transcendental ones at 16), i.e. about 8 n + 165 for an n-state
+    instance (n = 1, 8, 16, 32; the others extrapolated), so floor = waves x T x cycles / SIMDs.
+    Matrix form (k_scan_ssd): per 16 channels and 16 steps 24 v_mfma_f32_16x16x4f32 of 32 cycles
+    (16 states; 36 with 32), so floor = waves x T/16 x MFMA cycles / SIMDs.  At the 2.4 GHz peak
+    clock; frac = floor / measured."""
+    nch, wgs = 1, B * mc.H * ((mc.d + 255) // 256)
+    while wgs * nch < 512 and T // (nch * 2) >= 64:
+        nch *= 2
+    ssd = nch > 1 and mc.N <= 32 and mc.r <= 64 and mc.d % 16 == 0
+    if ssd:
+        waves = B * mc.H * (mc.d // 16)
+        per = (24 if mc.N <= 16 else 36) * 32
+        cyc = waves * ((T + 15) // 16) * per / SIMDS
+        kind, basis = "mfma", "fp32 MFMA cycles of the chunked matrix form (v_mfma_f32_16x16x4f32, 32 cycles each)"
+    else:
+        waves = B * mc.H * ((mc.d + 63) // 64)
+        n_inst = 16 if mc.N == 16 else 1 if mc.N == 1 else 32 if mc.N > 8 else 8
+        per = 290 if n_inst == 16 else 8 * n_inst + 165
+        cyc = waves * T * per / SIMDS
+        kind, basis = "valu", (f"VALU issue cycles of the per-step form ({per} per wave and step: counted in the compiled "
+                               f"16-state instance" + ("" if n_inst == 16 else ", extrapolated to this state count") + ")")
+    floor_ms = cyc / (CLOCK_GHZ * 1e6)
+    return dict(form="matrix" if ssd else "per-step", bound=kind, floor_ms=round(floor_ms, 4),
+                frac=round(floor_ms / ms, 4), basis=basis + "; floor at 2.4 GHz over 1024 SIMDs")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -486,6 +521,8 @@ def main() -> int:
             s = prof["stages"][n]
             g = s["bytes"] / s["ms"] / 1e6
             hbm[n] = dict(gbs=round(g, 1), frac=round(g / PEAK_HBM_GBS, 4))
+    if "scan" in hbm and not memory:
+        hbm["scan"]["compute_bound"] = scan_compute_bound(mc, B, T, prof["stages"]["scan"]["ms"])
 
     cpu = None
     if not args.no_cpu:
@@ -522,7 +559,8 @@ def main() -> int:
     if args.config == "C4" and "scan" in hbm:  # the configuration's own figure: the carrier scan
         sc = prof["stages"]["scan"]
         line["scan"] = dict(gbs=hbm["scan"]["gbs"], frac=hbm["scan"]["frac"], ms=round(sc["ms"], 4),
-                            bytes=sc["bytes"], basis="compulsory bytes: read h* and the carrier record, write y")
+                            bytes=sc["bytes"], basis="compulsory bytes: read h* and the carrier record, write y",
+                            compute_bound=hbm["scan"]["compute_bound"])
     print(json.dumps(line), flush=True)
     return 0
 
