@@ -419,6 +419,9 @@ template <int E, int HT, bool HIST, bool PART>
 __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur, int k, int max_iters,
                                                 float eps, const float *anchor, const float *norm_scale,
                                                 float beta) {
+    // no contracted multiply-adds: every kernel that forms the update (this one, k_update_tok and
+    // the Q|K|V product that applies it at a few rows) rounds each operation alike
+#pragma clang fp contract(off)
     __shared__ int keep_s[WAVES_PER_BLOCK];
     __shared__ int tok_s[WAVES_PER_BLOCK];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -603,6 +606,7 @@ template <int E, bool PART>
 __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int cur, int k, int max_iters,
                                                      float eps, const float *anchor, const float *norm_scale,
                                                      float beta) {
+#pragma clang fp contract(off)  // as in k_update
     __shared__ float rs[16];
     const int i = blockIdx.x;
     if (i >= b.cnt[cur]) return;

@@ -386,7 +386,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, (WGM * WGN >= 8) ? 1 : 2) void k_ge
 // mix in LDS: every thread loads its elements of every key slot at once (clamped addresses, so the
 // loads do not wait behind per-slot branches), the score shares are summed over the waves in order,
 // and the K loop then reads A from LDS.
-template <int ROLE, typename T, int TERMS, int KW, int WTN, bool ATTN = false>
+//
+// UPD (Q|K|V at a few rows, GemmParams::upd_o): A is h after the previous iteration's damped
+// update, formed here (fixed_point_memory_reasoning.rs:1386-1393, with k_update_tok's arithmetic
+// and summation order: one wave per row, a lane's elements lane + 64e summed in e order, then the
+// wave sum) into LDS, so that the update needs no kernel of its own; the slot's first column
+// block also stores the row.  Used only where no token can exit before the last iteration, so
+// that the update's residual and exit test are not needed.
+template <int ROLE, typename T, int TERMS, int KW, int WTN, bool ATTN = false, bool UPD = false>
 __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     typedef typename Vec8<T>::type V8;
     __shared__ float red[KW > 1 ? KW - 1 : 1][WTN * 16][64];  // [wave-1][element][lane]
@@ -398,7 +405,9 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     constexpr int NT = 64 * KW;
     __shared__ float sc_w[ATTN ? KW : 1][HM];                        // per wave: score shares
     __shared__ float attn_w[ATTN ? HM : 1];                          // the softmax weights
-    __shared__ __attribute__((aligned(16))) float mix_l[ATTN ? ATTN_FUSE_ROWS : 1][ATTN ? DM : 1];
+    constexpr bool LA = ATTN || UPD;  // A rows formed in LDS
+    __shared__ __attribute__((aligned(16))) float mix_l[LA ? ATTN_FUSE_ROWS : 1][LA ? DM : 1];
+    __shared__ float hold_l[UPD ? ATTN_FUSE_ROWS : 1][UPD ? DM : 1];
     constexpr int BNt = 32 * WTN;
     const int nN = (p.N + BNt - 1) / BNt;
     int s, mt, nt;
@@ -504,6 +513,54 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
             __syncthreads();  // sc_w and attn_w are reused by the next row; mix_l complete
         }
     }
+    if constexpr (UPD) {
+#pragma clang fp contract(off)  // as in k_update_tok
+        const int dd = p.K, E = dd / 64;
+        const long hd = (long)p.S * dd;
+        const float beta = p.upd_beta, omb = 1.0f - beta;
+        for (int r = wave; r < M; r += KW) {  // M <= ATTN_FUSE_ROWS
+            long t = p.a_idx ? (long)p.a_idx[r] : (long)r;
+            if (t < 0 || t >= p.a_idx_max) t = 0;  // flagged below
+            const float *o = p.upd_o + ((long)r * p.S + s) * dd;
+            const float *sg = p.upd_sig + t * hd + (long)s * dd;
+            const float *an = p.upd_anchor + (long)s * dd;
+            const float *hp = p.A + t * hd + (long)s * dd;
+            float ss = 0.0f;
+            for (int e0 = 0; e0 < E; e0 += 8) {  // 8 elements' loads in flight per lane
+                float ov[8], sv[8], av[8], hv[8], gv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int idx = lane + 64 * min(e0 + u, E - 1);
+                    ov[u] = o[idx];
+                    sv[u] = sg[idx];
+                    av[u] = an[idx];
+                    hv[u] = hp[idx];
+                    gv[u] = p.upd_norm[idx];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (e0 + u < E) {
+                        const int idx = lane + 64 * (e0 + u);
+                        const float as_ = (ov[u] + sv[u]) + 0.0f;  // k_update_tok adds a zero history term
+                        const float c = as_ + av[u];
+                        ss += p.upd_excl ? as_ * as_ : c * c;
+                        mix_l[r][idx] = gv[u] * c;
+                        hold_l[r][idx] = hv[u];
+                    }
+            }
+            ss = wave_sum(ss);
+            const float rms = sqrtf(ss / (float)dd + 1e-6f);
+            float *hw = p.upd_hout + t * hd + (long)s * dd;
+            for (int e = 0; e < E; ++e) {  // each lane reads back only what it wrote
+                const int idx = lane + 64 * e;
+                const float f = mix_l[r][idx] / rms;
+                const float hn = f * beta + hold_l[r][idx] * omb;
+                mix_l[r][idx] = hn;
+                if (nt == 0) hw[idx] = hn;
+            }
+        }
+        __syncthreads();
+    }
 
     // rows past M read row 0, columns past N row 0 of B (their outputs are not stored)
     long ar = 0;
@@ -555,7 +612,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
                 bh[j][st] = *reinterpret_cast<const V8 *>(bhp[j] + e);
                 if constexpr (TERMS == 3) bl[j][st] = *reinterpret_cast<const V8 *>(blp[j] + e);
             }
-        if constexpr (ATTN) {  // the mix rows formed above (rows past M read row 0)
+        if constexpr (LA) {  // the rows formed above (rows past M read row 0)
 #pragma unroll
             for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const floatx4 *>(&mix_l[q < M ? q : 0][ko + 4 * i]);
         } else {
@@ -632,15 +689,15 @@ int ring_grid(int total, int per_cu) {
     return (int)std::min<long>(total, g);
 }
 
-template <int ROLE, typename T, int TERMS, int WTN, bool ATTN = false>
+template <int ROLE, typename T, int TERMS, int WTN, bool ATTN = false, bool UPD = false>
 void launch_skinny(const GemmParams &p, int kw, hipStream_t st) {
     const int total = ((p.N + 32 * WTN - 1) / (32 * WTN)) * p.S;
     if (total <= 0) return;
     switch (kw) {  // kw divides K / 64
-        case 8: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 8, WTN, ATTN>), dim3(total), dim3(512), 0, st, p); break;
-        case 4: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 4, WTN, ATTN>), dim3(total), dim3(256), 0, st, p); break;
-        case 2: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 2, WTN, ATTN>), dim3(total), dim3(128), 0, st, p); break;
-        default: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 1, WTN, ATTN>), dim3(total), dim3(64), 0, st, p); break;
+        case 8: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 8, WTN, ATTN, UPD>), dim3(total), dim3(512), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 4, WTN, ATTN, UPD>), dim3(total), dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 2, WTN, ATTN, UPD>), dim3(total), dim3(128), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_gemm_skinny<ROLE, T, TERMS, 1, WTN, ATTN, UPD>), dim3(total), dim3(64), 0, st, p); break;
     }
 }
 
@@ -675,6 +732,15 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
                         launch_skinny<ROLE, T, TERMS, 2, true>(p, kw, st);
                     else
                         launch_skinny<ROLE, T, TERMS, 1, true>(p, kw, st);
+                    return;
+                }
+            }
+            if constexpr (ROLE == ROLE_QKV) {
+                if (p.upd_o) {  // the previous iteration's update formed in the kernel (a few rows)
+                    if (p.N >= 1024)
+                        launch_skinny<ROLE, T, TERMS, 2, false, true>(p, kw, st);
+                    else
+                        launch_skinny<ROLE, T, TERMS, 1, false, true>(p, kw, st);
                     return;
                 }
             }

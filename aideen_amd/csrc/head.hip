@@ -90,7 +90,20 @@ __device__ __forceinline__ void am_combine(float &v, int &i, float v2, int i2) {
     }
 }
 
-__global__ __launch_bounds__(AM_NT) void k_argmax(const float *logits, int V, int32_t *out) {
+// the chosen token of row `row` (see TokenAppend)
+__device__ __forceinline__ void am_store(int32_t *out, int row, int tok, const TokenAppend &app) {
+    out[row] = tok;
+    if (app.seq) {
+        app.seq[(long)row * app.stride + app.len] = tok;
+        app.out[(long)row * app.n_new + app.j] = tok;
+    }
+    if (app.bounds && row == 0) {
+        for (int i = 0; i < ADN_BOUNDS; ++i) app.bounds[i] = i == 0 ? app.bound0 : 0u;
+        if (app.absmax) *app.absmax = 0u;
+    }
+}
+
+__global__ __launch_bounds__(AM_NT) void k_argmax(const float *logits, int V, int32_t *out, TokenAppend app) {
     __shared__ float sv[AM_NT / 64];
     __shared__ int si[AM_NT / 64];
     const long row = blockIdx.x;
@@ -119,7 +132,7 @@ __global__ __launch_bounds__(AM_NT) void k_argmax(const float *logits, int V, in
         float v = sv[0];
         int i = si[0];
         for (int w = 1; w < AM_NT / 64; ++w) am_combine(v, i, sv[w], si[w]);
-        out[row] = i < 0 ? 0 : i;
+        am_store(out, (int)row, i < 0 ? 0 : i, app);
     }
 }
 
@@ -130,7 +143,8 @@ __global__ __launch_bounds__(AM_NT) void k_argmax(const float *logits, int V, in
 constexpr int AR_W = 16;
 
 __global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val, const int32_t *am_idx,
-                                                            int ntok, int ntiles, int32_t *out) {
+                                                            int ntok, int ntiles, int32_t *out,
+                                                            TokenAppend app) {
     // 32 rows per block: half-wave hw of wave w takes tiles 2w + hw, 2w + hw + 2 AR_W, ... (the
     // combination is a maximum with ties to the larger index, so its order does not matter), four
     // tiles' loads in flight at a time
@@ -163,7 +177,7 @@ __global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val
     __syncthreads();
     if (threadIdx.x < 32 && row < ntok) {
         for (int q = 1; q < QS; ++q) am_combine(bv, bi, sv[q][rl], si[q][rl]);
-        out[row] = bi < 0 ? 0 : bi;
+        am_store(out, row, bi < 0 ? 0 : bi, app);
     }
 }
 
@@ -184,7 +198,8 @@ constexpr int dq_waves(int E) { return E <= 8 ? 16 : (E <= 16 ? 8 : 4); }
 
 template <int E, bool PART>
 __global__ __launch_bounds__(64 * dq_waves(E)) void k_decode_query(const float *Emb, int d, const int32_t *seq,
-                                                                   int stride, int len, int ctx, float *q) {
+                                                                   int stride, int len, int ctx, float *q,
+                                                                   unsigned *absmax) {
     constexpr int W = dq_waves(E);
     __shared__ double part[W][64 * E];
     __shared__ double red[W];
@@ -236,7 +251,18 @@ __global__ __launch_bounds__(64 * dq_waves(E)) void k_decode_query(const float *
     for (int w = 0; w < W; ++w) n2 += red[w];
     const double nv = sqrt(n2);
     const double inv = 1.0 / (nv > 1e-6 * (double)L ? nv : (double)L);
-    for (int j = threadIdx.x; j < d; j += 64 * W) q[(long)b * d + j] = (float)(part[0][j] * inv);
+    unsigned mb = 0;  // largest finite |q| of this lane, as float bits
+    for (int j = threadIdx.x; j < d; j += 64 * W) {
+        const float v = (float)(part[0][j] * inv);
+        q[(long)b * d + j] = v;
+        const float a = fabsf(v);
+        if (a < INFINITY) mb = max(mb, __float_as_uint(a));
+    }
+    if (absmax) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, off, 64));
+        if (lane == 0 && mb) atomicMax(absmax, mb);
+    }
 }
 
 // LmHead::sample's repetition penalty (lm_head.rs:81-99) on each sequence's logits row: every
@@ -258,16 +284,6 @@ __global__ __launch_bounds__(256) void k_rep_penalty(float *logits, int V, const
     }
 }
 
-// seq[b][len] = out[b][j] = tok[b]
-__global__ void k_decode_append(const int32_t *tok, int32_t *seq, int stride, int len, int32_t *out, int n_new, int j,
-                                int B) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) return;
-    const int32_t v = tok[b];
-    seq[(long)b * stride + len] = v;
-    out[(long)b * n_new + j] = v;
-}
-
 // last[b] = seq[b][len - 1]
 __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -285,34 +301,30 @@ void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, f
     });
 }
 
-void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st) {
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)ntok), dim3(AM_NT), 0, st, logits, V, out);
+void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st, const TokenAppend *app) {
+    const TokenAppend a = app ? *app : TokenAppend{};
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)ntok), dim3(AM_NT), 0, st, logits, V, out, a);
 }
 
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
-                          hipStream_t st) {
+                          hipStream_t st, const TokenAppend *app) {
+    const TokenAppend a = app ? *app : TokenAppend{};
     hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 31) / 32)), dim3(64 * AR_W), 0, st, am_val, am_idx, ntok,
-                       ntiles, out);
+                       ntiles, out, a);
 }
 
 void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
-                         hipStream_t st) {
+                         hipStream_t st, unsigned *absmax) {
     dispatch_width(d, [&](auto Ec, auto Pc) {
         constexpr int EC = decltype(Ec)::value;
         hipLaunchKernelGGL((k_decode_query<EC, decltype(Pc)::value>), dim3((unsigned)B), dim3(64 * dq_waves(EC)), 0, st,
-                           E, d, seq, stride, len, ctx, q);
+                           E, d, seq, stride, len, ctx, q, absmax);
     });
 }
 
 void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
                         hipStream_t st) {
     hipLaunchKernelGGL(k_rep_penalty, dim3((unsigned)B), dim3(256), 0, st, logits, V, seq, stride, len, ctx, pen);
-}
-
-void launch_decode_append(const int32_t *tok, int32_t *seq, int stride, int len, int32_t *out, int n_new, int j, int B,
-                          hipStream_t st) {
-    hipLaunchKernelGGL(k_decode_append, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, tok, seq, stride, len,
-                       out, n_new, j, B);
 }
 
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {

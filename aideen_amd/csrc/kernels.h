@@ -88,6 +88,19 @@ struct GemmParams {
     int attn_clamp;            // ADN_F_SCORE_CLAMP4
     int32_t *attn_cnt_next;
     int32_t *attn_cnt_hist;
+    // Q|K|V on at most ATTN_FUSE_ROWS rows (the skinny kernel, split arithmetic) when no token can
+    // exit early: with upd_o set the kernel first applies the previous iteration's damped update
+    // to its A rows (A = h before it, K = d, S = H; per slot c = o + signal + anchor, h' =
+    // g c / rms(c) beta + h (1 - beta), as k_update_tok computes it) and multiplies h'; the
+    // slot's first column block writes h' to upd_hout (rows indexed like A).  upd_o is the
+    // previous W_o output, compact by active index like the A index list.
+    const float *upd_o;
+    const float *upd_sig;
+    const float *upd_anchor;
+    const float *upd_norm;
+    float *upd_hout;
+    float upd_beta;
+    int upd_excl;              // ADN_F_RMS_EXCL_ANCHOR
 };
 constexpr int ATTN_FUSE_ROWS = 4;
 constexpr int GEMM_BN = 128;
@@ -171,21 +184,35 @@ void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, in
 // pnorm * pre_scale instead of fp32.
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
                       float *pnorm, float *rec, int REC, float pre_scale, hipStream_t st);
+// A greedy decode step's token append, done by the arg-max kernel that picks the token: row b's
+// token also goes to seq[b][len] and out[b][j] (out is [B][n_new]); seq null = none.  bounds,
+// when set, gets the next forward's range-guard reset (launch_reset_bounds's work: bounds[0] =
+// bound0, the other ADN_BOUNDS words and *absmax zero), so that the next step needs no reset
+// launch before its query.
+struct TokenAppend {
+    int32_t *seq;
+    int stride, len;
+    int32_t *out;
+    int n_new, j;
+    unsigned *bounds;
+    unsigned bound0;
+    unsigned *absmax;
+};
 // argmax over each row of logits with the last-max tie rule.
-void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st);
+void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream_t st,
+                   const TokenAppend *app = nullptr);
 // final reduction of the per-tile arg-max partials written by the LM-head GEMM
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
-                          hipStream_t st);
+                          hipStream_t st, const TokenAppend *app = nullptr);
 // Greedy decode.  seq [B][stride] holds each sequence's tokens; step j uses the first len.
-// q [B][d] = embed_context of the last ctx of them (d <= 2048).
+// q [B][d] = embed_context of the last ctx of them (d <= 2048).  absmax, when set, is raised
+// (atomic max of float bits) to the largest finite |q| written, as launch_absmax would; it must
+// have been cleared before the call.
 void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
-                         hipStream_t st);
+                         hipStream_t st, unsigned *absmax = nullptr);
 // the repetition penalty over the same context, in place on logits [B][V]
 void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
                         hipStream_t st);
-// seq[b][len] = out[b][j] = tok[b]  (out is [B][n_new])
-void launch_decode_append(const int32_t *tok, int32_t *seq, int stride, int len, int32_t *out, int n_new, int j, int B,
-                          hipStream_t st);
 // last[b] = seq[b][len - 1]
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st);
 

@@ -85,6 +85,9 @@ struct adn_ctx {
     float *am_val = nullptr;      // [cap_tok][ceil(V/128)] LM-head tile arg-max partials
     int32_t *am_idx = nullptr;
     unsigned *absmax = nullptr;   // max |s_in| (float bits) for the signal GEMM's A scale
+    // the iterates of a few-row solve with a fixed iteration count (two [ATTN_FUSE_ROWS][H][d]
+    // buffers, alternating): there each Q|K|V product applies the previous update itself
+    float *fix_h = nullptr;
     // fp16-split range guard: the A operands' magnitude bounds (ADN_BOUNDS words, reset per forward)
     // and the weight-derived constants they are combined with (set at upload)
     unsigned *bounds = nullptr;
@@ -290,14 +293,17 @@ float max_row_l1(const float *w, int H, int d, bool in_out) {
 // the forward pipeline (device pointers; enqueue only)
 // ---------------------------------------------------------------------------------------
 // signal[t][s] = W_in[s] x_t for every token, h0 and the first active list (all tokens).
-void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int ntok, Prof *prof) {
+// s_in_ready: the bounds were reset and max |s_in| accumulated into c->absmax by the caller's
+// kernels (a decode step: the previous step's arg-max and this step's query).
+void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int ntok, Prof *prof,
+                         bool s_in_ready = false) {
     const Dims &D = c->D;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
     // caller-supplied rows on the fp16 split: the signal GEMM's A scale also honours their actual
     // magnitude (max |s_in|, accumulated into c->absmax, which the reset clears)
     const bool dyn_scale = r.s_in && c->prec == PREC_F16X3;
-    launch_reset_bounds(c->bounds, c->h_bound, dyn_scale ? c->absmax : nullptr, st);
+    if (!s_in_ready) launch_reset_bounds(c->bounds, c->h_bound, dyn_scale ? c->absmax : nullptr, st);
     // x gathered from the embedding when tokens are given
     {
         GemmParams g{};
@@ -323,7 +329,7 @@ void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, in
         if (dyn_scale) {
             // rows of any size stay inside the fp16 range (rows no larger than the embedding
             // table's entries keep the embedding's scale, and match the token path bit for bit)
-            launch_absmax(r.s_in, (long)ntok * d, c->absmax, st);
+            if (!s_in_ready) launch_absmax(r.s_in, (long)ntok * d, c->absmax, st);
             g.a_absmax = c->absmax;
             g.a_headroom = 1024.0f;
         }
@@ -351,12 +357,31 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         ba.mix_bound = c->bounds;
         ba.mix_headroom = c->l1_wv > 0.0f ? 16384.0f / c->l1_wv : INFINITY;
     }
+    // A few rows where no token can exit before the last iteration (a tolerance of zero or less,
+    // no plateau exit, no Anderson mixing, no history term): each Q|K|V product applies the
+    // previous iteration's update to its rows itself (GemmParams::upd_o), so the update runs only
+    // at the last iteration, where it records the iteration counts.  The iterates alternate
+    // between two small buffers (a product's column blocks read h_{k-1} while the slot's first
+    // block writes h_k), and the active list stays list 0.
+    const bool fixed = gemm_attn_fusable(c->prec, rows, d, H) && rows == ntok && !(r.eps > 0.0f) &&
+                       !b.rprev && m == 0 && !b.mem_hist && r.max_iters >= 2;
+    const long fix_stride = (long)std::min<long>(c->cap_tok, ATTN_FUSE_ROWS) * H * d;
+    auto iterate = [&](int j) { return j == 0 ? b.h : c->fix_h + (long)(j & 1) * fix_stride; };
     for (int k = 0; k < r.max_iters; ++k) {
-        const int cur = k & 1;
+        const int cur = fixed ? 0 : k & 1;
         {  // Q|K|V for every slot of every active token
             GemmParams g{};
             g.role = ROLE_QKV;
-            g.A = b.h;
+            g.A = fixed ? iterate(k > 0 ? k - 1 : 0) : b.h;
+            if (fixed && k > 0) {
+                g.upd_o = b.o;
+                g.upd_sig = b.signal;
+                g.upd_anchor = c->anchor;
+                g.upd_norm = c->norm_scale;
+                g.upd_hout = iterate(k);
+                g.upd_beta = r.damping;
+                g.upd_excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
+            }
             g.a_idx = b.act[cur];
             g.a_idx_max = ntok;
             g.a_sm = (long)H * d;
@@ -426,12 +451,16 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         // runs.
         const bool mix = m > 0 && k + 1 < r.max_iters;
         const bool from_slot = mix && anderson_from_slot_ok(D);
-        {
+        if (!fixed || k + 1 == r.max_iters) {
             Span sp(prof, ADN_STAGE_UPDATE, k, st);
             SolveBuffers bu = b;
             if (from_slot) {
                 bu.h_out = b.hist + (long)(k % m) * ntok * H * d;
                 bu.h_both = k < 2;
+            }
+            if (fixed) {  // from the last small buffer into h
+                bu.h = iterate(k);
+                bu.h_out = b.h;
             }
             launch_update(D, bu, cur, k, r.max_iters, r.eps, rows, c->anchor, c->norm_scale, r.damping, st);
         }
@@ -479,8 +508,9 @@ void enqueue_scan_prep(adn_ctx *c, int ntok, const SolveBuffers &b, Prof *prof, 
 // pass also writes every row's RMS into the carrier record, and the carrier's projections
 // follow it at once, before the LM head, while h* is still in the caches (the LM head's logits
 // stream would evict it).  Returns whether it did (the scan then skips its preparation).
+// app: a decode step's token append, done by the arg-max kernel.
 bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int ntok, Prof *prof,
-                  bool scan_rms = false) {
+                  bool scan_rms = false, const TokenAppend *app = nullptr) {
     const Dims &D = c->D;
     const int d = D.d;
     hipStream_t st = c->stream;
@@ -530,7 +560,7 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
         }
         if (o.argmax) {
             Span sp(prof, ADN_STAGE_ARGMAX, -1, st);
-            launch_argmax_reduce(c->am_val, c->am_idx, ntok, ntiles, o.argmax, st);
+            launch_argmax_reduce(c->am_val, c->am_idx, ntok, ntiles, o.argmax, st, app);
         }
     }
     return pool && scan_rms;
@@ -581,7 +611,15 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
     }
 }
 
-void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
+// A greedy decode step's extras: the query kernel has reset the range guard's bounds and
+// accumulated max |s_in| (s_in_ready), and the arg-max kernel appends the token (app).
+struct DecodeStep {
+    bool s_in_ready;
+    const TokenAppend *app;
+};
+
+void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr,
+                     const DecodeStep *ds = nullptr) {
     const int ntok = r.batch * r.seq;
     SolveBuffers b = c->sb;
     if (o.h_star) b.h = o.h_star;
@@ -591,9 +629,9 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     b.amax_h = c->bounds;
     c->last_h = b.h;  // the adjoint reads this forward's h* and signal
     c->last_ntok = ntok;
-    enqueue_signal_init(c, r, b, ntok, prof);
+    enqueue_signal_init(c, r, b, ntok, prof, ds && ds->s_in_ready);
     enqueue_iterations(c, r, b, ntok, ntok, prof);
-    const bool prep_done = enqueue_head(c, o, b, ntok, prof, o.scan_y || o.scan_state);
+    const bool prep_done = enqueue_head(c, o, b, ntok, prof, o.scan_y || o.scan_state, ds ? ds->app : nullptr);
     enqueue_scan(c, r, o, b, prof, prep_done);
 }
 
@@ -603,7 +641,8 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
 // position form the active list; positions run in order.  m_t of every token lands in scan_y
 // (or scratch), the last one in scan_state; scan_state_in is m_{-1} (null = zero state, no
 // history context at t = 0).
-void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
+void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr,
+                            const TokenAppend *app = nullptr) {
     const Dims &D = c->D;
     const int B = r.batch, T = r.seq, ntok = B * T;
     const int d = D.d, H = D.H;
@@ -699,7 +738,7 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
         ADN_HIP(hipMemcpy2DAsync(o.scan_state, hd * sizeof(float), mseq + (long)(T - 1) * hd,
                                  (size_t)T * hd * sizeof(float), hd * sizeof(float), B, hipMemcpyDeviceToDevice,
                                  st));
-    enqueue_head(c, o, b, ntok, prof);
+    enqueue_head(c, o, b, ntok, prof, false, app);
 }
 
 void enqueue_run(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *prof = nullptr) {
@@ -807,6 +846,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
         c->absmax = (unsigned *)dmalloc(c, sizeof(unsigned));
+        c->fix_h = (float *)dmalloc(c, 2 * (size_t)std::min<long>(T, ATTN_FUSE_ROWS) * H * d * sizeof(float));
         c->bounds = (unsigned *)dmalloc(c, ADN_BOUNDS * sizeof(unsigned));
         b.err = c->d_err;
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
@@ -1140,7 +1180,15 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
             enqueue_forward_memory(c, rp, op);
         } else {
             q = staging_f(c, 28, (size_t)batch * D.d * sizeof(float));
+            // the first step's range-guard reset; each step's arg-max kernel then does the next one's
+            launch_reset_bounds(c->bounds, c->h_bound, c->absmax, st);
         }
+        // The token is appended to seq and out by the arg-max kernel that picks it; on the
+        // canonical path that kernel also resets the range guard's bounds and max |s_in| for the
+        // next step, whose query kernel accumulates max |q|, so the step's forward launches neither
+        // (the same values as launch_reset_bounds and launch_absmax).
+        unsigned hb;
+        std::memcpy(&hb, &c->h_bound, sizeof hb);
         for (int j = 0; j < n_new; ++j) {
             const int len = prompt_len + j;
             adn_outputs o{};
@@ -1148,6 +1196,8 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
                 o.logits = lg;
             else
                 o.argmax = am;
+            TokenAppend app{seq, stride, len, outd, n_new, j, memory ? nullptr : c->bounds, hb,
+                            memory ? nullptr : c->absmax};
             if (memory) {
                 // query = embed(last context token) with the history of m (trainer.rs:4395-4400)
                 launch_decode_last(seq, stride, len, last, batch, st);
@@ -1155,20 +1205,21 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
                 r.s_in = nullptr;
                 r.scan_state_in = m_cur;
                 o.scan_state = m_nxt;
-                enqueue_forward_memory(c, r, o);
+                enqueue_forward_memory(c, r, o, nullptr, penalise ? nullptr : &app);
                 std::swap(m_cur, m_nxt);
             } else {
                 // query = embed_context(context, ctx_len) (trainer.rs:4388-4392)
-                launch_decode_query(c->embed, D.d, seq, stride, len, ctx_len, batch, q, st);
+                launch_decode_query(c->embed, D.d, seq, stride, len, ctx_len, batch, q, st,
+                                    c->prec == PREC_F16X3 ? c->absmax : nullptr);
                 r.tokens = nullptr;
                 r.s_in = q;
-                enqueue_forward(c, r, o);
+                const DecodeStep ds{true, penalise ? nullptr : &app};
+                enqueue_forward(c, r, o, nullptr, &ds);
             }
             if (penalise) {
                 launch_rep_penalty(lg, D.V, seq, stride, len, ctx_len, repetition_penalty, batch, st);
-                launch_argmax(lg, batch, D.V, am, st);
+                launch_argmax(lg, batch, D.V, am, st, &app);
             }
-            launch_decode_append(am, seq, stride, len, outd, n_new, j, batch, st);
         }
         ADN_HIP(hipGetLastError());
         ADN_HIP(hipMemcpyAsync(out_tokens, outd, (size_t)batch * n_new * sizeof(int32_t), hipMemcpyDeviceToHost, st));
