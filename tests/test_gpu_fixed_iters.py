@@ -8,6 +8,8 @@ kernel runs only at the last iteration, where it records the iteration counts.  
 at every iteration: the two runs must agree bit for bit, and match the oracle.  A greedy decode
 (generate's 10 steps at tolerance 0) takes the first form at every step.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -50,7 +52,27 @@ def test_fixed_iteration_solve_matches_per_iteration_update(oracle_lib, var):
     for k in ALL:
         assert np.array_equal(fused[k], per_iter[k]), f"{k}: fused update differs from the update kernel"
         assert np.array_equal(fused[k], s_in[k]), f"{k}: s_in path differs"
-    import dataclasses
     ref = oracle_lib.Oracle(dataclasses.replace(mc, max_iters=7, eps=0.0), w).forward(toks)
     assert_forward_parity(fused, ref, f"fixed {var}")
     assert np.array_equal(fused["argmax"], ref["argmax"])
+
+
+@pytest.mark.parametrize("prec", ["bf16x3", "bf16", "fp32"])
+def test_fixed_iteration_solve_every_gemm_arithmetic(oracle_lib, prec):
+    """The same comparison in the other GEMM arithmetics (the fused update runs in the split
+    products, bf16 halves included; with fp32 GEMMs every iteration runs the update kernel)."""
+    flag = {"bf16x3": synth.F_GEMM_BF16X3, "bf16": synth.F_GEMM_BF16, "fp32": synth.F_GEMM_FP32}[prec]
+    mc = synth.ModelConfig(d=256, H=4, V=600, N=4, r=32, flags=flag)
+    w = synth.make_token_sensitive_weights(mc, seed=6)
+    toks = synth.make_tokens("uniform", 1, 4, mc.V, seed=3)
+    be = GpuDeqBackend(mc, 1, 4)
+    be.upload_weights(w)
+    log(f"fixed-iteration solve, {prec} GEMMs")
+    fused = be.forward(toks, max_iters=6, eps=0.0, want=ALL)
+    per_iter = be.forward(toks, max_iters=6, eps=1e-30, want=ALL)
+    be.close()
+    for k in ALL:
+        assert np.array_equal(fused[k], per_iter[k]), f"{prec} {k}: fused update differs from the update kernel"
+    if prec != "bf16":  # the bf16-input products are a reduced-precision variant
+        ref = oracle_lib.Oracle(dataclasses.replace(mc, max_iters=6, eps=0.0), w).forward(toks)
+        assert_forward_parity(fused, ref, f"fixed {prec}")
