@@ -63,6 +63,48 @@ __device__ __forceinline__ void track_absmax(unsigned *word, float v) {
     if ((threadIdx.x & 63) == 0 && a > __uint_as_float(*word)) atomicMax(word, __float_as_uint(a));
 }
 
+// The LM head's prologue after the slot sum (lm_head.rs:35-54): pv[e] holds the sum over the
+// slots, in slot order, of element lane + 64e of one token's rows (zeros past the row for e >=
+// er).  pooled = pv / H (stored when `pooled` is set), pnorm = (pooled / rms) * g with eps 1e-5
+// (g null = 1), stored in fp32, or (pre > 0) as the split GEMM's pre-split A operand of pnorm *
+// pre: fp16 halves hi = f16(x), lo = f16(x - hi), each 8 consecutive elements as 8 hi halves then
+// 8 lo halves.  One wave per token; every kernel that pools calls this, so that they agree bit
+// for bit.
+template <int E>
+__device__ __forceinline__ void pool_finish(float (&pv)[E], int H, int d, int er, int lane, long t, const float *g,
+                                            float *pooled, float *pnorm, float pre) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        pv[e] = pv[e] / (float)H;
+        if (pooled && e < er) pooled[t * d + i] = pv[e];
+        ss += pv[e] * pv[e];
+    }
+    if (!pnorm) return;
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / (float)d + 1e-5f);
+    if (pre > 0.0f) {
+        _Float16 *row = reinterpret_cast<_Float16 *>(pnorm + t * d);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = lane + 64 * e;
+            if (e < er) {
+                const float x = ((pv[e] / rms) * (g ? g[i] : 1.0f)) * pre;
+                const _Float16 hv = (_Float16)x;
+                row[(i >> 3) * 16 + (i & 7)] = hv;
+                row[(i >> 3) * 16 + 8 + (i & 7)] = (_Float16)(x - (float)hv);
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = lane + 64 * e;
+        if (e < er) pnorm[t * d + i] = (pv[e] / rms) * (g ? g[i] : 1.0f);
+    }
+}
+
 // Sequential-in-slot order of the reference is kept where it matters (pooling); wave
 // reductions are tree-ordered (fp32 reassociation within the parity tolerance).
 

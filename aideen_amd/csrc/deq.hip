@@ -608,6 +608,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
                                                      float beta) {
 #pragma clang fp contract(off)  // as in k_update
     __shared__ float rs[16];
+    extern __shared__ float hl[];  // [H][d] the new rows, with b.pool
     const int i = blockIdx.x;
     if (i >= b.cnt[cur]) return;
     const int s = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -648,6 +649,7 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
         if (!PART || e < er) {
             hw[lane + 64 * e] = hn;
             if (b.h_both) h[lane + 64 * e] = hn;
+            if (b.pool) hl[s * d + lane + 64 * e] = hn;
         }
         const float df = hn - hold[e];
         r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
@@ -667,6 +669,15 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
             const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
             b.act[cur ^ 1][pos] = t;
         }
+    }
+    if (b.pool && threadIdx.x < 64) {  // the token's LM-head prologue, the slots summed in order as k_pool_norm does
+        float pv[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) pv[e] = 0.0f;
+        for (int q = 0; q < H; ++q)
+#pragma unroll
+            for (int e = 0; e < E; ++e) pv[e] = pv[e] + ((!PART || e < er) ? hl[q * d + lane + 64 * e] : 0.0f);
+        pool_finish<E>(pv, H, d, er, lane, t, b.pool_g, b.pool_out, b.pool_norm, 0.0f);
     }
 }
 
@@ -975,8 +986,9 @@ void launch_update(const Dims &D, const SolveBuffers &b, int cur, int k, int max
                    const float *anchor, const float *norm_scale, float beta, hipStream_t st) {
     if (ntok <= SMALL_ROWS) {
         const dim3 tgrid((unsigned)ntok), tblk(64 * D.H);
+        const size_t lds = b.pool ? (size_t)D.H * D.d * sizeof(float) : 0;
         dispatch_width(D.d, [&](auto Ec, auto Pc) {
-            hipLaunchKernelGGL((k_update_tok<decltype(Ec)::value, decltype(Pc)::value>), tgrid, tblk, 0, st, D, b,
+            hipLaunchKernelGGL((k_update_tok<decltype(Ec)::value, decltype(Pc)::value>), tgrid, tblk, lds, st, D, b,
                                cur, k, max_iters, eps, anchor, norm_scale, beta);
         });
         return;

@@ -44,38 +44,7 @@ __global__ __launch_bounds__(256) void k_pool_norm(Dims D, const float *h, int n
         }
     }
     if (rec && lane < H) rec[((long)t * H + lane) * REC] = my_rms;
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = lane + 64 * e;
-        pv[e] = pv[e] / (float)H;
-        if (pooled && (!PART || e < er)) pooled[(long)t * d + i] = pv[e];
-        ss += pv[e] * pv[e];
-    }
-    if (!pnorm) return;
-    ss = wave_sum(ss);
-    const float rms = sqrtf(ss / (float)d + 1e-5f);
-    if (pre > 0.0f) {
-        // the LM head's A operand pre-split: fp16 halves of x = pnorm * pre, hi = f16(x) and
-        // lo = f16(x - hi), each 8 consecutive elements as 8 hi halves then 8 lo halves
-        _Float16 *row = reinterpret_cast<_Float16 *>(pnorm + (long)t * d);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const int i = lane + 64 * e;
-            if (!PART || e < er) {
-                const float x = ((pv[e] / rms) * (g ? g[i] : 1.0f)) * pre;
-                const _Float16 hv = (_Float16)x;
-                row[(i >> 3) * 16 + (i & 7)] = hv;
-                row[(i >> 3) * 16 + 8 + (i & 7)] = (_Float16)(x - (float)hv);
-            }
-        }
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int i = lane + 64 * e;
-        if (!PART || e < er) pnorm[(long)t * d + i] = (pv[e] / rms) * (g ? g[i] : 1.0f);
-    }
+    pool_finish<E>(pv, H, d, er, lane, t, g, pooled, pnorm, pre);
 }
 
 // Arg-max of one logits row; ties go to the LAST maximal index, as Iterator::max_by does
@@ -199,7 +168,7 @@ constexpr int dq_waves(int E) { return E <= 8 ? 16 : (E <= 16 ? 8 : 4); }
 template <int E, bool PART>
 __global__ __launch_bounds__(64 * dq_waves(E)) void k_decode_query(const float *Emb, int d, const int32_t *seq,
                                                                    int stride, int len, int ctx, float *q,
-                                                                   unsigned *absmax) {
+                                                                   unsigned *absmax, QueryInit qi) {
     constexpr int W = dq_waves(E);
     __shared__ double part[W][64 * E];
     __shared__ double red[W];
@@ -252,16 +221,39 @@ __global__ __launch_bounds__(64 * dq_waves(E)) void k_decode_query(const float *
     const double nv = sqrt(n2);
     const double inv = 1.0 / (nv > 1e-6 * (double)L ? nv : (double)L);
     unsigned mb = 0;  // largest finite |q| of this lane, as float bits
+    float hmax = 0.0f;  // largest finite |h0| of this lane
     for (int j = threadIdx.x; j < d; j += 64 * W) {
         const float v = (float)(part[0][j] * inv);
         q[(long)b * d + j] = v;
         const float a = fabsf(v);
         if (a < INFINITY) mb = max(mb, __float_as_uint(a));
+        if (qi.h) {  // h0 = x + anchor, as k_init forms it
+            for (int s = 0; s < qi.H; ++s) {
+                const float hv = v + qi.anchor[(long)s * d + j];
+                qi.h[((long)b * qi.H + s) * d + j] = hv;
+                hmax = fmaxf(hmax, fabsf(hv) < INFINITY ? fabsf(hv) : 0.0f);
+            }
+        }
     }
     if (absmax) {
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, off, 64));
         if (lane == 0 && mb) atomicMax(absmax, mb);
+    }
+    if (qi.h) {
+        if (qi.amax_h) track_absmax(qi.amax_h, hmax);
+        if (threadIdx.x == 0) {
+            qi.act0[b] = b;
+            qi.iters[b] = 0;
+            if (qi.rprev) qi.rprev[b] = 1.0f;
+        }
+        if (b == 0) {
+            if (threadIdx.x == 0) {
+                qi.cnt[0] = (int)gridDim.x;
+                qi.cnt[1] = 0;
+            }
+            for (int k = threadIdx.x; k < ADN_PROFILE_MAX_ITERS; k += 64 * W) qi.cnt_hist[k] = 0;
+        }
     }
 }
 
@@ -314,11 +306,12 @@ void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, 
 }
 
 void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
-                         hipStream_t st, unsigned *absmax) {
+                         hipStream_t st, unsigned *absmax, const QueryInit *init) {
+    const QueryInit qi = init ? *init : QueryInit{};
     dispatch_width(d, [&](auto Ec, auto Pc) {
         constexpr int EC = decltype(Ec)::value;
         hipLaunchKernelGGL((k_decode_query<EC, decltype(Pc)::value>), dim3((unsigned)B), dim3(64 * dq_waves(EC)), 0, st,
-                           E, d, seq, stride, len, ctx, q, absmax);
+                           E, d, seq, stride, len, ctx, q, absmax, qi);
     });
 }
 

@@ -153,6 +153,14 @@ struct SolveBuffers {
     float *h_out;
     // with h_out: write the iterate into h as well (iterations before the first mix)
     int h_both;
+    // a few-token update at which every token exits (the last iteration of a fixed-iteration
+    // solve) also forms each token's LM-head prologue from its new rows (pool_finish): pooled
+    // rows into pool_out (or null), the normalised rows in fp32 into pool_norm (or null), gain
+    // pool_g; pool = 0: none
+    int pool;
+    float *pool_out;
+    float *pool_norm;
+    const float *pool_g;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -204,12 +212,24 @@ void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream
 // final reduction of the per-tile arg-max partials written by the LM-head GEMM
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
                           hipStream_t st, const TokenAppend *app = nullptr);
+// The init of a forward over B query rows (launch_init's work for the rule h0 = x + anchor), done
+// by the kernel that writes the rows: h [B][H][d] = q + anchor[s] per slot, the bound word
+// raised to the largest finite |h0|, the first active list (all B rows), iteration counts and
+// plateau residuals reset, the list counts and the per-iteration active counts.
+struct QueryInit {
+    float *h;
+    const float *anchor;
+    int H;
+    int32_t *act0, *iters, *cnt, *cnt_hist;
+    float *rprev;      // or null
+    unsigned *amax_h;  // or null
+};
 // Greedy decode.  seq [B][stride] holds each sequence's tokens; step j uses the first len.
 // q [B][d] = embed_context of the last ctx of them (d <= 2048).  absmax, when set, is raised
 // (atomic max of float bits) to the largest finite |q| written, as launch_absmax would; it must
-// have been cleared before the call.
+// have been cleared before the call.  init, when set, also does the forward's init (QueryInit).
 void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, int len, int ctx, int B, float *q,
-                         hipStream_t st, unsigned *absmax = nullptr);
+                         hipStream_t st, unsigned *absmax = nullptr, const QueryInit *init = nullptr);
 // the repetition penalty over the same context, in place on logits [B][V]
 void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
                         hipStream_t st);

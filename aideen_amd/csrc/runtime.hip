@@ -196,6 +196,7 @@ struct Prof {
     struct Rec {
         int stage, k, n;  // n: rows of the launch (-1: every token of the forward)
         hipEvent_t e0, e1;
+        int fused;        // PROF_FUSED_* stages done inside this launch
     };
     std::vector<Rec> recs;
     std::vector<hipEvent_t> pool;
@@ -213,13 +214,18 @@ struct Prof {
     }
 };
 
+// work of another stage done inside a launch (its bytes and flops are counted with the launch)
+constexpr int PROF_FUSED_ATTN = 1;    // the attention mix, inside the W_o product
+constexpr int PROF_FUSED_UPDATE = 2;  // the previous iteration's update, inside the Q|K|V product
+constexpr int PROF_FUSED_POOL = 4;    // the LM head's pool, inside the last update
+
 struct Span {
     Prof *p;
     hipStream_t st;
     size_t idx;
-    Span(Prof *p_, int stage, int k, hipStream_t st_, int n = -1) : p(p_), st(st_), idx(0) {
+    Span(Prof *p_, int stage, int k, hipStream_t st_, int n = -1, int fused = 0) : p(p_), st(st_), idx(0) {
         if (!p) return;
-        Prof::Rec r{stage, k, n, p->get(), p->get()};
+        Prof::Rec r{stage, k, n, p->get(), p->get(), fused};
         ADN_HIP(hipEventRecord(r.e0, st));
         idx = p->recs.size();
         p->recs.push_back(r);
@@ -294,9 +300,10 @@ float max_row_l1(const float *w, int H, int d, bool in_out) {
 // ---------------------------------------------------------------------------------------
 // signal[t][s] = W_in[s] x_t for every token, h0 and the first active list (all tokens).
 // s_in_ready: the bounds were reset and max |s_in| accumulated into c->absmax by the caller's
-// kernels (a decode step: the previous step's arg-max and this step's query).
+// kernels (a decode step: the previous step's arg-max and this step's query); init_done: so was
+// the init (the query kernel, QueryInit).
 void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int ntok, Prof *prof,
-                         bool s_in_ready = false) {
+                         bool s_in_ready = false, bool init_done = false) {
     const Dims &D = c->D;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
@@ -335,7 +342,7 @@ void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, in
         }
         launch_gemm(g, st);
     }
-    {
+    if (!init_done) {
         Span sp(prof, ADN_STAGE_INIT, -1, st);
         launch_init(D, b, r.tokens ? c->embed : r.s_in, r.tokens, ntok, c->anchor, st);
     }
@@ -343,7 +350,10 @@ void enqueue_signal_init(adn_ctx *c, const adn_run &r, const SolveBuffers &b, in
 
 // max_iters Picard steps over the active list b.act[0] / b.cnt[0]: at most `rows` tokens are
 // active, token indices are < ntok (the row stride of h, signal and the Anderson ring).
-void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int rows, int ntok, Prof *prof) {
+// pool: the head's pool outputs (SolveBuffers::pool_*), formed by the last update where it can
+// (a fixed-iteration solve whose rows fit in LDS); returns whether it did.
+bool enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int rows, int ntok, Prof *prof,
+                        const SolveBuffers *pool = nullptr) {
     const Dims &D = c->D;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
@@ -366,6 +376,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
     const bool fixed = gemm_attn_fusable(c->prec, rows, d, H) && rows == ntok && !(r.eps > 0.0f) &&
                        !b.rprev && m == 0 && !b.mem_hist && r.max_iters >= 2;
     const long fix_stride = (long)std::min<long>(c->cap_tok, ATTN_FUSE_ROWS) * H * d;
+    const bool pool_here = fixed && pool && (long)H * d <= 16384;  // the update's LDS holds a token's rows
     auto iterate = [&](int j) { return j == 0 ? b.h : c->fix_h + (long)(j & 1) * fix_stride; };
     for (int k = 0; k < r.max_iters; ++k) {
         const int cur = fixed ? 0 : k & 1;
@@ -403,7 +414,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             g.epi = c->qk_bias ? EPI_BIAS : EPI_NONE;
             set_split(c, g, c->sp_qkv);
             set_range(c, g, 0);
-            Span sp(prof, ADN_STAGE_QKV_GEMM, k, st);
+            Span sp(prof, ADN_STAGE_QKV_GEMM, k, st, -1, g.upd_o ? PROF_FUSED_UPDATE : 0);
             launch_gemm(g, st);
         }
         // At a few rows the attention is formed inside the W_o product (one launch less per
@@ -440,7 +451,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
                 g.attn_cnt_next = b.cnt + (cur ^ 1);
                 g.attn_cnt_hist = b.cnt_hist + k;
             }
-            Span sp(prof, ADN_STAGE_WO_GEMM, k, st);
+            Span sp(prof, ADN_STAGE_WO_GEMM, k, st, -1, attn_in_wo ? PROF_FUSED_ATTN : 0);
             launch_gemm(g, st);
         }
         // With Anderson mixing after this update, the update writes its iterate straight into the
@@ -452,7 +463,6 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         const bool mix = m > 0 && k + 1 < r.max_iters;
         const bool from_slot = mix && anderson_from_slot_ok(D);
         if (!fixed || k + 1 == r.max_iters) {
-            Span sp(prof, ADN_STAGE_UPDATE, k, st);
             SolveBuffers bu = b;
             if (from_slot) {
                 bu.h_out = b.hist + (long)(k % m) * ntok * H * d;
@@ -461,7 +471,14 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
             if (fixed) {  // from the last small buffer into h
                 bu.h = iterate(k);
                 bu.h_out = b.h;
+                if (pool_here) {
+                    bu.pool = 1;
+                    bu.pool_out = pool->pool_out;
+                    bu.pool_norm = pool->pool_norm;
+                    bu.pool_g = pool->pool_g;
+                }
             }
+            Span sp(prof, ADN_STAGE_UPDATE, k, st, -1, bu.pool ? PROF_FUSED_POOL : 0);
             launch_update(D, bu, cur, k, r.max_iters, r.eps, rows, c->anchor, c->norm_scale, r.damping, st);
         }
         if (mix && !(from_slot && k < 2)) {
@@ -472,6 +489,7 @@ void enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
                 launch_anderson(D, b, cur ^ 1, ntok, rows, k, m, st);
         }
     }
+    return pool_here;
 }
 
 // The carrier's per-row record: rms (unless the pooling pass wrote it: rms_done) and the
@@ -510,7 +528,7 @@ void enqueue_scan_prep(adn_ctx *c, int ntok, const SolveBuffers &b, Prof *prof, 
 // stream would evict it).  Returns whether it did (the scan then skips its preparation).
 // app: a decode step's token append, done by the arg-max kernel.
 bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int ntok, Prof *prof,
-                  bool scan_rms = false, const TokenAppend *app = nullptr) {
+                  bool scan_rms = false, const TokenAppend *app = nullptr, bool pool_done = false) {
     const Dims &D = c->D;
     const int d = D.d;
     hipStream_t st = c->stream;
@@ -519,7 +537,7 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
     // the LM head on the 256x256 fp16-split tiles reads its A pre-split, written so by the pool
     // kernel with the head's A scale
     const bool lm_pre = want_logits && gemm_presplit_ok(c->prec, ntok, D.V);
-    if (pool) {
+    if (pool && !pool_done) {
         Span sp(prof, ADN_STAGE_POOL, -1, st);
         launch_pool_norm(D, b.h, ntok, c->lm_g, o.pooled, want_logits ? c->pnorm : nullptr,
                          scan_rms ? c->scb.rec : nullptr, scan_rec_len(D), lm_pre ? c->lm_a_scale : 0.0f, st);
@@ -615,6 +633,7 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
 // accumulated max |s_in| (s_in_ready), and the arg-max kernel appends the token (app).
 struct DecodeStep {
     bool s_in_ready;
+    bool init_done;
     const TokenAppend *app;
 };
 
@@ -629,9 +648,18 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     b.amax_h = c->bounds;
     c->last_h = b.h;  // the adjoint reads this forward's h* and signal
     c->last_ntok = ntok;
-    enqueue_signal_init(c, r, b, ntok, prof, ds && ds->s_in_ready);
-    enqueue_iterations(c, r, b, ntok, ntok, prof);
-    const bool prep_done = enqueue_head(c, o, b, ntok, prof, o.scan_y || o.scan_state, ds ? ds->app : nullptr);
+    enqueue_signal_init(c, r, b, ntok, prof, ds && ds->s_in_ready, ds && ds->init_done);
+    // the pool may be formed by the last update (fixed-iteration solves): not where the head's
+    // pool also feeds the carrier or writes the LM head's A pre-split
+    const bool want_logits = o.logits || o.argmax;
+    const bool scan = o.scan_y || o.scan_state;
+    SolveBuffers pr{};
+    pr.pool_out = o.pooled;
+    pr.pool_norm = want_logits ? c->pnorm : nullptr;
+    pr.pool_g = c->lm_g;
+    const bool pool_ok = (want_logits || o.pooled) && !scan && !(want_logits && gemm_presplit_ok(c->prec, ntok, c->D.V));
+    const bool pooled = enqueue_iterations(c, r, b, ntok, ntok, prof, pool_ok ? &pr : nullptr);
+    const bool prep_done = enqueue_head(c, o, b, ntok, prof, scan, ds ? ds->app : nullptr, pooled);
     enqueue_scan(c, r, o, b, prof, prep_done);
 }
 
@@ -1208,12 +1236,16 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
                 enqueue_forward_memory(c, r, o, nullptr, penalise ? nullptr : &app);
                 std::swap(m_cur, m_nxt);
             } else {
-                // query = embed_context(context, ctx_len) (trainer.rs:4388-4392)
+                // query = embed_context(context, ctx_len) (trainer.rs:4388-4392); the query
+                // kernel also does the init where it is h0 = query + anchor
+                const bool init_q = !(D.flags & ADN_F_INIT_SIGNAL_RMS);
+                const SolveBuffers &sb = c->sb;
+                const QueryInit qi{sb.h, c->anchor, D.H, sb.act[0], sb.iters, sb.cnt, sb.cnt_hist, sb.rprev, c->bounds};
                 launch_decode_query(c->embed, D.d, seq, stride, len, ctx_len, batch, q, st,
-                                    c->prec == PREC_F16X3 ? c->absmax : nullptr);
+                                    c->prec == PREC_F16X3 ? c->absmax : nullptr, init_q ? &qi : nullptr);
                 r.tokens = nullptr;
                 r.s_in = q;
-                const DecodeStep ds{true, penalise ? nullptr : &app};
+                const DecodeStep ds{true, init_q, penalise ? nullptr : &app};
                 enqueue_forward(c, r, o, nullptr, &ds);
             }
             if (penalise) {
@@ -1623,10 +1655,31 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
             switch (st) {
                 case ADN_STAGE_SIGNAL_GEMM: fl = 2 * ntok * H * d * d; by = f * (ntok * d + H * d * d + ntok * H * d); break;
                 case ADN_STAGE_INIT: by = f * (ntok * d + ntok * H * d); break;
-                case ADN_STAGE_QKV_GEMM: fl = 6 * n * H * d * d; by = n > 0 ? f * (n * H * d + 3 * H * d * d + 3 * n * H * d) : 0; break;
+                case ADN_STAGE_QKV_GEMM:
+                    fl = 6 * n * H * d * d;
+                    by = n > 0 ? f * (n * H * d + 3 * H * d * d + 3 * n * H * d) : 0;
+                    if (rec.fused & PROF_FUSED_UPDATE) {  // reads o, the signal and h_{k-1}; writes h_k
+                        fl += 10 * n * H * d;
+                        by += f * 3 * n * H * d;
+                    }
+                    break;
                 case ADN_STAGE_ATTN: fl = 4 * n * H * H * d; by = f * 4 * n * H * d; break;
-                case ADN_STAGE_WO_GEMM: fl = 2 * n * H * d * d; by = n > 0 ? f * (2 * n * H * d + H * d * d) : 0; break;
-                case ADN_STAGE_UPDATE: fl = 10 * n * H * d; by = f * (4 * n * H * d + 3 * n); break;
+                case ADN_STAGE_WO_GEMM:
+                    fl = 2 * n * H * d * d;
+                    by = n > 0 ? f * (2 * n * H * d + H * d * d) : 0;
+                    if (rec.fused & PROF_FUSED_ATTN) {  // A from the Q|K|V rows instead of the mix
+                        fl += 4 * n * H * H * d;
+                        by += f * 2 * n * H * d;
+                    }
+                    break;
+                case ADN_STAGE_UPDATE:
+                    fl = 10 * n * H * d;
+                    by = f * (4 * n * H * d + 3 * n);
+                    if (rec.fused & PROF_FUSED_POOL) {  // the pooled and normalised rows written
+                        fl += n * H * d;
+                        by += f * 2 * n * d;
+                    }
+                    break;
                 case ADN_STAGE_CONVERGE: by = f * (n * (rec.k >= 0 ? H + 3 : 1) + 2); break;
                 case ADN_STAGE_ANDERSON: {
                     const double nn = act(st, rec.k, rec.k + 1);

@@ -367,6 +367,10 @@ int adn_aidn_weights(adn_aidn *model, adn_weights *w, adn_config *cfg, adn_run *
 #define ADN_STAGE_COUNT 17
 #define ADN_PROFILE_MAX_ITERS 256
 
+/* A stage done inside another stage's launch (at <= 4 tokens: the attention mix inside the W_o
+ * product; with no early exit possible, the previous update inside the Q|K|V product and the
+ * pool inside the last update) has no launches of its own: its FLOPs and bytes are counted with
+ * the launch that does it. */
 typedef struct adn_profile {
     double ms[ADN_STAGE_COUNT];       /* device time summed over the stage's launches   */
     double flops[ADN_STAGE_COUNT];    /* algorithmic FLOPs summed over those launches   */
