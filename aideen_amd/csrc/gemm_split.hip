@@ -722,29 +722,25 @@ void launch_cfg(const GemmParams &p, hipStream_t st) {
     } else {
         if (p.M <= 32 && p.K % 64 == 0) {
             // skinny: K split over the waves of a workgroup, about two 64-K steps per wave;
-            // wide outputs take two column tiles per wave (each A fragment feeds both)
+            // wide outputs take two column tiles per wave (each A fragment feeds both) except at
+            // a few rows, where twice the workgroups stream the weights sooner (decode Q|K|V at
+            // one row: 248 -> 238 us per token; at 32 rows the two-tile waves are 7% faster)
             const int steps = p.K / 64;
             int kw = steps >= 16 ? 8 : steps >= 8 ? 4 : steps >= 4 ? 2 : 1;
             while (steps % kw) kw >>= 1;  // each wave's K range is whole 64-K steps
             if constexpr (ROLE == ROLE_WO) {
                 if (p.attn_qkv) {  // the attention formed in the kernel (a few rows)
-                    if (p.N >= 1024)
-                        launch_skinny<ROLE, T, TERMS, 2, true>(p, kw, st);
-                    else
-                        launch_skinny<ROLE, T, TERMS, 1, true>(p, kw, st);
+                    launch_skinny<ROLE, T, TERMS, 1, true>(p, kw, st);
                     return;
                 }
             }
             if constexpr (ROLE == ROLE_QKV) {
                 if (p.upd_o) {  // the previous iteration's update formed in the kernel (a few rows)
-                    if (p.N >= 1024)
-                        launch_skinny<ROLE, T, TERMS, 2, false, true>(p, kw, st);
-                    else
-                        launch_skinny<ROLE, T, TERMS, 1, false, true>(p, kw, st);
+                    launch_skinny<ROLE, T, TERMS, 1, false, true>(p, kw, st);
                     return;
                 }
             }
-            if (p.N >= 1024)
+            if (p.N >= 1024 && p.M > ATTN_FUSE_ROWS)
                 launch_skinny<ROLE, T, TERMS, 2>(p, kw, st);
             else
                 launch_skinny<ROLE, T, TERMS, 1>(p, kw, st);
