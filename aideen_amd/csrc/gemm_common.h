@@ -249,7 +249,8 @@ __device__ __forceinline__ void epi_rows(const GemmParams &p, floatx16 (&acc)[WT
     if constexpr (I + 1 < WTM) epi_rows<I + 1, WTM, WTN, WGM, EPI, AM, CHECK, STREAM>(p, acc, c, bj, nv);
 }
 
-template <int WTM, int WTN, int WGM, int WGN, int EPI, bool AM, bool CHECK, bool STREAM = false>
+// PW: columns per arg-max partial (128; 64 for the few-row LM head's one-wave 64-column blocks)
+template <int WTM, int WTN, int WGM, int WGN, int EPI, bool AM, bool CHECK, bool STREAM = false, int PW = 128>
 __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WTM][WTN], const EpiCtx &c) {
     constexpr int BMt = WGM * WTM * 32;
     float bj[WTN];
@@ -266,11 +267,11 @@ __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WT
     }
     epi_rows<0, WTM, WTN, WGM, EPI, AM, CHECK, STREAM>(p, acc, c, bj, nv);
     if constexpr (AM) {
-        // partials are per 128 columns: waves covering 64 columns are combined in pairs
+        // partials are per PW columns: waves covering fewer columns are combined
         constexpr int CPW = WTN * 32;
-        static_assert(CPW == 64 || CPW == 128, "arg-max partials need 64 or 128 columns per wave");
-        constexpr int TPW = 128 / CPW;
-        constexpr int QT = WGN / TPW;  // 128-column tiles per block
+        static_assert((CPW == 64 || CPW == 128) && PW >= CPW, "arg-max partials need whole waves per partial");
+        constexpr int TPW = PW / CPW;
+        constexpr int QT = WGN * CPW / PW;  // partial tiles per block (the LM head's blocks hold whole ones)
         // the partials are exchanged through LDS; the logits stores need not wait.  A one-wave
         // block reads back its own writes (a wave's LDS operations complete in order).
         if constexpr (WGM * WGN > 1) lds_barrier();
@@ -278,8 +279,8 @@ __device__ __forceinline__ void epi_tile(const GemmParams &p, floatx16 (&acc)[WT
         for (int idx = tid; idx < BMt * QT; idx += 64 * WGM * WGN) {
             const int ml = idx % BMt, q = idx / BMt;
             const int m = c.m0 + ml;
-            const int tile = (c.n0 >> 7) + q;
-            if (m < c.M && tile * 128 < p.N) {
+            const int tile = c.n0 / PW + q;
+            if (m < c.M && tile * PW < p.N) {
                 float v = c.scratch_v[q * TPW * BMt + ml];
                 int ix = c.scratch_i[q * TPW * BMt + ml];
 #pragma unroll
@@ -318,17 +319,18 @@ __device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[
         // the forward reads them back) are stored non-temporally, which keeps the A rows and weights
         // of the tiles still being multiplied in L2
         constexpr bool LM_ST = true;
+        constexpr int PW = (WGM * WGN == 1 && WTN == 2) ? 64 : 128;  // gemm_lm_partial_cols
         if (p.am_val) {
             if (p.epi == EPI_BIAS) {
                 if (interior)
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, false, LM_ST>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, false, LM_ST, PW>(p, acc, c);
                 else
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, true, LM_ST>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_BIAS, true, true, LM_ST, PW>(p, acc, c);
             } else {
                 if (interior)
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, false, LM_ST>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, false, LM_ST, PW>(p, acc, c);
                 else
-                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, true, LM_ST>(p, acc, c);
+                    epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, true, true, LM_ST, PW>(p, acc, c);
             }
         } else {
             if (p.epi == EPI_BIAS) {

@@ -711,12 +711,16 @@ template <int ROLE, typename T, int TERMS>
 void launch_cfg(const GemmParams &p, hipStream_t st) {
     if constexpr (ROLE == ROLE_LMHEAD) {
         if (p.M <= 32 && p.K % 64 == 0) {
-            // skinny LM head (a decode step): 128-column blocks, the arg-max partials' width,
-            // K split as below
+            // skinny LM head (a decode step): 128-column blocks, the arg-max partials' width; at
+            // a few rows 64-column blocks with partials per 64 columns (twice the workgroups on
+            // the weight stream, as for the other products); K split as below
             const int steps = p.K / 64;
             int kw = steps >= 16 ? 8 : steps >= 8 ? 4 : steps >= 4 ? 2 : 1;
             while (steps % kw) kw >>= 1;
-            launch_skinny<ROLE, T, TERMS, 4>(p, kw, st);
+            if (gemm_lm_partial_cols(p.prec, p.M, p.K) == 64)
+                launch_skinny<ROLE, T, TERMS, 2>(p, kw, st);
+            else
+                launch_skinny<ROLE, T, TERMS, 4>(p, kw, st);
             return;
         }
     } else {
@@ -811,6 +815,10 @@ void launch_gemm_split(const GemmParams &p, hipStream_t st) {
 }
 
 bool gemm_presplit_ok(int prec, int M, int N) { return prec == PREC_F16X3 && M >= 1024 && N >= 512; }
+
+int gemm_lm_partial_cols(int prec, int M, int K) {
+    return (prec != PREC_FP32 && M <= ATTN_FUSE_ROWS && K % 64 == 0) ? 64 : GEMM_BN;
+}
 
 bool gemm_attn_fusable(int prec, int M, int K, int S) {
     return prec != PREC_FP32 && M <= ATTN_FUSE_ROWS && K % 64 == 0 && K <= 2048 && S <= 16;

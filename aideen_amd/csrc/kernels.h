@@ -112,6 +112,9 @@ bool gemm_presplit_ok(int prec, int M, int N);
 // Whether W_o on at most M rows runs with the attention formed in its kernel (GemmParams::attn_qkv):
 // the skinny split-arithmetic kernel, M <= ATTN_FUSE_ROWS, K a multiple of 64, at most 16 slots.
 bool gemm_attn_fusable(int prec, int M, int K, int S);
+// Columns per arg-max partial of the LM head over M rows (GEMM_BN, or 64 for the few-row skinny
+// LM head): the partial count is ceil(V / this), and the partial buffers hold that many per row.
+int gemm_lm_partial_cols(int prec, int M, int K);
 // hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16, from [S][N][K]
 // fp32 weights into the split GEMM's blocked layout (split_weight_elems halves each, N padded to
 // a multiple of 32); lo may be null.  The GEMMs' b_ss is then 0 (one matrix for every slot) or

@@ -567,7 +567,8 @@ bool enqueue_head(adn_ctx *c, const adn_outputs &o, const SolveBuffers &b, int n
         g.epi = c->lm_b ? EPI_BIAS : EPI_NONE;
         set_split(c, g, c->sp_lm, c->lm_a_scale);
         if (lm_pre) g.a_pre = c->pnorm;
-        const int ntiles = (D.V + GEMM_BN - 1) / GEMM_BN;
+        const int pcols = gemm_lm_partial_cols(c->prec, ntok, d);
+        const int ntiles = (D.V + pcols - 1) / pcols;
         if (o.argmax) {
             g.am_val = c->am_val;
             g.am_idx = c->am_idx;
@@ -880,9 +881,11 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));
         c->pnorm = (float *)dmalloc(c, (size_t)T * d * sizeof(float));
         c->argmax_scratch = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
+        // arg-max partials: per 128 columns, or per 64 at up to ATTN_FUSE_ROWS rows
         const size_t ntiles = ((size_t)cfg->vocab + GEMM_BN - 1) / GEMM_BN;
-        c->am_val = (float *)dmalloc(c, (size_t)T * ntiles * sizeof(float));
-        c->am_idx = (int32_t *)dmalloc(c, (size_t)T * ntiles * sizeof(int32_t));
+        const size_t am_n = std::max((size_t)T * ntiles, (size_t)std::min<long>(T, ATTN_FUSE_ROWS) * ((cfg->vocab + 63) / 64));
+        c->am_val = (float *)dmalloc(c, am_n * sizeof(float));
+        c->am_idx = (int32_t *)dmalloc(c, am_n * sizeof(int32_t));
         c->scb.rec = (float *)dmalloc(c, (size_t)T * H * scan_rec_len(c->D) * sizeof(float));
         c->scb.y = (float *)dmalloc(c, hd);
         if (cfg->flags & ADN_F_MEMORY) {
@@ -1691,7 +1694,9 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
                 }
                 case ADN_STAGE_POOL: fl = ntok * H * d; by = f * (ntok * H * d + 2 * ntok * d); break;
                 case ADN_STAGE_LMHEAD_GEMM: fl = 2 * ntok * V * d; by = f * (ntok * d + V * d + ntok * V); break;
-                case ADN_STAGE_ARGMAX: by = f * (2 * ntok * std::ceil(V / GEMM_BN) + ntok); break;  // tile partials
+                case ADN_STAGE_ARGMAX:  // tile partials
+                    by = f * (2 * ntok * std::ceil(V / gemm_lm_partial_cols(c->prec, (int)ntok, (int)d)) + ntok);
+                    break;
                 case ADN_STAGE_SCAN_PREP: fl = 2 * ntok * H * d * (R + 2 * N); by = f * (ntok * H * d + ntok * H * REC + H * d * (R + 2 * N)); break;
                 case ADN_STAGE_SCAN:  // compulsory: read h*, the record; write y
                     fl = ntok * H * d * (2 * R + 4 * N + 10);
