@@ -410,6 +410,41 @@ def test_greedy_decode_repeated_calls(oracle_lib, pen):
         assert np.array_equal(be.decode_greedy(prompts[0], 14, 6, repetition_penalty=pen), ref2), f"new weights {call}"
 
 
+DECODE_VARIANTS = [
+    dict(flags=synth.F_INIT_SIGNAL_RMS, B=3),                                 # init not done by the query kernel
+    dict(flags=synth.F_GEMM_FP32, B=3),                                       # no fused stages (fp32 products)
+    dict(flags=synth.F_GEMM_BF16X3, B=2),                                     # the fused stages on bf16 halves
+    dict(flags=synth.F_RMS_EXCL_ANCHOR | synth.F_SCORE_CLAMP4, qk_bias=True, B=4),
+    dict(flags=0, B=5),                                                       # above the few-row bound: kernels per stage
+]
+
+
+@pytest.mark.parametrize("var", DECODE_VARIANTS, ids=lambda v: "-".join(f"{k}{v[k]}" for k in v))
+def test_greedy_decode_variants(oracle_lib, var):
+    """The decode step's kernel choices (the init in the query kernel, the attention in W_o, the
+    update in the next Q|K|V product, the pool in the last update, the token append in the
+    arg-max) on and off: the init rule, each GEMM arithmetic, the anchor-excluding RMS with the
+    score clamp and q/k bias, and a batch above the few-row bound; token for token, on the
+    token-sensitive weights.  Two Picard steps keep the tokens sensitive to the init rule (after
+    generate's 10 steps the contractive map has forgotten h0: both rules decode the same tokens);
+    10 is generate's count."""
+    var = dict(var)
+    B = var.pop("B")
+    for iters in (2, 10):
+        mc = synth.ModelConfig(d=128, H=4, V=600, N=1, r=32, max_iters=iters, eps=0.0, **var)
+        w = synth.make_token_sensitive_weights(mc, seed=3)
+        prompt = synth.make_tokens("uniform", B, 9, mc.V, seed=31)
+        be = make(mc, B, 1)
+        be.upload_weights(w)
+        for pen in (1.0, 1.3):
+            log(f"decode variant {var} B={B} iters={iters} pen={pen}")
+            ref = oracle_lib.Oracle(mc, w).decode_greedy(prompt, 12, 6, pen)
+            assert len(set(ref.ravel().tolist())) >= 16
+            got = be.decode_greedy(prompt, 12, 6, max_iters=iters, repetition_penalty=pen)
+            assert np.array_equal(got, ref), f"iters {iters} pen {pen}: {np.argwhere(got != ref)[:4].tolist()}"
+        be.close()
+
+
 @pytest.mark.parametrize("d,H", [(64, 2), (192, 3), (1024, 2), (2048, 1)])
 def test_greedy_decode_widths(oracle_lib, d, H):
     """The decode's context query at every width bucket of its kernel (16 waves up to d = 512,
