@@ -520,7 +520,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
         const float beta = p.upd_beta, omb = 1.0f - beta;
         for (int r = wave; r < M; r += KW) {  // M <= ATTN_FUSE_ROWS
             long t = p.a_idx ? (long)p.a_idx[r] : (long)r;
-            if (t < 0 || t >= p.a_idx_max) t = 0;  // flagged below
+            if (p.a_idx && (t < 0 || t >= p.a_idx_max)) t = 0;  // flagged below
             const float *o = p.upd_o + ((long)r * p.S + s) * dd;
             const float *sg = p.upd_sig + t * hd + (long)s * dd;
             const float *an = p.upd_anchor + (long)s * dd;
