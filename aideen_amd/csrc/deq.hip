@@ -516,7 +516,7 @@ __global__ __launch_bounds__(256) void k_update(Dims D, SolveBuffers b, int cur,
             b.iters[t] = k + 1;
             if (b.conv) b.conv[t] = ex == 1;
         }
-        keep = !ex;
+        keep = !ex || (ex == 2 && b.cap_mix);
     }
     if (lane == 0) {
         keep_s[wave] = keep;
@@ -665,7 +665,8 @@ __global__ __launch_bounds__(1024) void k_update_tok(Dims D, SolveBuffers b, int
         if (ex) {
             b.iters[t] = k + 1;
             if (b.conv) b.conv[t] = ex == 1;
-        } else {
+        }
+        if (!ex || (ex == 2 && b.cap_mix)) {
             const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
             b.act[cur ^ 1][pos] = t;
         }
@@ -805,7 +806,9 @@ __global__ __launch_bounds__(AND_NT) void k_anderson_reg(Dims D, SolveBuffers b,
     auto X = [&](int j) { return b.hist + ((long)(j % m) * ntok + t) * hd; };
     float *slot = X(k);
     if constexpr (SLOT) {
-        if (NRES == 0 || b.iters[t] == k + 1) {  // h = the update's iterate
+        // h = the update's iterate: a token that exited at this iteration (unless it stopped at the
+        // cap unconverged, which is mixed), or any token while there is nothing to mix
+        if (NRES == 0 || (b.iters[t] == k + 1 && !(b.cap_mix && !b.conv[t]))) {
             float v[EPT];
 #pragma unroll
             for (int q = 0; q < EPT; ++q) {

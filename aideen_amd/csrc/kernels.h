@@ -156,6 +156,12 @@ struct SolveBuffers {
     float *h_out;
     // with h_out: write the iterate into h as well (iterations before the first mix)
     int h_both;
+    // the last iteration with Anderson mixing (k >= 2): a token that stops at the cap without
+    // converging is mixed like a continuing one (the solve mixes after every step that does not
+    // exit on the tolerance): the update appends it to the next list as well, and the mixing pass
+    // over the update's own list (SolveBuffers::h_out) tells it from a converged one by conv
+    // (non-null whenever this is set)
+    int cap_mix;
     // a few-token update at which every token exits (the last iteration of a fixed-iteration
     // solve) also forms each token's LM-head prologue from its new rows (pool_finish): pooled
     // rows into pool_out (or null), the normalised rows in fp32 into pool_norm (or null), gain

@@ -88,6 +88,9 @@ struct adn_ctx {
     // the iterates of a few-row solve with a fixed iteration count (two [ATTN_FUSE_ROWS][H][d]
     // buffers, alternating): there each Q|K|V product applies the previous update itself
     float *fix_h = nullptr;
+    // per-token exit flags when the caller asks for none (the mixing pass of the last iteration
+    // reads them)
+    int32_t *conv_scratch = nullptr;
     // fp16-split range guard: the A operands' magnitude bounds (ADN_BOUNDS words, reset per forward)
     // and the weight-derived constants they are combined with (set at upload)
     unsigned *bounds = nullptr;
@@ -460,10 +463,14 @@ bool enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         // and then again to the slot.
         // Before the first mix (k < 2) the update writes the iterate into both, and no mixing pass
         // runs.
-        const bool mix = m > 0 && k + 1 < r.max_iters;
+        // Anderson mixes after every step that a token does not exit on the tolerance, the last
+        // one included (a token stopped at the cap unconverged ends with the mix)
+        const bool mix = m > 0;
         const bool from_slot = mix && anderson_from_slot_ok(D);
+        const int cap_mix = mix && k + 1 == r.max_iters && k >= 2;
         if (!fixed || k + 1 == r.max_iters) {
             SolveBuffers bu = b;
+            bu.cap_mix = cap_mix;
             if (from_slot) {
                 bu.h_out = b.hist + (long)(k % m) * ntok * H * d;
                 bu.h_both = k < 2;
@@ -483,10 +490,12 @@ bool enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         }
         if (mix && !(from_slot && k < 2)) {
             Span sp(prof, ADN_STAGE_ANDERSON, k, st);
+            SolveBuffers ba2 = b;
+            ba2.cap_mix = cap_mix;
             if (from_slot)
-                launch_anderson_from_slot(D, b, cur, ntok, rows, k, m, st);
+                launch_anderson_from_slot(D, ba2, cur, ntok, rows, k, m, st);
             else
-                launch_anderson(D, b, cur ^ 1, ntok, rows, k, m, st);
+                launch_anderson(D, ba2, cur ^ 1, ntok, rows, k, m, st);
         }
     }
     return pool_here;
@@ -644,7 +653,7 @@ void enqueue_forward(adn_ctx *c, const adn_run &r, const adn_outputs &o, Prof *p
     SolveBuffers b = c->sb;
     if (o.h_star) b.h = o.h_star;
     if (o.iters) b.iters = o.iters;
-    b.conv = o.converged;
+    b.conv = o.converged ? o.converged : c->conv_scratch;
     b.mem_hist = nullptr;
     b.amax_h = c->bounds;
     c->last_h = b.h;  // the adjoint reads this forward's h* and signal
@@ -680,7 +689,7 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
     SolveBuffers b = c->sb;
     if (o.h_star) b.h = o.h_star;
     if (o.iters) b.iters = o.iters;
-    b.conv = o.converged;
+    b.conv = o.converged ? o.converged : c->conv_scratch;
     b.mem_hist = nullptr;
     b.amax_h = c->bounds;
     b.mem_T = T;
@@ -876,6 +885,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
         c->absmax = (unsigned *)dmalloc(c, sizeof(unsigned));
         c->fix_h = (float *)dmalloc(c, 2 * (size_t)std::min<long>(T, ATTN_FUSE_ROWS) * H * d * sizeof(float));
+        c->conv_scratch = (int32_t *)dmalloc(c, (size_t)T * sizeof(int32_t));
         c->bounds = (unsigned *)dmalloc(c, ADN_BOUNDS * sizeof(unsigned));
         b.err = c->d_err;
         ADN_HIP(hipMemsetAsync(c->d_err, 0, sizeof(unsigned), c->stream));

@@ -951,3 +951,43 @@ def test_noncontractive_weights_report_nonconvergence(oracle_lib):
     assert (ref["converged"] == 0).all() and (got["converged"] == 0).all()
     assert (got["iters"] == 15).all()
     assert float((got["h_star"].astype(np.float64) ** 2).sum(axis=(2, 3)).max()) < 1e6
+
+
+def test_anderson_tokens_stopped_at_the_cap_end_mixed(oracle_lib):
+    """With Anderson mixing the solve mixes after every step a token does not exit on the
+    tolerance, the last allowed one included: a token stopped at the cap unconverged ends with the
+    mix, one that converges at the last step with its iterate (fixed_point_memory_reasoning.rs
+    loop; staged_adjoint_picard_clean.wgsl's mix after every step).  Few-token and many-token
+    update kernels with the one-pass mixing from the ring slot (H*d <= 4096), and the two-pass
+    mixing of a wider state, at tolerance 0 (every token stops at the cap); then a cap at which
+    tokens exit before it, at it converged, and at it unconverged, compared on the tokens whose
+    residuals stay 20% or more away from eps at every step (an exit decided by rounding can move
+    by two with Anderson mixing)."""
+    for d, H, B, T in ((128, 4, 1, 3), (128, 4, 2, 40), (512, 16, 1, 12)):
+        mc = synth.ModelConfig(d=d, H=H, V=500, N=4, r=32, anderson_m=3, eps=0.0, max_iters=6)
+        w = synth.make_token_sensitive_weights(mc, seed=8)
+        toks = synth.make_tokens("uniform", B, T, mc.V, seed=8)
+        log(f"Anderson at the cap: d={d} H={H} B={B} T={T}")
+        be = make(mc, B, T)
+        be.upload_weights(w)
+        got = be.forward(toks, want=("h_star", "pooled", "logits", "argmax", "iters", "converged"))
+        be.close()
+        ref = oracle_lib.Oracle(mc, w).forward(toks, want_scan=False, nthreads=16)
+        assert (got["iters"] == 6).all() and not got["converged"].any()
+        assert_forward_parity(got, ref, f"Anderson cap d={d}")
+    mc = synth.ModelConfig(d=128, H=4, V=500, N=4, r=32, anderson_m=3, eps=1e-4, max_iters=21)
+    w = synth.make_token_sensitive_weights(mc, seed=7)
+    toks = synth.make_tokens("uniform", 2, 40, mc.V, seed=7)
+    be = make(mc, 2, 40)
+    be.upload_weights(w)
+    got = be.forward(toks, want=("h_star", "iters", "converged"))
+    be.close()
+    o = oracle_lib.Oracle(mc, w)
+    ref = o.forward(toks, want_scan=False, nthreads=16)
+    robust = np.array([all(abs(r - mc.eps) > 0.2 * mc.eps for r in o.solve(w["embed"][tk])[2][:int(n)])
+                       for tk, n in zip(toks.ravel(), ref["iters"].ravel())]).reshape(toks.shape)
+    kinds = {(int(n), int(c)) for n, c, r in zip(ref["iters"].ravel(), ref["converged"].ravel(), robust.ravel()) if r}
+    assert {(20, 1), (21, 1), (21, 0)} <= kinds, kinds
+    assert np.array_equal(got["iters"][robust], ref["iters"][robust])
+    assert np.array_equal(got["converged"][robust], ref["converged"][robust])
+    np.testing.assert_allclose(got["h_star"][robust], ref["h_star"][robust], rtol=RTOL, atol=ATOL)
