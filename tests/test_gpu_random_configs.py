@@ -7,7 +7,8 @@ chosen by size (few-token attention inside W_o, the fixed-iteration update insid
 inside the last update, skinny and tiled products, per-step and matrix-form scans) meet every
 switch of the forward spec (fixed_point_memory_reasoning.rs:1300-1486) in combinations no
 hand-written case lists.  Every output of every token is compared with the oracle on the
-token-sensitive weights.  With Anderson mixing the tolerance is 0 (the residual is not
+token-sensitive weights (the carrier's outputs against the oracle's scan of the GPU's own h*, as
+everywhere: the scan is a long recurrence that would otherwise compound h*'s own tolerance).  With Anderson mixing the tolerance is 0 (the residual is not
 monotone, so an exit near eps can move by two iterations; every iteration then runs), as it is
 in the fixed-iteration cases.
 """
@@ -21,6 +22,16 @@ from test_gpu_parity import assert_forward_parity, log
 pytestmark = pytest.mark.gpu
 
 ALL = ("h_star", "pooled", "logits", "argmax", "iters", "converged", "scan_y", "scan_state")
+
+
+def check(oracle_lib, mc, w, toks, got, ctx):
+    o = oracle_lib.Oracle(mc, w)
+    ref = o.forward(toks, want_scan=False, nthreads=16)
+    assert_forward_parity({k: v for k, v in got.items() if not k.startswith("scan")}, ref, ctx)
+    for b in range(toks.shape[0]):
+        y, st = o.scan(got["h_star"][b])
+        np.testing.assert_allclose(got["scan_y"][b], y, rtol=1e-4, atol=1e-3, err_msg=f"{ctx}: scan_y[{b}]")
+        np.testing.assert_allclose(got["scan_state"][b], st, rtol=1e-4, atol=1e-3, err_msg=f"{ctx}: scan_state[{b}]")
 
 
 def draw(seed):
@@ -57,7 +68,88 @@ def test_random_config_matches_oracle(oracle_lib, seed):
     be.upload_weights(w)
     got = be.forward(toks, want=ALL)
     be.close()
-    ref = oracle_lib.Oracle(mc, w).forward(toks, nthreads=16)
-    assert_forward_parity(got, ref, f"random config {seed}")
+    check(oracle_lib, mc, w, toks, got, f"random config {seed}")
     if mc.eps == 0.0:
         assert (got["iters"] == mc.max_iters).all()
+
+
+def draw_large(seed):
+    """At least 1024 tokens and a vocabulary of at least 512: the persistent 256 x 256 tiles of
+    every product (pre-split W_o and LM-head operands), the many-token update, Anderson's one- or
+    two-pass mixing, and the per-step or matrix-form carrier scan."""
+    rng = np.random.default_rng(2000 + seed)
+    d = int(rng.choice([128, 256, 512]))
+    H = int(rng.choice([2, 4, 8]))
+    V = int(rng.choice([600, 1500, 2100]))
+    N = int(rng.choice([4, 16]))
+    flags = synth.F_SCAN_SELECTIVE if rng.random() < 0.6 else 0
+    for f in (synth.F_SCORE_CLAMP4, synth.F_RMS_EXCL_ANCHOR, synth.F_INIT_SIGNAL_RMS, synth.F_WIN_TRANSPOSED):
+        if rng.random() < 0.3:
+            flags |= f
+    flags |= int(rng.choice([0, synth.F_RESID_L2]))
+    m = int(rng.choice([0, 0, 3, 5]))
+    B = int(rng.choice([1, 2, 4]))
+    T = int(rng.integers(1024, 1600)) // B
+    eps = 0.0 if m > 0 else 1e-4
+    max_iters = 7 if eps == 0.0 else 20
+    mc = synth.ModelConfig(d=d, H=H, V=V, N=N, r=32, flags=flags, anderson_m=m, eps=eps, max_iters=max_iters,
+                           qk_bias=bool(rng.random() < 0.3))
+    return mc, B, T
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_large_config_matches_oracle(oracle_lib, seed):
+    mc, B, T = draw_large(seed)
+    log(f"random large config {seed}: {mc} B={B} T={T}")
+    w = synth.make_token_sensitive_weights(mc, seed=seed)
+    toks = synth.make_tokens("zipf", B, T, mc.V, seed=seed)
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks, want=ALL)
+    be.close()
+    check(oracle_lib, mc, w, toks, got, f"random large config {seed}")
+
+
+def draw_memory(seed):
+    """The memory-coupled forward (fixed-history mode): position-sequential solves of B tokens
+    with the history term, optional warm start, Anderson, and caller state."""
+    rng = np.random.default_rng(3000 + seed)
+    d = int(rng.choice([64, 128, 256]))
+    H = int(rng.choice([1, 2, 4, 8]))
+    V = int(rng.choice([300, 700]))
+    flags = synth.F_MEMORY
+    for f in (synth.F_SCORE_CLAMP4, synth.F_RMS_EXCL_ANCHOR, synth.F_TOKEN_CARRY, synth.F_INIT_SIGNAL_RMS):
+        if rng.random() < 0.3:
+            flags |= f
+    m = int(rng.choice([0, 0, 2, 3]))
+    eps = 0.0 if (m > 0 or rng.random() < 0.5) else 1e-4
+    max_iters = int(rng.choice([3, 8, 12])) if eps == 0.0 else 20
+    mc = synth.ModelConfig(d=d, H=H, V=V, N=1, r=32, flags=flags, anderson_m=m, eps=eps, max_iters=max_iters,
+                           qk_bias=bool(rng.random() < 0.3))
+    B, T = int(rng.integers(1, 5)), int(rng.integers(1, 14))
+    return mc, B, T, bool(rng.random() < 0.5), bool(rng.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_memory_config_matches_oracle(oracle_lib, seed):
+    mc, B, T, strong, state_in = draw_memory(seed)
+    log(f"random memory config {seed}: {mc} B={B} T={T} strong={strong} state_in={state_in}")
+    w = dict(synth.make_token_sensitive_weights(mc, seed=seed))
+    w.update(synth.make_hist_weights(mc, seed=seed + 1, strong=strong))
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=seed)
+    m_in = (0.5 * np.random.default_rng(seed).standard_normal((B, mc.H, mc.d))).astype(np.float32) if state_in else None
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks, scan_state_in=None if m_in is None else m_in[..., None])
+    be.close()
+    ref = oracle_lib.Oracle(mc, w).forward_memory(toks, m_in=m_in, nthreads=16)
+    ctx = f"random memory config {seed}"
+    assert np.abs(got["iters"].astype(int) - ref["iters"].astype(int)).max() <= 1, ctx
+    for g, r in (("h_star", "h_star"), ("pooled", "pooled"), ("logits", "logits"), ("scan_y", "m_seq")):
+        np.testing.assert_allclose(got[g], ref[r], rtol=1e-4, atol=1e-3, err_msg=f"{ctx}: {g}")
+    np.testing.assert_allclose(got["scan_state"][..., 0], ref["m_seq"][:, -1], rtol=1e-4, atol=1e-3,
+                               err_msg=f"{ctx}: scan_state")
+    bad = np.argwhere(got["argmax"] != ref["argmax"])
+    for idx in bad:
+        lg = np.sort(ref["logits"][tuple(idx)])
+        assert lg[-1] - lg[-2] < 1e-5, f"{ctx}: argmax differs at {idx} without a near-tie"
