@@ -153,3 +153,45 @@ def test_random_memory_config_matches_oracle(oracle_lib, seed):
     for idx in bad:
         lg = np.sort(ref["logits"][tuple(idx)])
         assert lg[-1] - lg[-2] < 1e-5, f"{ctx}: argmax differs at {idx} without a near-tie"
+
+
+def draw_decode(seed):
+    """Greedy decode (Trainer::generate's loop, trainer.rs:4388-4406; the fixed-history form with
+    ADN_F_MEMORY, :4395-4400): width, slots, flags, GEMM arithmetic, batch, prompt, window,
+    generated count, Picard steps and repetition penalty."""
+    rng = np.random.default_rng(4000 + seed)
+    d = int(rng.choice([64, 128, 192, 256]))
+    H = int(rng.choice([1, 2, 3, 4, 8]))
+    V = int(rng.choice([300, 600]))
+    flags = 0
+    for f in (synth.F_SCORE_CLAMP4, synth.F_RMS_EXCL_ANCHOR, synth.F_INIT_SIGNAL_RMS, synth.F_WIN_TRANSPOSED):
+        if rng.random() < 0.3:
+            flags |= f
+    flags |= int(rng.choice([0, 0, synth.F_GEMM_BF16X3, synth.F_GEMM_FP32]))
+    memory = rng.random() < 0.3
+    if memory:
+        flags |= synth.F_MEMORY
+    iters = int(rng.choice([2, 5, 10]))
+    mc = synth.ModelConfig(d=d, H=H, V=V, N=1, r=32, flags=flags, eps=0.0, max_iters=iters,
+                           qk_bias=bool(rng.random() < 0.3))
+    B, T0 = int(rng.integers(1, 6)), int(rng.integers(1, 13))
+    n_new = int(rng.integers(3, 9))
+    ctx = int(rng.integers(1, T0 + n_new + 1))
+    pen = float(rng.choice([1.0, 1.3]))
+    return mc, B, T0, n_new, ctx, pen
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_decode_config_matches_oracle(oracle_lib, seed):
+    mc, B, T0, n_new, ctx, pen = draw_decode(seed)
+    log(f"random decode config {seed}: {mc} B={B} T0={T0} n_new={n_new} ctx={ctx} pen={pen}")
+    w = dict(synth.make_token_sensitive_weights(mc, seed=seed))
+    if mc.flags & synth.F_MEMORY:
+        w.update(synth.make_hist_weights(mc, seed=seed + 1, strong=True))
+    prompt = synth.make_tokens("uniform", B, T0, mc.V, seed=seed)
+    ref = oracle_lib.Oracle(mc, w).decode_greedy(prompt, n_new, ctx, pen)
+    be = GpuDeqBackend(mc, B, T0 if mc.flags & synth.F_MEMORY else 1)
+    be.upload_weights(w)
+    got = be.decode_greedy(prompt, n_new, ctx, max_iters=mc.max_iters, repetition_penalty=pen)
+    be.close()
+    assert np.array_equal(got, ref), f"decode config {seed}: {np.argwhere(got != ref)[:4].tolist()}"
