@@ -12,6 +12,8 @@ everywhere: the scan is a long recurrence that would otherwise compound h*'s own
 monotone, so an exit near eps can move by two iterations; every iteration then runs), as it is
 in the fixed-iteration cases.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -195,3 +197,41 @@ def test_random_decode_config_matches_oracle(oracle_lib, seed):
     got = be.decode_greedy(prompt, n_new, ctx, max_iters=mc.max_iters, repetition_penalty=pen)
     be.close()
     assert np.array_equal(got, ref), f"decode config {seed}: {np.argwhere(got != ref)[:4].tolist()}"
+
+
+def test_random_call_sequence_on_one_context(oracle_lib):
+    """One context serving a seeded random sequence of calls of different shapes and kinds
+    (token and row inputs, tolerance 0 or 1e-4, iteration caps, few-token and multi-sequence
+    batches, greedy decodes with and without a penalty): every result against the oracle, so
+    that no call depends on what an earlier one left in the context's buffers (active lists and
+    counts, range-guard bounds, the small iterate buffers, exit flags, arg-max partials of either
+    width, staging)."""
+    mc0 = synth.ModelConfig(d=128, H=4, V=700, N=4, r=32, flags=synth.F_SCAN_SELECTIVE | synth.F_SCORE_CLAMP4)
+    w = synth.make_token_sensitive_weights(mc0, seed=21)
+    be = GpuDeqBackend(mc0, 4, 300)
+    be.upload_weights(w)
+    rng = np.random.default_rng(21)
+    for call in range(16):
+        kind = rng.choice(["forward", "s_in", "decode"])
+        iters = int(rng.choice([2, 6, 20]))
+        eps = float(rng.choice([0.0, 1e-4])) if iters == 20 else 0.0
+        mc = dataclasses.replace(mc0, max_iters=iters, eps=eps)
+        if kind == "decode":
+            B, T0 = int(rng.integers(1, 5)), int(rng.integers(1, 10))
+            pen = float(rng.choice([1.0, 1.3]))
+            prompt = synth.make_tokens("uniform", B, T0, mc.V, seed=100 + call)
+            log(f"call {call}: decode B={B} T0={T0} iters={iters} pen={pen}")
+            got = be.decode_greedy(prompt, 5, 8, max_iters=iters, repetition_penalty=pen)
+            ref = oracle_lib.Oracle(dataclasses.replace(mc0, max_iters=iters, eps=0.0), w).decode_greedy(prompt, 5, 8, pen)
+            assert np.array_equal(got, ref), f"call {call}"
+            continue
+        B = int(rng.integers(1, 5))
+        T = int(rng.choice([1, 2, int(rng.integers(3, 300))]))
+        toks = synth.make_tokens("uniform", B, T, mc.V, seed=100 + call)
+        log(f"call {call}: {kind} B={B} T={T} iters={iters} eps={eps}")
+        if kind == "forward":
+            got = be.forward(toks, max_iters=iters, eps=eps, want=ALL)
+        else:
+            got = be.forward(s_in=np.ascontiguousarray(w["embed"][toks]), max_iters=iters, eps=eps, want=ALL)
+        check(oracle_lib, mc, w, toks, got, f"call {call}")
+    be.close()
