@@ -214,7 +214,7 @@ def test_random_call_sequence_on_one_context(oracle_lib):
     for call in range(16):
         kind = rng.choice(["forward", "s_in", "decode"])
         iters = int(rng.choice([2, 6, 20]))
-        eps = float(rng.choice([0.0, 1e-4])) if iters == 20 else 0.0
+        eps = 1e-4 if iters == 20 else 0.0
         mc = dataclasses.replace(mc0, max_iters=iters, eps=eps)
         if kind == "decode":
             B, T0 = int(rng.integers(1, 5)), int(rng.integers(1, 10))
