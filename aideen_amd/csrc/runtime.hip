@@ -1695,7 +1695,9 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
                     break;
                 case ADN_STAGE_CONVERGE: by = f * (n * (rec.k >= 0 ? H + 3 : 1) + 2); break;
                 case ADN_STAGE_ANDERSON: {
-                    const double nn = act(st, rec.k, rec.k + 1);
+                    // the tokens continuing past iteration k; at the last one the tokens that entered
+                    // it (those stopped at the cap are mixed; an upper bound)
+                    const double nn = rec.k + 1 < r->max_iters ? act(st, rec.k, rec.k + 1) : act(st, rec.k, rec.k);
                     const int k = rec.k, n_res = k < m - 1 ? k : m - 1;
                     const double nr = (k >= 2 && n_res >= 2) ? n_res : 0;
                     fl = nn * H * d * (nr * (nr + 1) + 2 * nr);
