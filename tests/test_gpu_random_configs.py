@@ -235,3 +235,35 @@ def test_random_call_sequence_on_one_context(oracle_lib):
             got = be.forward(s_in=np.ascontiguousarray(w["embed"][toks]), max_iters=iters, eps=eps, want=ALL)
         check(oracle_lib, mc, w, toks, got, f"call {call}")
     be.close()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_adjoint_config_matches_oracle(oracle_lib, seed):
+    """The clean adjoint Picard (staged_adjoint_picard_clean.wgsl:143-337) with its source gradient
+    at random widths (multiples of 64, powers of two or not), slot counts, token counts, step
+    counts and damping, without Anderson mixing (with it the coefficients of a nearly singular
+    Gram system are compared elsewhere); both sides read the GPU forward's h*.  Bar as in
+    test_gpu_adjoint: |got - ref| <= 1e-4 |ref| + 2e-5 max(1, max |ref|)."""
+    rng = np.random.default_rng(5000 + seed)
+    d = int(rng.choice([64, 128, 192, 320, 512, 768]))
+    H = int(rng.choice([1, 2, 3, 4, 8]))
+    mc = synth.ModelConfig(d=d, H=H, V=300, N=1, r=32)
+    w = dict(synth.make_weights(mc, seed=seed))
+    w["norm_scale"] = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    B, T = int(rng.integers(1, 4)), int(rng.choice([1, 3, int(rng.integers(10, 200))]))
+    iters = int(rng.integers(0, 13))
+    damping = float(rng.choice([0.3, 0.7, 1.0]))
+    toks = synth.make_tokens("uniform", B, T, mc.V, seed=seed)
+    dl = rng.standard_normal((B, T, d)).astype(np.float32)
+    log(f"random adjoint {seed}: d={d} H={H} B={B} T={T} iters={iters} damping={damping}")
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    h = be.forward(toks, want=("h_star",))["h_star"]
+    v, src = be.adjoint(dl, iters, damping=damping)
+    be.close()
+    o = oracle_lib.Oracle(mc, w)
+    sig = np.stack([o.signal(w["embed"][t]) for t in toks.reshape(-1)])
+    vr, sr = o.adjoint(sig, h.reshape(B * T, H, d), dl.reshape(B * T, d), iters, beta=damping)
+    for got, ref, what in ((v, vr.reshape(B, T, H, d), "v"), (src, sr.reshape(B, T, d), "source gradient")):
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=2e-5 * max(1.0, float(np.abs(ref).max())),
+                                   err_msg=f"random adjoint {seed}: {what}")
