@@ -403,8 +403,7 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     constexpr int HM = 16;         // slots at most
     constexpr int DM = 2048;       // row width at most
     constexpr int NT = 64 * KW;
-    __shared__ float sc_w[ATTN ? KW : 1][HM];                        // per wave: score shares
-    __shared__ float attn_w[ATTN ? HM : 1];                          // the softmax weights
+    __shared__ float sc_w[ATTN ? ATTN_FUSE_ROWS : 1][ATTN ? KW : 1][HM];  // per row and wave: score shares
     constexpr bool LA = ATTN || UPD;  // A rows formed in LDS
     __shared__ __attribute__((aligned(16))) float mix_l[LA ? ATTN_FUSE_ROWS : 1][LA ? DM : 1];
     __shared__ float hold_l[UPD ? ATTN_FUSE_ROWS : 1][UPD ? DM : 1];
@@ -427,24 +426,29 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
     const int q = lane & 31, g = lane >> 5;
     const int kw = p.K / KW;  // a multiple of 64 (checked by the launcher)
     if constexpr (ATTN) {
+        // Wave w takes the elements of its own K range [w kw, (w+1) kw) (lane l: kb + l + 64j), so
+        // that the mix it forms there is the A its k loop reads: only the score shares cross the
+        // waves (one barrier per row; each row has its own sc_w slice, so none is reused).  Every
+        // wave then forms the softmax itself, lane c holding slot c, with the sequential form's
+        // order (scores summed over the waves in order, max and sum over the slots in key order).
         const int H = p.S, dd = p.K;
         const long rs3 = 3L * dd;
         const float scale = 1.0f / sqrtf((float)dd);
+        const int kb = wave * kw;
+        const bool one = kw <= 128;  // the V elements loaded with Q and K, one round trip for the three
         for (int r = 0; r < M; ++r) {  // M <= ATTN_FUSE_ROWS
             const float *row = p.attn_qkv + (long)r * H * rs3;
             float part[HM];
 #pragma unroll
             for (int c = 0; c < HM; ++c) part[c] = 0.0f;
-            // up to d = 2 NT (512 at 4 waves) the V elements are loaded with Q and K, one round
-            // trip for the three; wider rows load V in the mix loop below
             float vpre[HM][2];
-            const bool one = dd <= 2 * NT;
-            for (int e0 = 0; e0 < dd; e0 += 2 * NT) {
+            for (int e0 = 0; e0 < kw; e0 += 128) {
                 float qv[2], kv[HM][2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int e = min(e0 + tid + j * NT, dd - 1);
-                    qv[j] = e0 + tid + j * NT < dd ? row[(long)s * rs3 + e] : 0.0f;
+                    const int el = e0 + lane + 64 * j;
+                    const int e = kb + min(el, kw - 1);
+                    qv[j] = el < kw ? row[(long)s * rs3 + e] : 0.0f;
 #pragma unroll
                     for (int c = 0; c < HM; ++c) kv[c][j] = row[(long)(c < H ? c : 0) * rs3 + dd + e];
                     if (one) {
@@ -467,36 +471,30 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
             }
             if (lane == 0) {
 #pragma unroll
-                for (int c = 0; c < HM; ++c) sc_w[wave][c] = part[c];
+                for (int c = 0; c < HM; ++c) sc_w[r][wave][c] = part[c];
             }
             __syncthreads();
-            if (tid == 0) {
-                float e[HM];
-                float mx = -INFINITY;
-                for (int c = 0; c < H; ++c) {
-                    float t = 0.0f;
-                    for (int w = 0; w < KW; ++w) t += sc_w[w][c];
-                    float sc = t * scale;
-                    if (p.attn_clamp) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
-                    e[c] = sc;
-                    mx = fmaxf(mx, sc);
-                }
-                float sum = 0.0f;
-                for (int c = 0; c < H; ++c) {
-                    e[c] = expf(e[c] - mx);
-                    sum += e[c];
-                }
-                for (int c = 0; c < H; ++c) attn_w[c] = e[c] / sum;
+            float sc = -INFINITY;
+            if (lane < H) {
+                float t = 0.0f;
+                for (int w = 0; w < KW; ++w) t += sc_w[r][w][lane];
+                sc = t * scale;
+                if (p.attn_clamp) sc = fminf(fmaxf(sc, -4.0f), 4.0f);
             }
-            __syncthreads();
+            float mx = -INFINITY;
+            for (int c = 0; c < H; ++c) mx = fmaxf(mx, __shfl(sc, c, 64));
+            const float ex = lane < H ? expf(sc - mx) : 0.0f;
+            float sum = 0.0f;
+            for (int c = 0; c < H; ++c) sum += __shfl(ex, c, 64);
+            const float wl = ex / sum;
             float wv[HM];
 #pragma unroll
-            for (int c = 0; c < HM; ++c) wv[c] = c < H ? attn_w[c] : 0.0f;
-            for (int e0 = 0; e0 < dd; e0 += 2 * NT) {
+            for (int c = 0; c < HM; ++c) wv[c] = c < H ? __shfl(wl, c, 64) : 0.0f;
+            for (int e0 = 0; e0 < kw; e0 += 128) {
                 float vv[HM][2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int e = min(e0 + tid + j * NT, dd - 1);
+                    const int e = kb + min(e0 + lane + 64 * j, kw - 1);
 #pragma unroll
                     for (int c = 0; c < HM; ++c)
                         vv[c][j] = one ? vpre[c][j] : row[(long)(c < H ? c : 0) * rs3 + 2 * dd + e];
@@ -507,11 +505,11 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
 #pragma unroll
                     for (int c = 0; c < HM; ++c)
                         if (c < H) acc = acc + vv[c][j] * wv[c];
-                    if (e0 + tid + j * NT < dd) mix_l[r][e0 + tid + j * NT] = acc;
+                    if (e0 + lane + 64 * j < kw) mix_l[r][kb + e0 + lane + 64 * j] = acc;
                 }
             }
-            __syncthreads();  // sc_w and attn_w are reused by the next row; mix_l complete
         }
+        // mix_l: each wave reads back only its own K range (a wave's LDS operations complete in order)
     }
     if constexpr (UPD) {
 #pragma clang fp contract(off)  // as in k_update_tok
