@@ -686,6 +686,180 @@ constexpr int AND_NT = 256;
 // at most this many tokens in flight: the few-token kernel shapes (more waves per token)
 constexpr int SMALL_ROWS = 512;
 
+// The Anderson mix as one multiply-add chain per element, acc = fma(c_n-1, x_n-1, ... fma(c_0, x_0, 0)):
+// the fused update recomputes the previous iteration's mix with it, so both must round alike.
+// Terms x[OFF + ri][e], ri < n <= NX - OFF.
+template <int OFF, int NX, int E>
+__device__ __forceinline__ float mix_chain(int n, const float *c, const float (&x)[NX][E], int e) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int ri = 0; ri + OFF < NX; ++ri)
+        if (ri < n) acc = fmaf(c[ri], x[OFF + ri][e], acc);
+    return acc;
+}
+
+// Damped update and Anderson mix in one pass, one block per active token and one wave per slot
+// (the update of FPMR:1386-1393, then the mixing of staged_adjoint_picard_clean.wgsl:1012-1134 in
+// the store-then-mix order of gpu_deq.rs:4278-4293), at iterations k >= 2 with NRES = min(k, m-1)
+// >= 2 residuals.  The iterate is formed as k_update_tok forms it (the same elements per lane,
+// wave sums and slot order) from the previous iterate, which is not read from h: a token active
+// at iteration k continued at k - 1, so its h is the mix formed then from ring slots X(k-1) ..
+// X(k-pn) that this kernel loads anyway (pn = the previous mix's term count, its coefficients
+// kept per token in mix_coef; pn = 0: no mix at k - 1, h = X(k-1)), and mix_chain recomputes it
+// bit for bit.  The iterate goes to ring slot k % m; h gets the mix, or the iterate for a token
+// that converged at this step (a token stopped at the cap unconverged is mixed).  The Gram sums:
+// per lane over its elements, the wave sums, then the waves in slot order.  Per token 2 + NRES
+// state vectors are read and 2 written, where the update and a mixing pass read 4 + NRES and
+// write 2.
+template <int E, bool PART, int NRES, bool HIST>
+__global__ __launch_bounds__(1024) void k_update_mix(Dims D, SolveBuffers b, int cur, int k, int m, int ntok, int pn,
+                                                     int max_iters, float eps, const float *anchor,
+                                                     const float *norm_scale, float beta) {
+#pragma clang fp contract(off)  // the update as in k_update; the mix by explicit multiply-adds
+    constexpr int NPK = NRES * (NRES + 1) / 2;
+    __shared__ float rs[16];
+    __shared__ float red[16][NPK];
+    __shared__ float cf_s[4];
+    __shared__ int mix_s;
+    const int i = blockIdx.x;
+    if (i >= b.cnt[cur]) return;
+    const int s = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int H = D.H;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
+    const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
+    const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
+    const int t = b.act[cur][i];
+    const long hd = (long)H * d, row = (long)s * d;
+    auto X = [&](int j) { return b.hist + ((long)(j % m) * ntok + t) * hd + row; };
+    const float *o = b.o + ((long)i * H + s) * d;
+    const float *sg = b.signal + (long)t * hd + row;
+    const float *an = anchor + row;
+    const float *hc = HIST ? b.mem_hist + ((long)(t / b.mem_T) * H + s) * d : nullptr;
+    // x[0]: this iteration's iterate, x[ri]: X(k - ri); every load before the first store
+    float x[NRES + 1][E], cval[E], gs[E];
+    float ss = 0.0f;
+#pragma unroll
+    for (int ri = 1; ri <= NRES; ++ri) {
+        const float *src = X(k + m - ri);
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[ri][e] = (!PART || e < er) ? src[lane + 64 * e] : 0.0f;
+    }
+    float cp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cp[q] = q < pn ? b.mix_coef[(long)t * 4 + q] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int idx = lane + 64 * e;
+        const bool on = !PART || e < er;  // zeros outside the row add nothing below
+        const float as_ =
+            on ? (__builtin_nontemporal_load(o + idx) + __builtin_nontemporal_load(sg + idx)) + (HIST ? hc[idx] : 0.0f)
+               : 0.0f;
+        const float c = as_ + (on ? an[idx] : 0.0f);
+        cval[e] = c;
+        gs[e] = on ? norm_scale[idx] : 0.0f;
+        ss += excl ? as_ * as_ : c * c;
+    }
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / (float)d + 1e-6f);
+    const float omb = 1.0f - beta;
+    float r = 0.0f;
+    float *slot = X(k);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        // the previous iterate: X(k-1), or the mix of X(k-1) .. X(k-pn) (x[1 ..] here, x[0 ..] then)
+        const float hold = pn ? mix_chain<1>(pn, cp, x, e) : x[1][e];
+        const float f = gs[e] * cval[e] / rms;
+        const float hn = f * beta + hold * omb;
+        x[0][e] = hn;
+        if (!PART || e < er) slot[lane + 64 * e] = hn;
+        const float df = hn - hold;
+        r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
+    }
+    r = rmode ? wave_sum(r) : wave_max(r);
+    // the Gram partials of the pseudo-residuals X(k-ri) - X(k-ri-1), the NPK wave sums interleaved
+    float gp[NPK];
+#pragma unroll
+    for (int q = 0; q < NPK; ++q) gp[q] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        float dl[NRES];
+#pragma unroll
+        for (int ri = 0; ri < NRES; ++ri) dl[ri] = x[ri][e] - x[ri + 1][e];
+        int p = 0;
+#pragma unroll
+        for (int ri = 0; ri < NRES; ++ri)
+#pragma unroll
+            for (int rj = ri; rj < NRES; ++rj) gp[p++] += dl[ri] * dl[rj];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        float ov[NPK];
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) ov[q] = __shfl_xor(gp[q], off, 64);
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) gp[q] += ov[q];
+    }
+    if (lane == 0) {
+        rs[s] = slot_resid(rmode, r, rms, d);
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) red[s][q] = gp[q];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float rtok = 0.0f;
+        for (int q = 0; q < H; ++q) rtok = combine_resid(rmode, rtok, rs[q]);
+        if (rmode == 1) rtok = nan_to_inf(sqrtf(rtok));
+        const int ex = token_exit(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, true);
+        if (ex) {
+            b.iters[t] = k + 1;
+            if (b.conv) b.conv[t] = ex == 1;
+        }
+        const bool mixit = !ex || (ex == 2 && b.cap_mix);
+        mix_s = mixit;
+        if (mixit) {
+            float g[16];
+            int q = 0;
+            for (int ri = 0; ri < NRES; ++ri)
+                for (int rj = ri; rj < NRES; ++rj) {
+                    float v = 0.0f;
+                    for (int w = 0; w < H; ++w) v += red[w][q];
+                    g[ri * NRES + rj] = v;
+                    g[rj * NRES + ri] = v;
+                    ++q;
+                }
+            float bt[4];
+            anderson_coeffs(NRES, g, bt);
+            for (int q2 = 0; q2 < NRES; ++q2) {
+                cf_s[q2] = bt[q2];
+                b.mix_coef[(long)t * 4 + q2] = bt[q2];
+            }
+            const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
+            b.act[cur ^ 1][pos] = t;
+        }
+    }
+    __syncthreads();
+    float *h = b.h + (long)t * hd + row;
+    if (mix_s) {
+        float bl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bl[q] = q < NRES ? cf_s[q] : 0.0f;
+        float hmax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float v = mix_chain<0>(NRES, bl, x, e);
+            if (!PART || e < er) {
+                h[lane + 64 * e] = v;
+                hmax = fmaxf(hmax, fabsf(v) < INFINITY ? fabsf(v) : 0.0f);
+            }
+        }
+        if (b.amax_h) track_absmax(b.amax_h, hmax);
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if (!PART || e < er) h[lane + 64 * e] = x[0][e];
+    }
+}
+
 // NRES = 0: store only; NRES in 2..4: store, Gram, solve, mix.
 template <int NRES>
 __global__ __launch_bounds__(AND_NT) void k_anderson(Dims D, SolveBuffers b, int nxt, int ntok, int k,
@@ -1073,6 +1247,36 @@ void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, in
         go(std::integral_constant<int, 8>{});
     else
         go(std::integral_constant<int, 16>{});
+}
+
+bool update_mix_ok(const Dims &D) { return D.H >= 1 && D.H <= 16 && D.d <= 512; }
+
+void launch_update_mix(const Dims &D, const SolveBuffers &b, int cur, int k, int m, int ntok, int rows,
+                       int max_iters, float eps, const float *anchor, const float *norm_scale, float beta,
+                       hipStream_t st) {
+    const int nres = k < m - 1 ? k : m - 1;                  // >= 2 (k >= 2, m >= 3)
+    const int pn = k - 1 >= 2 ? (k - 1 < m - 1 ? k - 1 : m - 1) : 0;  // terms of the mix at k - 1
+    const dim3 grid((unsigned)rows), blk(64 * D.H);
+    dispatch_width(D.d, [&](auto Ec, auto Pc) {
+        constexpr int E = decltype(Ec)::value;
+        constexpr bool P = decltype(Pc)::value;
+        if constexpr (E <= 8) {
+            auto go = [&](auto hist) {
+                constexpr bool HS = decltype(hist)::value;
+#define ADN_UM_ARGS D, b, cur, k, m, ntok, pn, max_iters, eps, anchor, norm_scale, beta
+                switch (nres) {
+                    case 2: hipLaunchKernelGGL((k_update_mix<E, P, 2, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                    case 3: hipLaunchKernelGGL((k_update_mix<E, P, 3, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                    default: hipLaunchKernelGGL((k_update_mix<E, P, 4, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                }
+#undef ADN_UM_ARGS
+            };
+            if (b.mem_hist)
+                go(std::true_type{});
+            else
+                go(std::false_type{});
+        }
+    });
 }
 
 }  // namespace adn

@@ -170,6 +170,8 @@ struct SolveBuffers {
     float *pool_out;
     float *pool_norm;
     const float *pool_g;
+    // [ntok][4] the coefficients of each token's last Anderson mix (launch_update_mix), or null
+    float *mix_coef;
 };
 
 // h0 per token and the first active list (all tokens, in order).
@@ -193,6 +195,15 @@ bool anderson_from_slot_ok(const Dims &D);
 // exist).  The ring slot is not written again.
 void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, int ntok, int rows, int k, int m,
                                hipStream_t st);
+// Whether launch_update_mix serves these rows (up to 16 slots of up to 512 floats).
+bool update_mix_ok(const Dims &D);
+// The update and the Anderson mix of iteration k >= 2 (m >= 3) in one launch over list cur: the
+// iterate into ring slot k % m, h = the mix (or the iterate of a token that converged at k), the
+// continuing tokens appended to list cur ^ 1.  Every iteration from 2 on must run here: the
+// previous iterate is recomputed from the ring and SolveBuffers::mix_coef, not read from h.
+void launch_update_mix(const Dims &D, const SolveBuffers &b, int cur, int k, int m, int ntok, int rows,
+                       int max_iters, float eps, const float *anchor, const float *norm_scale, float beta,
+                       hipStream_t st);
 
 // ---- LM head (head.hip) -----------------------------------------------------------------
 // pooled = mean_s h*, pnorm = (pooled/rms(pooled, 1e-5)) * g

@@ -221,6 +221,7 @@ struct Prof {
 constexpr int PROF_FUSED_ATTN = 1;    // the attention mix, inside the W_o product
 constexpr int PROF_FUSED_UPDATE = 2;  // the previous iteration's update, inside the Q|K|V product
 constexpr int PROF_FUSED_POOL = 4;    // the LM head's pool, inside the last update
+constexpr int PROF_FUSED_ANDERSON = 8;  // the Anderson mix, inside the update
 
 struct Span {
     Prof *p;
@@ -468,6 +469,16 @@ bool enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         const bool mix = m > 0;
         const bool from_slot = mix && anderson_from_slot_ok(D);
         const int cap_mix = mix && k + 1 == r.max_iters && k >= 2;
+        if (m >= 3 && k >= 2 && b.mix_coef && update_mix_ok(D)) {
+            // from the first mix on, the update and the mix in one pass (the previous iterate
+            // rebuilt from the ring, so h is not read)
+            SolveBuffers bu = b;
+            bu.cap_mix = cap_mix;
+            Span sp(prof, ADN_STAGE_UPDATE, k, st, -1, PROF_FUSED_ANDERSON);
+            launch_update_mix(D, bu, cur, k, m, ntok, rows, r.max_iters, r.eps, c->anchor, c->norm_scale, r.damping,
+                              st);
+            continue;
+        }
         if (!fixed || k + 1 == r.max_iters) {
             SolveBuffers bu = b;
             bu.cap_mix = cap_mix;
@@ -882,6 +893,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
         b.rprev = (cfg->flags & ADN_F_HOMEOSTATIC_EXIT) ? (float *)dmalloc(c, (size_t)T * sizeof(float)) : nullptr;
         b.cnt_hist = (int32_t *)dmalloc(c, ADN_PROFILE_MAX_ITERS * sizeof(int32_t));
         b.hist = cfg->anderson_m > 0 ? (float *)dmalloc(c, hd * cfg->anderson_m) : nullptr;
+        b.mix_coef = cfg->anderson_m >= 3 ? (float *)dmalloc(c, (size_t)T * 4 * sizeof(float)) : nullptr;
         c->d_err = (unsigned *)dmalloc(c, sizeof(unsigned));
         c->absmax = (unsigned *)dmalloc(c, sizeof(unsigned));
         c->fix_h = (float *)dmalloc(c, 2 * (size_t)std::min<long>(T, ATTN_FUSE_ROWS) * H * d * sizeof(float));
@@ -1691,6 +1703,11 @@ int adn_profile_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o, adn_
                     if (rec.fused & PROF_FUSED_POOL) {  // the pooled and normalised rows written
                         fl += n * H * d;
                         by += f * 2 * n * d;
+                    }
+                    if (rec.fused & PROF_FUSED_ANDERSON) {  // reads n_res ring slots instead of h, writes the slot too
+                        const int k = rec.k, nr = k < m - 1 ? k : m - 1;
+                        fl += n * H * d * (nr * (nr + 1) + 2 * nr);
+                        by += f * (n * H * d * nr + 4 * n);
                     }
                     break;
                 case ADN_STAGE_CONVERGE: by = f * (n * (rec.k >= 0 ? H + 3 : 1) + 2); break;

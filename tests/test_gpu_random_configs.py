@@ -10,7 +10,10 @@ hand-written case lists.  Every output of every token is compared with the oracl
 token-sensitive weights (the carrier's outputs against the oracle's scan of the GPU's own h*, as
 everywhere: the scan is a long recurrence that would otherwise compound h*'s own tolerance).  With Anderson mixing the tolerance is 0 (the residual is not
 monotone, so an exit near eps can move by two iterations; every iteration then runs), as it is
-in the fixed-iteration cases.
+in the fixed-iteration cases.  Under that mixing a token whose oracle result itself moves by a
+twentieth of the bar when a few values of each input row change by one ulp is ill-conditioned
+(the last steps' Gram matrices are nearly singular): such tokens, at most 10%, are held to 50
+times that response instead.
 """
 import dataclasses
 
@@ -26,10 +29,55 @@ pytestmark = pytest.mark.gpu
 ALL = ("h_star", "pooled", "logits", "argmax", "iters", "converged", "scan_y", "scan_state")
 
 
+COND_KEYS = ("h_star", "pooled", "logits")
+
+
+def ulp_response(oracle_lib, mc, w, toks, ref):
+    """Per token and output, how far the oracle's own result moves when a few values of every
+    embedding row move by one ulp, the largest over four such changes ([B, T] arrays): with
+    Anderson mixing at tolerance 0 the last steps' Gram matrices are nearly singular and some
+    tokens' coefficients are set by rounding, so two correct fp32 forwards that round differently
+    can disagree beyond the bar.  The response depends on the direction of the change, hence
+    several."""
+    d = mc.d
+    probes = ((slice(0, 8), np.inf), (slice(d - 8, d), -np.inf), (slice(d // 2, d // 2 + 8), np.inf),
+              (slice(0, d, 16), -np.inf))
+    B, T = toks.shape
+    resp = {k: np.zeros((B, T)) for k in COND_KEYS}
+    for cols, to in probes:
+        w2 = dict(w)
+        e = np.array(w["embed"], dtype=np.float32, copy=True)
+        e[:, cols] = np.nextafter(e[:, cols], np.float32(to))
+        w2["embed"] = e
+        ref2 = oracle_lib.Oracle(mc, w2).forward(toks, want_scan=False, nthreads=16)
+        for k in COND_KEYS:
+            resp[k] = np.maximum(resp[k], np.abs(ref[k] - ref2[k]).reshape(B, T, -1).max(axis=2))
+    return resp
+
+
 def check(oracle_lib, mc, w, toks, got, ctx):
     o = oracle_lib.Oracle(mc, w)
     ref = o.forward(toks, want_scan=False, nthreads=16)
-    assert_forward_parity({k: v for k, v in got.items() if not k.startswith("scan")}, ref, ctx)
+    fwd = {k: v for k, v in got.items() if not k.startswith("scan")}
+    ill = np.zeros(toks.shape, dtype=bool)
+    if mc.anderson_m >= 3:
+        resp = ulp_response(oracle_lib, mc, w, toks, ref)
+        for k in COND_KEYS:
+            ill |= resp[k] > 0.05 * 1e-3
+    if ill.any():
+        # tokens whose oracle result moves by a twentieth of the bar under a one-ulp input change:
+        # at most 10% of them, each within 50 times that response; every other token at the bar
+        log(f"{ctx}: {int(ill.sum())} of {ill.size} tokens ill-conditioned under the Anderson mix "
+            f"(oracle h* moves by up to {resp['h_star'].max():.2e} under one ulp)")
+        assert ill.mean() <= 0.10, f"{ctx}: {ill.mean():.3f} of the tokens ill-conditioned"
+        for k in COND_KEYS:
+            B, T = toks.shape
+            dif = np.abs(got[k] - ref[k]).reshape(B, T, -1).max(axis=2)[ill]
+            lim = 1e-3 + 1e-4 * np.abs(ref[k]).reshape(B, T, -1).max(axis=2)[ill] + 50 * resp[k][ill]
+            assert (dif <= lim).all(), f"{ctx}: {k} beyond 50x the oracle's one-ulp response"
+        assert_forward_parity({k: v[~ill] for k, v in fwd.items()}, {k: v[~ill] for k, v in ref.items()}, ctx)
+    else:
+        assert_forward_parity(fwd, ref, ctx)
     for b in range(toks.shape[0]):
         y, st = o.scan(got["h_star"][b])
         np.testing.assert_allclose(got["scan_y"][b], y, rtol=1e-4, atol=1e-3, err_msg=f"{ctx}: scan_y[{b}]")
