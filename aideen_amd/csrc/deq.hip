@@ -698,6 +698,46 @@ __device__ __forceinline__ float mix_chain(int n, const float *c, const float (&
     return acc;
 }
 
+// Thread 0 of a fused update-and-mix block: the token residual from the slot residuals rs (combined
+// in slot order), the exit test, and for a token that is mixed (continuing, or stopped at the cap
+// unconverged) the Gram matrix from the waves' partials red (summed in wave order), the
+// coefficients into cf and mix_coef, and the token's place in the next list.  Returns whether the
+// token is mixed.
+template <int NRES>
+__device__ bool update_mix_decide(const SolveBuffers &b, int cur, int k, int max_iters, float eps, int t, int H,
+                                  int rmode, const float *rs, const float (*red)[NRES * (NRES + 1) / 2], float *cf) {
+    float rtok = 0.0f;
+    for (int q = 0; q < H; ++q) rtok = combine_resid(rmode, rtok, rs[q]);
+    if (rmode == 1) rtok = nan_to_inf(sqrtf(rtok));
+    const int ex = token_exit(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, true);
+    if (ex) {
+        b.iters[t] = k + 1;
+        if (b.conv) b.conv[t] = ex == 1;
+    }
+    const bool mixit = !ex || (ex == 2 && b.cap_mix);
+    if (mixit) {
+        float g[16];
+        int q = 0;
+        for (int ri = 0; ri < NRES; ++ri)
+            for (int rj = ri; rj < NRES; ++rj) {
+                float v = 0.0f;
+                for (int w = 0; w < H; ++w) v += red[w][q];
+                g[ri * NRES + rj] = v;
+                g[rj * NRES + ri] = v;
+                ++q;
+            }
+        float bt[4];
+        anderson_coeffs(NRES, g, bt);
+        for (int q2 = 0; q2 < NRES; ++q2) {
+            cf[q2] = bt[q2];
+            b.mix_coef[(long)t * 4 + q2] = bt[q2];
+        }
+        const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
+        b.act[cur ^ 1][pos] = t;
+    }
+    return mixit;
+}
+
 // Damped update and Anderson mix in one pass, one block per active token and one wave per slot
 // (the update of FPMR:1386-1393, then the mixing of staged_adjoint_picard_clean.wgsl:1012-1134 in
 // the store-then-mix order of gpu_deq.rs:4278-4293), at iterations k >= 2 with NRES = min(k, m-1)
@@ -805,38 +845,7 @@ __global__ __launch_bounds__(1024) void k_update_mix(Dims D, SolveBuffers b, int
         for (int q = 0; q < NPK; ++q) red[s][q] = gp[q];
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float rtok = 0.0f;
-        for (int q = 0; q < H; ++q) rtok = combine_resid(rmode, rtok, rs[q]);
-        if (rmode == 1) rtok = nan_to_inf(sqrtf(rtok));
-        const int ex = token_exit(rtok, eps, k, max_iters, b.rprev ? b.rprev + t : nullptr, true);
-        if (ex) {
-            b.iters[t] = k + 1;
-            if (b.conv) b.conv[t] = ex == 1;
-        }
-        const bool mixit = !ex || (ex == 2 && b.cap_mix);
-        mix_s = mixit;
-        if (mixit) {
-            float g[16];
-            int q = 0;
-            for (int ri = 0; ri < NRES; ++ri)
-                for (int rj = ri; rj < NRES; ++rj) {
-                    float v = 0.0f;
-                    for (int w = 0; w < H; ++w) v += red[w][q];
-                    g[ri * NRES + rj] = v;
-                    g[rj * NRES + ri] = v;
-                    ++q;
-                }
-            float bt[4];
-            anderson_coeffs(NRES, g, bt);
-            for (int q2 = 0; q2 < NRES; ++q2) {
-                cf_s[q2] = bt[q2];
-                b.mix_coef[(long)t * 4 + q2] = bt[q2];
-            }
-            const int pos = atomicAdd(&b.cnt[cur ^ 1], 1);
-            b.act[cur ^ 1][pos] = t;
-        }
-    }
+    if (threadIdx.x == 0) mix_s = update_mix_decide<NRES>(b, cur, k, max_iters, eps, t, H, rmode, rs, red, cf_s);
     __syncthreads();
     float *h = b.h + (long)t * hd + row;
     if (mix_s) {
@@ -857,6 +866,211 @@ __global__ __launch_bounds__(1024) void k_update_mix(Dims D, SolveBuffers b, int
 #pragma unroll
         for (int e = 0; e < E; ++e)
             if (!PART || e < er) h[lane + 64 * e] = x[0][e];
+    }
+}
+
+// k_update_mix for rows of 1024 or 2048 floats (E = 16, 32), whose ring values do not fit in
+// registers: a lane walks its elements in groups of SUB, two groups per pass of a loop that is not
+// unrolled (unrolled, the per-element addresses alone overflow the registers), each group's ring
+// values and norm scale loaded into a register set before the previous group's iterate is stored;
+// the row's c values and then its iterate are kept in LDS (H * d floats, dynamic).  After the
+// coefficient solve the mix reads X(k-1) .. X(k-NRES+1) again (mostly from the caches: the block
+// read them a moment before).  Same arithmetic per element as k_update_mix (a lane's Gram partials
+// in element order).  Per token 2 + NRES vectors read and 2 written, plus the NRES - 1 re-read;
+// the update and the two-pass mixing read 4 + 2 NRES + 1 and write 3.
+template <int E, bool PART, int NRES, bool HIST>
+__global__ __launch_bounds__(1024) void k_update_mix_wide(Dims D, SolveBuffers b, int cur, int k, int m, int ntok,
+                                                          int pn, int max_iters, float eps, const float *anchor,
+                                                          const float *norm_scale, float beta) {
+#pragma clang fp contract(off)  // as in k_update_mix
+    constexpr int SUB = 4, NG = E / SUB;
+    static_assert(NG % 2 == 0, "pairs of element groups");
+    constexpr int NPK = NRES * (NRES + 1) / 2;
+    __shared__ float rs[16];
+    __shared__ float red[16][NPK];
+    __shared__ float cf_s[4];
+    __shared__ int mix_s;
+    extern __shared__ float cl[];  // [H][E][64]: a lane's c values, then its iterate
+    const int i = blockIdx.x;
+    if (i >= b.cnt[cur]) return;
+    const int s = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int H = D.H;
+    const int d = PART ? D.d : 64 * E, er = PART ? D.d / 64 : E;  // chunks e >= er are outside the row
+    const bool excl = (D.flags & ADN_F_RMS_EXCL_ANCHOR) != 0;
+    const int rmode = (D.flags & ADN_F_RESID_L2) ? 1 : (D.flags & ADN_F_RESID_RELRMS) ? 2 : 0;
+    const int t = b.act[cur][i];
+    const long hd = (long)H * d, row = (long)s * d;
+    auto X = [&](int j) { return b.hist + ((long)(j % m) * ntok + t) * hd + row; };
+    const float *o = b.o + ((long)i * H + s) * d;
+    const float *sg = b.signal + (long)t * hd + row;
+    const float *an = anchor + row;
+    const float *hc = HIST ? b.mem_hist + ((long)(t / b.mem_T) * H + s) * d : nullptr;
+    const float *xr[NRES + 1];  // xr[ri] = X(k - ri), ri >= 1
+#pragma unroll
+    for (int ri = 1; ri <= NRES; ++ri) xr[ri] = X(k + m - ri);
+    float *slot = X(k);
+    float *h = b.h + (long)t * hd + row;
+    float cp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cp[q] = q < pn ? b.mix_coef[(long)t * 4 + q] : 0.0f;
+    float *cv = cl + (long)s * E * 64 + lane;  // element e of this lane at cv[64 e]
+    // element ee of a lane is lane + 64 ee; groups past the row (PART) load zeros and store nothing
+    auto on = [&](int ee) { return !PART || ee < er; };
+
+    // c = o + signal (+ history) + anchor into LDS, and the sum of squares
+    float ss = 0.0f;
+    struct In {
+        float o[SUB], sg[SUB], an[SUB], hc[HIST ? SUB : 1];
+    };
+    auto load_in = [&](int j, In &q) {
+#pragma unroll
+        for (int e = 0; e < SUB; ++e) {
+            const int ee = j * SUB + e, idx = lane + 64 * ee;
+            q.o[e] = on(ee) ? __builtin_nontemporal_load(o + idx) : 0.0f;
+            q.sg[e] = on(ee) ? __builtin_nontemporal_load(sg + idx) : 0.0f;
+            q.an[e] = on(ee) ? an[idx] : 0.0f;
+            if constexpr (HIST) q.hc[e] = on(ee) ? hc[idx] : 0.0f;
+        }
+    };
+    auto sum_in = [&](int j, const In &q) {
+#pragma unroll
+        for (int e = 0; e < SUB; ++e) {
+            const float as_ = (q.o[e] + q.sg[e]) + (HIST ? q.hc[e] : 0.0f);
+            const float c = as_ + q.an[e];
+            cv[64 * (j * SUB + e)] = c;
+            ss += excl ? as_ * as_ : c * c;
+        }
+    };
+    {
+        In in0, in1;
+        load_in(0, in0);
+#pragma unroll 1
+        for (int j = 0; j < NG; j += 2) {
+            load_in(j + 1, in1);
+            sum_in(j, in0);
+            load_in(j + 2 < NG ? j + 2 : NG - 1, in0);  // clamped: the last pass loads a group again
+            sum_in(j + 1, in1);
+        }
+    }
+    ss = wave_sum(ss);
+    const float rms = sqrtf(ss / (float)d + 1e-6f);
+    const float omb = 1.0f - beta;
+
+    // the iterate into the ring slot and LDS, the residual and the Gram partials
+    struct Grp {
+        float x[NRES + 1][SUB];  // x[ri]: X(k - ri) for ri >= 1 (x[0] unused)
+        float g[SUB];
+    };
+    auto load_grp = [&](int j, Grp &q) {
+#pragma unroll
+        for (int ri = 1; ri <= NRES; ++ri)
+#pragma unroll
+            for (int e = 0; e < SUB; ++e) {
+                const int ee = j * SUB + e;
+                q.x[ri][e] = on(ee) ? xr[ri][lane + 64 * ee] : 0.0f;
+            }
+#pragma unroll
+        for (int e = 0; e < SUB; ++e) {
+            const int ee = j * SUB + e;
+            q.g[e] = on(ee) ? norm_scale[lane + 64 * ee] : 0.0f;
+        }
+    };
+    float r = 0.0f;
+    float gp[NPK];
+#pragma unroll
+    for (int q = 0; q < NPK; ++q) gp[q] = 0.0f;
+    auto upd = [&](int j, const Grp &q) {
+#pragma unroll
+        for (int e = 0; e < SUB; ++e) {
+            const int ee = j * SUB + e;
+            const float hold = pn ? mix_chain<1>(pn, cp, q.x, e) : q.x[1][e];
+            const float f = q.g[e] * cv[64 * ee] / rms;
+            const float hn = f * beta + hold * omb;
+            cv[64 * ee] = hn;
+            if (on(ee)) slot[lane + 64 * ee] = hn;
+            const float df = hn - hold;
+            r = rmode ? r + df * df : fmaxf(r, nan_to_inf(fabsf(df)));
+            float dl[NRES];
+            dl[0] = hn - q.x[1][e];
+#pragma unroll
+            for (int ri = 1; ri < NRES; ++ri) dl[ri] = q.x[ri][e] - q.x[ri + 1][e];
+            int p = 0;
+#pragma unroll
+            for (int ri = 0; ri < NRES; ++ri)
+#pragma unroll
+                for (int rj = ri; rj < NRES; ++rj) gp[p++] += dl[ri] * dl[rj];
+        }
+    };
+    {
+        Grp g0, g1;
+        load_grp(0, g0);
+#pragma unroll 1
+        for (int j = 0; j < NG; j += 2) {
+            load_grp(j + 1, g1);
+            upd(j, g0);
+            load_grp(j + 2 < NG ? j + 2 : NG - 1, g0);
+            upd(j + 1, g1);
+        }
+    }
+    r = rmode ? wave_sum(r) : wave_max(r);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        float ov[NPK];
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) ov[q] = __shfl_xor(gp[q], off, 64);
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) gp[q] += ov[q];
+    }
+    if (lane == 0) {
+        rs[s] = slot_resid(rmode, r, rms, d);
+#pragma unroll
+        for (int q = 0; q < NPK; ++q) red[s][q] = gp[q];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) mix_s = update_mix_decide<NRES>(b, cur, k, max_iters, eps, t, H, rmode, rs, red, cf_s);
+    __syncthreads();
+    if (mix_s) {
+        float bl[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bl[q] = q < NRES ? cf_s[q] : 0.0f;
+        float hmax = 0.0f;
+        // the mix's terms: the iterate from LDS and X(k-1) .. X(k-NRES+1) read again
+        auto load_mix = [&](int j, float (&xq)[NRES][SUB]) {
+#pragma unroll
+            for (int ri = 1; ri < NRES; ++ri)
+#pragma unroll
+                for (int e = 0; e < SUB; ++e) {
+                    const int ee = j * SUB + e;
+                    xq[ri][e] = on(ee) ? xr[ri][lane + 64 * ee] : 0.0f;
+                }
+        };
+        auto mix = [&](int j, float (&xq)[NRES][SUB]) {
+#pragma unroll
+            for (int e = 0; e < SUB; ++e) xq[0][e] = cv[64 * (j * SUB + e)];
+#pragma unroll
+            for (int e = 0; e < SUB; ++e) {
+                const int ee = j * SUB + e;
+                const float v = mix_chain<0>(NRES, bl, xq, e);
+                if (on(ee)) {
+                    h[lane + 64 * ee] = v;
+                    hmax = fmaxf(hmax, fabsf(v) < INFINITY ? fabsf(v) : 0.0f);
+                }
+            }
+        };
+        float x0[NRES][SUB], x1[NRES][SUB];
+        load_mix(0, x0);
+#pragma unroll 1
+        for (int j = 0; j < NG; j += 2) {
+            load_mix(j + 1, x1);
+            mix(j, x0);
+            load_mix(j + 2 < NG ? j + 2 : NG - 1, x0);
+            mix(j + 1, x1);
+        }
+        if (b.amax_h) track_absmax(b.amax_h, hmax);
+    } else {
+#pragma unroll 1
+        for (int e = 0; e < E; ++e)
+            if (on(e)) h[lane + 64 * e] = cv[64 * e];
     }
 }
 
@@ -1249,7 +1463,17 @@ void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, in
         go(std::integral_constant<int, 16>{});
 }
 
-bool update_mix_ok(const Dims &D) { return D.H >= 1 && D.H <= 16 && D.d <= 512; }
+bool update_mix_ok(const Dims &D) {
+    if (D.H < 1 || D.H > 16 || D.d > 2048) return false;
+    if (D.d <= 512) return true;
+    // rows above 512 floats keep a token's rows in LDS (a padded 64 * E floats per row)
+    int dev = 0, max_lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return false;
+    const long e = D.d <= 1024 ? 16 : 32;
+    return (long)D.H * e * 64 * (long)sizeof(float) + 1024 <= max_lds;
+}
 
 void launch_update_mix(const Dims &D, const SolveBuffers &b, int cur, int k, int m, int ntok, int rows,
                        int max_iters, float eps, const float *anchor, const float *norm_scale, float beta,
@@ -1260,14 +1484,23 @@ void launch_update_mix(const Dims &D, const SolveBuffers &b, int cur, int k, int
     dispatch_width(D.d, [&](auto Ec, auto Pc) {
         constexpr int E = decltype(Ec)::value;
         constexpr bool P = decltype(Pc)::value;
-        if constexpr (E <= 8) {
+        if constexpr (E <= 32) {
             auto go = [&](auto hist) {
                 constexpr bool HS = decltype(hist)::value;
 #define ADN_UM_ARGS D, b, cur, k, m, ntok, pn, max_iters, eps, anchor, norm_scale, beta
-                switch (nres) {
-                    case 2: hipLaunchKernelGGL((k_update_mix<E, P, 2, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
-                    case 3: hipLaunchKernelGGL((k_update_mix<E, P, 3, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
-                    default: hipLaunchKernelGGL((k_update_mix<E, P, 4, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                if constexpr (E <= 8) {
+                    switch (nres) {
+                        case 2: hipLaunchKernelGGL((k_update_mix<E, P, 2, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                        case 3: hipLaunchKernelGGL((k_update_mix<E, P, 3, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                        default: hipLaunchKernelGGL((k_update_mix<E, P, 4, HS>), grid, blk, 0, st, ADN_UM_ARGS); break;
+                    }
+                } else {
+                    const size_t lds = (size_t)D.H * E * 64 * sizeof(float);
+                    switch (nres) {
+                        case 2: hipLaunchKernelGGL((k_update_mix_wide<E, P, 2, HS>), grid, blk, lds, st, ADN_UM_ARGS); break;
+                        case 3: hipLaunchKernelGGL((k_update_mix_wide<E, P, 3, HS>), grid, blk, lds, st, ADN_UM_ARGS); break;
+                        default: hipLaunchKernelGGL((k_update_mix_wide<E, P, 4, HS>), grid, blk, lds, st, ADN_UM_ARGS); break;
+                    }
                 }
 #undef ADN_UM_ARGS
             };

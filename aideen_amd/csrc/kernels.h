@@ -195,7 +195,9 @@ bool anderson_from_slot_ok(const Dims &D);
 // exist).  The ring slot is not written again.
 void launch_anderson_from_slot(const Dims &D, const SolveBuffers &b, int cur, int ntok, int rows, int k, int m,
                                hipStream_t st);
-// Whether launch_update_mix serves these rows (up to 16 slots of up to 512 floats).
+// Whether launch_update_mix serves these rows (up to 16 slots of up to 2048 floats; above 512, a
+// token's rows must fit in the device's LDS per workgroup).  Otherwise the update runs with a
+// separate mixing pass.
 bool update_mix_ok(const Dims &D);
 // The update and the Anderson mix of iteration k >= 2 (m >= 3) in one launch over list cur: the
 // iterate into ring slot k % m, h = the mix (or the iterate of a token that converged at k), the

@@ -953,13 +953,16 @@ def test_noncontractive_weights_report_nonconvergence(oracle_lib):
     assert float((got["h_star"].astype(np.float64) ** 2).sum(axis=(2, 3)).max()) < 1e6
 
 
-@pytest.mark.parametrize("d,H,m", [(256, 8, 3), (256, 8, 4), (256, 8, 5), (192, 4, 4), (64, 16, 3)])
+@pytest.mark.parametrize("d,H,m", [(256, 8, 3), (256, 8, 4), (256, 8, 5), (192, 4, 4), (64, 16, 3), (1024, 4, 3),
+                                   (1536, 2, 3), (2048, 2, 4)])
 def test_anderson_fused_update_every_depth(oracle_lib, d, H, m):
     """The update with the Anderson mix fused: from the first mix on it rebuilds each token's
     previous iterate from the ring and the previous mix's coefficients instead of reading h, so
     every transition of the term count (k = 2: two residuals after no mix; then 3 after 2, 4 after
     3, and the steady depth) must reproduce the oracle's iterates; at tolerance 0 every token runs
-    all nine updates.  Depths 3-5, a width that is not a power of two and 16 slots of 64 (at depth
+    all nine updates.  Depths 3-5, widths that are not a power of two (192, and 1536 on the kernel
+    for rows above 512 floats, which walks a lane's elements in groups and keeps the rows in LDS),
+    rows of 1024 and 2048, and 16 slots of 64 (at depth
     5 that shape's h* moves by 3e-4 when 8 input values of a row change by one ulp, in the oracle
     alone, and the unfused kernels miss the bar there too: the case is kept at depth 3)."""
     mc = synth.ModelConfig(d=d, H=H, V=400, N=4, r=32, anderson_m=m, eps=0.0, max_iters=9)
@@ -980,9 +983,8 @@ def test_anderson_tokens_stopped_at_the_cap_end_mixed(oracle_lib):
     tolerance, the last allowed one included: a token stopped at the cap unconverged ends with the
     mix, one that converges at the last step with its iterate (fixed_point_memory_reasoning.rs
     loop; staged_adjoint_picard_clean.wgsl's mix after every step).  The update with the mix
-    fused (rows up to 512 floats, few and many tokens, 16 slots), the update followed by the
-    one-pass mixing from the ring slot (H*d <= 4096) and by the two-pass mixing of a wider state,
-    at tolerance 0 (every token stops at the cap); then a cap at which
+    fused, on rows up to 512 floats (few and many tokens, 16 slots) and on wider rows (1024
+    floats, 4 and 8 slots), at tolerance 0 (every token stops at the cap); then a cap at which
     tokens exit before it, at it converged, and at it unconverged, compared on the tokens whose
     residuals stay 20% or more away from eps at every step (an exit decided by rounding can move
     by two with Anderson mixing)."""
