@@ -310,10 +310,18 @@ __device__ __forceinline__ void epilogue_t(const GemmParams &p, floatx16 (&acc)[
     const EpiCtx c{M, s, m0, n0, wave / WGN, wave % WGN, lane & 31, lane >> 5, osc, scratch_v, scratch_i};
     const bool interior = m0 + BMt <= M && n0 + BNt <= p.N;
     if constexpr (ROLE == ROLE_READOUT) {
-        if (interior)
-            epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, false>(p, acc, c);
-        else
-            epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, true>(p, acc, c);
+        // y + W y: the residual added here, or already in the weights (I + W, EPI_NONE)
+        if (p.epi == EPI_ADD_A) {
+            if (interior)
+                epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, false>(p, acc, c);
+            else
+                epi_tile<WTM, WTN, WGM, WGN, EPI_ADD_A, false, true>(p, acc, c);
+        } else {
+            if (interior)
+                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, false>(p, acc, c);
+            else
+                epi_tile<WTM, WTN, WGM, WGN, EPI_NONE, false, true>(p, acc, c);
+        }
     } else if constexpr (ROLE == ROLE_LMHEAD) {
         // the arg-max branch and the bias branch are uniform over the grid; the logits (nothing in
         // the forward reads them back) are stored non-temporally, which keeps the A rows and weights

@@ -659,15 +659,16 @@ __global__ __launch_bounds__(64 * KW) void k_gemm_skinny(GemmParams p) {
 // the blocked layout: per slot, rows in groups of 32 (N padded to a multiple of 32 with zeros),
 // each group's K in blocks of 16, a block (32 rows x 16 halves, 1 KB) contiguous and row-major:
 //   (s, n, k) -> s * split_slot_stride + ((n / 32) * (K / 16) + k / 16) * 512 + (n % 32) * 16 + k % 16
-// so that a GEMM's 32-row x 16-K load is one contiguous kilobyte.
+// so that a GEMM's 32-row x 16-K load is one contiguous kilobyte.  eye: split w + I instead (square
+// matrices), so that a product with a residual, y + W y, runs as the plain product (I + W) y.
 template <typename T>
-__global__ void k_split(const float *w, int S, int N, int K, float scale, T *hi, T *lo) {
+__global__ void k_split(const float *w, int S, int N, int K, float scale, T *hi, T *lo, bool eye) {
     const long np = ((long)N + 31) / 32 * 32, total = (long)S * np * K, kb = K / 16;
     for (long o = (long)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (long)gridDim.x * blockDim.x) {
         const long sl = o / (np * K), ro = o - sl * np * K;
         const long blk = ro >> 9, in = ro & 511;
         const long n = (blk / kb) * 32 + (in >> 4), k = (blk % kb) * 16 + (in & 15);
-        const float x = n < N ? w[(sl * N + n) * K + k] * scale : 0.0f;
+        const float x = n < N ? (w[(sl * N + n) * K + k] + (eye && n == k ? 1.0f : 0.0f)) * scale : 0.0f;
         const T h = (T)x;
         hi[o] = h;
         if (lo) lo[o] = (T)(x - (float)h);
@@ -825,15 +826,15 @@ bool gemm_attn_fusable(int prec, int M, int K, int S) {
 long split_weight_elems(int S, int N, int K) { return (long)S * ((N + 31) / 32 * 32) * K; }
 
 void launch_split_weights(const float *w, int S, int N, int K, float scale, int prec, void *hi, void *lo,
-                          hipStream_t st) {
+                          hipStream_t st, bool eye) {
     const long n = split_weight_elems(S, N, K);
     const long blocks = std::min<long>((n + 255) / 256, 8192);
     if (prec == PREC_F16X3)
         hipLaunchKernelGGL(k_split<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st, w, S, N, K, scale,
-                           (_Float16 *)hi, (_Float16 *)lo);
+                           (_Float16 *)hi, (_Float16 *)lo, eye);
     else
         hipLaunchKernelGGL(k_split<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st, w, S, N, K, scale,
-                           (__bf16 *)hi, (__bf16 *)lo);
+                           (__bf16 *)hi, (__bf16 *)lo, eye);
 }
 
 }  // namespace adn

@@ -118,10 +118,10 @@ int gemm_lm_partial_cols(int prec, int M, int K);
 // hi = T(w * scale), lo = T(w * scale - hi) with T = fp16 (PREC_F16X3) or bf16, from [S][N][K]
 // fp32 weights into the split GEMM's blocked layout (split_weight_elems halves each, N padded to
 // a multiple of 32); lo may be null.  The GEMMs' b_ss is then 0 (one matrix for every slot) or
-// non-zero (a matrix per slot, N x K).
+// non-zero (a matrix per slot, N x K).  eye: split w + I (square matrices).
 long split_weight_elems(int S, int N, int K);
 void launch_split_weights(const float *w, int S, int N, int K, float scale, int prec, void *hi, void *lo,
-                          hipStream_t st);
+                          hipStream_t st, bool eye = false);
 
 // ---- DEQ solve kernels (deq.hip) ------------------------------------------------------
 struct SolveBuffers {

@@ -257,15 +257,24 @@ float split_scale(int prec, float maxabs, int headroom_log2 = 14) {
 }
 
 // split copies of S matrices [N][K] (the GEMMs' B operand) in the blocked layout
-void make_split(adn_ctx *c, adn_ctx::Split &sp, const float *dev_w, int S, int N, int K, float maxabs) {
+// (eye: of w + I, square matrices; maxabs bounds |w|)
+void make_split(adn_ctx *c, adn_ctx::Split &sp, const float *dev_w, int S, int N, int K, float maxabs,
+                bool eye = false) {
     if (c->prec == PREC_FP32) return;
     const size_t bytes = (size_t)split_weight_elems(S, N, K) * 2;
     if (!sp.hi) sp.hi = dmalloc(c, bytes);
     if (c->prec != PREC_BF16X1 && !sp.lo) sp.lo = dmalloc(c, bytes);
-    sp.scale = split_scale(c->prec, maxabs);
+    sp.scale = split_scale(c->prec, eye ? maxabs + 1.0f : maxabs);
     launch_split_weights(dev_w, S, N, K, sp.scale, c->prec, sp.hi, c->prec == PREC_BF16X1 ? nullptr : sp.lo,
-                         c->stream);
+                         c->stream, eye);
 }
+
+// The carrier readout y + W_out y (and memory mode's m_inner + W_out m_inner) runs as the plain
+// product (I + W_out) y where W_out is split into two halves: the residual then costs the
+// epilogue no second read of y, and I + W_out keeps ~22 bits in the hi/lo pair, as every split
+// weight does.  With fp32 GEMMs, or the single bf16 half (8 bits would round y itself), the
+// epilogue adds y.
+bool readout_eye(const adn_ctx *c) { return c->prec == PREC_F16X3 || c->prec == PREC_BF16X3; }
 
 void set_split(const adn_ctx *c, GemmParams &g, const adn_ctx::Split &sp, float a_scale = 1.0f) {
     g.prec = c->prec;
@@ -641,7 +650,7 @@ void enqueue_scan(adn_ctx *c, const adn_run &r, const adn_outputs &o, const Solv
             g.K = d;
             g.S = H;
             g.err = b.err;
-            g.epi = EPI_ADD_A;
+            g.epi = readout_eye(c) ? EPI_NONE : EPI_ADD_A;
             set_split(c, g, c->sp_out);
             set_range(c, g, 1);
             Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st);
@@ -773,7 +782,7 @@ void enqueue_forward_memory(adn_ctx *c, const adn_run &r, const adn_outputs &o, 
             g.K = d;
             g.S = H;
             g.err = b.err;
-            g.epi = EPI_ADD_A;
+            g.epi = readout_eye(c) ? EPI_NONE : EPI_ADD_A;
             set_split(c, g, c->sp_out);
             set_range(c, g, 2);
             Span sp(prof, ADN_STAGE_READOUT_GEMM, -1, st, B);
@@ -1061,7 +1070,7 @@ int adn_upload_weights(adn_ctx *c, const adn_weights *w, uint32_t layout) {
                    host_maxabs({{w->w_q, nmat}, {w->w_k, nmat}, {w->w_v, nmat}}));
         make_split(c, c->sp_o, c->w_o, H, d, d, host_maxabs({{w->w_o, nmat}}));
         make_split(c, c->sp_in, c->w_in, H, d, d, host_maxabs({{w->w_in, nmat}}));
-        if (c->w_out) make_split(c, c->sp_out, c->w_out, H, d, d, host_maxabs({{w->w_out, nmat}}));
+        if (c->w_out) make_split(c, c->sp_out, c->w_out, H, d, d, host_maxabs({{w->w_out, nmat}}), readout_eye(c));
         make_split(c, c->sp_cat, c->w_cat, H, r + 2 * N, d,
                    host_maxabs({{w->w_kw, (size_t)H * d * r}, {w->w_b, (size_t)H * N * d},
                                 {w->w_c, (size_t)H * N * d}}));
@@ -1378,7 +1387,7 @@ int adn_renormalize_spectral(adn_ctx *c, float attn_threshold, float win_thresho
         make_split(c, c->sp_qkv, c->w_qkv, H, 3 * d, d, mx[0]);
         make_split(c, c->sp_o, c->w_o, H, d, d, mx[1]);
         make_split(c, c->sp_in, c->w_in, H, d, d, mx[2]);
-        if (c->w_out) make_split(c, c->sp_out, c->w_out, H, d, d, mx[3]);
+        if (c->w_out) make_split(c, c->sp_out, c->w_out, H, d, d, mx[3], readout_eye(c));
         // row-L1 bounds of W_v and W_out (the range guard's): a slot scaled by f has f times its
         // rows' L1 norms, so the largest factor keeps the bound valid
         auto factor = [&](int role, float thr) {
