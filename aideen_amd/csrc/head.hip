@@ -150,6 +150,35 @@ __global__ __launch_bounds__(64 * AR_W) void k_argmax_reduce(const float *am_val
     }
 }
 
+// The same reduction for a few rows (a decode step): one block per row, its threads over the
+// row's tiles (a block of 32 rows would leave 31 of every 32 lanes idle and walk the tiles in
+// dependent rounds), the candidates combined by wave shuffles and then across the waves.
+constexpr int ARR_NT = 256;
+__global__ __launch_bounds__(ARR_NT) void k_argmax_reduce_rows(const float *am_val, const int32_t *am_idx,
+                                                             int ntok, int ntiles, int32_t *out,
+                                                             TokenAppend app) {
+    __shared__ float sv[ARR_NT / 64];
+    __shared__ int si[ARR_NT / 64];
+    const int row = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int t = threadIdx.x; t < ntiles; t += ARR_NT)
+        am_combine(bv, bi, am_val[(long)t * ntok + row], am_idx[(long)t * ntok + row]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        am_combine(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < ARR_NT / 64; ++w) am_combine(bv, bi, sv[w], si[w]);
+        am_store(out, row, bi < 0 ? 0 : bi, app);
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Greedy decode (Trainer::generate, trainer.rs:4219-4431).  seq [B][stride] holds each
 // sequence's tokens so far (the prompt, then the appended arg-maxes); step j works on the first
@@ -301,6 +330,11 @@ void launch_argmax(const float *logits, int ntok, int V, int32_t *out, hipStream
 void launch_argmax_reduce(const float *am_val, const int32_t *am_idx, int ntok, int ntiles, int32_t *out,
                           hipStream_t st, const TokenAppend *app) {
     const TokenAppend a = app ? *app : TokenAppend{};
+    if (ntok <= 4) {
+        hipLaunchKernelGGL(k_argmax_reduce_rows, dim3((unsigned)ntok), dim3(ARR_NT), 0, st, am_val, am_idx, ntok,
+                           ntiles, out, a);
+        return;
+    }
     hipLaunchKernelGGL(k_argmax_reduce, dim3((unsigned)((ntok + 31) / 32)), dim3(64 * AR_W), 0, st, am_val, am_idx, ntok,
                        ntiles, out, a);
 }

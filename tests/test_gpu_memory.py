@@ -69,6 +69,10 @@ MEM_VARIANTS = [
     dict(d=128, H=4, V=500, sigma=0.7, anderson_m=3),
     dict(d=128, H=4, V=500, flags=synth.F_TOKEN_CARRY),  # warm start from h*_{t-1}
     dict(d=256, H=8, V=700, flags=synth.F_TOKEN_CARRY | synth.F_INIT_SIGNAL_RMS, anderson_m=2),
+    # the fused update-and-mix kernel for wide rows with the history term (1024, and 1536: not a
+    # power of two), at tolerance 0 so that every position runs all 8 steps
+    dict(d=1024, H=2, V=400, sigma=0.7, anderson_m=3, eps=0.0, max_iters=8),
+    dict(d=1536, H=2, V=400, sigma=0.7, anderson_m=3, eps=0.0, max_iters=8),
 ]
 
 
