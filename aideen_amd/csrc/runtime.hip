@@ -370,7 +370,9 @@ bool enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
     const Dims &D = c->D;
     const int d = D.d, H = D.H;
     hipStream_t st = c->stream;
-    const int m = c->cfg.anderson_m;
+    // Anderson depths 1 and 2 never mix (n_res = min(k, m - 1) < 2), so they run as plain Picard
+    // (no ring of iterates)
+    const int m = c->cfg.anderson_m >= 3 ? c->cfg.anderson_m : 0;
     // W_o on the 256x256 fp16-split tiles reads its A (mix) pre-split: the attention writes the
     // halves, in mix's memory, with the scale the GEMM derives from the h bound (set_range below)
     const bool wo_pre = gemm_presplit_ok(c->prec, rows, d);
