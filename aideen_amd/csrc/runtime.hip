@@ -91,6 +91,8 @@ struct adn_ctx {
     // per-token exit flags when the caller asks for none (the mixing pass of the last iteration
     // reads them)
     int32_t *conv_scratch = nullptr;
+    // Anderson's update and mix in one pass (launch_update_mix) serve this shape on this device
+    bool fuse_mix = false;
     // fp16-split range guard: the A operands' magnitude bounds (ADN_BOUNDS words, reset per forward)
     // and the weight-derived constants they are combined with (set at upload)
     unsigned *bounds = nullptr;
@@ -480,7 +482,7 @@ bool enqueue_iterations(adn_ctx *c, const adn_run &r, const SolveBuffers &b, int
         const bool mix = m > 0;
         const bool from_slot = mix && anderson_from_slot_ok(D);
         const int cap_mix = mix && k + 1 == r.max_iters && k >= 2;
-        if (m >= 3 && k >= 2 && b.mix_coef && update_mix_ok(D)) {
+        if (m >= 3 && k >= 2 && b.mix_coef && c->fuse_mix) {
             // from the first mix on, the update and the mix in one pass (the previous iterate
             // rebuilt from the ring, so h is not read)
             SolveBuffers bu = b;
@@ -877,6 +879,7 @@ int adn_create(const adn_config *cfg, adn_ctx **out) {
                                                      : PREC_F16X3;
         ADN_HIP(hipGetDevice(&c->device));
         if (c->device < 0 || c->device >= 256) throw HipError{hipErrorInvalidDevice, "adn_create: device ordinal"};
+        c->fuse_mix = cfg->anderson_m >= 3 && update_mix_ok(c->D);
         {  // the allocation-free entry point's per-device array (once per device)
             std::lock_guard<std::mutex> lk(g_scratch_mu);
             if (!g_scratch_ptr[c->device]) {
