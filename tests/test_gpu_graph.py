@@ -77,6 +77,18 @@ def test_forward_graph_replays_match_eager(anderson_m):
     capture_and_replay(mc, w, B, T, toks)
 
 
+def test_forward_graph_wide_rows_anderson_replays_match_eager():
+    """Rows of 1024 floats with Anderson mixing: the fused update and mix for wide rows (a lane's
+    elements walked in groups, the rows in dynamic LDS, the per-token mix coefficients kept between
+    iterations) captured in the graph with the rest of the forward."""
+    log("graph capture, canonical forward, d=1024, anderson m=4")
+    mc = synth.ModelConfig(d=1024, H=2, V=600, N=4, r=32, anderson_m=4, max_iters=12)
+    w = synth.make_weights(mc, seed=15)
+    B, T = 2, 520
+    toks = synth.make_tokens("zipf", B, T, mc.V, seed=16)
+    capture_and_replay(mc, w, B, T, toks)
+
+
 def test_memory_forward_graph_replays_match_eager():
     """The memory-coupled forward (positions in order, the per-position Picard loops, the history
     context and the carrier state copied between buffers on the device) captured whole."""
