@@ -160,6 +160,43 @@ def test_random_large_config_matches_oracle(oracle_lib, seed):
     check(oracle_lib, mc, w, toks, got, f"random large config {seed}")
 
 
+def draw_wide(seed):
+    """Rows of 1024 or 1536 floats at >= 1024 tokens with Anderson mixing of depth 3 or 4 at
+    tolerance 0: the fused update and mix for wide rows (a lane's elements walked in groups, the
+    rows in LDS) on the 256 x 256 tile paths.  (Depth 5 at these widths leaves up to 15% of the
+    tokens ill-conditioned in the sense below.)"""
+    rng = np.random.default_rng(5000 + seed)
+    d = int(rng.choice([1024, 1536]))
+    H = (2, 4)[seed % 2]
+    V = int(rng.choice([600, 1500]))
+    N = int(rng.choice([4, 16]))
+    flags = synth.F_SCAN_SELECTIVE if rng.random() < 0.5 else 0
+    for f in (synth.F_SCORE_CLAMP4, synth.F_RMS_EXCL_ANCHOR, synth.F_INIT_SIGNAL_RMS):
+        if rng.random() < 0.3:
+            flags |= f
+    flags |= int(rng.choice([0, synth.F_RESID_L2]))
+    m = int(rng.choice([3, 4]))
+    B = int(rng.choice([1, 2]))
+    T = int(rng.integers(1024, 1300)) // B
+    mc = synth.ModelConfig(d=d, H=H, V=V, N=N, r=32, flags=flags, anderson_m=m, eps=0.0, max_iters=7,
+                           qk_bias=bool(rng.random() < 0.3))
+    return mc, B, T
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_wide_anderson_config_matches_oracle(oracle_lib, seed):
+    mc, B, T = draw_wide(seed)
+    log(f"random wide Anderson config {seed}: {mc} B={B} T={T}")
+    w = synth.make_token_sensitive_weights(mc, seed=seed)
+    toks = synth.make_tokens("zipf", B, T, mc.V, seed=seed)
+    be = GpuDeqBackend(mc, B, T)
+    be.upload_weights(w)
+    got = be.forward(toks, want=ALL)
+    be.close()
+    check(oracle_lib, mc, w, toks, got, f"random wide Anderson config {seed}")
+    assert (got["iters"] == mc.max_iters).all()
+
+
 def draw_memory(seed):
     """The memory-coupled forward (fixed-history mode): position-sequential solves of B tokens
     with the history term, optional warm start, Anderson, and caller state."""
