@@ -148,6 +148,7 @@ __device__ __forceinline__ void store_presplit_pair(float *row, int e0, const fl
 
 template <int H, int QA, int VEC>
 __global__ __launch_bounds__(256) void k_attn(Dims D, SolveBuffers b, int cur, int k) {
+    static_assert(QA * H <= 64, "the score butterfly leaves one score per lane: at most 64 per wave");
     constexpr int NG = H / QA;
     const int gw = blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
