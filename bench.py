@@ -379,6 +379,28 @@ def scan_compute_bound(mc, B, T, ms):
                 frac=round(floor_ms / ms, 4), basis=basis + "; floor at 2.4 GHz over 1024 SIMDs")
 
 
+def stream_calib(dev, mib: int, reps: int = 20) -> dict:
+    """o = a + b * c over four arrays of `mib` MiB each (three reads and one write per element, as
+    in the attention and update kernels), timed with events over `reps` launches after warm-up."""
+    import torch
+    n = mib << 18
+    a, b, c = (torch.full((n,), 1.0 + q, dtype=torch.float32, device=dev) for q in range(3))
+    o = torch.empty_like(a)
+    for _ in range(3):
+        torch.addcmul(a, b, c, out=o)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.addcmul(a, b, c, out=o)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    gbs = 4.0 * n * 4 / (us * 1e-6) / 1e9
+    del a, b, c, o
+    return dict(pattern="3 reads + 1 write (torch.addcmul)", mib_per_array=mib, us=round(us, 1),
+                gbs=round(gbs, 1), frac=round(gbs / PEAK_HBM_GBS, 4))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -389,6 +411,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this size (calibrates HBM byte counters)")
+    ap.add_argument("--stream-mib", type=int, default=0,
+                    help="also time a three-read-one-write pass (torch.addcmul) over four arrays of this "
+                         "size: the practical HBM rate of the attention's and update's access pattern "
+                         "(reported as stream_calib; 128 MiB arrays exceed the memory-side cache together)")
     ap.add_argument("--mode", choices=["forward", "memory", "embed", "adjoint", "decode"], default="forward",
                     help="forward: the canonical (token-parallel) forward, the headline metric; memory: "
                          "the memory-coupled forward (positions in order, history context and carrier "
@@ -556,6 +582,8 @@ def main() -> int:
         "stages": stages,
         "profiled_forward_ms": round(prof["total_ms"], 3),
     }
+    if args.stream_mib:
+        line["stream_calib"] = stream_calib(dev, args.stream_mib)
     if args.config == "C4" and "scan" in hbm:  # the configuration's own figure: the carrier scan
         sc = prof["stages"]["scan"]
         line["scan"] = dict(gbs=hbm["scan"]["gbs"], frac=hbm["scan"]["frac"], ms=round(sc["ms"], 4),
