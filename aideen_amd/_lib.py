@@ -104,6 +104,11 @@ def lib():
         "adn_forward_async": (C.c_int, [ctx_p, C.POINTER(AdnRun), C.POINTER(AdnOutputs)]),
         "adn_decode_greedy": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, C.c_int32, C.c_int32,
                                         C.c_float, C.c_float, C.c_float, I32P]),
+        "adn_lm_sample": (C.c_int, [ctx_p, C.c_int32, C.c_int32, F32P, I32P, C.c_int32, I32P, C.c_float, C.c_float,
+                                    C.c_int32, C.c_float, F32P, I32P]),
+        "adn_decode_sample": (C.c_int, [ctx_p, C.c_int32, C.c_int32, I32P, C.c_int32, C.c_int32, C.c_int32,
+                                        C.c_float, C.c_float, C.c_float, C.c_float, C.c_int32, C.c_float, F32P,
+                                        I32P]),
         "adn_spectral_norm": (C.c_int, [ctx_p, F32P, C.c_int32, C.c_int32, C.c_int32, F32P]),
         "adn_normalize_if_needed": (C.c_int, [ctx_p, F32P, C.c_int32, C.c_int32, C.c_float, C.c_int32]),
         "adn_renormalize_spectral": (C.c_int, [ctx_p, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float,

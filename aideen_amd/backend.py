@@ -271,6 +271,51 @@ class GpuDeqBackend:
                                       float(repetition_penalty), _ip(out)))
         return out
 
+    def decode_sample(self, prompt, n_new: int, ctx_len: int, *, temperature: float, top_p: float, top_k: int,
+                      repetition_penalty: float = 1.0, uniforms=None, seed: Optional[int] = None,
+                      max_iters: int = 10, eps: float = 0.0, damping: Optional[float] = None) -> np.ndarray:
+        """``Trainer::generate`` (trainer.rs:4219-4431) with ``LmHead::sample``'s temperature, top_p,
+        top_k and repetition penalty (lm_head.rs:78-168).  The reference draws each step's uniform from
+        ``thread_rng``; here ``uniforms`` [B][n_new] in [0, 1) are the draws (or, when None, 24-bit
+        draws as ``rng.gen::<f32>()`` makes them, from a numpy generator seeded with ``seed``)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        if prompt.ndim == 1:
+            prompt = prompt[:, None]
+        B, T0 = prompt.shape
+        if uniforms is None:
+            rng = np.random.default_rng(seed)
+            uniforms = (rng.integers(0, 1 << 24, size=(B, n_new)) * 2.0 ** -24).astype(np.float32)
+        uni = np.ascontiguousarray(uniforms, np.float32).reshape(B, n_new)
+        out = np.zeros((B, n_new), np.int32)
+        check(lib().adn_decode_sample(self._ctx, B, T0, _ip(prompt), int(n_new), int(ctx_len), int(max_iters),
+                                      float(eps), self.model.beta if damping is None else float(damping),
+                                      float(temperature), float(top_p), int(top_k), float(repetition_penalty),
+                                      _fp(uni), _ip(out)))
+        return out
+
+    def lm_sample(self, logits, uniforms, *, temperature: float, top_p: float, top_k: int,
+                  repetition_penalty: float = 1.0, context=None) -> np.ndarray:
+        """``LmHead::sample`` (lm_head.rs:78-168) on rows of logits [rows][V] with the draws
+        ``uniforms`` [rows]; ``context`` is a list of each row's context token ids (or None)."""
+        lg = np.ascontiguousarray(logits, np.float32)
+        if lg.ndim == 1:
+            lg = lg[None, :]
+        rows, V = lg.shape
+        uni = np.ascontiguousarray(uniforms, np.float32).reshape(rows)
+        if context is None:
+            ctx = np.zeros((rows, 0), np.int32)
+            lens = np.zeros(rows, np.int32)
+        else:
+            width = max(1, max(len(c) for c in context))
+            ctx = np.zeros((rows, width), np.int32)
+            lens = np.array([len(c) for c in context], np.int32)
+            for i, c in enumerate(context):
+                ctx[i, :len(c)] = c
+        out = np.zeros(rows, np.int32)
+        check(lib().adn_lm_sample(self._ctx, rows, V, _fp(lg), _ip(ctx), ctx.shape[1], _ip(lens), float(temperature),
+                                  float(top_p), int(top_k), float(repetition_penalty), _fp(uni), _ip(out)))
+        return out
+
     # weight preparation --------------------------------------------------------------------
     def spectral_norm(self, w: np.ndarray, n_iter: int = 20) -> float:
         w = np.ascontiguousarray(w, np.float32)

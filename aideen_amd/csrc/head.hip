@@ -311,6 +311,428 @@ __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *
     if (b < B) last[b] = seq[(long)b * stride + len - 1];
 }
 
+// ---- LmHead::sample (lm_head.rs:78-168) ------------------------------------------------------
+// One workgroup per logits row.  The row goes through a workspace row ws[V]: the penalised and
+// scaled logits, then e = exp(l - max), then the bit pattern ("key") of p = e / S.  p lies in
+// [0, 1] (the maximum contributes exp(0) = 1 to S), so keys order as p does, and the reference's
+// sorted list (p descending by a stable sort: ties keep index order) is the order "key
+// descending, index ascending".  A probability weighs floor(p * 2^60) in exact integer sums
+// (the sum over a row stays below 2^61).
+//
+// The cut points of the list (the top_k-th item, the first item past which the running sum
+// exceeds top_p, the item at which it reaches the draw) are found without sorting the row: three
+// 10-bit radix levels over the keys with LDS histograms of counts and weights, then the item of
+// the equal-key group in index order.  When the kept list has at most SP_CAP items (top_k <=
+// SP_CAP, or a top_p cut within that many items, or a vocabulary that small) it is gathered,
+// sorted in LDS, and one thread runs the reference's loops on it in float arithmetic; otherwise
+// the cuts are taken on the exact sums.
+constexpr int SP_NT = 1024;
+constexpr int SP_CAP = 2048;
+constexpr double SP_ONE = 1152921504606846976.0;  // 2^60
+typedef unsigned long long u64;
+
+struct SampleSmem {
+    unsigned hc[SP_NT];  // one bucket per thread
+    u64 hm[SP_NT];
+    u64 list[SP_CAP];  // (~key << 32) | index: ascending = key descending, index ascending
+    u64 wc[SP_NT / 64], wm[SP_NT / 64];
+    float wf[SP_NT / 64];
+    int wi[SP_NT / 64];
+    u64 bc, bm;
+    unsigned cnt;
+    int tok, need_exact;
+};
+
+struct SpCut {  // keeps the items up to and including (key, idx) in the list order; `on` false keeps all
+    bool on;
+    unsigned key;
+    int idx;
+};
+
+struct SpSel {  // an item and the count and weight of the list up to and including it
+    unsigned key;
+    int idx;
+    u64 cnt, mass;
+    bool found;
+};
+
+__device__ __forceinline__ u64 sp_mass(unsigned k) { return (u64)((double)__uint_as_float(k) * SP_ONE); }
+
+__device__ __forceinline__ bool sp_in(const SpCut &c, unsigned k, int i) {
+    return !c.on || k > c.key || (k == c.key && i <= c.idx);
+}
+
+__device__ float sp_max(float v, SampleSmem &sm) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) sm.wf[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = sm.wf[0];
+    for (int u = 1; u < SP_NT / 64; ++u) v = fmaxf(v, sm.wf[u]);
+    __syncthreads();
+    return v;
+}
+
+// the block's sum in a fixed order (wave butterflies, then the waves in order)
+__device__ float sp_sum(float v, SampleSmem &sm) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == 0) sm.wf[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = sm.wf[0];
+    for (int u = 1; u < SP_NT / 64; ++u) v += sm.wf[u];
+    __syncthreads();
+    return v;
+}
+
+// inclusive scan of (c, m) over the threads in thread order
+__device__ void sp_scan(u64 &c, u64 &m, SampleSmem &sm) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int off = 1; off < 64; off <<= 1) {
+        const u64 c2 = __shfl_up(c, off, 64), m2 = __shfl_up(m, off, 64);
+        if (lane >= off) {
+            c += c2;
+            m += m2;
+        }
+    }
+    if (lane == 63) {
+        sm.wc[w] = c;
+        sm.wm[w] = m;
+    }
+    __syncthreads();
+    u64 pc = 0, pm = 0;
+    for (int u = 0; u < w; ++u) {
+        pc += sm.wc[u];
+        pm += sm.wm[u];
+    }
+    c += pc;
+    m += pm;
+    __syncthreads();
+}
+
+// The first item of the list that `cut` keeps at which the running count (by_mass false) or the
+// running weight (true) exceeds T.  Not found: cnt and mass are the kept list's totals.
+__device__ SpSel sp_select(const unsigned *wk, int V, bool by_mass, u64 T, const SpCut &cut, SampleSmem &sm) {
+    const int tid = threadIdx.x;
+    u64 cb = 0, mb = 0;  // the items before the current key prefix
+    unsigned prefix = 0;
+    for (int lv = 0; lv < 3; ++lv) {
+        const int sh = 20 - 10 * lv;  // keys of p <= 1 are below 2^30
+        sm.hc[tid] = 0u;
+        sm.hm[tid] = 0ull;
+        __syncthreads();
+        for (int i = tid; i < V; i += SP_NT) {
+            const unsigned k = wk[i];
+            if (!sp_in(cut, k, i) || (lv > 0 && (k >> (sh + 10)) != prefix)) continue;
+            const unsigned b = (k >> sh) & 1023u;
+            atomicAdd(&sm.hc[b], 1u);
+            atomicAdd(&sm.hm[b], sp_mass(k));
+        }
+        __syncthreads();
+        u64 c = sm.hc[SP_NT - 1 - tid], m = sm.hm[SP_NT - 1 - tid];  // buckets from the largest key down
+        sp_scan(c, m, sm);
+        const bool ok = (by_mass ? mb + m : cb + c) > T;
+        const int ts = __syncthreads_count(!ok);  // the running sums only grow: the buckets before the crossing
+        if (ts == SP_NT) {
+            if (tid == SP_NT - 1) {
+                sm.bc = c;
+                sm.bm = m;
+            }
+            __syncthreads();
+            const SpSel r{0u, -1, cb + sm.bc, mb + sm.bm, false};
+            __syncthreads();
+            return r;
+        }
+        if (ts > 0 && tid == ts - 1) {
+            sm.bc = c;
+            sm.bm = m;
+        }
+        if (ts == 0 && tid == 0) {
+            sm.bc = 0;
+            sm.bm = 0;
+        }
+        __syncthreads();
+        cb += sm.bc;
+        mb += sm.bm;
+        prefix = (prefix << 10) | (unsigned)(SP_NT - 1 - ts);
+        __syncthreads();
+    }
+    // the crossing lies in the group of items with key == prefix, each weighing mu
+    const unsigned key = prefix;
+    const u64 mu = sp_mass(key);
+    const u64 j = by_mass ? (mu ? (T - mb) / mu : 0) : T - cb;
+    // its j-th item in index order: a thread takes a contiguous index range
+    const int CH = (V + SP_NT - 1) / SP_NT;
+    const int i0 = min(V, tid * CH), i1 = min(V, i0 + CH);
+    u64 n = 0;
+    for (int i = i0; i < i1; ++i) {
+        const unsigned k = wk[i];
+        n += (k == key && sp_in(cut, k, i)) ? 1 : 0;
+    }
+    u64 incl = n, unused = 0;
+    sp_scan(incl, unused, sm);
+    if (tid == 0) sm.tok = -1;
+    __syncthreads();
+    if (j >= incl - n && j < incl) {
+        u64 q = incl - n;
+        for (int i = i0; i < i1; ++i) {
+            const unsigned k = wk[i];
+            if (k == key && sp_in(cut, k, i)) {
+                if (q == j) {
+                    sm.tok = i;
+                    break;
+                }
+                ++q;
+            }
+        }
+    }
+    __syncthreads();
+    const SpSel r{key, sm.tok, cb + j + 1, mb + (j + 1) * mu, sm.tok >= 0};
+    __syncthreads();
+    return r;
+}
+
+// LmHead::argmax (lm_head.rs:62-69) as Iterator::max_by folds: NaN compares Equal, so the fold
+// restarts after the last NaN and returns the last maximum after it (the NaN itself when last).
+__device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int jn = -1;
+    for (int i = tid; i < V; i += SP_NT)
+        if (x[i] != x[i]) jn = i;
+    for (int off = 32; off > 0; off >>= 1) jn = max(jn, __shfl_xor(jn, off, 64));
+    if (lane == 0) sm.wi[w] = jn;
+    __syncthreads();
+    jn = sm.wi[0];
+    for (int u = 1; u < SP_NT / 64; ++u) jn = max(jn, sm.wi[u]);
+    __syncthreads();
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int i = tid; i < V; i += SP_NT) {
+        const float v = x[i];
+        if (i > jn && !(v < bv)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float v2 = __shfl_xor(bv, off, 64);
+        const int i2 = __shfl_xor(bi, off, 64);
+        am_combine(bv, bi, v2, i2);
+    }
+    if (lane == 0) {
+        sm.wf[w] = bv;
+        sm.wi[w] = bi;
+    }
+    __syncthreads();
+    bv = sm.wf[0];
+    bi = sm.wi[0];
+    for (int u = 1; u < SP_NT / 64; ++u) am_combine(bv, bi, sm.wf[u], sm.wi[u]);
+    __syncthreads();
+    return bi >= 0 ? bi : (jn >= 0 ? jn : 0);
+}
+
+__global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, unsigned *ws, SampleParams a,
+                                                  int32_t *out, TokenAppend app) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float *lg = logits + (long)row * V;
+    unsigned *wk = ws + (long)row * V;
+    float *wf = reinterpret_cast<float *>(wk);
+    // 1. the row, then the repetition penalty once per distinct context token (lm_head.rs:81-99)
+    for (int i = tid; i < V; i += SP_NT) wf[i] = lg[i];
+    __syncthreads();
+    const int len = a.lens ? a.lens[row] : a.len;
+    const int start = len > a.window ? len - a.window : 0, L = len - start;
+    if (fabsf(a.penalty - 1.0f) > 1e-4f && L > 0) {
+        const int32_t *tk = a.seq + (long)row * a.stride + start;
+        for (int p = tid; p < L; p += SP_NT) {
+            const int tok = tk[p];
+            bool seen = false;
+            for (int u = 0; u < p && !seen; ++u) seen = tk[u] == tok;
+            if (seen || tok < 0 || tok >= V) continue;
+            const float sc = wf[tok];
+            wf[tok] = sc < 0.0f ? sc * a.penalty : sc / a.penalty;
+        }
+    }
+    __syncthreads();
+    if (a.greedy) {
+        const int g = sp_argmax(wf, V, sm);
+        if (tid == 0) am_store(out, row, g, app);
+        return;
+    }
+    // 2. the temperature (lm_head.rs:103-111), the
+    // maximum as f32::max folds it (NaN skipped), e = exp(l - max) and S (softmax, :71-76).  From
+    // here each thread touches only its own elements until the keys are complete.
+    const float Tm = a.temperature;
+    const bool scale = Tm > 0.0f && fabsf(Tm - 1.0f) > 1e-4f;
+    float mx = -INFINITY;
+    for (int i = tid; i < V; i += SP_NT) {
+        float v = wf[i];
+        if (scale) {
+            v = v / Tm;
+            wf[i] = v;
+        }
+        mx = fmaxf(mx, v);
+    }
+    mx = sp_max(mx, sm);
+    float s = 0.0f;
+    for (int i = tid; i < V; i += SP_NT) {
+        const float e = (float)exp((double)(wf[i] - mx));  // exp rounded once to float
+        wf[i] = e;
+        s += e;
+    }
+    const float S = sp_sum(s, sm);
+    const float r = a.uni[(long)row * a.uni_stride];
+    int tok = -2;  // -2: LmHead::argmax of the row as given (lm_head.rs:148-150)
+    // a NaN S (a NaN or infinite logit, or no finite one) makes every p NaN: the reference's kept
+    // sum then fails `sum > 1e-6`
+    if (S == S) {
+        u64 tm = 0;
+        for (int i = tid; i < V; i += SP_NT) {
+            const unsigned k = __float_as_uint(wf[i] / S);
+            wk[i] = k;
+            tm += sp_mass(k);
+        }
+        u64 unused = 0;
+        sp_scan(tm, unused, sm);  // the last thread's inclusive value is the total
+        if (tid == SP_NT - 1) sm.bm = tm;
+        __syncthreads();
+        const u64 total = sm.bm;
+        __syncthreads();
+        const bool kon = a.top_k > 0 && a.top_k < V, pon = a.top_p > 0.0f && a.top_p < 1.0f;
+        const SpCut none{false, 0u, 0};
+        // 3. top-k (:121-125): the list ends at its top_k-th item
+        SpCut ck = none;
+        u64 nk = (u64)V, mk = total;
+        if (kon) {
+            const SpSel sk = sp_select(wk, V, false, (u64)(a.top_k - 1), none, sm);
+            ck = SpCut{true, sk.key, sk.idx};
+            nk = sk.cnt;
+            mk = sk.mass;
+        }
+        // 4. the short list: past top_p by 2^-10 of slack (the float running sum of <= SP_CAP items
+        // stays within 2^-12 of the exact one), or the whole kept list
+        SpCut cl = ck;
+        u64 M = nk;
+        bool full = true;
+        if (!(kon && a.top_k <= SP_CAP) && pon) {
+            const SpSel sp = sp_select(wk, V, true, (u64)((double)a.top_p * SP_ONE) + (1ull << 50), ck, sm);
+            if (sp.found) {
+                cl = SpCut{true, sp.key, sp.idx};
+                M = sp.cnt;
+                full = M == nk;
+            }
+        }
+        bool exact = M > (u64)SP_CAP;
+        if (!exact) {
+            if (tid == 0) {
+                sm.cnt = 0u;
+                sm.tok = -1;
+                sm.need_exact = 0;
+            }
+            for (int u = tid; u < SP_CAP; u += SP_NT) sm.list[u] = ~0ull;
+            __syncthreads();
+            for (int i = tid; i < V; i += SP_NT) {
+                const unsigned k = wk[i];
+                if (!sp_in(cl, k, i)) continue;
+                const unsigned q = atomicAdd(&sm.cnt, 1u);
+                if (q < (unsigned)SP_CAP) sm.list[q] = ((u64)(~k) << 32) | (unsigned)i;
+            }
+            __syncthreads();
+            int n2 = 2;
+            while (n2 < (int)M) n2 <<= 1;
+            for (int k = 2; k <= n2; k <<= 1)
+                for (int j = k >> 1; j > 0; j >>= 1) {
+                    if (tid < n2 / 2) {
+                        const int i = 2 * tid - (tid & (j - 1)), l = i + j;
+                        const u64 x = sm.list[i], y = sm.list[l];
+                        if ((x > y) == ((i & k) == 0)) {
+                            sm.list[i] = y;
+                            sm.list[l] = x;
+                        }
+                    }
+                    __syncthreads();
+                }
+            if (tid == 0) {
+                // the reference's loops (:127-166) over the sorted list
+                auto pk = [&](int i) { return __uint_as_float(~(unsigned)(sm.list[i] >> 32)); };
+                auto ix = [&](int i) { return (int)(unsigned)(sm.list[i] & 0xffffffffull); };
+                int n = (int)M;
+                bool ok = true;
+                if (pon) {
+                    float cum = 0.0f;
+                    int cut = -1;
+                    for (int i = 0; i < n; ++i) {
+                        cum += pk(i);
+                        if (cum > a.top_p) {
+                            cut = i + 1;
+                            break;
+                        }
+                    }
+                    if (cut < 0) {
+                        if (full)
+                            cut = n;
+                        else
+                            ok = false;  // the float sum crossed later than the slack allowed for
+                    }
+                    n = cut < 1 ? 1 : cut;
+                }
+                if (!ok) {
+                    sm.need_exact = 1;
+                } else {
+                    float sum = -0.0f;
+                    for (int i = 0; i < n; ++i) sum += pk(i);
+                    if (sum > 1e-6f) {
+                        float cum = 0.0f;
+                        int t = ix(0);
+                        for (int i = 0; i < n; ++i) {
+                            cum += pk(i) / sum;
+                            if (r <= cum) {
+                                t = ix(i);
+                                break;
+                            }
+                        }
+                        sm.tok = t;
+                    } else {
+                        sm.tok = -2;
+                    }
+                }
+            }
+            __syncthreads();
+            tok = sm.tok;
+            exact = sm.need_exact != 0;
+            __syncthreads();
+        }
+        if (exact) {
+            // 5. top-p (:127-140), the renormalisation (:142-150) and the draw (:152-166) on the
+            // exact sums: the first item past which the weight exceeds top_p; then the first at
+            // which it reaches r times the kept weight (the first item when r <= 0 or NaN)
+            SpCut cf = ck;
+            u64 mkept = mk;
+            if (pon) {
+                const SpSel sp = sp_select(wk, V, true, (u64)((double)a.top_p * SP_ONE), ck, sm);
+                if (sp.found) {
+                    cf = SpCut{true, sp.key, sp.idx};
+                    mkept = sp.mass;
+                }
+            }
+            if ((double)mkept > 1e-6 * SP_ONE) {
+                SpSel sd{};
+                bool first = !(r > 0.0f);
+                if (!first) {
+                    const u64 Tt = (u64)ceil((double)r * (double)mkept);  // >= 1
+                    sd = sp_select(wk, V, true, Tt - 1, cf, sm);
+                    first = !sd.found;
+                }
+                if (first) sd = sp_select(wk, V, false, 0, cf, sm);
+                tok = sd.idx;
+            } else {
+                tok = -2;
+            }
+        }
+    }
+    if (tok == -2) tok = sp_argmax(lg, V, sm);
+    if (tid == 0) am_store(out, row, tok < 0 ? 0 : tok, app);
+}
+
 }  // namespace
 
 void launch_pool_norm(const Dims &D, const float *h, int ntok, const float *g, float *pooled,
@@ -352,6 +774,12 @@ void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, 
 void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
                         hipStream_t st) {
     hipLaunchKernelGGL(k_rep_penalty, dim3((unsigned)B), dim3(256), 0, st, logits, V, seq, stride, len, ctx, pen);
+}
+
+void launch_sample(const float *logits, int rows, int V, unsigned *ws, const SampleParams &sp, int32_t *out,
+                   hipStream_t st, const TokenAppend *app) {
+    const TokenAppend a = app ? *app : TokenAppend{};
+    hipLaunchKernelGGL(k_sample, dim3((unsigned)rows), dim3(SP_NT), 0, st, logits, V, ws, sp, out, a);
 }
 
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {

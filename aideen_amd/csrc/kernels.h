@@ -255,6 +255,25 @@ void launch_decode_query(const float *E, int d, const int32_t *seq, int stride, 
 // the repetition penalty over the same context, in place on logits [B][V]
 void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, int len, int ctx, float pen, int B,
                         hipStream_t st);
+// LmHead::sample (lm_head.rs:78-168) on logits [rows][V] with temperature > 0 (or NaN): the
+// repetition penalty over each row's context (the last `window` of seq[row][0, len), len from
+// lens[row] when lens is set), the temperature, softmax, top-k, top-p, the renormalisation and the
+// draw uni[row * uni_stride] (rng.gen::<f32>(), in [0, 1)); with `greedy` (temperature <= 0) the
+// arg-max of the penalised row.  ws [rows][V] is workspace; the token is stored as the arg-max
+// kernels store theirs.
+struct SampleParams {
+    const int32_t *seq;
+    int stride, len;
+    const int32_t *lens;
+    int window;
+    float temperature, top_p, penalty;
+    int top_k;
+    const float *uni;
+    int uni_stride;
+    bool greedy;
+};
+void launch_sample(const float *logits, int rows, int V, unsigned *ws, const SampleParams &sp, int32_t *out,
+                   hipStream_t st, const TokenAppend *app = nullptr);
 // last[b] = seq[b][len - 1]
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st);
 

@@ -1189,9 +1189,19 @@ int adn_forward(adn_ctx *c, const adn_run *r, const adn_outputs *o) {
     }
 }
 
-int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
-                      int32_t ctx_len, int32_t max_iters, float eps, float damping, float repetition_penalty,
-                      int32_t *out_tokens) {
+namespace {
+
+// LmHead::sample's arguments beyond greedy; uniforms [batch][n_new] host memory
+struct SampleCfg {
+    float temperature, top_p;
+    int top_k;
+    const float *uniforms;
+};
+
+// Trainer::generate's loop; smp null = greedy (LmHead::sample at temperature <= 0)
+int decode_run(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new, int32_t ctx_len,
+               int32_t max_iters, float eps, float damping, float repetition_penalty, const SampleCfg *smp,
+               int32_t *out_tokens) {
     if (!c || !prompt || !out_tokens) return fail(ADN_E_INVALID, "null argument");
     if (!c->has_weights) return fail(ADN_E_NO_WEIGHTS, "decode before adn_upload_weights");
     if (batch < 1 || prompt_len < 1 || n_new < 0 || ctx_len < 1)
@@ -1227,8 +1237,18 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
         int32_t *outd = (int32_t *)staging_f(c, 11, (size_t)batch * n_new * sizeof(int32_t));
         ADN_HIP(hipMemcpy2DAsync(seq, (size_t)stride * sizeof(int32_t), prompt, (size_t)prompt_len * sizeof(int32_t),
                                  (size_t)prompt_len * sizeof(int32_t), batch, hipMemcpyHostToDevice, st));
-        float *lg = penalise ? staging_f(c, 24, (size_t)batch * D.V * sizeof(float)) : nullptr;
+        // sampling reads the logits rows (and applies the penalty in its own workspace)
+        const bool rows_out = penalise || smp;
+        float *lg = rows_out ? staging_f(c, 24, (size_t)batch * D.V * sizeof(float)) : nullptr;
         int32_t *am = c->argmax_scratch;
+        unsigned *sws = nullptr;
+        float *uni = nullptr;
+        if (smp) {
+            sws = (unsigned *)staging_f(c, 31, (size_t)batch * D.V * sizeof(float));
+            uni = staging_f(c, 32, (size_t)batch * n_new * sizeof(float));
+            ADN_HIP(hipMemcpyAsync(uni, smp->uniforms, (size_t)batch * n_new * sizeof(float), hipMemcpyHostToDevice,
+                                   st));
+        }
         float *q = nullptr, *m_cur = nullptr, *m_nxt = nullptr;
         int32_t *last = nullptr;
         if (memory) {
@@ -1259,7 +1279,7 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
         for (int j = 0; j < n_new; ++j) {
             const int len = prompt_len + j;
             adn_outputs o{};
-            if (penalise)
+            if (rows_out)
                 o.logits = lg;
             else
                 o.argmax = am;
@@ -1272,7 +1292,7 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
                 r.s_in = nullptr;
                 r.scan_state_in = m_cur;
                 o.scan_state = m_nxt;
-                enqueue_forward_memory(c, r, o, nullptr, penalise ? nullptr : &app);
+                enqueue_forward_memory(c, r, o, nullptr, rows_out ? nullptr : &app);
                 std::swap(m_cur, m_nxt);
             } else {
                 // query = embed_context(context, ctx_len) (trainer.rs:4388-4392); the query
@@ -1284,16 +1304,97 @@ int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
                                     c->prec == PREC_F16X3 ? c->absmax : nullptr, init_q ? &qi : nullptr);
                 r.tokens = nullptr;
                 r.s_in = q;
-                const DecodeStep ds{true, init_q, penalise ? nullptr : &app};
+                const DecodeStep ds{true, init_q, rows_out ? nullptr : &app};
                 enqueue_forward(c, r, o, nullptr, &ds);
             }
-            if (penalise) {
+            if (smp) {
+                const SampleParams sp{seq, stride, len, nullptr, ctx_len, smp->temperature, smp->top_p,
+                                      repetition_penalty, smp->top_k, uni + j, n_new, false};
+                launch_sample(lg, batch, D.V, sws, sp, am, st, &app);
+            } else if (penalise) {
                 launch_rep_penalty(lg, D.V, seq, stride, len, ctx_len, repetition_penalty, batch, st);
                 launch_argmax(lg, batch, D.V, am, st, &app);
             }
         }
         ADN_HIP(hipGetLastError());
         ADN_HIP(hipMemcpyAsync(out_tokens, outd, (size_t)batch * n_new * sizeof(int32_t), hipMemcpyDeviceToHost, st));
+        ADN_HIP(hipStreamSynchronize(st));
+        return check_device_error(c);
+    } catch (const HipError &e) {
+        return hip_fail(e);
+    }
+}
+
+}  // namespace
+
+int adn_decode_greedy(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
+                      int32_t ctx_len, int32_t max_iters, float eps, float damping, float repetition_penalty,
+                      int32_t *out_tokens) {
+    return decode_run(c, batch, prompt_len, prompt, n_new, ctx_len, max_iters, eps, damping, repetition_penalty,
+                      nullptr, out_tokens);
+}
+
+// LmHead::sample's argument checks shared by the sampling entry points
+static int check_sample_args(float temperature, float top_p, int32_t top_k, float repetition_penalty) {
+    (void)temperature;
+    (void)top_p;  // any value: outside (0, 1) (NaN included) there is no top-p cut, as in the reference
+    if (top_k < 0) return fail(ADN_E_INVALID, "top_k must be >= 0 (0 = no top-k cut)");
+    if (!(repetition_penalty > 0.0f) || !std::isfinite(repetition_penalty))
+        return fail(ADN_E_INVALID, "repetition_penalty must be finite and > 0");
+    return ADN_OK;
+}
+
+int adn_decode_sample(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
+                      int32_t ctx_len, int32_t max_iters, float eps, float damping, float temperature, float top_p,
+                      int32_t top_k, float repetition_penalty, const float *uniforms, int32_t *out_tokens) {
+    int rc = check_sample_args(temperature, top_p, top_k, repetition_penalty);
+    if (rc) return rc;
+    // lm_head.rs:104-111: a temperature <= 0 is the arg-max of the penalised logits
+    if (!(temperature > 0.0f) && temperature <= 1e-4f)
+        return decode_run(c, batch, prompt_len, prompt, n_new, ctx_len, max_iters, eps, damping, repetition_penalty,
+                          nullptr, out_tokens);
+    if (!uniforms && n_new > 0) return fail(ADN_E_INVALID, "null uniforms");
+    const SampleCfg smp{temperature, top_p, top_k, uniforms};
+    return decode_run(c, batch, prompt_len, prompt, n_new, ctx_len, max_iters, eps, damping, repetition_penalty, &smp,
+                      out_tokens);
+}
+
+int adn_lm_sample(adn_ctx *c, int32_t rows, int32_t vocab, const float *logits, const int32_t *context,
+                  int32_t ctx_stride, const int32_t *ctx_len, float temperature, float top_p, int32_t top_k,
+                  float repetition_penalty, const float *uniforms, int32_t *tokens) {
+    if (!c || !logits || !tokens || !uniforms) return fail(ADN_E_INVALID, "null argument");
+    if (rows < 0 || vocab < 1) return fail(ADN_E_INVALID, "rows must be >= 0 and vocab >= 1");
+    if (ctx_stride < 0 || (ctx_stride > 0 && (!context || !ctx_len)))
+        return fail(ADN_E_INVALID, "a context needs its tokens and lengths");
+    int rc = check_sample_args(temperature, top_p, top_k, repetition_penalty);
+    if (rc) return rc;
+    for (int i = 0; ctx_stride > 0 && i < rows; ++i)
+        if (ctx_len[i] < 0 || ctx_len[i] > ctx_stride) return fail(ADN_E_INVALID, "ctx_len outside [0, ctx_stride]");
+    if (rows == 0) return ADN_OK;
+    const bool greedy = !(temperature > 0.0f) && temperature <= 1e-4f;
+    hipStream_t st = c->stream;
+    try {
+        const size_t n = (size_t)rows * vocab;
+        float *lg = staging_f(c, 33, n * sizeof(float));
+        int32_t *out = (int32_t *)staging_f(c, 34, (size_t)rows * sizeof(int32_t));
+        const int cs = ctx_stride > 0 ? ctx_stride : 1;
+        int32_t *ctx = (int32_t *)staging_f(c, 35, (size_t)rows * cs * sizeof(int32_t));
+        int32_t *lens = (int32_t *)staging_f(c, 36, (size_t)rows * sizeof(int32_t));
+        ADN_HIP(hipMemcpyAsync(lg, logits, n * sizeof(float), hipMemcpyHostToDevice, st));
+        if (ctx_stride > 0) {
+            ADN_HIP(hipMemcpyAsync(ctx, context, (size_t)rows * cs * sizeof(int32_t), hipMemcpyHostToDevice, st));
+            ADN_HIP(hipMemcpyAsync(lens, ctx_len, (size_t)rows * sizeof(int32_t), hipMemcpyHostToDevice, st));
+        } else {
+            ADN_HIP(hipMemsetAsync(lens, 0, (size_t)rows * sizeof(int32_t), st));
+        }
+        unsigned *ws = (unsigned *)staging_f(c, 31, n * sizeof(float));
+        float *uni = staging_f(c, 32, (size_t)rows * sizeof(float));
+        ADN_HIP(hipMemcpyAsync(uni, uniforms, (size_t)rows * sizeof(float), hipMemcpyHostToDevice, st));
+        // lm_head.rs:104-111: a temperature <= 0 is the arg-max of the penalised row
+        const SampleParams sp{ctx, cs, 0, lens, cs, temperature, top_p, repetition_penalty, top_k, uni, 1, greedy};
+        launch_sample(lg, rows, vocab, ws, sp, out, st);
+        ADN_HIP(hipGetLastError());
+        ADN_HIP(hipMemcpyAsync(tokens, out, (size_t)rows * sizeof(int32_t), hipMemcpyDeviceToHost, st));
         ADN_HIP(hipStreamSynchronize(st));
         return check_device_error(c);
     } catch (const HipError &e) {

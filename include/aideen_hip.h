@@ -196,7 +196,8 @@ int adn_forward(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
 int adn_forward_async(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
 
 /* Greedy decode, host memory, blocking: Trainer::generate (trainer.rs:4219-4431) with
- * LmHead::sample at temperature <= 1e-4 (lm_head.rs:72-112).  prompt [B][prompt_len] token ids,
+ * LmHead::sample at temperature <= 0 (lm_head.rs:104-111; a temperature in (0, 1e-4] still
+ * divides and samples, see adn_decode_sample).  prompt [B][prompt_len] token ids,
  * out_tokens [B][n_new] the appended tokens.  At step j the context of sequence b is the last
  * ctx_len of its prompt_len + j tokens (trainer.rs:4248-4249) and
  *   - the canonical forward (trainer.rs:4388-4392, 4402-4406): the query is embed_context(context,
@@ -213,6 +214,36 @@ int adn_forward_async(adn_ctx *ctx, const adn_run *run, const adn_outputs *out);
 int adn_decode_greedy(adn_ctx *ctx, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
                       int32_t ctx_len, int32_t max_iters, float eps, float damping, float repetition_penalty,
                       int32_t *out_tokens);
+
+/* LmHead::sample (aideen-backbone/src/lm_head.rs:78-168) on rows of logits, host memory, blocking.
+ * logits [rows][vocab]; row i's context is context[i][0, ctx_len[i]) (context [rows][ctx_stride];
+ * ctx_stride 0 = no context, context and ctx_len may then be null).  Per row, as the reference:
+ *   1. the repetition penalty once per distinct context token when |repetition_penalty - 1| > 1e-4
+ *      (a negative logit multiplied by it, any other divided);
+ *   2. temperature > 0 with |temperature - 1| > 1e-4 divides every logit by it; a temperature <= 0
+ *      returns the arg-max of the penalised row (last maximum, NaN as Iterator::max_by folds it);
+ *   3. softmax (exp(l - max) / sum), the list sorted by probability, descending and stable;
+ *   4. top_k in (0, vocab) keeps the first top_k (0 = no cut);
+ *   5. top_p in (0, 1) keeps the list up to the first item at which the running sum exceeds it;
+ *   6. the kept probabilities renormalised (the arg-max of the row as given if their sum is
+ *      <= 1e-6 or not a number);
+ *   7. the first item at which the running sum reaches uniforms[i] (rng.gen::<f32>() in the
+ *      reference, thread_rng: here the caller's draw in [0, 1)), the first item if none does.
+ * The decisions are taken on the device's own probabilities; where the kept list has at most 2048
+ * items the running sums are the reference's float loops, beyond that exact sums (a token can then
+ * differ from the reference only where a running sum lies within its rounding of top_p or the
+ * draw).  tokens [rows].  repetition_penalty must be finite and > 0, top_k >= 0. */
+int adn_lm_sample(adn_ctx *ctx, int32_t rows, int32_t vocab, const float *logits, const int32_t *context,
+                  int32_t ctx_stride, const int32_t *ctx_len, float temperature, float top_p, int32_t top_k,
+                  float repetition_penalty, const float *uniforms, int32_t *tokens);
+
+/* Trainer::generate (trainer.rs:4219-4431) with LmHead::sample's temperature, top_p, top_k and
+ * repetition penalty (lm_head.rs:78-168, as adn_lm_sample): the steps of adn_decode_greedy, then
+ * each step's token drawn from its logits with uniforms[b][j] (uniforms [B][n_new]).  A
+ * temperature <= 0 is adn_decode_greedy (uniforms unused). */
+int adn_decode_sample(adn_ctx *ctx, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
+                      int32_t ctx_len, int32_t max_iters, float eps, float damping, float temperature, float top_p,
+                      int32_t top_k, float repetition_penalty, const float *uniforms, int32_t *out_tokens);
 
 /* --- weight preparation (spectral_norm.rs:25-80; spectral_renorm.wgsl:83-196) ----------- */
 /* sigma_max by n_iter power iterations from u0 = 1/sqrt(rows); host memory, blocking. */

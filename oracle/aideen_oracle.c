@@ -1032,8 +1032,8 @@ static void embed_window(int d, const float *embed, const int32_t *ctx, int len,
 
 /* LmHead::sample's repetition penalty (lm_head.rs:81-99): every distinct token of the context has
  * its logit multiplied by the penalty when negative, divided by it otherwise; nothing happens when
- * |penalty - 1| <= 1e-4 or the context is empty.  Greedy sampling (temperature <= 1e-4) then takes
- * the arg-max of the penalised logits (lm_head.rs:101-112). */
+ * |penalty - 1| <= 1e-4 or the context is empty.  Greedy sampling (temperature <= 0) then takes
+ * the arg-max of the penalised logits (lm_head.rs:104-111). */
 static void repetition_penalty(float *logits, int V, const int32_t *ctx, int len, float pen) {
     if (!(fabsf(pen - 1.0f) > 1e-4f) || len == 0) return;
     for (int p = 0; p < len; ++p) {
@@ -1058,8 +1058,20 @@ static void repetition_penalty(float *logits, int V, const int32_t *ctx, int len
  *     m = temporal_step(m, h*) (each solve from the init rule, as solve_query_with_fixed_history);
  * then logits = LmHead::forward(h) (lm_head.rs:50-54), the repetition penalty over the context,
  * and the arg-max with the last-max tie rule; the token is appended. */
-void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
-                       const int32_t *prompt, int n_new, int ctx_len, float rep_penalty,
+int orc_lm_sample(const float *logits_in, int V, const int32_t *ctx, int L, float temperature, float top_p,
+                  int top_k, float rep_penalty, float r, double *cond);
+
+/* smp: temperature, top_p, top_k (as a float) per LmHead::sample, uniforms [B][n_new] the draws and
+ * cond [B][n_new] (or NULL) each step's conditioning; NULL = greedy */
+typedef struct {
+    float temperature, top_p;
+    int top_k;
+    const float *uniforms;
+    double *cond;
+} samp_cfg;
+
+static void decode_run(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
+                       const int32_t *prompt, int n_new, int ctx_len, float rep_penalty, const samp_cfg *smp,
                        int32_t *out_tokens, int nthreads) {
     const int d = c->d, H = c->H, V = c->V;
     const size_t hd = (size_t)H * d;
@@ -1120,8 +1132,17 @@ void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_we
                     solve_p(&p, &sc, q, NULL, h, NULL, 0, NULL);
                 }
                 lm_head_tok(c, w, lm_wt, h, NULL, lg, tmp);
-                repetition_penalty(lg, V, ctx, L, rep_penalty);
-                const int32_t tok = orc_argmax(lg, V);
+                int32_t tok;
+                if (smp) {
+                    const size_t jb = (size_t)b * n_new + j;
+                    double cd[2];
+                    tok = orc_lm_sample(lg, V, ctx, L, smp->temperature, smp->top_p, smp->top_k, rep_penalty,
+                                        smp->uniforms[jb], cd);
+                    if (smp->cond) smp->cond[jb] = cd[0];
+                } else {
+                    repetition_penalty(lg, V, ctx, L, rep_penalty);
+                    tok = orc_argmax(lg, V);
+                }
                 toks[len] = tok;
                 out_tokens[(size_t)b * n_new + j] = tok;
             }
@@ -1131,6 +1152,218 @@ void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_we
     }
     free(lm_wt);
     prep_free(&p);
+}
+
+void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
+                       const int32_t *prompt, int n_new, int ctx_len, float rep_penalty,
+                       int32_t *out_tokens, int nthreads) {
+    decode_run(c, w, hw, B, T0, prompt, n_new, ctx_len, rep_penalty, NULL, out_tokens, nthreads);
+}
+
+/* The same loop with LmHead::sample (lm_head.rs:78-168) in place of the arg-max (TRAINER:4410-4417):
+ * step j of sequence b draws with uniforms[b][j]; cond [B][n_new] (or NULL) receives each step's
+ * conditioning as orc_lm_sample gives it. */
+void orc_decode_sample(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
+                       const int32_t *prompt, int n_new, int ctx_len, float temperature, float top_p, int top_k,
+                       float rep_penalty, const float *uniforms, int32_t *out_tokens, double *cond,
+                       int nthreads) {
+    const samp_cfg smp = {temperature, top_p, top_k, uniforms, cond};
+    decode_run(c, w, hw, B, T0, prompt, n_new, ctx_len, rep_penalty, &smp, out_tokens, nthreads);
+}
+
+/* LmHead::sample's sorted list (lm_head.rs:115-117): probability descending by a stable sort,
+ * so equal probabilities keep index order. */
+typedef struct {
+    float p;
+    int32_t i;
+} samp_item;
+
+static int samp_cmp(const void *a, const void *b) {
+    const samp_item *x = (const samp_item *)a, *y = (const samp_item *)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return (x->i > y->i) - (x->i < y->i);
+}
+
+/* Conditioning of one decision, for the tests: the smallest ratio of a decisive distance to the
+ * rounding that could move it on a device with its own exp (within an ulp) and summation orders.
+ * >= 1: that device takes the same decision.  Order: the scaled logits of adjacent list items
+ * whose order decides differ by at least 5e-7 (four ulps of relative probability; equal logits
+ * give equal probabilities everywhere).  Cuts: where rounding could move the top-k cut (its two
+ * items' logits closer than that) or the top-p cut (the running sum within its own float error,
+ * twice, plus top_p times the float error of the softmax sum, plus 1e-7, of top_p), the kept
+ * weight may change by the items involved and the items from the first of them on may enter or
+ * leave: a draw landing there reads 0, any other has that weight added to its tolerance.  Draw:
+ * the normalised running sum lies from the draw by at least twice its float error plus 1e-7 plus
+ * that weight.  0 when the float running sums take another decision than the same sums in double. */
+static double samp_dw(const float *w, float mx, const samp_item *it, int a, int b) {
+    const float x = w[it[a].i], y = w[it[b].i];
+    if (x == y) return INFINITY;
+    /* exp(l - max) below 2^-150 is 0 on every device: such items are ordered by index alone */
+    if (it[a].p == 0.0f && it[b].p == 0.0f && fmaxf(x, y) - mx < -105.0f) return INFINITY;
+    return fabs((double)x - (double)y) / 5e-7;
+}
+
+/* LmHead::sample (lm_head.rs:78-168) with the draw r = rng.gen::<f32>() given (the reference
+ * draws it from thread_rng).  ctx [L] the context.  cond (or NULL) receives [2]: the
+ * conditioning above (INFINITY where no rounding enters: greedy, the fallback arg-max) and the
+ * length of the kept list (0 where there is none). */
+int orc_lm_sample(const float *logits_in, int V, const int32_t *ctx, int L, float temperature, float top_p,
+                  int top_k, float rep_penalty, float r, double *cond) {
+    if (cond) {
+        cond[0] = INFINITY;
+        cond[1] = 0.0;
+    }
+    if (V <= 0) return 0;
+    float *w = (float *)malloc(sizeof(float) * (size_t)V);
+    memcpy(w, logits_in, sizeof(float) * (size_t)V);
+    /* 1. repetition penalty (:81-99) */
+    repetition_penalty(w, V, ctx, L, rep_penalty);
+    /* 2. temperature (:103-111): a temperature in (0, 1e-4] takes the first branch */
+    if (temperature > 0.0f && fabsf(temperature - 1.0f) > 1e-4f) {
+        for (int v = 0; v < V; ++v) w[v] /= temperature;
+    } else if (temperature <= 1e-4f) {
+        const int t = orc_argmax(w, V);
+        free(w);
+        return t;
+    }
+    /* 3. softmax (:71-76): max by f32::max (NaN skipped), exp(l - max), the sum folded in index
+     * order, each exp divided by it */
+    float mx = -INFINITY;
+    for (int v = 0; v < V; ++v) mx = fmaxf(mx, w[v]);
+    samp_item *it = (samp_item *)malloc(sizeof(samp_item) * (size_t)V);
+    float S = 0.0f;
+    double S_d = 0.0;
+    for (int v = 0; v < V; ++v) {
+        it[v].p = expf(w[v] - mx);
+        it[v].i = v;
+    }
+    for (int v = 0; v < V; ++v) {
+        S += it[v].p;
+        S_d += (double)it[v].p;
+    }
+    /* a NaN sum makes every probability NaN; the kept sum then fails `sum > 1e-6` (:146-150) */
+    if (S != S) {
+        free(w);
+        free(it);
+        return orc_argmax(logits_in, V);
+    }
+    for (int v = 0; v < V; ++v) it[v].p = it[v].p / S;
+    qsort(it, (size_t)V, sizeof(samp_item), samp_cmp);
+    double cm = INFINITY;
+    /* a cut that rounding could move changes the kept weight by at most mshift and the membership
+     * of the items from position win on */
+    double mshift = 0.0;
+    int win = V;
+    /* 4. top-k (:120-125) */
+    int n = V;
+    const int k = top_k < V ? top_k : V;
+    if (k > 0 && k < V) {
+        n = k;
+        if (samp_dw(w, mx, it, k - 1, k) < 1.0) {
+            mshift += (double)it[k - 1].p + (double)it[k].p;
+            win = k - 1;
+        }
+    }
+    /* 5. top-p (:127-140) */
+    if (top_p > 0.0f && top_p < 1.0f) {
+        float cum = 0.0f;
+        double cd = 0.0;
+        int cut = n, cut_d = n;
+        for (int i = 0; i < n; ++i) {
+            cum += it[i].p;
+            if (cum > top_p) {
+                cut = i + 1;
+                break;
+            }
+        }
+        for (int i = 0; i < n; ++i) {
+            cd += (double)it[i].p;
+            if (cd > (double)top_p) {
+                cut_d = i + 1;
+                break;
+            }
+        }
+        /* the running sums just before and at the cut, in float and in double */
+        double before = 0.0;
+        float bf = 0.0f;
+        for (int i = 0; i + 1 < cut; ++i) {
+            before += (double)it[i].p;
+            bf += it[i].p;
+        }
+        const double at = before + (double)it[cut - 1].p;
+        const float af = bf + it[cut - 1].p;
+        const double err = fmax(fabs((double)bf - before), fabs((double)af - at));
+        const double tol = 2.0 * err + (double)top_p * fabs((double)S - S_d) / S_d + 1e-7;
+        double mp = ((double)top_p - before) / tol;
+        if (cut < n || n < V) mp = fmin(mp, fabs(at - (double)top_p) / tol);
+        if (cut < V) mp = fmin(mp, samp_dw(w, mx, it, cut - 1, cut));
+        if (cut != cut_d || mp < 1.0) {
+            /* the cut may move over the items whose running sum lies within 2 tol of top_p */
+            double acc = 0.0;
+            int i0 = 0;
+            while (i0 < n && acc + (double)it[i0].p < (double)top_p - 2.0 * tol) acc += (double)it[i0++].p;
+            win = i0 < win ? i0 : win;
+            mshift += 4.0 * tol + (double)it[cut - 1].p + (cut < V ? (double)it[cut].p : 0.0);
+        }
+        n = cut > 1 ? cut : 1;
+    }
+    /* 6. renormalisation (:142-150) */
+    float sum = -0.0f;
+    double sd = 0.0;
+    for (int i = 0; i < n; ++i) {
+        sum += it[i].p;
+        sd += (double)it[i].p;
+    }
+    if (!(sum > 1e-6f)) {
+        free(w);
+        free(it);
+        return orc_argmax(logits_in, V);
+    }
+    /* 7. the draw (:152-166) */
+    float cum = 0.0f;
+    int s = -1;
+    for (int i = 0; i < n; ++i) {
+        cum += it[i].p / sum;
+        if (r <= cum) {
+            s = i;
+            break;
+        }
+    }
+    /* the normalised running sums in double, and their float error up to the decision */
+    double cn = 0.0, err = 0.0;
+    float cf = 0.0f;
+    int s_d = -1;
+    double lo = INFINITY, hi = INFINITY, at = 1.0;
+    for (int i = 0; i < n; ++i) {
+        const double nx = cn + (double)it[i].p / sd;
+        cf += it[i].p / sum;
+        err = fmax(err, fabs((double)cf - nx));
+        if ((double)r <= nx) {
+            s_d = i;
+            hi = nx - (double)r;
+            if (i > 0) lo = (double)r - cn;
+            at = nx;
+            break;
+        }
+        cn = nx;
+    }
+    if (s_d < 0) lo = (double)r - cn;
+    cm = fmin(cm, fmin(lo, hi) / (2.0 * err + 1e-7 + at * mshift / sd));
+    if (s != s_d || (s >= 0 ? s : 0) >= win) cm = 0.0;
+    const int pos = s >= 0 ? s : 0;
+    if (s >= 0) {
+        if (pos > 0) cm = fmin(cm, samp_dw(w, mx, it, pos - 1, pos));
+        if (pos + 1 < n) cm = fmin(cm, samp_dw(w, mx, it, pos, pos + 1));
+    }
+    const int tok = it[pos].i;
+    if (cond) {
+        cond[0] = cm;
+        cond[1] = (double)n;
+    }
+    free(w);
+    free(it);
+    return tok;
 }
 
 /* ------------------------------------------------------------------------- */

@@ -130,6 +130,20 @@ void orc_model_free(orc_model *m);
 void orc_decode_greedy(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
                        const int32_t *prompt, int n_new, int ctx_len, float rep_penalty,
                        int32_t *out_tokens, int nthreads);
+/* The same loop with LmHead::sample in place of the arg-max: uniforms [B][n_new] the draws, cond
+ * [B][n_new] (or NULL) each step's conditioning (orc_lm_sample). */
+void orc_decode_sample(const orc_cfg *c, const orc_weights *w, const orc_hist_weights *hw, int B, int T0,
+                       const int32_t *prompt, int n_new, int ctx_len, float temperature, float top_p, int top_k,
+                       float rep_penalty, const float *uniforms, int32_t *out_tokens, double *cond,
+                       int nthreads);
+
+/* LmHead::sample (lm_head.rs:78-168): logits [V], context ctx [L], the draw r (rng.gen::<f32>()
+ * in the reference).  cond (or NULL) receives [2]: how far the decision lies from the roundings
+ * that could change it (>= 1: a device with its own exp and sum orders takes the same decision;
+ * 0: the float running sums already decide otherwise than the same sums in double), and the
+ * length of the kept list (0 for greedy or the fallback arg-max). */
+int orc_lm_sample(const float *logits_in, int V, const int32_t *ctx, int L, float temperature, float top_p,
+                  int top_k, float rep_penalty, float r, double *cond);
 
 /* --- other trait surfaces --------------------------------------------------- */
 /* Clean adjoint Picard (staged_adjoint_picard_clean.wgsl:143-337; driver gpu_deq.rs:4736-4975):

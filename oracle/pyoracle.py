@@ -85,6 +85,12 @@ def lib():
         L.orc_model_free.argtypes = [C.c_void_p]
         L.orc_decode_greedy.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcHistWeights),
                                         C.c_int, C.c_int, I32P, C.c_int, C.c_int, C.c_float, I32P, C.c_int]
+        L.orc_decode_sample.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcHistWeights),
+                                        C.c_int, C.c_int, I32P, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int,
+                                        C.c_float, F32P, I32P, C.POINTER(C.c_double), C.c_int]
+        L.orc_lm_sample.restype = C.c_int
+        L.orc_lm_sample.argtypes = [F32P, C.c_int, I32P, C.c_int, C.c_float, C.c_float, C.c_int, C.c_float,
+                                    C.c_float, C.POINTER(C.c_double)]
         L.orc_hist_ctx.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcHistWeights), F32P, F32P, F32P]
         L.orc_temporal_step.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), F32P, F32P, F32P]
         L.orc_forward_memory.argtypes = [C.POINTER(OrcCfg), C.POINTER(OrcWeights), C.POINTER(OrcHistWeights),
@@ -260,6 +266,21 @@ class Oracle:
         return out
 
 
+    def decode_sample(self, prompt, n_new, ctx_len, temperature, top_p, top_k, rep_penalty, uniforms,
+                      nthreads=0):
+        """The same loop with LmHead::sample: uniforms [B][n_new] the draws -> (tokens [B][n_new],
+        each step's conditioning [B][n_new], >= 1 where rounding cannot change the draw)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        B, T0 = prompt.shape
+        uni = np.ascontiguousarray(uniforms, np.float32).reshape(B, n_new)
+        out = np.zeros((B, n_new), np.int32)
+        cond = np.zeros((B, n_new), np.float64)
+        self.L.orc_decode_sample(C.byref(self.c), C.byref(self.w), C.byref(self.hw), B, T0, ip(prompt), n_new,
+                                 ctx_len, float(temperature), float(top_p), int(top_k), float(rep_penalty),
+                                 fp(uni), ip(out), cond.ctypes.data_as(C.POINTER(C.c_double)), nthreads)
+        return out, cond
+
+
 class _Prepared:
     def __init__(self, o: "Oracle"):
         self.o = o
@@ -363,6 +384,17 @@ def anderson_coeffs(g: np.ndarray) -> np.ndarray:
 def argmax(logits: np.ndarray) -> int:
     logits = np.ascontiguousarray(logits, np.float32)
     return lib().orc_argmax(fp(logits), logits.size)
+
+
+def lm_sample(logits, context, temperature: float, top_p: float, top_k: int, rep_penalty: float, r: float):
+    """LmHead::sample (lm_head.rs:78-168) with the draw r given: (token, conditioning, length of
+    the kept list)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    ctx = np.ascontiguousarray(context if context is not None else [], np.int32)
+    cond = (C.c_double * 2)()
+    t = lib().orc_lm_sample(fp(logits), logits.size, ip(ctx), ctx.size, float(temperature), float(top_p),
+                            int(top_k), float(rep_penalty), float(r), cond)
+    return t, cond[0], int(cond[1])
 
 
 def zoh_step(x, dt, a, b, c):
