@@ -312,35 +312,45 @@ __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *
 }
 
 // ---- LmHead::sample (lm_head.rs:78-168) ------------------------------------------------------
-// One workgroup per logits row.  The row goes through a workspace row ws[V]: the penalised and
-// scaled logits, then e = exp(l - max), then the bit pattern ("key") of p = e / S.  p lies in
-// [0, 1] (the maximum contributes exp(0) = 1 to S), so keys order as p does, and the reference's
-// sorted list (p descending by a stable sort: ties keep index order) is the order "key
-// descending, index ascending".  A probability weighs floor(p * 2^60) in exact integer sums
-// (the sum over a row stays below 2^61).
+// The per-element work runs over many workgroups per row (SP_EPB elements each), through a
+// workspace row ws[V]: k_samp_scale writes the penalised and scaled logits and each block's
+// maximum; k_samp_exp writes e = exp(l - max) and each block's sum; k_samp_keys writes the bit
+// pattern ("key") of p = e / S and each block's histogram of count and weight over SP_NBIN bins
+// of p below its largest value (128 per octave).  p lies in [0, 1] (the maximum contributes exp(0) = 1 to S),
+// so keys order as p does, and the reference's sorted list (p descending by a stable sort: ties
+// keep index order) is the order "key descending, index ascending".  A probability weighs
+// floor(p * 2^60) in exact integer sums (the sum over a row stays below 2^61).
 //
-// The cut points of the list (the top_k-th item, the first item past which the running sum
-// exceeds top_p, the item at which it reaches the draw) are found without sorting the row: three
-// 10-bit radix levels over the keys with LDS histograms of counts and weights, then the item of
-// the equal-key group in index order.  When the kept list has at most SP_CAP items (top_k <=
+// k_sample (one workgroup per row) takes the cut points of the list (the top_k-th item, the
+// first item past which the running sum exceeds top_p, the item at which it reaches the draw)
+// without sorting the row: the row's bin histogram names the bin of the crossing, 256-bin LDS
+// histograms of the items inside it narrow it further where it holds more than SP_CAP items, and
+// an interval of at most SP_CAP items is gathered, sorted in LDS and scanned.  When the kept list has at most SP_CAP items (top_k <=
 // SP_CAP, or a top_p cut within that many items, or a vocabulary that small) it is gathered,
-// sorted in LDS, and one thread runs the reference's loops on it in float arithmetic; otherwise
-// the cuts are taken on the exact sums.
-constexpr int SP_NT = 1024;
-constexpr int SP_CAP = 2048;
-constexpr double SP_ONE = 1152921504606846976.0;  // 2^60
+// sorted, and one thread runs the reference's loops on it in float arithmetic; otherwise the cuts
+// are taken on the exact sums.
+constexpr int SP_NT = 1024;          // k_sample's threads
+constexpr int SP_CAP = 2048;         // lists sorted in LDS
+constexpr int SP_PT = 256;           // threads of the per-element kernels
+constexpr int SP_EPB = SP_PT * 8;    // elements per block of the per-element kernels
+constexpr int SP_NBIN = 1024;        // bins of p below the largest: 128 per octave over 8 octaves
+constexpr int SP_BSH = 16;           // (the last takes all below); a bin spans 2^16 key values
+static_assert(SP_NBIN == SP_NT, "k_sample's thread t takes bin t");
 typedef unsigned long long u64;
 
 struct SampleSmem {
-    unsigned hc[SP_NT];  // one bucket per thread
+    unsigned hc[SP_NT];  // sub-interval bins / wave partials
     u64 hm[SP_NT];
     u64 list[SP_CAP];  // (~key << 32) | index: ascending = key descending, index ascending
+    unsigned oc[SP_NBIN];  // the row's bins (sums of the blocks' histograms)
+    u64 om[SP_NBIN];
     u64 wc[SP_NT / 64], wm[SP_NT / 64];
     float wf[SP_NT / 64];
     int wi[SP_NT / 64];
-    u64 bc, bm;
-    unsigned cnt;
-    int tok, need_exact;
+    float wf2[SP_NT];  // the blocks' partial sums
+    u64 bc, bm, bn;
+    unsigned cnt, blo, bhi;
+    int tok, need_exact, bsel;
 };
 
 struct SpCut {  // keeps the items up to and including (key, idx) in the list order; `on` false keeps all
@@ -356,29 +366,65 @@ struct SpSel {  // an item and the count and weight of the list up to and includ
     bool found;
 };
 
-__device__ __forceinline__ u64 sp_mass(unsigned k) { return (u64)((double)__uint_as_float(k) * SP_ONE); }
+// f(i, value, u) over this thread's elements i = tid + u * SP_NT of ws, in index order, the
+// loads of each batch of 8 issued together; every lane takes every step (value 0 for i >= V,
+// which f must skip), so f may use wave-wide operations
+template <int KPT, typename F>
+__device__ __forceinline__ void sp_each(const unsigned *ws, int V, F &&f) {
+    constexpr int BT = KPT < 8 ? KPT : 8;
+#pragma unroll 1
+    for (int b0 = 0; b0 < KPT; b0 += BT) {
+        unsigned kb[BT];
+#pragma unroll
+        for (int v = 0; v < BT; ++v) {
+            const int i = threadIdx.x + (b0 + v) * SP_NT;
+            kb[v] = i < V ? ws[i] : 0u;
+        }
+#pragma unroll
+        for (int v = 0; v < BT; ++v) f(threadIdx.x + (b0 + v) * SP_NT, kb[v], b0 + v);
+    }
+}
+
+// Gather of the elements pred(i, k) selects into sm.list as (~key << 32) | index, in index order of
+// threads (the caller sorts): a count pass, a block scan of the counts, a write pass.  At most
+// SP_CAP are written; returns how many there are.
+template <int KPT, typename P>
+__device__ unsigned sp_gather(const unsigned *ws, int V, P &&pred, struct SampleSmem &sm);
+
+// floor(p * 2^60) from p's bit pattern: p = m 2^(max(e, 1) - 150)
+__device__ __forceinline__ u64 sp_mass(unsigned k) {
+    const int e = (int)(k >> 23);
+    const u64 m = (k & 0x7fffffu) | (e ? 0x800000u : 0u);
+    const int sh = (e ? e : 1) - 90;
+    return sh >= 0 ? (m << sh) : (sh > -64 ? (m >> -sh) : 0ull);
+}
 
 __device__ __forceinline__ bool sp_in(const SpCut &c, unsigned k, int i) {
     return !c.on || k > c.key || (k == c.key && i <= c.idx);
 }
 
-__device__ float sp_max(float v, SampleSmem &sm) {
+// the bin of key k below the largest key khi (k <= khi)
+__device__ __forceinline__ int sp_bin(unsigned khi, unsigned k) { return min(SP_NBIN - 1, (int)((khi - k) >> SP_BSH)); }
+
+template <int NT>
+__device__ float sp_bmax(float v, float *red) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    if ((threadIdx.x & 63) == 0) sm.wf[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    v = sm.wf[0];
-    for (int u = 1; u < SP_NT / 64; ++u) v = fmaxf(v, sm.wf[u]);
+    v = red[0];
+    for (int u = 1; u < NT / 64; ++u) v = fmaxf(v, red[u]);
     __syncthreads();
     return v;
 }
 
 // the block's sum in a fixed order (wave butterflies, then the waves in order)
-__device__ float sp_sum(float v, SampleSmem &sm) {
+template <int NT>
+__device__ float sp_bsum(float v, float *red) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    if ((threadIdx.x & 63) == 0) sm.wf[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    v = sm.wf[0];
-    for (int u = 1; u < SP_NT / 64; ++u) v += sm.wf[u];
+    v = red[0];
+    for (int u = 1; u < NT / 64; ++u) v += red[u];
     __syncthreads();
     return v;
 }
@@ -408,95 +454,331 @@ __device__ void sp_scan(u64 &c, u64 &m, SampleSmem &sm) {
     __syncthreads();
 }
 
+// 1. the repetition penalty (lm_head.rs:81-99: the context's distinct tokens, here a bit set of
+// the block's range), 2. the temperature (:103-111; none with `greedy`), the block's maximum as
+// f32::max folds it (NaN skipped)
+__global__ __launch_bounds__(SP_PT) void k_samp_scale(const float *logits, int V, float *w, float *pmax,
+                                                      SampleParams a) {
+    __shared__ unsigned bits[SP_EPB / 32];
+    __shared__ float red[SP_PT / 64];
+    const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int i0 = b * SP_EPB;
+    const float *lg = logits + (long)row * V;
+    float *wr = w + (long)row * V;
+    const int len = a.lens ? a.lens[row] : a.len;
+    const int start = len > a.window ? len - a.window : 0, L = len - start;
+    const bool pen = fabsf(a.penalty - 1.0f) > 1e-4f && L > 0;
+    if (pen) {
+        for (int q = tid; q < SP_EPB / 32; q += SP_PT) bits[q] = 0u;
+        __syncthreads();
+        const int32_t *tk = a.seq + (long)row * a.stride + start;
+        for (int p = tid; p < L; p += SP_PT) {
+            const int t = tk[p] - i0;
+            if (t >= 0 && t < SP_EPB && t + i0 < V) atomicOr(&bits[t >> 5], 1u << (t & 31));
+        }
+        __syncthreads();
+    }
+    const float Tm = a.temperature;
+    const bool scale = !a.greedy && Tm > 0.0f && fabsf(Tm - 1.0f) > 1e-4f;
+    float v[SP_EPB / SP_PT];
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int i = i0 + tid + e * SP_PT;
+        v[e] = i < V ? lg[i] : 0.0f;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int o = tid + e * SP_PT, i = i0 + o;
+        if (i < V) {
+            float x = v[e];
+            if (pen && ((bits[o >> 5] >> (o & 31)) & 1u)) x = x < 0.0f ? x * a.penalty : x / a.penalty;
+            if (scale) x = x / Tm;
+            wr[i] = x;
+            mx = fmaxf(mx, x);
+        }
+    }
+    mx = sp_bmax<SP_PT>(mx, red);
+    if (tid == 0) pmax[(long)row * NB + b] = mx;
+}
+
+// e = exp(l - max) and the block's sum (softmax, lm_head.rs:71-76)
+__global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float *pmax, float *psum) {
+    __shared__ float red[SP_PT / 64];
+    __shared__ float part[SP_PT];
+    const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int i0 = b * SP_EPB;
+    float *wr = w + (long)row * V;
+    for (int q = tid; q < NB; q += SP_PT) part[q] = pmax[(long)row * NB + q];
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int q = 0; q < NB; ++q) mx = fmaxf(mx, part[q]);
+    float v[SP_EPB / SP_PT];
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int i = i0 + tid + e * SP_PT;
+        v[e] = i < V ? wr[i] : 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int i = i0 + tid + e * SP_PT;
+        if (i < V) {
+            const float x = expf(v[e] - mx);
+            wr[i] = x;
+            s += x;
+        }
+    }
+    s = sp_bsum<SP_PT>(s, red);
+    if (tid == 0) psum[(long)row * NB + b] = s;
+}
+
+// S = the blocks' sums in block order; the keys, and the block's histogram of them by bin
+__global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const float *psum, unsigned *hc, u64 *hm) {
+    __shared__ unsigned c[SP_NBIN];
+    __shared__ u64 m[SP_NBIN];
+    __shared__ float part[SP_PT];
+    const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int i0 = b * SP_EPB;
+    unsigned *wr = w + (long)row * V;
+    for (int q = tid; q < NB; q += SP_PT) part[q] = psum[(long)row * NB + q];
+    __syncthreads();
+    float S = 0.0f;
+    for (int q = 0; q < NB; ++q) S += part[q];
+    if (!(S == S)) return;  // k_sample takes the arg-max of the row as given
+    const unsigned khi = __float_as_uint(1.0f / S);
+    for (int q = tid; q < SP_NBIN; q += SP_PT) {
+        c[q] = 0u;
+        m[q] = 0ull;
+    }
+    __syncthreads();
+    unsigned v[SP_EPB / SP_PT];
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int i = i0 + tid + e * SP_PT;
+        v[e] = i < V ? wr[i] : 0u;
+    }
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int i = i0 + tid + e * SP_PT;
+        if (i < V) {
+            const unsigned k = __float_as_uint(__uint_as_float(v[e]) / S);
+            wr[i] = k;
+            const int d = sp_bin(khi, k);
+            atomicAdd(&c[d], 1u);
+            atomicAdd(&m[d], sp_mass(k));
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < SP_NBIN; q += SP_PT) {
+        hc[((long)row * NB + b) * SP_NBIN + q] = c[q];
+        hm[((long)row * NB + b) * SP_NBIN + q] = m[q];
+    }
+}
+
 // The first item of the list that `cut` keeps at which the running count (by_mass false) or the
-// running weight (true) exceeds T.  Not found: cnt and mass are the kept list's totals.
-__device__ SpSel sp_select(const unsigned *wk, int V, bool by_mass, u64 T, const SpCut &cut, SampleSmem &sm) {
-    const int tid = threadIdx.x;
-    u64 cb = 0, mb = 0;  // the items before the current key prefix
-    unsigned prefix = 0;
-    for (int lv = 0; lv < 3; ++lv) {
-        const int sh = 20 - 10 * lv;  // keys of p <= 1 are below 2^30
+// running weight (true) exceeds T.  Not found: cnt and mass are the kept list's totals.  The
+// row's bin histogram (sm.oc, sm.om) names the bin of the crossing (with a cut, the cut item's bin
+// is recounted and the bins below it are empty); 256-bin histograms of the items inside the
+// interval narrow it until it holds at most SP_CAP items, which are gathered, sorted and scanned;
+// one key value held by more (equal probabilities) is searched in index order.
+template <int KPT>
+__device__ __noinline__ SpSel sp_select(const unsigned *ws, int V, bool by_mass, u64 T, const SpCut &cut, unsigned khi,
+                                        SampleSmem &sm) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int dcut = cut.on ? sp_bin(khi, cut.key) : SP_NBIN - 1;
+    u64 cp = 0, mp = 0;  // the kept items of the cut item's bin
+    if (cut.on) {
+        sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
+            if (i < V && sp_bin(khi, k) == dcut && sp_in(cut, k, i)) {
+                cp += 1;
+                mp += sp_mass(k);
+            }
+        });
+        sp_scan(cp, mp, sm);
+        if (tid == SP_NT - 1) {
+            sm.bc = cp;
+            sm.bm = mp;
+        }
+        __syncthreads();
+        cp = sm.bc;
+        mp = sm.bm;
+        __syncthreads();
+    }
+    // bin tid (SP_NT == SP_NBIN) as the cut keeps it; the running sums over the bins in order
+    const u64 cd = tid < dcut ? sm.oc[tid] : (tid == dcut ? (cut.on ? cp : sm.oc[tid]) : 0ull);
+    const u64 md = tid < dcut ? sm.om[tid] : (tid == dcut ? (cut.on ? mp : sm.om[tid]) : 0ull);
+    u64 ic = cd, im = md;
+    sp_scan(ic, im, sm);
+    const int dd0 = __syncthreads_count(!((by_mass ? im : ic) > T));  // the bins before the crossing
+    if (dd0 == SP_NBIN && tid == SP_NT - 1) {  // no crossing: the totals
+        sm.bc = ic;
+        sm.bm = im;
+    }
+    if (dd0 < SP_NBIN && tid == dd0) {
+        sm.bc = ic - cd;
+        sm.bm = im - md;
+        sm.bn = cd;
+        // bin dd0: keys in [khi + 1 - (dd0 + 1) 2^16, khi + 1 - dd0 2^16) (the last bin down to 0)
+        const u64 top = (u64)khi + 1;
+        const u64 lo = dd0 == SP_NBIN - 1 ? 0 : (top > ((u64)(dd0 + 1) << SP_BSH) ? top - ((u64)(dd0 + 1) << SP_BSH) : 0);
+        sm.blo = (unsigned)lo;
+        sm.bhi = (unsigned)(top - ((u64)dd0 << SP_BSH));
+    }
+    __syncthreads();
+    const int dd = dd0 < SP_NBIN ? dd0 : -1;
+    u64 cb = sm.bc, mb = sm.bm, n_int = sm.bn;
+    unsigned lo = sm.blo, hi = sm.bhi;
+    __syncthreads();
+    if (dd < 0) return SpSel{0u, -1, cb, mb, false};
+    for (int pass = 0; pass < 8 && n_int > (u64)SP_CAP && hi - lo > 1u; ++pass) {
+        // 256 bins over [lo, hi)
+        const unsigned wd = hi - lo;
+        int sh = 0;
+        while (((wd - 1u) >> sh) >= 256u) ++sh;
         sm.hc[tid] = 0u;
         sm.hm[tid] = 0ull;
         __syncthreads();
-        for (int i = tid; i < V; i += SP_NT) {
-            const unsigned k = wk[i];
-            if (!sp_in(cut, k, i) || (lv > 0 && (k >> (sh + 10)) != prefix)) continue;
-            const unsigned b = (k >> sh) & 1023u;
-            atomicAdd(&sm.hc[b], 1u);
-            atomicAdd(&sm.hm[b], sp_mass(k));
-        }
-        __syncthreads();
-        u64 c = sm.hc[SP_NT - 1 - tid], m = sm.hm[SP_NT - 1 - tid];  // buckets from the largest key down
-        sp_scan(c, m, sm);
-        const bool ok = (by_mass ? mb + m : cb + c) > T;
-        const int ts = __syncthreads_count(!ok);  // the running sums only grow: the buckets before the crossing
-        if (ts == SP_NT) {
-            if (tid == SP_NT - 1) {
-                sm.bc = c;
-                sm.bm = m;
+        sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
+            if (i < V && k >= lo && k < hi && sp_in(cut, k, i)) {
+                const unsigned bn = (k - lo) >> sh;
+                atomicAdd(&sm.hc[bn], 1u);
+                atomicAdd(&sm.hm[bn], sp_mass(k));
             }
-            __syncthreads();
-            const SpSel r{0u, -1, cb + sm.bc, mb + sm.bm, false};
-            __syncthreads();
-            return r;
-        }
-        if (ts > 0 && tid == ts - 1) {
-            sm.bc = c;
-            sm.bm = m;
-        }
-        if (ts == 0 && tid == 0) {
-            sm.bc = 0;
-            sm.bm = 0;
-        }
+        });
         __syncthreads();
-        cb += sm.bc;
-        mb += sm.bm;
-        prefix = (prefix << 10) | (unsigned)(SP_NT - 1 - ts);
-        __syncthreads();
-    }
-    // the crossing lies in the group of items with key == prefix, each weighing mu
-    const unsigned key = prefix;
-    const u64 mu = sp_mass(key);
-    const u64 j = by_mass ? (mu ? (T - mb) / mu : 0) : T - cb;
-    // its j-th item in index order: a thread takes a contiguous index range
-    const int CH = (V + SP_NT - 1) / SP_NT;
-    const int i0 = min(V, tid * CH), i1 = min(V, i0 + CH);
-    u64 n = 0;
-    for (int i = i0; i < i1; ++i) {
-        const unsigned k = wk[i];
-        n += (k == key && sp_in(cut, k, i)) ? 1 : 0;
-    }
-    u64 incl = n, unused = 0;
-    sp_scan(incl, unused, sm);
-    if (tid == 0) sm.tok = -1;
-    __syncthreads();
-    if (j >= incl - n && j < incl) {
-        u64 q = incl - n;
-        for (int i = i0; i < i1; ++i) {
-            const unsigned k = wk[i];
-            if (k == key && sp_in(cut, k, i)) {
-                if (q == j) {
-                    sm.tok = i;
+        if (tid == 0) {
+            const int nb = (int)((wd - 1u) >> sh) + 1;
+            u64 c2 = cb, m2 = mb;
+            int sel = 0;
+            for (int q = nb - 1; q >= 0; --q) {  // the largest keys first
+                if ((by_mass ? m2 + sm.hm[q] : c2 + sm.hc[q]) > T) {
+                    sel = q;
                     break;
                 }
-                ++q;
+                c2 += sm.hc[q];
+                m2 += sm.hm[q];
             }
+            sm.bc = c2;
+            sm.bm = m2;
+            sm.bn = sm.hc[sel];
+            sm.blo = lo + ((unsigned)sel << sh);
+            sm.bhi = min(hi, lo + ((unsigned)(sel + 1) << sh));
         }
+        __syncthreads();
+        cb = sm.bc;
+        mb = sm.bm;
+        n_int = sm.bn;
+        lo = sm.blo;
+        hi = sm.bhi;
+        __syncthreads();
+    }
+    if (n_int <= (u64)SP_CAP) {
+        // the interval's items, sorted; the running sums from (cb, mb) find the crossing
+        sp_gather<KPT>(ws, V, [&](int i, unsigned k) { return k >= lo && k < hi && sp_in(cut, k, i); }, sm);
+        const int n = (int)n_int;
+        int n2 = 2;
+        while (n2 < n) n2 <<= 1;
+        for (int k = 2; k <= n2; k <<= 1)
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                if (tid < n2 / 2) {
+                    const int i = 2 * tid - (tid & (j - 1)), l = i + j;
+                    const u64 xa = sm.list[i], ya = sm.list[l];
+                    if ((xa > ya) == ((i & k) == 0)) {
+                        sm.list[i] = ya;
+                        sm.list[l] = xa;
+                    }
+                }
+                __syncthreads();
+            }
+        // entries 2 tid and 2 tid + 1: inclusive running sums, then the first past T
+        const int e0 = 2 * tid, e1 = 2 * tid + 1;
+        const u64 m0 = e0 < n ? sp_mass(~(unsigned)(sm.list[e0] >> 32)) : 0ull;
+        const u64 m1 = e1 < n ? sp_mass(~(unsigned)(sm.list[e1] >> 32)) : 0ull;
+        u64 ic = (u64)(e0 < n) + (u64)(e1 < n), im = m0 + m1;
+        sp_scan(ic, im, sm);
+        const u64 v0 = by_mass ? mb + im - m1 : cb + ic - (u64)(e1 < n);
+        const u64 v1 = by_mass ? mb + im : cb + ic;
+        const bool p0 = e0 < n && v0 > T, p1 = e1 < n && v1 > T;
+        const int before = __syncthreads_count(e0 < n && !p0) + __syncthreads_count(e1 < n && !p1);
+        if (tid == 0) sm.tok = -1;
+        __syncthreads();
+        if (before < n && (e0 == before || e1 == before)) {
+            sm.tok = (int)(unsigned)(sm.list[before] & 0xffffffffull);
+            sm.bm = mb + (e0 == before ? im - m1 : im);
+            sm.bc = ~(unsigned)(sm.list[before] >> 32);
+        }
+        __syncthreads();
+        const SpSel r{(unsigned)sm.bc, sm.tok, cb + (u64)before + 1, sm.bm, sm.tok >= 0};
+        __syncthreads();
+        return r;
+    }
+    // one key value (lo) held by more than SP_CAP items, each weighing mu: the j-th in index order
+    // (slot u first, then thread), from this thread's matches as a bit per slot
+    const unsigned kk = lo;
+    const u64 mu = sp_mass(kk);
+    const u64 j = by_mass ? (mu ? (T - mb) / mu : 0) : T - cb;
+    u64 mine = 0;
+    sp_each<KPT>(ws, V, [&](int i, unsigned k, int u) {
+        if (i < V && k == kk && sp_in(cut, k, i)) mine |= 1ull << u;
+    });
+    if (tid == 0) sm.tok = -1;
+    u64 run = 0;
+    for (int u = 0; u < KPT; ++u) {
+        const bool pr = (mine >> u) & 1ull;
+        const int cu = __syncthreads_count(pr);
+        if (run + (u64)cu > j) {
+            const u64 bal = __ballot(pr);
+            if (lane == 0) sm.wi[w] = __popcll(bal);
+            __syncthreads();
+            int bw = 0;
+            for (int x = 0; x < w; ++x) bw += sm.wi[x];
+            const int rank = bw + __popcll(bal & ((1ull << lane) - 1ull));
+            if (pr && (u64)rank == j - run) sm.tok = tid + u * SP_NT;
+            break;
+        }
+        run += (u64)cu;
     }
     __syncthreads();
-    const SpSel r{key, sm.tok, cb + j + 1, mb + (j + 1) * mu, sm.tok >= 0};
+    const SpSel r{kk, sm.tok, cb + j + 1, mb + (j + 1) * mu, sm.tok >= 0};
     __syncthreads();
     return r;
 }
 
-// LmHead::argmax (lm_head.rs:62-69) as Iterator::max_by folds: NaN compares Equal, so the fold
-// restarts after the last NaN and returns the last maximum after it (the NaN itself when last).
+template <int KPT, typename P>
+__device__ unsigned sp_gather(const unsigned *ws, int V, P &&pred, SampleSmem &sm) {
+    u64 n = 0, unused = 0;
+    sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
+        if (i < V && pred(i, k)) ++n;
+    });
+    const u64 mine = n;
+    sp_scan(n, unused, sm);  // inclusive
+    if (threadIdx.x == SP_NT - 1) sm.cnt = (unsigned)n;
+    u64 q = n - mine;
+    for (int u = threadIdx.x; u < SP_CAP; u += SP_NT) sm.list[u] = ~0ull;
+    __syncthreads();
+    sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
+        if (i < V && pred(i, k)) {
+            if (q < (u64)SP_CAP) sm.list[q] = ((u64)(~k) << 32) | (unsigned)i;
+            ++q;
+        }
+    });
+    __syncthreads();
+    return sm.cnt;
+}
+
+// LmHead::argmax (lm_head.rs:62-69) as Iterator::max_by folds over x[0, V): NaN compares Equal,
+// so the fold restarts after the last NaN and returns the last maximum after it (the NaN itself
+// when last).
+template <int KPT>
 __device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const unsigned *xb = reinterpret_cast<const unsigned *>(x);
     int jn = -1;
-    for (int i = tid; i < V; i += SP_NT)
-        if (x[i] != x[i]) jn = i;
+    sp_each<KPT>(xb, V, [&](int i, unsigned b, int) {
+        const float v = __uint_as_float(b);
+        if (i < V && v != v) jn = i;
+    });
     for (int off = 32; off > 0; off >>= 1) jn = max(jn, __shfl_xor(jn, off, 64));
     if (lane == 0) sm.wi[w] = jn;
     __syncthreads();
@@ -505,13 +787,13 @@ __device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
     __syncthreads();
     float bv = -INFINITY;
     int bi = -1;
-    for (int i = tid; i < V; i += SP_NT) {
-        const float v = x[i];
-        if (i > jn && !(v < bv)) {
+    sp_each<KPT>(xb, V, [&](int i, unsigned b, int) {
+        const float v = __uint_as_float(b);
+        if (i < V && i > jn && !(v < bv)) {
             bv = v;
             bi = i;
         }
-    }
+    });
     for (int off = 32; off > 0; off >>= 1) {
         const float v2 = __shfl_xor(bv, off, 64);
         const int i2 = __shfl_xor(bi, off, 64);
@@ -529,72 +811,47 @@ __device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
     return bi >= 0 ? bi : (jn >= 0 ? jn : 0);
 }
 
-__global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, unsigned *ws, SampleParams a,
-                                                  int32_t *out, TokenAppend app) {
+template <int KPT>
+__global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, int NB, unsigned *ws, const float *psum,
+                                                  const unsigned *hc, const u64 *hm, SampleParams a, int32_t *out,
+                                                  TokenAppend app) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *lg = logits + (long)row * V;
     unsigned *wk = ws + (long)row * V;
-    float *wf = reinterpret_cast<float *>(wk);
-    // 1. the row, then the repetition penalty once per distinct context token (lm_head.rs:81-99)
-    for (int i = tid; i < V; i += SP_NT) wf[i] = lg[i];
-    __syncthreads();
-    const int len = a.lens ? a.lens[row] : a.len;
-    const int start = len > a.window ? len - a.window : 0, L = len - start;
-    if (fabsf(a.penalty - 1.0f) > 1e-4f && L > 0) {
-        const int32_t *tk = a.seq + (long)row * a.stride + start;
-        for (int p = tid; p < L; p += SP_NT) {
-            const int tok = tk[p];
-            bool seen = false;
-            for (int u = 0; u < p && !seen; ++u) seen = tk[u] == tok;
-            if (seen || tok < 0 || tok >= V) continue;
-            const float sc = wf[tok];
-            wf[tok] = sc < 0.0f ? sc * a.penalty : sc / a.penalty;
-        }
-    }
-    __syncthreads();
-    if (a.greedy) {
-        const int g = sp_argmax(wf, V, sm);
+    if (a.greedy) {  // lm_head.rs:104-111: the arg-max of the penalised row
+        const int g = sp_argmax<KPT>(reinterpret_cast<const float *>(wk), V, sm);
         if (tid == 0) am_store(out, row, g, app);
         return;
     }
-    // 2. the temperature (lm_head.rs:103-111), the
-    // maximum as f32::max folds it (NaN skipped), e = exp(l - max) and S (softmax, :71-76).  From
-    // here each thread touches only its own elements until the keys are complete.
-    const float Tm = a.temperature;
-    const bool scale = Tm > 0.0f && fabsf(Tm - 1.0f) > 1e-4f;
-    float mx = -INFINITY;
-    for (int i = tid; i < V; i += SP_NT) {
-        float v = wf[i];
-        if (scale) {
-            v = v / Tm;
-            wf[i] = v;
-        }
-        mx = fmaxf(mx, v);
-    }
-    mx = sp_max(mx, sm);
-    float s = 0.0f;
-    for (int i = tid; i < V; i += SP_NT) {
-        const float e = (float)exp((double)(wf[i] - mx));  // exp rounded once to float
-        wf[i] = e;
-        s += e;
-    }
-    const float S = sp_sum(s, sm);
+    // the blocks' partials staged through LDS (one load per thread, not a chain of loads)
+    for (int q = tid; q < NB; q += SP_NT) sm.wf2[q] = psum[(long)row * NB + q];
+    __syncthreads();
+    float S = 0.0f;
+    for (int q = 0; q < NB; ++q) S += sm.wf2[q];
     const float r = a.uni[(long)row * a.uni_stride];
     int tok = -2;  // -2: LmHead::argmax of the row as given (lm_head.rs:148-150)
     // a NaN S (a NaN or infinite logit, or no finite one) makes every p NaN: the reference's kept
     // sum then fails `sum > 1e-6`
     if (S == S) {
-        u64 tm = 0;
-        for (int i = tid; i < V; i += SP_NT) {
-            const unsigned k = __float_as_uint(wf[i] / S);
-            wk[i] = k;
-            tm += sp_mass(k);
+        const unsigned khi = __float_as_uint(1.0f / S);  // the largest key: exp(0) / S
+        {
+            // bin tid over the blocks (NB <= 32), the loads issued together
+            unsigned c = 0u;
+            u64 m = 0ull;
+#pragma unroll
+            for (int q = 0; q < (SAMPLE_VMAX + SP_EPB - 1) / SP_EPB; ++q)
+                if (q < NB) {
+                    c += hc[((long)row * NB + q) * SP_NBIN + tid];
+                    m += hm[((long)row * NB + q) * SP_NBIN + tid];
+                }
+            sm.oc[tid] = c;
+            sm.om[tid] = m;
+            u64 cc = c, mm = m;
+            sp_scan(cc, mm, sm);
+            if (tid == SP_NT - 1) sm.bm = mm;
+            __syncthreads();
         }
-        u64 unused = 0;
-        sp_scan(tm, unused, sm);  // the last thread's inclusive value is the total
-        if (tid == SP_NT - 1) sm.bm = tm;
-        __syncthreads();
         const u64 total = sm.bm;
         __syncthreads();
         const bool kon = a.top_k > 0 && a.top_k < V, pon = a.top_p > 0.0f && a.top_p < 1.0f;
@@ -603,7 +860,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, un
         SpCut ck = none;
         u64 nk = (u64)V, mk = total;
         if (kon) {
-            const SpSel sk = sp_select(wk, V, false, (u64)(a.top_k - 1), none, sm);
+            const SpSel sk = sp_select<KPT>(wk, V, false, (u64)(a.top_k - 1), none, khi, sm);
             ck = SpCut{true, sk.key, sk.idx};
             nk = sk.cnt;
             mk = sk.mass;
@@ -614,7 +871,8 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, un
         u64 M = nk;
         bool full = true;
         if (!(kon && a.top_k <= SP_CAP) && pon) {
-            const SpSel sp = sp_select(wk, V, true, (u64)((double)a.top_p * SP_ONE) + (1ull << 50), ck, sm);
+            const SpSel sp = sp_select<KPT>(wk, V, true, (u64)((double)a.top_p * 1152921504606846976.0) + (1ull << 50),
+                                            ck, khi, sm);
             if (sp.found) {
                 cl = SpCut{true, sp.key, sp.idx};
                 M = sp.cnt;
@@ -623,30 +881,21 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, un
         }
         bool exact = M > (u64)SP_CAP;
         if (!exact) {
+            sp_gather<KPT>(wk, V, [&](int i, unsigned k) { return sp_in(cl, k, i); }, sm);
             if (tid == 0) {
-                sm.cnt = 0u;
                 sm.tok = -1;
                 sm.need_exact = 0;
             }
-            for (int u = tid; u < SP_CAP; u += SP_NT) sm.list[u] = ~0ull;
-            __syncthreads();
-            for (int i = tid; i < V; i += SP_NT) {
-                const unsigned k = wk[i];
-                if (!sp_in(cl, k, i)) continue;
-                const unsigned q = atomicAdd(&sm.cnt, 1u);
-                if (q < (unsigned)SP_CAP) sm.list[q] = ((u64)(~k) << 32) | (unsigned)i;
-            }
-            __syncthreads();
             int n2 = 2;
             while (n2 < (int)M) n2 <<= 1;
             for (int k = 2; k <= n2; k <<= 1)
                 for (int j = k >> 1; j > 0; j >>= 1) {
                     if (tid < n2 / 2) {
                         const int i = 2 * tid - (tid & (j - 1)), l = i + j;
-                        const u64 x = sm.list[i], y = sm.list[l];
-                        if ((x > y) == ((i & k) == 0)) {
-                            sm.list[i] = y;
-                            sm.list[l] = x;
+                        const u64 xa = sm.list[i], ya = sm.list[l];
+                        if ((xa > ya) == ((i & k) == 0)) {
+                            sm.list[i] = ya;
+                            sm.list[l] = xa;
                         }
                     }
                     __syncthreads();
@@ -708,28 +957,28 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, un
             SpCut cf = ck;
             u64 mkept = mk;
             if (pon) {
-                const SpSel sp = sp_select(wk, V, true, (u64)((double)a.top_p * SP_ONE), ck, sm);
+                const SpSel sp = sp_select<KPT>(wk, V, true, (u64)((double)a.top_p * 1152921504606846976.0), ck, khi, sm);
                 if (sp.found) {
                     cf = SpCut{true, sp.key, sp.idx};
                     mkept = sp.mass;
                 }
             }
-            if ((double)mkept > 1e-6 * SP_ONE) {
+            if ((double)mkept > 1e-6 * 1152921504606846976.0) {
                 SpSel sd{};
                 bool first = !(r > 0.0f);
                 if (!first) {
                     const u64 Tt = (u64)ceil((double)r * (double)mkept);  // >= 1
-                    sd = sp_select(wk, V, true, Tt - 1, cf, sm);
+                    sd = sp_select<KPT>(wk, V, true, Tt - 1, cf, khi, sm);
                     first = !sd.found;
                 }
-                if (first) sd = sp_select(wk, V, false, 0, cf, sm);
+                if (first) sd = sp_select<KPT>(wk, V, false, 0, cf, khi, sm);
                 tok = sd.idx;
             } else {
                 tok = -2;
             }
         }
     }
-    if (tok == -2) tok = sp_argmax(lg, V, sm);
+    if (tok == -2) tok = sp_argmax<KPT>(lg, V, sm);
     if (tid == 0) am_store(out, row, tok < 0 ? 0 : tok, app);
 }
 
@@ -776,10 +1025,36 @@ void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, in
     hipLaunchKernelGGL(k_rep_penalty, dim3((unsigned)B), dim3(256), 0, st, logits, V, seq, stride, len, ctx, pen);
 }
 
-void launch_sample(const float *logits, int rows, int V, unsigned *ws, const SampleParams &sp, int32_t *out,
+size_t sample_workspace_bytes(int rows, int V) {
+    const size_t NB = (size_t)(V + SP_EPB - 1) / SP_EPB, R = (size_t)rows;
+    return R * NB * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + 2 * R * NB * sizeof(float) + R * (size_t)V * 4;
+}
+
+void launch_sample(const float *logits, int rows, int V, void *ws, const SampleParams &sp, int32_t *out,
                    hipStream_t st, const TokenAppend *app) {
     const TokenAppend a = app ? *app : TokenAppend{};
-    hipLaunchKernelGGL(k_sample, dim3((unsigned)rows), dim3(SP_NT), 0, st, logits, V, ws, sp, out, a);
+    const int NB = (V + SP_EPB - 1) / SP_EPB;
+    const size_t R = (size_t)rows;
+    u64 *hm = (u64 *)ws;
+    unsigned *hc = (unsigned *)(hm + R * NB * SP_NBIN);
+    float *pmax = (float *)(hc + R * NB * SP_NBIN), *psum = pmax + R * NB;
+    unsigned *wk = (unsigned *)(psum + R * NB);
+    const dim3 ge((unsigned)NB, (unsigned)rows);
+    hipLaunchKernelGGL(k_samp_scale, ge, dim3(SP_PT), 0, st, logits, V, (float *)wk, pmax, sp);
+    if (!sp.greedy) {
+        hipLaunchKernelGGL(k_samp_exp, ge, dim3(SP_PT), 0, st, V, (float *)wk, pmax, psum);
+        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, hc, hm);
+    }
+    const dim3 g((unsigned)rows), b(SP_NT);
+    const int kpt = (V + SP_NT - 1) / SP_NT;
+    if (kpt <= 4)
+        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+    else if (kpt <= 16)
+        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+    else if (kpt <= 32)
+        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+    else
+        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
 }
 
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {

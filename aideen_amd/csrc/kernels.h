@@ -259,8 +259,9 @@ void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, in
 // repetition penalty over each row's context (the last `window` of seq[row][0, len), len from
 // lens[row] when lens is set), the temperature, softmax, top-k, top-p, the renormalisation and the
 // draw uni[row * uni_stride] (rng.gen::<f32>(), in [0, 1)); with `greedy` (temperature <= 0) the
-// arg-max of the penalised row.  ws [rows][V] is workspace; the token is stored as the arg-max
-// kernels store theirs.
+// arg-max of the penalised row.  ws (sample_workspace_bytes) is workspace; the token is stored as
+// the arg-max kernels store theirs.  V <= SAMPLE_VMAX.
+constexpr int SAMPLE_VMAX = 65536;
 struct SampleParams {
     const int32_t *seq;
     int stride, len;
@@ -272,7 +273,8 @@ struct SampleParams {
     int uni_stride;
     bool greedy;
 };
-void launch_sample(const float *logits, int rows, int V, unsigned *ws, const SampleParams &sp, int32_t *out,
+size_t sample_workspace_bytes(int rows, int V);
+void launch_sample(const float *logits, int rows, int V, void *ws, const SampleParams &sp, int32_t *out,
                    hipStream_t st, const TokenAppend *app = nullptr);
 // last[b] = seq[b][len - 1]
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st);

@@ -1244,7 +1244,7 @@ int decode_run(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32_t *pro
         unsigned *sws = nullptr;
         float *uni = nullptr;
         if (smp) {
-            sws = (unsigned *)staging_f(c, 31, (size_t)batch * D.V * sizeof(float));
+            sws = (unsigned *)staging_f(c, 31, sample_workspace_bytes(batch, D.V));
             uni = staging_f(c, 32, (size_t)batch * n_new * sizeof(float));
             ADN_HIP(hipMemcpyAsync(uni, smp->uniforms, (size_t)batch * n_new * sizeof(float), hipMemcpyHostToDevice,
                                    st));
@@ -1354,6 +1354,7 @@ int adn_decode_sample(adn_ctx *c, int32_t batch, int32_t prompt_len, const int32
         return decode_run(c, batch, prompt_len, prompt, n_new, ctx_len, max_iters, eps, damping, repetition_penalty,
                           nullptr, out_tokens);
     if (!uniforms && n_new > 0) return fail(ADN_E_INVALID, "null uniforms");
+    if (c && c->D.V > SAMPLE_VMAX) return fail(ADN_E_INVALID, "sampling supports vocabularies up to 65536");
     const SampleCfg smp{temperature, top_p, top_k, uniforms};
     return decode_run(c, batch, prompt_len, prompt, n_new, ctx_len, max_iters, eps, damping, repetition_penalty, &smp,
                       out_tokens);
@@ -1363,7 +1364,8 @@ int adn_lm_sample(adn_ctx *c, int32_t rows, int32_t vocab, const float *logits, 
                   int32_t ctx_stride, const int32_t *ctx_len, float temperature, float top_p, int32_t top_k,
                   float repetition_penalty, const float *uniforms, int32_t *tokens) {
     if (!c || !logits || !tokens || !uniforms) return fail(ADN_E_INVALID, "null argument");
-    if (rows < 0 || vocab < 1) return fail(ADN_E_INVALID, "rows must be >= 0 and vocab >= 1");
+    if (rows < 0 || vocab < 1 || vocab > SAMPLE_VMAX)
+        return fail(ADN_E_INVALID, "rows must be >= 0 and vocab in [1, 65536]");
     if (ctx_stride < 0 || (ctx_stride > 0 && (!context || !ctx_len)))
         return fail(ADN_E_INVALID, "a context needs its tokens and lengths");
     int rc = check_sample_args(temperature, top_p, top_k, repetition_penalty);
@@ -1387,7 +1389,7 @@ int adn_lm_sample(adn_ctx *c, int32_t rows, int32_t vocab, const float *logits, 
         } else {
             ADN_HIP(hipMemsetAsync(lens, 0, (size_t)rows * sizeof(int32_t), st));
         }
-        unsigned *ws = (unsigned *)staging_f(c, 31, n * sizeof(float));
+        unsigned *ws = (unsigned *)staging_f(c, 31, sample_workspace_bytes(rows, vocab));
         float *uni = staging_f(c, 32, (size_t)rows * sizeof(float));
         ADN_HIP(hipMemcpyAsync(uni, uniforms, (size_t)rows * sizeof(float), hipMemcpyHostToDevice, st));
         // lm_head.rs:104-111: a temperature <= 0 is the arg-max of the penalised row
