@@ -456,12 +456,17 @@ __device__ void sp_scan(u64 &c, u64 &m, SampleSmem &sm) {
 
 // 1. the repetition penalty (lm_head.rs:81-99: the context's distinct tokens, here a bit set of
 // the block's range), 2. the temperature (:103-111; none with `greedy`), the block's maximum as
-// f32::max folds it (NaN skipped)
+// f32::max folds it (NaN skipped); the row's bin histogram cleared
 __global__ __launch_bounds__(SP_PT) void k_samp_scale(const float *logits, int V, float *w, float *pmax,
-                                                      SampleParams a) {
+                                                      unsigned *gc, u64 *gm, SampleParams a) {
     __shared__ unsigned bits[SP_EPB / 32];
     __shared__ float red[SP_PT / 64];
     const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    // the row's bin histogram starts at zero (k_samp_keys adds to it)
+    for (int q = b * SP_PT + tid; q < SP_NBIN; q += NB * SP_PT) {
+        gc[(long)row * SP_NBIN + q] = 0u;
+        gm[(long)row * SP_NBIN + q] = 0ull;
+    }
     const int i0 = b * SP_EPB;
     const float *lg = logits + (long)row * V;
     float *wr = w + (long)row * V;
@@ -533,8 +538,9 @@ __global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float
     if (tid == 0) psum[(long)row * NB + b] = s;
 }
 
-// S = the blocks' sums in block order; the keys, and the block's histogram of them by bin
-__global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const float *psum, unsigned *hc, u64 *hm) {
+// S = the blocks' sums in block order; the keys, and their histogram by bin added into the row's
+// (integer sums: their order does not matter)
+__global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const float *psum, unsigned *gc, u64 *gm) {
     __shared__ unsigned c[SP_NBIN];
     __shared__ u64 m[SP_NBIN];
     __shared__ float part[SP_PT];
@@ -570,10 +576,11 @@ __global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const f
         }
     }
     __syncthreads();
-    for (int q = tid; q < SP_NBIN; q += SP_PT) {
-        hc[((long)row * NB + b) * SP_NBIN + q] = c[q];
-        hm[((long)row * NB + b) * SP_NBIN + q] = m[q];
-    }
+    for (int q = tid; q < SP_NBIN; q += SP_PT)
+        if (c[q]) {
+            atomicAdd(&gc[(long)row * SP_NBIN + q], c[q]);
+            atomicAdd(&gm[(long)row * SP_NBIN + q], m[q]);
+        }
 }
 
 // The first item of the list that `cut` keeps at which the running count (by_mass false) or the
@@ -813,7 +820,7 @@ __device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
 
 template <int KPT>
 __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, int NB, unsigned *ws, const float *psum,
-                                                  const unsigned *hc, const u64 *hm, SampleParams a, int32_t *out,
+                                                  const unsigned *gc, const u64 *gm, SampleParams a, int32_t *out,
                                                   TokenAppend app) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x, tid = threadIdx.x;
@@ -835,27 +842,119 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
     // sum then fails `sum > 1e-6`
     if (S == S) {
         const unsigned khi = __float_as_uint(1.0f / S);  // the largest key: exp(0) / S
-        {
-            // bin tid over the blocks (NB <= 32), the loads issued together
-            unsigned c = 0u;
-            u64 m = 0ull;
-#pragma unroll
-            for (int q = 0; q < (SAMPLE_VMAX + SP_EPB - 1) / SP_EPB; ++q)
-                if (q < NB) {
-                    c += hc[((long)row * NB + q) * SP_NBIN + tid];
-                    m += hm[((long)row * NB + q) * SP_NBIN + tid];
-                }
-            sm.oc[tid] = c;
-            sm.om[tid] = m;
-            u64 cc = c, mm = m;
-            sp_scan(cc, mm, sm);
-            if (tid == SP_NT - 1) sm.bm = mm;
-            __syncthreads();
-        }
+        // the row's bins (thread t, bin t) and their running sums from the largest keys down
+        const unsigned c_t = gc[(long)row * SP_NBIN + tid];
+        const u64 m_t = gm[(long)row * SP_NBIN + tid];
+        sm.oc[tid] = c_t;
+        sm.om[tid] = m_t;
+        u64 ic_t = c_t, im_t = m_t;
+        sp_scan(ic_t, im_t, sm);
+        if (tid == SP_NT - 1) sm.bm = im_t;
+        __syncthreads();
         const u64 total = sm.bm;
         __syncthreads();
         const bool kon = a.top_k > 0 && a.top_k < V, pon = a.top_p > 0.0f && a.top_p < 1.0f;
         const SpCut none{false, 0u, 0};
+        // The common case: the list up to the decision lies in a prefix of bins of at most SP_CAP
+        // items: the bins through the top_k-th item; without top-k, the bins whose weight exceeds
+        // top_p by 2^-10 of slack, or (no cut at all) reaches the draw's share of the total by it.
+        // That prefix is gathered, sorted, and the reference's loops run on it.
+        bool done = false;
+        if (!kon || a.top_k <= SP_CAP) {
+            const u64 slack = 1ull << 50;
+            bool past;
+            if (kon)
+                past = ic_t >= (u64)a.top_k;
+            else if (pon)
+                past = im_t > (u64)((double)a.top_p * 1152921504606846976.0) + slack;
+            else
+                past = (double)im_t >= (double)r * (double)total + (double)slack;
+            const int db = min(SP_NBIN - 1, __syncthreads_count(!past));  // the bins before the deciding one
+            if (tid == db) {
+                sm.bn = ic_t;  // the prefix's items
+                const u64 top = (u64)khi + 1;
+                sm.blo = db == SP_NBIN - 1 ? 0u
+                                           : (unsigned)(top > ((u64)(db + 1) << SP_BSH) ? top - ((u64)(db + 1) << SP_BSH) : 0);
+            }
+            __syncthreads();
+            const u64 P = sm.bn;
+            const unsigned plo = sm.blo;
+            __syncthreads();
+            if (P <= (u64)SP_CAP) {
+                sp_gather<KPT>(wk, V, [&](int, unsigned k) { return k >= plo; }, sm);
+                int n2 = 2;
+                while (n2 < (int)P) n2 <<= 1;
+                for (int k = 2; k <= n2; k <<= 1)
+                    for (int j = k >> 1; j > 0; j >>= 1) {
+                        if (tid < n2 / 2) {
+                            const int i = 2 * tid - (tid & (j - 1)), l = i + j;
+                            const u64 xa = sm.list[i], ya = sm.list[l];
+                            if ((xa > ya) == ((i & k) == 0)) {
+                                sm.list[i] = ya;
+                                sm.list[l] = xa;
+                            }
+                        }
+                        __syncthreads();
+                    }
+                if (tid == 0) {
+                    // the reference's loops (:120-166) over the sorted prefix; `full`: the prefix
+                    // is the whole row
+                    auto pk = [&](int i) { return __uint_as_float(~(unsigned)(sm.list[i] >> 32)); };
+                    auto ix = [&](int i) { return (int)(unsigned)(sm.list[i] & 0xffffffffull); };
+                    const bool full = P == (u64)V;
+                    int n = kon ? a.top_k : (int)P;
+                    bool ok = true;
+                    if (pon) {
+                        float cum = 0.0f;
+                        int cut = -1;
+                        for (int i = 0; i < n; ++i) {
+                            cum += pk(i);
+                            if (cum > a.top_p) {
+                                cut = i + 1;
+                                break;
+                            }
+                        }
+                        if (cut < 0) {
+                            if (kon || full)
+                                cut = n;
+                            else
+                                ok = false;  // the float sum crossed later than the slack allowed for
+                        }
+                        n = cut < 1 ? 1 : cut;
+                    }
+                    int t = -1;
+                    if (ok) {
+                        // the kept list is in the prefix unless no cut applies to a partial prefix:
+                        // then its sum is the row's exact weight
+                        const bool whole = kon || pon || full;
+                        float sum = -0.0f;
+                        if (whole)
+                            for (int i = 0; i < n; ++i) sum += pk(i);
+                        else
+                            sum = (float)((double)total * (1.0 / 1152921504606846976.0));
+                        if (!(sum > 1e-6f)) {
+                            t = -2;
+                        } else {
+                            float cum = 0.0f;
+                            for (int i = 0; i < n; ++i) {
+                                cum += pk(i) / sum;
+                                if (r <= cum) {
+                                    t = ix(i);
+                                    break;
+                                }
+                            }
+                            if (t < 0 && whole) t = ix(0);
+                        }
+                    }
+                    sm.tok = t;  // -1: decide on the exact sums below
+                }
+                __syncthreads();
+                tok = sm.tok;
+                done = tok != -1;
+                __syncthreads();
+            }
+        }
+        if (!done) {
         // 3. top-k (:121-125): the list ends at its top_k-th item
         SpCut ck = none;
         u64 nk = (u64)V, mk = total;
@@ -977,6 +1076,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
                 tok = -2;
             }
         }
+        }  // !done
     }
     if (tok == -2) tok = sp_argmax<KPT>(lg, V, sm);
     if (tid == 0) am_store(out, row, tok < 0 ? 0 : tok, app);
@@ -1027,7 +1127,7 @@ void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, in
 
 size_t sample_workspace_bytes(int rows, int V) {
     const size_t NB = (size_t)(V + SP_EPB - 1) / SP_EPB, R = (size_t)rows;
-    return R * NB * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + 2 * R * NB * sizeof(float) + R * (size_t)V * 4;
+    return R * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + 2 * R * NB * sizeof(float) + R * (size_t)V * 4;
 }
 
 void launch_sample(const float *logits, int rows, int V, void *ws, const SampleParams &sp, int32_t *out,
@@ -1035,26 +1135,26 @@ void launch_sample(const float *logits, int rows, int V, void *ws, const SampleP
     const TokenAppend a = app ? *app : TokenAppend{};
     const int NB = (V + SP_EPB - 1) / SP_EPB;
     const size_t R = (size_t)rows;
-    u64 *hm = (u64 *)ws;
-    unsigned *hc = (unsigned *)(hm + R * NB * SP_NBIN);
-    float *pmax = (float *)(hc + R * NB * SP_NBIN), *psum = pmax + R * NB;
+    u64 *gm = (u64 *)ws;
+    unsigned *gc = (unsigned *)(gm + R * SP_NBIN);
+    float *pmax = (float *)(gc + R * SP_NBIN), *psum = pmax + R * NB;
     unsigned *wk = (unsigned *)(psum + R * NB);
     const dim3 ge((unsigned)NB, (unsigned)rows);
-    hipLaunchKernelGGL(k_samp_scale, ge, dim3(SP_PT), 0, st, logits, V, (float *)wk, pmax, sp);
+    hipLaunchKernelGGL(k_samp_scale, ge, dim3(SP_PT), 0, st, logits, V, (float *)wk, pmax, gc, gm, sp);
     if (!sp.greedy) {
         hipLaunchKernelGGL(k_samp_exp, ge, dim3(SP_PT), 0, st, V, (float *)wk, pmax, psum);
-        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, hc, hm);
+        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, gc, gm);
     }
     const dim3 g((unsigned)rows), b(SP_NT);
     const int kpt = (V + SP_NT - 1) / SP_NT;
     if (kpt <= 4)
-        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
     else if (kpt <= 16)
-        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
     else if (kpt <= 32)
-        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
     else
-        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, hc, hm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
 }
 
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {
