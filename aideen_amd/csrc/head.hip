@@ -316,7 +316,8 @@ __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *
 // workspace row ws[V]: k_samp_scale writes the penalised and scaled logits and each block's
 // maximum; k_samp_exp writes e = exp(l - max) and each block's sum; k_samp_keys writes the bit
 // pattern ("key") of p = e / S and each block's histogram of count and weight over SP_NBIN bins
-// of p below its largest value (128 per octave).  p lies in [0, 1] (the maximum contributes exp(0) = 1 to S),
+// of key below the largest (bins of 2^sh keys: the narrowest power of two, at most 1/128 octave,
+// at which the bins span the row's positive probabilities; a flat row gets fine bins).  p lies in [0, 1] (the maximum contributes exp(0) = 1 to S),
 // so keys order as p does, and the reference's sorted list (p descending by a stable sort: ties
 // keep index order) is the order "key descending, index ascending".  A probability weighs
 // floor(p * 2^60) in exact integer sums (the sum over a row stays below 2^61).
@@ -333,8 +334,9 @@ constexpr int SP_NT = 1024;          // k_sample's threads
 constexpr int SP_CAP = 2048;         // lists sorted in LDS
 constexpr int SP_PT = 256;           // threads of the per-element kernels
 constexpr int SP_EPB = SP_PT * 8;    // elements per block of the per-element kernels
-constexpr int SP_NBIN = 1024;        // bins of p below the largest: 128 per octave over 8 octaves
-constexpr int SP_BSH = 16;           // (the last takes all below); a bin spans 2^16 key values
+constexpr int SP_NBIN = 1024;        // bins of p below the largest (the last takes all below): a bin
+constexpr int SP_BSH = 16;           // spans 2^sh key values, sh <= SP_BSH (1/128 octave) chosen so
+                                     // that the bins span the row's keys where they fit
 static_assert(SP_NBIN == SP_NT, "k_sample's thread t takes bin t");
 typedef unsigned long long u64;
 
@@ -404,7 +406,16 @@ __device__ __forceinline__ bool sp_in(const SpCut &c, unsigned k, int i) {
 }
 
 // the bin of key k below the largest key khi (k <= khi)
-__device__ __forceinline__ int sp_bin(unsigned khi, unsigned k) { return min(SP_NBIN - 1, (int)((khi - k) >> SP_BSH)); }
+__device__ __forceinline__ int sp_bin(unsigned khi, unsigned k, int sh) { return min(SP_NBIN - 1, (int)((khi - k) >> sh)); }
+
+// the bin width for keys from kmin to khi: the narrowest power of two at which SP_NBIN bins span
+// them, at most 2^SP_BSH
+__device__ __forceinline__ int sp_bin_shift(unsigned khi, unsigned kmin) {
+    const unsigned span = khi - kmin;  // the bins must hold span + 1 key values
+    int sh = 0;
+    while (sh < SP_BSH && (span >> sh) >= (unsigned)SP_NBIN) ++sh;
+    return sh;
+}
 
 template <int NT>
 __device__ float sp_bmax(float v, float *red) {
@@ -507,8 +518,8 @@ __global__ __launch_bounds__(SP_PT) void k_samp_scale(const float *logits, int V
     if (tid == 0) pmax[(long)row * NB + b] = mx;
 }
 
-// e = exp(l - max) and the block's sum (softmax, lm_head.rs:71-76)
-__global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float *pmax, float *psum) {
+// e = exp(l - max), the block's sum (softmax, lm_head.rs:71-76) and its smallest positive e
+__global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float *pmax, float *psum, float *pmin) {
     __shared__ float red[SP_PT / 64];
     __shared__ float part[SP_PT];
     const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
@@ -524,7 +535,7 @@ __global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float
         const int i = i0 + tid + e * SP_PT;
         v[e] = i < V ? wr[i] : 0.0f;
     }
-    float s = 0.0f;
+    float s = 0.0f, mn = INFINITY;
 #pragma unroll
     for (int e = 0; e < SP_EPB / SP_PT; ++e) {
         const int i = i0 + tid + e * SP_PT;
@@ -532,27 +543,40 @@ __global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float
             const float x = expf(v[e] - mx);
             wr[i] = x;
             s += x;
+            if (x > 0.0f) mn = fminf(mn, x);
         }
     }
     s = sp_bsum<SP_PT>(s, red);
-    if (tid == 0) psum[(long)row * NB + b] = s;
+    mn = -sp_bmax<SP_PT>(-mn, red);
+    if (tid == 0) {
+        psum[(long)row * NB + b] = s;
+        pmin[(long)row * NB + b] = mn;
+    }
 }
 
 // S = the blocks' sums in block order; the keys, and their histogram by bin added into the row's
 // (integer sums: their order does not matter)
-__global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const float *psum, unsigned *gc, u64 *gm) {
+__global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const float *psum, const float *pmin,
+                                                     unsigned *gc, u64 *gm) {
     __shared__ unsigned c[SP_NBIN];
     __shared__ u64 m[SP_NBIN];
-    __shared__ float part[SP_PT];
+    __shared__ float part[SP_PT], partm[SP_PT];
     const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int i0 = b * SP_EPB;
     unsigned *wr = w + (long)row * V;
-    for (int q = tid; q < NB; q += SP_PT) part[q] = psum[(long)row * NB + q];
+    for (int q = tid; q < NB; q += SP_PT) {
+        part[q] = psum[(long)row * NB + q];
+        partm[q] = pmin[(long)row * NB + q];
+    }
     __syncthreads();
-    float S = 0.0f;
-    for (int q = 0; q < NB; ++q) S += part[q];
+    float S = 0.0f, emin = INFINITY;
+    for (int q = 0; q < NB; ++q) {
+        S += part[q];
+        emin = fminf(emin, partm[q]);
+    }
     if (!(S == S)) return;  // k_sample takes the arg-max of the row as given
     const unsigned khi = __float_as_uint(1.0f / S);
+    const int sh = sp_bin_shift(khi, __float_as_uint(emin / S));
     for (int q = tid; q < SP_NBIN; q += SP_PT) {
         c[q] = 0u;
         m[q] = 0ull;
@@ -570,7 +594,7 @@ __global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const f
         if (i < V) {
             const unsigned k = __float_as_uint(__uint_as_float(v[e]) / S);
             wr[i] = k;
-            const int d = sp_bin(khi, k);
+            const int d = sp_bin(khi, k, sh);
             atomicAdd(&c[d], 1u);
             atomicAdd(&m[d], sp_mass(k));
         }
@@ -591,13 +615,13 @@ __global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const f
 // one key value held by more (equal probabilities) is searched in index order.
 template <int KPT>
 __device__ __noinline__ SpSel sp_select(const unsigned *ws, int V, bool by_mass, u64 T, const SpCut &cut, unsigned khi,
-                                        SampleSmem &sm) {
+                                        int bsh, SampleSmem &sm) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int dcut = cut.on ? sp_bin(khi, cut.key) : SP_NBIN - 1;
+    const int dcut = cut.on ? sp_bin(khi, cut.key, bsh) : SP_NBIN - 1;
     u64 cp = 0, mp = 0;  // the kept items of the cut item's bin
     if (cut.on) {
         sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
-            if (i < V && sp_bin(khi, k) == dcut && sp_in(cut, k, i)) {
+            if (i < V && sp_bin(khi, k, bsh) == dcut && sp_in(cut, k, i)) {
                 cp += 1;
                 mp += sp_mass(k);
             }
@@ -626,11 +650,11 @@ __device__ __noinline__ SpSel sp_select(const unsigned *ws, int V, bool by_mass,
         sm.bc = ic - cd;
         sm.bm = im - md;
         sm.bn = cd;
-        // bin dd0: keys in [khi + 1 - (dd0 + 1) 2^16, khi + 1 - dd0 2^16) (the last bin down to 0)
+        // bin dd0: keys in [khi + 1 - (dd0 + 1) 2^bsh, khi + 1 - dd0 2^bsh) (the last bin down to 0)
         const u64 top = (u64)khi + 1;
-        const u64 lo = dd0 == SP_NBIN - 1 ? 0 : (top > ((u64)(dd0 + 1) << SP_BSH) ? top - ((u64)(dd0 + 1) << SP_BSH) : 0);
+        const u64 lo = dd0 == SP_NBIN - 1 ? 0 : (top > ((u64)(dd0 + 1) << bsh) ? top - ((u64)(dd0 + 1) << bsh) : 0);
         sm.blo = (unsigned)lo;
-        sm.bhi = (unsigned)(top - ((u64)dd0 << SP_BSH));
+        sm.bhi = (unsigned)(top - ((u64)dd0 << bsh));
     }
     __syncthreads();
     const int dd = dd0 < SP_NBIN ? dd0 : -1;
@@ -820,8 +844,8 @@ __device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
 
 template <int KPT>
 __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, int NB, unsigned *ws, const float *psum,
-                                                  const unsigned *gc, const u64 *gm, SampleParams a, int32_t *out,
-                                                  TokenAppend app) {
+                                                  const float *pmin, const unsigned *gc, const u64 *gm, SampleParams a,
+                                                  int32_t *out, TokenAppend app) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x, tid = threadIdx.x;
     const float *lg = logits + (long)row * V;
@@ -832,16 +856,23 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
         return;
     }
     // the blocks' partials staged through LDS (one load per thread, not a chain of loads)
-    for (int q = tid; q < NB; q += SP_NT) sm.wf2[q] = psum[(long)row * NB + q];
+    for (int q = tid; q < NB; q += SP_NT) {
+        sm.wf2[q] = psum[(long)row * NB + q];
+        sm.wf2[SP_NT / 2 + q] = pmin[(long)row * NB + q];
+    }
     __syncthreads();
-    float S = 0.0f;
-    for (int q = 0; q < NB; ++q) S += sm.wf2[q];
+    float S = 0.0f, emin = INFINITY;
+    for (int q = 0; q < NB; ++q) {
+        S += sm.wf2[q];
+        emin = fminf(emin, sm.wf2[SP_NT / 2 + q]);
+    }
     const float r = a.uni[(long)row * a.uni_stride];
     int tok = -2;  // -2: LmHead::argmax of the row as given (lm_head.rs:148-150)
     // a NaN S (a NaN or infinite logit, or no finite one) makes every p NaN: the reference's kept
     // sum then fails `sum > 1e-6`
     if (S == S) {
         const unsigned khi = __float_as_uint(1.0f / S);  // the largest key: exp(0) / S
+        const int bsh = sp_bin_shift(khi, __float_as_uint(emin / S));  // as k_samp_keys binned
         // the row's bins (thread t, bin t) and their running sums from the largest keys down
         const unsigned c_t = gc[(long)row * SP_NBIN + tid];
         const u64 m_t = gm[(long)row * SP_NBIN + tid];
@@ -874,7 +905,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
                 sm.bn = ic_t;  // the prefix's items
                 const u64 top = (u64)khi + 1;
                 sm.blo = db == SP_NBIN - 1 ? 0u
-                                           : (unsigned)(top > ((u64)(db + 1) << SP_BSH) ? top - ((u64)(db + 1) << SP_BSH) : 0);
+                                           : (unsigned)(top > ((u64)(db + 1) << bsh) ? top - ((u64)(db + 1) << bsh) : 0);
             }
             __syncthreads();
             const u64 P = sm.bn;
@@ -959,7 +990,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
         SpCut ck = none;
         u64 nk = (u64)V, mk = total;
         if (kon) {
-            const SpSel sk = sp_select<KPT>(wk, V, false, (u64)(a.top_k - 1), none, khi, sm);
+            const SpSel sk = sp_select<KPT>(wk, V, false, (u64)(a.top_k - 1), none, khi, bsh, sm);
             ck = SpCut{true, sk.key, sk.idx};
             nk = sk.cnt;
             mk = sk.mass;
@@ -971,7 +1002,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
         bool full = true;
         if (!(kon && a.top_k <= SP_CAP) && pon) {
             const SpSel sp = sp_select<KPT>(wk, V, true, (u64)((double)a.top_p * 1152921504606846976.0) + (1ull << 50),
-                                            ck, khi, sm);
+                                            ck, khi, bsh, sm);
             if (sp.found) {
                 cl = SpCut{true, sp.key, sp.idx};
                 M = sp.cnt;
@@ -1056,7 +1087,7 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
             SpCut cf = ck;
             u64 mkept = mk;
             if (pon) {
-                const SpSel sp = sp_select<KPT>(wk, V, true, (u64)((double)a.top_p * 1152921504606846976.0), ck, khi, sm);
+                const SpSel sp = sp_select<KPT>(wk, V, true, (u64)((double)a.top_p * 1152921504606846976.0), ck, khi, bsh, sm);
                 if (sp.found) {
                     cf = SpCut{true, sp.key, sp.idx};
                     mkept = sp.mass;
@@ -1067,10 +1098,10 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
                 bool first = !(r > 0.0f);
                 if (!first) {
                     const u64 Tt = (u64)ceil((double)r * (double)mkept);  // >= 1
-                    sd = sp_select<KPT>(wk, V, true, Tt - 1, cf, khi, sm);
+                    sd = sp_select<KPT>(wk, V, true, Tt - 1, cf, khi, bsh, sm);
                     first = !sd.found;
                 }
-                if (first) sd = sp_select<KPT>(wk, V, false, 0, cf, khi, sm);
+                if (first) sd = sp_select<KPT>(wk, V, false, 0, cf, khi, bsh, sm);
                 tok = sd.idx;
             } else {
                 tok = -2;
@@ -1127,7 +1158,7 @@ void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, in
 
 size_t sample_workspace_bytes(int rows, int V) {
     const size_t NB = (size_t)(V + SP_EPB - 1) / SP_EPB, R = (size_t)rows;
-    return R * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + 2 * R * NB * sizeof(float) + R * (size_t)V * 4;
+    return R * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + 3 * R * NB * sizeof(float) + R * (size_t)V * 4;
 }
 
 void launch_sample(const float *logits, int rows, int V, void *ws, const SampleParams &sp, int32_t *out,
@@ -1137,24 +1168,24 @@ void launch_sample(const float *logits, int rows, int V, void *ws, const SampleP
     const size_t R = (size_t)rows;
     u64 *gm = (u64 *)ws;
     unsigned *gc = (unsigned *)(gm + R * SP_NBIN);
-    float *pmax = (float *)(gc + R * SP_NBIN), *psum = pmax + R * NB;
-    unsigned *wk = (unsigned *)(psum + R * NB);
+    float *pmax = (float *)(gc + R * SP_NBIN), *psum = pmax + R * NB, *pmin = psum + R * NB;
+    unsigned *wk = (unsigned *)(pmin + R * NB);
     const dim3 ge((unsigned)NB, (unsigned)rows);
     hipLaunchKernelGGL(k_samp_scale, ge, dim3(SP_PT), 0, st, logits, V, (float *)wk, pmax, gc, gm, sp);
     if (!sp.greedy) {
-        hipLaunchKernelGGL(k_samp_exp, ge, dim3(SP_PT), 0, st, V, (float *)wk, pmax, psum);
-        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, gc, gm);
+        hipLaunchKernelGGL(k_samp_exp, ge, dim3(SP_PT), 0, st, V, (float *)wk, pmax, psum, pmin);
+        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, pmin, gc, gm);
     }
     const dim3 g((unsigned)rows), b(SP_NT);
     const int kpt = (V + SP_NT - 1) / SP_NT;
     if (kpt <= 4)
-        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
     else if (kpt <= 16)
-        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
     else if (kpt <= 32)
-        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
     else
-        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
 }
 
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {

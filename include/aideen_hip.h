@@ -232,7 +232,7 @@ int adn_decode_greedy(adn_ctx *ctx, int32_t batch, int32_t prompt_len, const int
  * The decisions are taken on the device's own probabilities; where the kept list has at most 2048
  * items the running sums are the reference's float loops, beyond that exact sums (a token can then
  * differ from the reference only where a running sum lies within its rounding of top_p or the
- * draw).  tokens [rows].  repetition_penalty must be finite and > 0, top_k >= 0. */
+ * draw).  tokens [rows].  repetition_penalty must be finite and > 0, top_k >= 0, vocab <= 65536. */
 int adn_lm_sample(adn_ctx *ctx, int32_t rows, int32_t vocab, const float *logits, const int32_t *context,
                   int32_t ctx_stride, const int32_t *ctx_len, float temperature, float top_p, int32_t top_k,
                   float repetition_penalty, const float *uniforms, int32_t *tokens);
@@ -240,7 +240,7 @@ int adn_lm_sample(adn_ctx *ctx, int32_t rows, int32_t vocab, const float *logits
 /* Trainer::generate (trainer.rs:4219-4431) with LmHead::sample's temperature, top_p, top_k and
  * repetition penalty (lm_head.rs:78-168, as adn_lm_sample): the steps of adn_decode_greedy, then
  * each step's token drawn from its logits with uniforms[b][j] (uniforms [B][n_new]).  A
- * temperature <= 0 is adn_decode_greedy (uniforms unused). */
+ * temperature <= 0 is adn_decode_greedy (uniforms unused).  The model's vocab must be <= 65536. */
 int adn_decode_sample(adn_ctx *ctx, int32_t batch, int32_t prompt_len, const int32_t *prompt, int32_t n_new,
                       int32_t ctx_len, int32_t max_iters, float eps, float damping, float temperature, float top_p,
                       int32_t top_k, float repetition_penalty, const float *uniforms, int32_t *out_tokens);
