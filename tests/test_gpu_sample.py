@@ -190,3 +190,29 @@ def test_c2_decode_sample(oracle_lib):
     upto = first_difference(got[0], ref[0], cond[0], "C2")
     log(f"C2 decode sample: {upto} of 24 steps equal, {len(set(ref.ravel().tolist()))} distinct tokens")
     assert upto >= 12
+
+
+@pytest.mark.parametrize("grp", [(0.8, 0.9, 40, 1.1), (1.0, 1.0, 0, 1.5)], ids=lambda g: "T{}-p{}-k{}-pen{}".format(*g))
+def test_memory_decode_sample_matches_oracle(oracle_lib, grp):
+    """The fixed-history form of Trainer::generate (trainer.rs:4395-4400, 677-735) with
+    LmHead::sample: the memory primed over the prompt, each step the last token's solve with the
+    memory's history context, then the draw; token for token up to a first difference on a draw
+    within rounding of a boundary."""
+    from test_gpu_memory import mem_model
+    from aideen_amd.backend import GpuDeqBackend
+    T, top_p, top_k, pen = grp
+    mc, w = mem_model(128, 4, 400, max_iters=6, eps=0.0)
+    B, T0, n_new, ctx_len = 3, 7, 9, 5
+    prompt = synth.make_tokens("uniform", B, T0, mc.V, seed=14)
+    uni = draws(np.random.default_rng(31), B * n_new).reshape(B, n_new)
+    ref, cond = oracle_lib.Oracle(mc, w).decode_sample(prompt, n_new, ctx_len, T, top_p, top_k, pen, uni)
+    be = GpuDeqBackend(mc, B, T0)
+    be.upload_weights(w)
+    got = be.decode_sample(prompt, n_new, ctx_len, temperature=T, top_p=top_p, top_k=top_k, repetition_penalty=pen,
+                           uniforms=uni, max_iters=6, eps=0.0)
+    greedy = be.decode_greedy(prompt, n_new, ctx_len, max_iters=6, eps=0.0, repetition_penalty=pen)
+    be.close()
+    compared = sum(first_difference(got[b], ref[b], cond[b], f"memory sequence {b}") for b in range(B))
+    log(f"memory decode sample {grp}: {compared} of {B * n_new} steps compared")
+    assert compared >= 0.75 * B * n_new
+    assert not np.array_equal(ref, greedy)
