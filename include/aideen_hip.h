@@ -4,7 +4,8 @@
  * Drop-in boundary for the reference's wgpu compute block (SergioAriel/aideen):
  * the entry points below replace, one for one, the GPU surfaces the Rust crates bind to.
  * Each declaration cites the reference interface it replaces (file:line).  A thin Rust FFI
- * crate binds exactly these symbols (see INTEGRATION.md in the repository root).
+ * crate (an `extern "C"` block with one declaration per function here) binds exactly these
+ * symbols.
  *
  * Conventions
  *   - Every entry point returns ADN_OK (0) or a negative ADN_E_* code; adn_last_error()

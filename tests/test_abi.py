@@ -67,7 +67,7 @@ def test_null_arguments_are_errors():
 
 
 def test_integration_ffi_block_binds_every_header_symbol():
-    """INTEGRATION.md's `extern "C"` block (the Rust -sys crate a maintainer adds) declares every
+    """The integration guide's `extern "C"` block (the Rust -sys crate a maintainer adds) declares every
     function the header does, and nothing else."""
     import os
     text = open(os.path.join(os.path.dirname(_lib.HEADER), "..", "INTEGRATION.md")).read()
