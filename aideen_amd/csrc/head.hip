@@ -324,9 +324,10 @@ __global__ void k_decode_last(const int32_t *seq, int stride, int len, int32_t *
 //
 // k_sample (one workgroup per row) takes the cut points of the list (the top_k-th item, the
 // first item past which the running sum exceeds top_p, the item at which it reaches the draw)
-// without sorting the row: the row's bin histogram names the bin of the crossing, 256-bin LDS
-// histograms of the items inside it narrow it further where it holds more than SP_CAP items, and
-// an interval of at most SP_CAP items is gathered, sorted in LDS and scanned.  When the kept list has at most SP_CAP items (top_k <=
+// without sorting the row: the row's bin histogram names the bin of the crossing, passes counting
+// the items inside it above eight thresholds (in registers) narrow it further where it holds more
+// than SP_CAP items, and an interval of at most SP_CAP items is gathered, sorted in LDS and
+// scanned.  When the kept list has at most SP_CAP items (top_k <=
 // SP_CAP, or a top_p cut within that many items, or a vocabulary that small) it is gathered,
 // sorted, and one thread runs the reference's loops on it in float arithmetic; otherwise the cuts
 // are taken on the exact sums.
@@ -610,9 +611,9 @@ __global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const f
 // The first item of the list that `cut` keeps at which the running count (by_mass false) or the
 // running weight (true) exceeds T.  Not found: cnt and mass are the kept list's totals.  The
 // row's bin histogram (sm.oc, sm.om) names the bin of the crossing (with a cut, the cut item's bin
-// is recounted and the bins below it are empty); 256-bin histograms of the items inside the
-// interval narrow it until it holds at most SP_CAP items, which are gathered, sorted and scanned;
-// one key value held by more (equal probabilities) is searched in index order.
+// is recounted and the bins below it are empty); passes that count and weigh the interval's items
+// above eight thresholds narrow it until it holds at most SP_CAP items, which are gathered, sorted
+// and scanned; one key value held by more (equal probabilities) is searched in index order.
 template <int KPT>
 __device__ __noinline__ SpSel sp_select(const unsigned *ws, int V, bool by_mass, u64 T, const SpCut &cut, unsigned khi,
                                         int bsh, SampleSmem &sm) {
@@ -662,39 +663,98 @@ __device__ __noinline__ SpSel sp_select(const unsigned *ws, int V, bool by_mass,
     unsigned lo = sm.blo, hi = sm.bhi;
     __syncthreads();
     if (dd < 0) return SpSel{0u, -1, cb, mb, false};
-    for (int pass = 0; pass < 8 && n_int > (u64)SP_CAP && hi - lo > 1u; ++pass) {
-        // 256 bins over [lo, hi)
-        const unsigned wd = hi - lo;
-        int sh = 0;
-        while (((wd - 1u) >> sh) >= 256u) ++sh;
-        sm.hc[tid] = 0u;
-        sm.hm[tid] = 0ull;
-        __syncthreads();
+    if (n_int > (u64)SP_CAP) {
+        // the interval narrowed to its smallest and largest key (a tie holding most of the row
+        // then needs no narrowing passes)
+        unsigned kmn = 0xffffffffu, kmx = 0u;
         sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
             if (i < V && k >= lo && k < hi && sp_in(cut, k, i)) {
-                const unsigned bn = (k - lo) >> sh;
-                atomicAdd(&sm.hc[bn], 1u);
-                atomicAdd(&sm.hm[bn], sp_mass(k));
+                kmn = min(kmn, k);
+                kmx = max(kmx, k);
             }
         });
+        if (tid == 0) {
+            sm.blo = 0xffffffffu;
+            sm.bhi = 0u;
+        }
+        __syncthreads();
+        atomicMin(&sm.blo, kmn);
+        atomicMax(&sm.bhi, kmx);
+        __syncthreads();
+        lo = sm.blo;
+        hi = sm.bhi + 1u;
+        __syncthreads();
+    }
+    for (int pass = 0; pass < 12 && n_int > (u64)SP_CAP && hi - lo > 1u; ++pass) {
+        // eight thresholds over [lo, hi): each thread counts and weighs its items above them in
+        // registers (no atomics: a crowded interval holds tens of thousands of items)
+        const unsigned wd = hi - lo;
+        unsigned t[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) t[q] = lo + (unsigned)(((u64)wd * (unsigned)q) >> 3);
+        unsigned c8[8];
+        u64 m8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            c8[q] = 0u;
+            m8[q] = 0ull;
+        }
+        sp_each<KPT>(ws, V, [&](int i, unsigned k, int) {
+            if (i < V && k >= lo && k < hi && sp_in(cut, k, i)) {
+                const u64 mk = sp_mass(k);
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    if (k >= t[q]) {
+                        c8[q] += 1u;
+                        m8[q] += mk;
+                    }
+            }
+        });
+        // block totals: wave butterflies, the waves' partials through LDS, summed by one thread
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            for (int off = 32; off > 0; off >>= 1) {
+                c8[q] += __shfl_xor(c8[q], off, 64);
+                m8[q] += __shfl_xor(m8[q], off, 64);
+            }
+        if (lane == 0)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                sm.hc[w * 8 + q] = c8[q];
+                sm.hm[w * 8 + q] = m8[q];
+            }
+        __syncthreads();
+        if (tid < 8) {  // threshold tid's totals over the waves
+            unsigned ct = 0u;
+            u64 mt = 0ull;
+            for (int x = 0; x < SP_NT / 64; ++x) {
+                ct += sm.hc[x * 8 + tid];
+                mt += sm.hm[x * 8 + tid];
+            }
+            sm.hc[SP_NT / 8 + tid] = ct;
+            sm.hm[SP_NT / 8 + tid] = mt;
+        }
         __syncthreads();
         if (tid == 0) {
-            const int nb = (int)((wd - 1u) >> sh) + 1;
-            u64 c2 = cb, m2 = mb;
-            int sel = 0;
-            for (int q = nb - 1; q >= 0; --q) {  // the largest keys first
-                if ((by_mass ? m2 + sm.hm[q] : c2 + sm.hc[q]) > T) {
-                    sel = q;
-                    break;
+            // the last threshold whose items above it (and the items above the interval) pass T;
+            // the sums fall with q
+            unsigned nlo = lo, nhi = hi;
+            u64 ca = 0, ma = 0, cn = sm.hc[SP_NT / 8];
+            for (int q = 0; q < 8; ++q) {
+                const u64 cq = sm.hc[SP_NT / 8 + q], mq = sm.hm[SP_NT / 8 + q];
+                if ((by_mass ? mb + mq : cb + cq) > T) {
+                    nlo = t[q];
+                    nhi = q < 7 ? t[q < 7 ? q + 1 : 7] : hi;
+                    ca = q < 7 ? (u64)sm.hc[SP_NT / 8 + q + 1] : 0ull;
+                    ma = q < 7 ? sm.hm[SP_NT / 8 + q + 1] : 0ull;
+                    cn = cq - ca;
                 }
-                c2 += sm.hc[q];
-                m2 += sm.hm[q];
             }
-            sm.bc = c2;
-            sm.bm = m2;
-            sm.bn = sm.hc[sel];
-            sm.blo = lo + ((unsigned)sel << sh);
-            sm.bhi = min(hi, lo + ((unsigned)(sel + 1) << sh));
+            sm.bc = cb + ca;
+            sm.bm = mb + ma;
+            sm.bn = cn;
+            sm.blo = nlo;
+            sm.bhi = nhi;
         }
         __syncthreads();
         cb = sm.bc;
@@ -753,22 +813,40 @@ __device__ __noinline__ SpSel sp_select(const unsigned *ws, int V, bool by_mass,
     sp_each<KPT>(ws, V, [&](int i, unsigned k, int u) {
         if (i < V && k == kk && sp_in(cut, k, i)) mine |= 1ull << u;
     });
+    // the matches per slot u (index order is u first): one ballot per slot and wave, summed in LDS
+    for (int u = tid; u < KPT; u += SP_NT) sm.hc[u] = 0u;
     if (tid == 0) sm.tok = -1;
-    u64 run = 0;
+    __syncthreads();
     for (int u = 0; u < KPT; ++u) {
-        const bool pr = (mine >> u) & 1ull;
-        const int cu = __syncthreads_count(pr);
-        if (run + (u64)cu > j) {
-            const u64 bal = __ballot(pr);
-            if (lane == 0) sm.wi[w] = __popcll(bal);
-            __syncthreads();
-            int bw = 0;
-            for (int x = 0; x < w; ++x) bw += sm.wi[x];
-            const int rank = bw + __popcll(bal & ((1ull << lane) - 1ull));
-            if (pr && (u64)rank == j - run) sm.tok = tid + u * SP_NT;
-            break;
+        const u64 bal = __ballot((mine >> u) & 1ull);
+        if (lane == 0 && bal) atomicAdd(&sm.hc[u], (unsigned)__popcll(bal));
+    }
+    __syncthreads();
+    if (tid == 0) {
+        u64 run = 0;
+        int us = KPT;
+        for (int u = 0; u < KPT; ++u) {
+            if (run + sm.hc[u] > j) {
+                us = u;
+                break;
+            }
+            run += sm.hc[u];
         }
-        run += (u64)cu;
+        sm.bsel = us;
+        sm.bn = j - run;  // the rank within slot us
+    }
+    __syncthreads();
+    const int us = sm.bsel;
+    if (us < KPT) {
+        // the rank-th match of slot us in thread order
+        const bool pr = (mine >> us) & 1ull;
+        const u64 bal = __ballot(pr);
+        if (lane == 0) sm.wi[w] = __popcll(bal);
+        __syncthreads();
+        int bw = 0;
+        for (int x = 0; x < w; ++x) bw += sm.wi[x];
+        const int rank = bw + __popcll(bal & ((1ull << lane) - 1ull));
+        if (pr && (u64)rank == sm.bn) sm.tok = tid + us * SP_NT;
     }
     __syncthreads();
     const SpSel r{kk, sm.tok, cb + j + 1, mb + (j + 1) * mu, sm.tok >= 0};
