@@ -63,6 +63,9 @@ def test_null_arguments_are_errors():
     assert L.adn_create(None, None) == _lib.ADN_E_INVALID
     assert L.adn_synchronize(None) == _lib.ADN_E_INVALID
     assert L.adn_forward(None, None, None) == _lib.ADN_E_INVALID
+    assert L.adn_lm_sample(None, 1, 10, None, None, 0, None, 0.8, 0.9, 40, 1.1, None, None) == _lib.ADN_E_INVALID
+    assert L.adn_decode_sample(None, 1, 1, None, 1, 1, 10, 0.0, 0.7, 0.8, 0.9, 40, 1.1, None,
+                               None) == _lib.ADN_E_INVALID
     L.adn_destroy(None)
 
 
