@@ -352,6 +352,7 @@ struct SampleSmem {
     int wi[SP_NT / 64];
     float wf2[SP_NT];  // the blocks' partial sums
     u64 bc, bm, bn;
+    unsigned boff[SAMPLE_VMAX / SP_EPB + 1];  // the blocks' offsets in a gathered prefix
     unsigned cnt, blo, bhi;
     int tok, need_exact, bsel;
 };
@@ -558,9 +559,11 @@ __global__ __launch_bounds__(SP_PT) void k_samp_exp(int V, float *w, const float
 // S = the blocks' sums in block order; the keys, and their histogram by bin added into the row's
 // (integer sums: their order does not matter)
 __global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const float *psum, const float *pmin,
-                                                     unsigned *gc, u64 *gm) {
+                                                     unsigned *gc, u64 *gm, u64 *bucket, unsigned *bcum) {
     __shared__ unsigned c[SP_NBIN];
     __shared__ u64 m[SP_NBIN];
+    __shared__ unsigned cur[SP_NBIN];
+    __shared__ unsigned wsum[SP_PT / 64];
     __shared__ float part[SP_PT], partm[SP_PT];
     const int NB = gridDim.x, b = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
     const int i0 = b * SP_EPB;
@@ -606,6 +609,41 @@ __global__ __launch_bounds__(SP_PT) void k_samp_keys(int V, unsigned *w, const f
             atomicAdd(&gc[(long)row * SP_NBIN + q], c[q]);
             atomicAdd(&gm[(long)row * SP_NBIN + q], m[q]);
         }
+    // the block's items bucketed by bin (bin 0, the largest keys, first) as (~key << 32) | index,
+    // and the running count through each bin: the items of bins 0..d are the first bcum[d]
+    constexpr int BPT = SP_NBIN / SP_PT;  // bins per thread
+    unsigned run = 0;
+#pragma unroll
+    for (int x = 0; x < BPT; ++x) run += c[tid * BPT + x];
+    unsigned inc = run;  // inclusive scan over the threads
+    const int lane = tid & 63, wv = tid >> 6;
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned o = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += o;
+    }
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    for (int x = 0; x < wv; ++x) inc += wsum[x];
+    unsigned st = inc - run;
+    const long hb = ((long)row * NB + b) * SP_NBIN;
+#pragma unroll
+    for (int x = 0; x < BPT; ++x) {
+        const int q = tid * BPT + x;
+        cur[q] = st;
+        st += c[q];
+        bcum[hb + q] = st;
+    }
+    __syncthreads();
+    u64 *bk = bucket + ((long)row * NB + b) * SP_EPB;
+#pragma unroll
+    for (int e = 0; e < SP_EPB / SP_PT; ++e) {
+        const int i = i0 + tid + e * SP_PT;
+        if (i < V) {
+            const unsigned k = __float_as_uint(__uint_as_float(v[e]) / S);
+            const unsigned slot = atomicAdd(&cur[sp_bin(khi, k, sh)], 1u);
+            bk[slot] = ((u64)(~k) << 32) | (unsigned)i;
+        }
+    }
 }
 
 // The first item of the list that `cut` keeps at which the running count (by_mass false) or the
@@ -922,7 +960,8 @@ __device__ int sp_argmax(const float *x, int V, SampleSmem &sm) {
 
 template <int KPT>
 __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, int NB, unsigned *ws, const float *psum,
-                                                  const float *pmin, const unsigned *gc, const u64 *gm, SampleParams a,
+                                                  const float *pmin, const unsigned *gc, const u64 *gm,
+                                                  const u64 *bucket, const unsigned *bcum, SampleParams a,
                                                   int32_t *out, TokenAppend app) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x, tid = threadIdx.x;
@@ -990,7 +1029,23 @@ __global__ __launch_bounds__(SP_NT) void k_sample(const float *logits, int V, in
             const unsigned plo = sm.blo;
             __syncthreads();
             if (P <= (u64)SP_CAP) {
-                sp_gather<KPT>(wk, V, [&](int, unsigned k) { return k >= plo; }, sm);
+                // the prefix's items: block q's first bcum[q][db] bucketed items
+                if (tid < NB) sm.boff[tid + 1] = bcum[((long)row * NB + tid) * SP_NBIN + db];
+                if (tid == 0) sm.boff[0] = 0u;
+                __syncthreads();
+                if (tid == 0)
+                    for (int q = 0; q < NB; ++q) sm.boff[q + 1] += sm.boff[q];
+                __syncthreads();
+                for (int e = tid; e < SP_CAP; e += SP_NT) {
+                    u64 v = ~0ull;
+                    if (e < (int)P) {
+                        int q = 0;
+                        while (q + 1 < NB && sm.boff[q + 1] <= (unsigned)e) ++q;
+                        v = bucket[((long)row * NB + q) * SP_EPB + (e - (int)sm.boff[q])];
+                    }
+                    sm.list[e] = v;
+                }
+                __syncthreads();
                 int n2 = 2;
                 while (n2 < (int)P) n2 <<= 1;
                 for (int k = 2; k <= n2; k <<= 1)
@@ -1236,7 +1291,8 @@ void launch_rep_penalty(float *logits, int V, const int32_t *seq, int stride, in
 
 size_t sample_workspace_bytes(int rows, int V) {
     const size_t NB = (size_t)(V + SP_EPB - 1) / SP_EPB, R = (size_t)rows;
-    return R * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + 3 * R * NB * sizeof(float) + R * (size_t)V * 4;
+    return R * SP_NBIN * (sizeof(u64) + sizeof(unsigned)) + R * NB * SP_EPB * sizeof(u64) +
+           R * NB * SP_NBIN * sizeof(unsigned) + 3 * R * NB * sizeof(float) + R * (size_t)V * 4;
 }
 
 void launch_sample(const float *logits, int rows, int V, void *ws, const SampleParams &sp, int32_t *out,
@@ -1245,25 +1301,27 @@ void launch_sample(const float *logits, int rows, int V, void *ws, const SampleP
     const int NB = (V + SP_EPB - 1) / SP_EPB;
     const size_t R = (size_t)rows;
     u64 *gm = (u64 *)ws;
-    unsigned *gc = (unsigned *)(gm + R * SP_NBIN);
-    float *pmax = (float *)(gc + R * SP_NBIN), *psum = pmax + R * NB, *pmin = psum + R * NB;
+    u64 *bucket = gm + R * SP_NBIN;
+    unsigned *gc = (unsigned *)(bucket + R * NB * SP_EPB);
+    unsigned *bcum = gc + R * SP_NBIN;
+    float *pmax = (float *)(bcum + R * NB * SP_NBIN), *psum = pmax + R * NB, *pmin = psum + R * NB;
     unsigned *wk = (unsigned *)(pmin + R * NB);
     const dim3 ge((unsigned)NB, (unsigned)rows);
     hipLaunchKernelGGL(k_samp_scale, ge, dim3(SP_PT), 0, st, logits, V, (float *)wk, pmax, gc, gm, sp);
     if (!sp.greedy) {
         hipLaunchKernelGGL(k_samp_exp, ge, dim3(SP_PT), 0, st, V, (float *)wk, pmax, psum, pmin);
-        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, pmin, gc, gm);
+        hipLaunchKernelGGL(k_samp_keys, ge, dim3(SP_PT), 0, st, V, wk, psum, pmin, gc, gm, bucket, bcum);
     }
     const dim3 g((unsigned)rows), b(SP_NT);
     const int kpt = (V + SP_NT - 1) / SP_NT;
     if (kpt <= 4)
-        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<4>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, bucket, bcum, sp, out, a);
     else if (kpt <= 16)
-        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<16>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, bucket, bcum, sp, out, a);
     else if (kpt <= 32)
-        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<32>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, bucket, bcum, sp, out, a);
     else
-        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, sp, out, a);
+        hipLaunchKernelGGL(k_sample<64>, g, b, 0, st, logits, V, NB, wk, psum, pmin, gc, gm, bucket, bcum, sp, out, a);
 }
 
 void launch_decode_last(const int32_t *seq, int stride, int len, int32_t *last, int B, hipStream_t st) {
